@@ -1,0 +1,266 @@
+/*
+ * si_hip.h: C ABI of the MI355X (gfx950) GGUF K-quant matvec path.
+ *
+ * Drop-in boundary for super-inference's K-quant surface on `MetalContext`
+ * (src/metal.rs).  A Rust `hip` backend module binds these symbols with an
+ * `extern "C"` block and wraps them in a `HipContext` whose methods keep the
+ * names and `Result<_, String>` behaviour of the Metal methods cited below.
+ *
+ * Conventions
+ *   - Every entry point returns an int status: SI_HIP_OK (0) or a negative
+ *     SI_HIP_ERR_* code.  On failure si_hip_last_error() returns a message
+ *     for the calling thread (the reference's Err(String)).
+ *   - Argument validation runs on the host, before any device work, in the
+ *     same order as the reference; it needs no GPU, so every rejection can be
+ *     exercised on a machine without one (pass ctx = NULL: shape errors are
+ *     reported before the context is checked).
+ *   - "rows"/"columns" follow the reference: a GGUF 2-D tensor has
+ *     shape[0] = columns (contiguous) and shape[1] = rows (metal.rs:4356-4357);
+ *     rows are packed 256-weight super-blocks, row-major.
+ *   - Block bytes: Q4_K 144, Q5_K 176, Q6_K 210 per 256 weights
+ *     (src/quant.rs:8-16); ggml type ids 12 / 13 / 14.
+ *   - Host-pointer entry points are synchronous (the reference commits and
+ *     waits, metal.rs:2320-2337): they copy inputs to HBM, run, copy results
+ *     back, and return.  *_device entry points take device pointers and only
+ *     enqueue on the context's compute stream (see si_hip_synchronize).
+ *   - A context may be shared by several host threads; calls on one context
+ *     are serialised internally.
+ */
+#ifndef SI_HIP_H
+#define SI_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SI_HIP_ABI_VERSION 1u
+
+/* ---- status codes ------------------------------------------------------ */
+#define SI_HIP_OK 0
+#define SI_HIP_ERR_NULL (-1)              /* null context, handle or buffer */
+#define SI_HIP_ERR_DIMENSIONS (-2)        /* rows/cols 0, cols % 256, input length */
+#define SI_HIP_ERR_BYTE_LENGTH (-3)       /* byte length != rows*cols/256*block */
+#define SI_HIP_ERR_OVERFLOW (-4)          /* checked_mul overflow / > u32 limits */
+#define SI_HIP_ERR_UNSUPPORTED_TYPE (-5)  /* ggml type not 12/13/14 (or not Q4_K) */
+#define SI_HIP_ERR_BATCH (-6)             /* batch outside 1..=SI_HIP_MAX_BATCH */
+#define SI_HIP_ERR_RANGE (-7)             /* row range / token id / view range */
+#define SI_HIP_ERR_NO_FINITE (-8)         /* argmax over logits with no finite value */
+#define SI_HIP_ERR_DEVICE (-9)            /* HIP runtime or launch failure */
+#define SI_HIP_ERR_OUT_OF_MEMORY (-10)
+#define SI_HIP_ERR_EMPTY (-11)            /* empty weight upload */
+
+#define SI_HIP_GGML_TYPE_Q4_K 12u
+#define SI_HIP_GGML_TYPE_Q5_K 13u
+#define SI_HIP_GGML_TYPE_Q6_K 14u
+
+/* The reference caps candidate batches at 8 (metal.rs:4076, 1096); the HIP
+ * path accepts up to 16 (the multi-token verify sweep goes to M = 16). */
+#define SI_HIP_MAX_BATCH 16u
+
+/* Greedy argmax tie rules. */
+#define SI_HIP_ARGMAX_LAST_FINITE 0u   /* runtime.rs:4301-4309: finite only,
+                                          total_cmp, last maximum wins */
+#define SI_HIP_ARGMAX_FIRST_GREATER 1u /* qwen35_runtime.rs:2237-2244: strict
+                                          '>' from -inf, first maximum wins */
+
+typedef struct si_hip_context si_hip_context;
+typedef struct si_hip_quant_weight si_hip_quant_weight;
+
+/* CommandStatsSnapshot (metal.rs:1891-1946). */
+typedef struct si_hip_command_stats {
+  uint64_t submitted;
+  uint64_t async_submitted;
+  uint64_t waited;
+  uint64_t wait_nanos;
+} si_hip_command_stats;
+
+/* ---- errors ------------------------------------------------------------ */
+const char *si_hip_last_error(void);       /* thread-local; "" after success */
+const char *si_hip_status_name(int status);
+uint32_t si_hip_abi_version(void);
+
+/* ---- context: MetalContext::new (metal.rs:2170-2310) ------------------- */
+int si_hip_context_new(int device_ordinal, si_hip_context **out);
+void si_hip_context_free(si_hip_context *ctx);
+
+/* ---- quantized weights: QuantWeight (metal.rs:1840-1880) --------------- */
+/* upload_quant_weight_private (metal.rs:2502-2542): packed blocks copied
+ * as-is into a new HBM allocation on the upload stream. */
+int si_hip_upload_quant_weight_private(si_hip_context *ctx, const uint8_t *weight_bytes,
+                                       size_t weight_len, uint32_t ggml_type,
+                                       si_hip_quant_weight **out);
+/* bind_quant_weight_mapped (metal.rs:2549-2580).  MI355X cannot execute from
+ * the host mapping, so the bytes are uploaded once; the handle is marked
+ * mapped and counted as active (not persistent) weight memory. */
+int si_hip_bind_quant_weight_mapped(si_hip_context *ctx, const uint8_t *weight_bytes,
+                                    size_t weight_len, uint32_t ggml_type,
+                                    si_hip_quant_weight **out);
+/* Offset view of a parent's buffer, as PrivateStagedQwenLayer::quant_weight
+ * (metal.rs:1858-1868) hands out views of one staged layer buffer.  The
+ * view shares (and keeps alive) the parent's device memory. */
+int si_hip_quant_weight_view(const si_hip_quant_weight *parent, uint64_t offset, uint64_t bytes,
+                             uint32_t ggml_type, si_hip_quant_weight **out);
+void si_hip_quant_weight_free(si_hip_quant_weight *weight);
+uint64_t si_hip_quant_weight_byte_len(const si_hip_quant_weight *weight); /* metal.rs:1873 */
+uint32_t si_hip_quant_weight_ggml_type(const si_hip_quant_weight *weight); /* metal.rs:1877 */
+int si_hip_quant_weight_is_mapped(const si_hip_quant_weight *weight);
+/* Device address of the first packed byte (for callers that build their own
+ * launches or copies; valid while the handle or a view of it lives). */
+const void *si_hip_quant_weight_device_ptr(const si_hip_quant_weight *weight);
+
+/* ---- matvec: y[rows] = W[rows x columns] . input[columns] -------------- */
+/* q4_k_matvec (metal.rs:3357-3397), q5_k_matvec (4307-4323),
+ * q6_k_matvec (4325-4341): packed bytes from host memory, uploaded per call. */
+int si_hip_q4_k_matvec(si_hip_context *ctx, const uint8_t *weight_bytes, size_t weight_len,
+                       size_t rows, size_t columns, const float *input, size_t input_len,
+                       float *output);
+int si_hip_q5_k_matvec(si_hip_context *ctx, const uint8_t *weight_bytes, size_t weight_len,
+                       size_t rows, size_t columns, const float *input, size_t input_len,
+                       float *output);
+int si_hip_q6_k_matvec(si_hip_context *ctx, const uint8_t *weight_bytes, size_t weight_len,
+                       size_t rows, size_t columns, const float *input, size_t input_len,
+                       float *output);
+/* gguf_quant_matvec_bytes (metal.rs:4000-4061) */
+int si_hip_gguf_quant_matvec_bytes(si_hip_context *ctx, uint32_t ggml_type,
+                                   const uint8_t *weight_bytes, size_t weight_len, size_t rows,
+                                   size_t columns, const float *input, size_t input_len,
+                                   float *output);
+/* gguf_quant_matvec_weight (metal.rs:3923-3995): HBM-resident weight. */
+int si_hip_gguf_quant_matvec_weight(si_hip_context *ctx, const si_hip_quant_weight *weight,
+                                    size_t rows, size_t columns, const float *input,
+                                    size_t input_len, float *output);
+/* quant_k_matvec_tensor_rows / q4_k_matvec_tensor_rows (metal.rs:4346-4467,
+ * 4505-4527): rows [row_start, row_start+row_count) of a resident rank-2
+ * tensor of shape [shape_columns, shape_rows]. */
+int si_hip_gguf_quant_matvec_tensor_rows(si_hip_context *ctx, const si_hip_quant_weight *tensor,
+                                         size_t shape_columns, size_t shape_rows,
+                                         size_t row_start, size_t row_count, const float *input,
+                                         size_t input_len, float *output);
+/* gguf_quant_matvec_many_weights (metal.rs:4652-4775): several matvecs over
+ * one shared input, one submission and one wait. */
+int si_hip_gguf_quant_matvec_many_weights(si_hip_context *ctx,
+                                          const si_hip_quant_weight *const *weights,
+                                          const size_t *rows, size_t count, size_t columns,
+                                          const float *input, size_t input_len,
+                                          float *const *outputs);
+
+/* ---- fused SwiGLU ------------------------------------------------------ */
+/* q4_k_fused_gate_up (metal.rs:3402-3486): out = silu(gate.x) * (up.x). */
+int si_hip_q4_k_fused_gate_up(si_hip_context *ctx, const uint8_t *gate_bytes, size_t gate_len,
+                              const uint8_t *up_bytes, size_t up_len, size_t rows,
+                              size_t columns, const float *input, size_t input_len,
+                              float *output);
+/* q4_k_fused_gate_up_weights (metal.rs:3489-3562) */
+int si_hip_q4_k_fused_gate_up_weights(si_hip_context *ctx, const si_hip_quant_weight *gate,
+                                      const si_hip_quant_weight *up, size_t rows, size_t columns,
+                                      const float *input, size_t input_len, float *output);
+/* gguf_quant_fused_mlp_weights (metal.rs:3569-3732): gate/up (Q4_K) then the
+ * Q4_K/Q5_K/Q6_K down projection with the intermediate kept in HBM. */
+int si_hip_gguf_quant_fused_mlp_weights(si_hip_context *ctx, const si_hip_quant_weight *gate,
+                                        const si_hip_quant_weight *up,
+                                        const si_hip_quant_weight *down, size_t gate_rows,
+                                        size_t columns, size_t down_rows, const float *input,
+                                        size_t input_len, float *output);
+
+/* ---- embedding (bit-exact dequantisation of table rows) --------------- */
+/* q4_k_embedding_row (metal.rs:3734-3783) */
+int si_hip_q4_k_embedding_row(si_hip_context *ctx, const uint8_t *row_bytes, size_t row_len,
+                              size_t columns, float *output);
+/* q4_k_embedding_tensor (metal.rs:3785-3810), for a resident table. */
+int si_hip_q4_k_embedding_tensor(si_hip_context *ctx, const si_hip_quant_weight *table,
+                                 size_t shape_columns, size_t shape_rows, size_t token_id,
+                                 float *output);
+/* The same for n token ids in one launch: output is [n][shape_columns]. */
+int si_hip_q4_k_embedding_tokens(si_hip_context *ctx, const si_hip_quant_weight *table,
+                                 size_t shape_columns, size_t shape_rows,
+                                 const uint32_t *token_ids, size_t n_tokens, float *output);
+
+/* ---- multi-token verify: Y[b][rows] = W . X[b][columns], b < batch ----- */
+/* gguf_quant_matmul_many_bytes (metal.rs:4067-4158) */
+int si_hip_gguf_quant_matmul_many_bytes(si_hip_context *ctx, uint32_t ggml_type,
+                                        const uint8_t *weight_bytes, size_t weight_len,
+                                        size_t rows, size_t columns, size_t batch,
+                                        const float *inputs, size_t inputs_len, float *outputs);
+/* gguf_quant_matmul_many_weight (metal.rs:4161-4241) */
+int si_hip_gguf_quant_matmul_many_weight(si_hip_context *ctx, const si_hip_quant_weight *weight,
+                                         size_t rows, size_t columns, size_t batch,
+                                         const float *inputs, size_t inputs_len,
+                                         float *outputs);
+
+/* ---- output head + greedy argmax -------------------------------------- */
+/* Qwen35Runtime::logits' head matvec (qwen35_runtime.rs:2132-2192) followed
+ * by argmax (runtime.rs:4301-4309, or the first-wins rule of
+ * qwen35_runtime.rs:2237-2244), on the device; only the token id (and,
+ * when logits is non-NULL, the logits) come back. */
+int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_quant_weight *head,
+                                           size_t rows, size_t columns, const float *input,
+                                           size_t input_len, uint32_t rule, uint32_t *token,
+                                           float *logits);
+
+/* ---- dequantisation (quant.rs dequantize_q4_k/q5_k/q6_k on the GPU) ---- */
+int si_hip_dequantize(si_hip_context *ctx, uint32_t ggml_type, const uint8_t *bytes, size_t len,
+                      size_t elements, float *output);
+
+/* ---- device-resident API (async on the compute stream) ----------------- */
+int si_hip_device_alloc(si_hip_context *ctx, size_t bytes, void **device_ptr);
+int si_hip_device_free(si_hip_context *ctx, void *device_ptr);
+int si_hip_copy_to_device(si_hip_context *ctx, void *device_dst, const void *host_src,
+                          size_t bytes);
+int si_hip_copy_from_device(si_hip_context *ctx, void *host_dst, const void *device_src,
+                            size_t bytes);
+int si_hip_synchronize(si_hip_context *ctx);
+int si_hip_quant_matvec_device(si_hip_context *ctx, const si_hip_quant_weight *weight,
+                               size_t rows, size_t columns, const float *d_input,
+                               float *d_output);
+int si_hip_q4_k_fused_gate_up_device(si_hip_context *ctx, const si_hip_quant_weight *gate,
+                                     const si_hip_quant_weight *up, size_t rows, size_t columns,
+                                     const float *d_input, float *d_output);
+/* d_hidden: gate_rows floats of caller-owned device scratch. */
+int si_hip_fused_mlp_device(si_hip_context *ctx, const si_hip_quant_weight *gate,
+                            const si_hip_quant_weight *up, const si_hip_quant_weight *down,
+                            size_t gate_rows, size_t columns, size_t down_rows,
+                            const float *d_input, float *d_hidden, float *d_output);
+int si_hip_matmul_many_device(si_hip_context *ctx, const si_hip_quant_weight *weight,
+                              size_t rows, size_t columns, size_t batch, const float *d_inputs,
+                              float *d_outputs);
+/* d_logits: rows floats; d_result: one uint64 packed (key<<32 | index),
+ * decoded by si_hip_argmax_result_index. */
+int si_hip_matvec_argmax_device(si_hip_context *ctx, const si_hip_quant_weight *head,
+                                size_t rows, size_t columns, const float *d_input,
+                                uint32_t rule, float *d_logits, uint64_t *d_result);
+uint32_t si_hip_argmax_result_index(uint64_t packed, uint32_t rule);
+int si_hip_embedding_device(si_hip_context *ctx, const si_hip_quant_weight *table,
+                            size_t shape_columns, size_t shape_rows, const uint32_t *d_ids,
+                            size_t n_tokens, float *d_output);
+
+/* Timing on the compute stream: 16 event slots. */
+int si_hip_event_record(si_hip_context *ctx, uint32_t slot);
+int si_hip_event_elapsed_ms(si_hip_context *ctx, uint32_t start_slot, uint32_t end_slot,
+                            float *ms);
+/* Enqueue `iterations` matvecs back to back, cycling through n_weights
+ * resident copies (weights[i % n_weights]); used to time HBM streaming
+ * without host launch gaps. */
+int si_hip_quant_matvec_device_repeat(si_hip_context *ctx,
+                                      const si_hip_quant_weight *const *weights,
+                                      size_t n_weights, size_t rows, size_t columns,
+                                      const float *d_input, float *d_output, size_t iterations);
+
+/* ---- kernel selection (the reference picks variants via SI_QK_* env) --- */
+#define SI_HIP_KERNEL_AUTO 0u     /* tuned gfx950 kernels where they apply */
+#define SI_HIP_KERNEL_GENERIC 1u  /* one wavefront per row, exact per-weight decode */
+int si_hip_set_kernel_policy(si_hip_context *ctx, uint32_t policy);
+
+/* ---- telemetry (metal.rs:2312-2442) ------------------------------------ */
+uint64_t si_hip_current_allocated_bytes(const si_hip_context *ctx);
+uint64_t si_hip_peak_allocated_bytes(const si_hip_context *ctx);
+uint64_t si_hip_peak_active_weight_bytes(const si_hip_context *ctx);
+void si_hip_reset_peaks(si_hip_context *ctx);
+int si_hip_get_command_stats(const si_hip_context *ctx, si_hip_command_stats *out);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SI_HIP_H */

@@ -1,0 +1,1156 @@
+// C ABI of the gfx950 K-quant path (include/si_hip.h).
+//
+// Host side of the boundary: validation in the reference's order, HBM
+// residency of packed weights, staging of host inputs/outputs, stream and
+// event management, telemetry, and kernel selection.  Kernels live in the
+// *.hip files; this file only launches them through si_hip_internal.h.
+#include "si_hip.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <atomic>
+#include <chrono>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <string>
+#include <vector>
+
+#include "si_hip_internal.h"
+#include "si_hip_tuned.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int status, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+
+int ok() {
+  g_last_error.clear();
+  return SI_HIP_OK;
+}
+
+size_t block_bytes_of(uint32_t t) {
+  switch (t) {
+    case SI_HIP_GGML_TYPE_Q4_K: return 144;
+    case SI_HIP_GGML_TYPE_Q5_K: return 176;
+    case SI_HIP_GGML_TYPE_Q6_K: return 210;
+    default: return 0;
+  }
+}
+
+const char *type_label(uint32_t t) {
+  switch (t) {
+    case SI_HIP_GGML_TYPE_Q4_K: return "Q4_K";
+    case SI_HIP_GGML_TYPE_Q5_K: return "Q5_K";
+    case SI_HIP_GGML_TYPE_Q6_K: return "Q6_K";
+    default: return "unsupported";
+  }
+}
+
+bool checked_mul(size_t a, size_t b, size_t *out) {
+  if (a != 0 && b > SIZE_MAX / a) return false;
+  *out = a * b;
+  return true;
+}
+
+// rows * (columns/256) * block_bytes with the reference's overflow checks.
+int expected_weight_bytes(size_t rows, size_t columns, size_t block_bytes, const char *label,
+                          size_t *out) {
+  size_t blocks;
+  if (!checked_mul(rows, columns / 256, &blocks))
+    return fail(SI_HIP_ERR_OVERFLOW, "%s matvec block count overflows", label);
+  if (!checked_mul(blocks, block_bytes, out))
+    return fail(SI_HIP_ERR_OVERFLOW, "%s matvec byte length overflows", label);
+  return SI_HIP_OK;
+}
+
+int check_u32(size_t rows, size_t columns, const char *label) {
+  if (rows > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "%s rows exceed HIP limits", label);
+  if (columns > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "%s columns exceed HIP limits", label);
+  return SI_HIP_OK;
+}
+
+// Allocation counters shared by a context and every buffer/handle it made,
+// so handles may outlive the context (metal.rs:2339-2442).
+struct Telemetry {
+  std::atomic<uint64_t> allocated{0};
+  std::atomic<uint64_t> peak_allocated{0};
+  std::atomic<uint64_t> active_weights{0};
+  std::atomic<uint64_t> peak_active_weights{0};
+
+  void note_alloc(uint64_t b) {
+    const uint64_t now = allocated.fetch_add(b) + b;
+    uint64_t prev = peak_allocated.load();
+    while (now > prev && !peak_allocated.compare_exchange_weak(prev, now)) {
+    }
+  }
+  void note_free(uint64_t b) { allocated.fetch_sub(b); }
+  void note_active(int64_t delta) {
+    const uint64_t now = active_weights.fetch_add((uint64_t)delta) + (uint64_t)delta;
+    uint64_t prev = peak_active_weights.load();
+    while (delta > 0 && now > prev && !peak_active_weights.compare_exchange_weak(prev, now)) {
+    }
+  }
+};
+
+struct DeviceBuffer {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+  std::shared_ptr<Telemetry> tel;
+  ~DeviceBuffer() {
+    if (ptr) {
+      (void)hipFree(ptr);
+      if (tel) tel->note_free(bytes);
+    }
+  }
+};
+
+}  // namespace
+
+struct si_hip_context {
+  int device = 0;
+  hipStream_t stream = nullptr;         // compute queue (metal.rs `queue`)
+  hipStream_t upload_stream = nullptr;  // metal.rs `upload_queue`
+  std::mutex mu;
+  uint32_t policy = SI_HIP_KERNEL_AUTO;
+  // grow-only staging for the synchronous host-pointer API
+  void *stage_in = nullptr;
+  size_t stage_in_bytes = 0;
+  void *stage_out = nullptr;
+  size_t stage_out_bytes = 0;
+  void *stage_weights = nullptr;
+  size_t stage_weights_bytes = 0;
+  void *stage_aux = nullptr;
+  size_t stage_aux_bytes = 0;
+  hipEvent_t events[16] = {};
+  // telemetry
+  std::shared_ptr<Telemetry> tel = std::make_shared<Telemetry>();
+  std::atomic<uint64_t> submitted{0}, async_submitted{0}, waited{0}, wait_nanos{0};
+};
+
+struct si_hip_quant_weight {
+  std::shared_ptr<Telemetry> tel;
+  std::shared_ptr<DeviceBuffer> buffer;
+  uint64_t offset = 0;
+  uint64_t bytes = 0;
+  uint32_t ggml_type = 0;
+  bool mapped = false;
+  bool owner = false;  // counts toward active weight bytes
+  const uint8_t *data() const { return static_cast<const uint8_t *>(buffer->ptr) + offset; }
+};
+
+namespace {
+
+int hip_fail(hipError_t e, const char *what) {
+  return fail(SI_HIP_ERR_DEVICE, "HIP %s failed: %s", what, hipGetErrorString(e));
+}
+
+#define SIHIP_CHECK(expr, what)            \
+  do {                                     \
+    hipError_t _e = (expr);                \
+    if (_e != hipSuccess) return hip_fail(_e, what); \
+  } while (0)
+
+int grow(si_hip_context *ctx, void **buf, size_t *cap, size_t need) {
+  if (need <= *cap) return SI_HIP_OK;
+  size_t want = std::max(need, *cap * 2);
+  if (*buf) {
+    (void)hipFree(*buf);
+    ctx->tel->note_free(*cap);
+    *buf = nullptr;
+    *cap = 0;
+  }
+  if (hipMalloc(buf, want) != hipSuccess) {
+    *buf = nullptr;
+    return fail(SI_HIP_ERR_OUT_OF_MEMORY, "HIP could not allocate %zu staging bytes", want);
+  }
+  *cap = want;
+  ctx->tel->note_alloc(want);
+  return SI_HIP_OK;
+}
+
+int wait_stream(si_hip_context *ctx, const char *what) {
+  ctx->submitted.fetch_add(1);
+  const auto t0 = std::chrono::steady_clock::now();
+  hipError_t e = hipStreamSynchronize(ctx->stream);
+  const auto t1 = std::chrono::steady_clock::now();
+  ctx->waited.fetch_add(1);
+  ctx->wait_nanos.fetch_add(
+      (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count());
+  if (e != hipSuccess) return fail(SI_HIP_ERR_DEVICE, "HIP %s failed: %s", what, hipGetErrorString(e));
+  return SI_HIP_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Kernel dispatch.
+int dispatch_matvec(si_hip_context *ctx, uint32_t type, const uint8_t *w, const float *x,
+                    float *y, uint32_t rows, uint32_t cols, uint32_t batch) {
+  hipError_t e = hipErrorInvalidValue;
+  bool done = false;
+  if (ctx->policy == SI_HIP_KERNEL_AUTO) {
+    done = sihip::launch_matvec_tuned(type, w, x, y, rows, cols, batch, ctx->stream, &e);
+  }
+  if (!done) e = sihip::launch_matvec_generic(type, w, x, y, rows, cols, batch, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "matvec launch");
+  return SI_HIP_OK;
+}
+
+int dispatch_gate_up(si_hip_context *ctx, const uint8_t *g, const uint8_t *u, const float *x,
+                     float *h, uint32_t rows, uint32_t cols) {
+  hipError_t e = hipErrorInvalidValue;
+  bool done = false;
+  if (ctx->policy == SI_HIP_KERNEL_AUTO) {
+    done = sihip::launch_fused_gate_up_tuned(g, u, x, h, rows, cols, ctx->stream, &e);
+  }
+  if (!done) e = sihip::launch_fused_gate_up_generic(g, u, x, h, rows, cols, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "fused gate/up launch");
+  return SI_HIP_OK;
+}
+
+// Validation shared by the byte-slice matvec entry points
+// (quant_k_matvec_dispatch, metal.rs:3847-3858 and 3884-3887).
+int validate_matvec(uint32_t type, size_t weight_len, size_t rows, size_t columns,
+                    size_t input_len, const char *label) {
+  if (rows == 0 || columns == 0 || columns % 256 != 0 || input_len != columns)
+    return fail(SI_HIP_ERR_DIMENSIONS, "%s matvec dimensions are invalid", label);
+  size_t expected;
+  int rc = expected_weight_bytes(rows, columns, block_bytes_of(type), label, &expected);
+  if (rc) return rc;
+  if (weight_len != expected) return fail(SI_HIP_ERR_BYTE_LENGTH, "%s matvec byte length is invalid", label);
+  return check_u32(rows, columns, label);
+}
+
+int run_matvec_host(si_hip_context *ctx, uint32_t type, const uint8_t *dev_w, size_t rows,
+                    size_t columns, size_t batch, const float *input, float *output,
+                    const char *what) {
+  const size_t in_bytes = batch * columns * sizeof(float);
+  const size_t out_bytes = batch * rows * sizeof(float);
+  int rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, in_bytes);
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, out_bytes);
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, input, in_bytes, hipMemcpyHostToDevice, ctx->stream),
+              "input copy");
+  rc = dispatch_matvec(ctx, type, dev_w, static_cast<const float *>(ctx->stage_in),
+                       static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)columns,
+                       (uint32_t)batch);
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(output, ctx->stage_out, out_bytes, hipMemcpyDeviceToHost, ctx->stream),
+              "output copy");
+  rc = wait_stream(ctx, what);
+  if (rc) return rc;
+  return ok();
+}
+
+// Per-call upload of host bytes (the mapped/no-copy path of the reference).
+int stage_weights(si_hip_context *ctx, const uint8_t *bytes, size_t len, const uint8_t **dev) {
+  int rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, len);
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_weights, bytes, len, hipMemcpyHostToDevice, ctx->stream),
+              "weight copy");
+  *dev = static_cast<const uint8_t *>(ctx->stage_weights);
+  return SI_HIP_OK;
+}
+
+int typed_matvec(si_hip_context *ctx, uint32_t type, const uint8_t *weight_bytes,
+                 size_t weight_len, size_t rows, size_t columns, const float *input,
+                 size_t input_len, float *output) {
+  const char *label = type_label(type);
+  int rc = validate_matvec(type, weight_len, rows, columns, input_len, label);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!weight_bytes || !input || !output) return fail(SI_HIP_ERR_NULL, "%s matvec buffer is null", label);
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const uint8_t *dev_w = nullptr;
+  rc = stage_weights(ctx, weight_bytes, weight_len, &dev_w);
+  if (rc) return rc;
+  char what[64];
+  snprintf(what, sizeof what, "%s matvec command", label);
+  return run_matvec_host(ctx, type, dev_w, rows, columns, 1, input, output, what);
+}
+
+int make_weight(si_hip_context *ctx, const uint8_t *bytes, size_t len, uint32_t type, bool mapped,
+                si_hip_quant_weight **out) {
+  if (!out) return fail(SI_HIP_ERR_NULL, "output handle pointer is null");
+  *out = nullptr;
+  if (len == 0 || block_bytes_of(type) == 0)
+    return fail(len == 0 ? SI_HIP_ERR_EMPTY : SI_HIP_ERR_UNSUPPORTED_TYPE,
+                mapped ? "unsupported or empty mapped quantized weight"
+                       : "unsupported or empty quantized weight");
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!bytes) return fail(SI_HIP_ERR_NULL, "quantized weight bytes are null");
+  auto buf = std::make_shared<DeviceBuffer>();
+  if (hipMalloc(&buf->ptr, len) != hipSuccess) {
+    buf->ptr = nullptr;
+    return fail(SI_HIP_ERR_OUT_OF_MEMORY, "HIP could not allocate %zu weight bytes", len);
+  }
+  buf->bytes = len;
+  buf->tel = ctx->tel;
+  ctx->tel->note_alloc(len);
+  hipError_t e = hipMemcpyAsync(buf->ptr, bytes, len, hipMemcpyHostToDevice, ctx->upload_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(ctx->upload_stream);
+  ctx->submitted.fetch_add(1);
+  ctx->waited.fetch_add(1);
+  if (e != hipSuccess) return hip_fail(e, "quantized weight upload");
+  auto *w = new si_hip_quant_weight;
+  w->tel = ctx->tel;
+  w->buffer = std::move(buf);
+  w->bytes = len;
+  w->ggml_type = type;
+  w->mapped = mapped;
+  w->owner = true;
+  ctx->tel->note_active((int64_t)len);
+  *out = w;
+  return ok();
+}
+
+int check_weight(const si_hip_quant_weight *w, const char *what) {
+  if (!w) return fail(SI_HIP_ERR_NULL, "%s weight handle is null", what);
+  return SI_HIP_OK;
+}
+
+}  // namespace
+
+// ===========================================================================
+extern "C" {
+
+const char *si_hip_last_error(void) { return g_last_error.c_str(); }
+
+const char *si_hip_status_name(int s) {
+  switch (s) {
+    case SI_HIP_OK: return "SI_HIP_OK";
+    case SI_HIP_ERR_NULL: return "SI_HIP_ERR_NULL";
+    case SI_HIP_ERR_DIMENSIONS: return "SI_HIP_ERR_DIMENSIONS";
+    case SI_HIP_ERR_BYTE_LENGTH: return "SI_HIP_ERR_BYTE_LENGTH";
+    case SI_HIP_ERR_OVERFLOW: return "SI_HIP_ERR_OVERFLOW";
+    case SI_HIP_ERR_UNSUPPORTED_TYPE: return "SI_HIP_ERR_UNSUPPORTED_TYPE";
+    case SI_HIP_ERR_BATCH: return "SI_HIP_ERR_BATCH";
+    case SI_HIP_ERR_RANGE: return "SI_HIP_ERR_RANGE";
+    case SI_HIP_ERR_NO_FINITE: return "SI_HIP_ERR_NO_FINITE";
+    case SI_HIP_ERR_DEVICE: return "SI_HIP_ERR_DEVICE";
+    case SI_HIP_ERR_OUT_OF_MEMORY: return "SI_HIP_ERR_OUT_OF_MEMORY";
+    case SI_HIP_ERR_EMPTY: return "SI_HIP_ERR_EMPTY";
+    default: return "SI_HIP_ERR_UNKNOWN";
+  }
+}
+
+uint32_t si_hip_abi_version(void) { return SI_HIP_ABI_VERSION; }
+
+int si_hip_context_new(int device_ordinal, si_hip_context **out) {
+  if (!out) return fail(SI_HIP_ERR_NULL, "output context pointer is null");
+  *out = nullptr;
+  int count = 0;
+  hipError_t e = hipGetDeviceCount(&count);
+  if (e != hipSuccess || count == 0) return fail(SI_HIP_ERR_DEVICE, "no HIP device is available");
+  if (device_ordinal < 0 || device_ordinal >= count)
+    return fail(SI_HIP_ERR_RANGE, "HIP device %d does not exist (%d visible)", device_ordinal, count);
+  SIHIP_CHECK(hipSetDevice(device_ordinal), "set device");
+  auto ctx = std::make_unique<si_hip_context>();
+  ctx->device = device_ordinal;
+  SIHIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "stream create");
+  SIHIP_CHECK(hipStreamCreateWithFlags(&ctx->upload_stream, hipStreamNonBlocking), "stream create");
+  for (auto &ev : ctx->events) SIHIP_CHECK(hipEventCreate(&ev), "event create");
+  *out = ctx.release();
+  return ok();
+}
+
+void si_hip_context_free(si_hip_context *ctx) {
+  if (!ctx) return;
+  (void)hipSetDevice(ctx->device);
+  if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
+  for (void *p : {ctx->stage_in, ctx->stage_out, ctx->stage_weights, ctx->stage_aux})
+    if (p) (void)hipFree(p);
+  ctx->tel->note_free(ctx->stage_in_bytes + ctx->stage_out_bytes + ctx->stage_weights_bytes +
+                      ctx->stage_aux_bytes);
+  for (auto &ev : ctx->events)
+    if (ev) (void)hipEventDestroy(ev);
+  if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
+  if (ctx->upload_stream) (void)hipStreamDestroy(ctx->upload_stream);
+  delete ctx;
+}
+
+int si_hip_upload_quant_weight_private(si_hip_context *ctx, const uint8_t *weight_bytes,
+                                       size_t weight_len, uint32_t ggml_type,
+                                       si_hip_quant_weight **out) {
+  return make_weight(ctx, weight_bytes, weight_len, ggml_type, false, out);
+}
+
+int si_hip_bind_quant_weight_mapped(si_hip_context *ctx, const uint8_t *weight_bytes,
+                                    size_t weight_len, uint32_t ggml_type,
+                                    si_hip_quant_weight **out) {
+  return make_weight(ctx, weight_bytes, weight_len, ggml_type, true, out);
+}
+
+int si_hip_quant_weight_view(const si_hip_quant_weight *parent, uint64_t offset, uint64_t bytes,
+                             uint32_t ggml_type, si_hip_quant_weight **out) {
+  if (!out) return fail(SI_HIP_ERR_NULL, "output handle pointer is null");
+  *out = nullptr;
+  if (!parent) return fail(SI_HIP_ERR_NULL, "parent weight handle is null");
+  if (block_bytes_of(ggml_type) == 0) return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported quantized view type");
+  if (bytes == 0 || offset > parent->bytes || bytes > parent->bytes - offset)
+    return fail(SI_HIP_ERR_RANGE, "quantized weight view [%llu, +%llu) is outside its parent",
+                (unsigned long long)offset, (unsigned long long)bytes);
+  auto *w = new si_hip_quant_weight;
+  w->tel = parent->tel;
+  w->buffer = parent->buffer;
+  w->offset = parent->offset + offset;
+  w->bytes = bytes;
+  w->ggml_type = ggml_type;
+  w->mapped = parent->mapped;
+  w->owner = false;
+  *out = w;
+  return ok();
+}
+
+void si_hip_quant_weight_free(si_hip_quant_weight *w) {
+  if (!w) return;
+  if (w->owner && w->tel) w->tel->note_active(-(int64_t)w->bytes);
+  delete w;
+}
+
+uint64_t si_hip_quant_weight_byte_len(const si_hip_quant_weight *w) { return w ? w->bytes : 0; }
+uint32_t si_hip_quant_weight_ggml_type(const si_hip_quant_weight *w) { return w ? w->ggml_type : 0; }
+int si_hip_quant_weight_is_mapped(const si_hip_quant_weight *w) { return w && w->mapped ? 1 : 0; }
+const void *si_hip_quant_weight_device_ptr(const si_hip_quant_weight *w) { return w ? w->data() : nullptr; }
+
+// ---- matvec ---------------------------------------------------------------
+int si_hip_q4_k_matvec(si_hip_context *ctx, const uint8_t *wb, size_t wl, size_t rows, size_t cols,
+                       const float *in, size_t in_len, float *out) {
+  return typed_matvec(ctx, SI_HIP_GGML_TYPE_Q4_K, wb, wl, rows, cols, in, in_len, out);
+}
+int si_hip_q5_k_matvec(si_hip_context *ctx, const uint8_t *wb, size_t wl, size_t rows, size_t cols,
+                       const float *in, size_t in_len, float *out) {
+  return typed_matvec(ctx, SI_HIP_GGML_TYPE_Q5_K, wb, wl, rows, cols, in, in_len, out);
+}
+int si_hip_q6_k_matvec(si_hip_context *ctx, const uint8_t *wb, size_t wl, size_t rows, size_t cols,
+                       const float *in, size_t in_len, float *out) {
+  return typed_matvec(ctx, SI_HIP_GGML_TYPE_Q6_K, wb, wl, rows, cols, in, in_len, out);
+}
+
+int si_hip_gguf_quant_matvec_bytes(si_hip_context *ctx, uint32_t type, const uint8_t *wb, size_t wl,
+                                   size_t rows, size_t cols, const float *in, size_t in_len,
+                                   float *out) {
+  if (block_bytes_of(type) == 0)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported staged quantized weight type");
+  return typed_matvec(ctx, type, wb, wl, rows, cols, in, in_len, out);
+}
+
+int si_hip_gguf_quant_matvec_weight(si_hip_context *ctx, const si_hip_quant_weight *w, size_t rows,
+                                    size_t cols, const float *in, size_t in_len, float *out) {
+  int rc = check_weight(w, "retained matvec");
+  if (rc) return rc;
+  if (block_bytes_of(w->ggml_type) == 0)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported retained quantized weight type");
+  const char *label = type_label(w->ggml_type);
+  if (rows == 0 || cols == 0 || cols % 256 != 0 || in_len != cols)
+    return fail(SI_HIP_ERR_DIMENSIONS, "%s retained matvec dimensions are invalid", label);
+  size_t expected;
+  rc = expected_weight_bytes(rows, cols, block_bytes_of(w->ggml_type), label, &expected);
+  if (rc) return rc;
+  if ((uint64_t)expected != w->bytes)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "%s retained matvec byte length is invalid", label);
+  rc = check_u32(rows, cols, label);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!in || !out) return fail(SI_HIP_ERR_NULL, "%s matvec buffer is null", label);
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  char what[64];
+  snprintf(what, sizeof what, "%s retained matvec command", label);
+  return run_matvec_host(ctx, w->ggml_type, w->data(), rows, cols, 1, in, out, what);
+}
+
+int si_hip_gguf_quant_matvec_tensor_rows(si_hip_context *ctx, const si_hip_quant_weight *t,
+                                         size_t shape_cols, size_t shape_rows, size_t row_start,
+                                         size_t row_count, const float *in, size_t in_len,
+                                         float *out) {
+  int rc = check_weight(t, "tensor");
+  if (rc) return rc;
+  if (block_bytes_of(t->ggml_type) == 0)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "GGUF tensor has unsupported quantized type %u", t->ggml_type);
+  const char *label = type_label(t->ggml_type);
+  if (row_count == 0 || row_start >= shape_rows || row_count > shape_rows - row_start)
+    return fail(SI_HIP_ERR_RANGE, "%s row range is invalid", label);
+  if (shape_cols % 256 != 0 || in_len != shape_cols)
+    return fail(SI_HIP_ERR_DIMENSIONS, "%s tensor columns or input length is invalid", label);
+  const size_t row_bytes = shape_cols / 256 * block_bytes_of(t->ggml_type);
+  size_t byte_start, byte_len;
+  if (!checked_mul(row_start, row_bytes, &byte_start))
+    return fail(SI_HIP_ERR_OVERFLOW, "%s row byte range overflows", label);
+  if (!checked_mul(row_count, row_bytes, &byte_len))
+    return fail(SI_HIP_ERR_OVERFLOW, "%s row byte length overflows", label);
+  if (byte_start > SIZE_MAX - byte_len)
+    return fail(SI_HIP_ERR_OVERFLOW, "%s row byte range overflows", label);
+  if (byte_start + byte_len > t->bytes)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "%s tensor payload is shorter than its shape", label);
+  rc = check_u32(row_count, shape_cols, label);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!in || !out) return fail(SI_HIP_ERR_NULL, "%s matvec buffer is null", label);
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  char what[64];
+  snprintf(what, sizeof what, "%s matvec command", label);
+  return run_matvec_host(ctx, t->ggml_type, t->data() + byte_start, row_count, shape_cols, 1, in,
+                         out, what);
+}
+
+int si_hip_gguf_quant_matvec_many_weights(si_hip_context *ctx,
+                                          const si_hip_quant_weight *const *weights,
+                                          const size_t *rows, size_t count, size_t cols,
+                                          const float *in, size_t in_len, float *const *outputs) {
+  if (!weights || !rows || !outputs) return fail(SI_HIP_ERR_NULL, "grouped matvec arrays are null");
+  if (count == 0) return fail(SI_HIP_ERR_DIMENSIONS, "grouped quantized matvec needs at least one weight");
+  if (cols == 0 || cols % 256 != 0 || in_len != cols)
+    return fail(SI_HIP_ERR_DIMENSIONS, "grouped quantized matvec dimensions are invalid");
+  size_t total_rows = 0;
+  for (size_t i = 0; i < count; ++i) {
+    int rc = check_weight(weights[i], "grouped matvec");
+    if (rc) return rc;
+    const uint32_t t = weights[i]->ggml_type;
+    if (block_bytes_of(t) == 0)
+      return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported grouped quantized weight type");
+    if (rows[i] == 0) return fail(SI_HIP_ERR_DIMENSIONS, "grouped quantized matvec rows are invalid");
+    size_t expected;
+    rc = expected_weight_bytes(rows[i], cols, block_bytes_of(t), type_label(t), &expected);
+    if (rc) return rc;
+    if ((uint64_t)expected != weights[i]->bytes)
+      return fail(SI_HIP_ERR_BYTE_LENGTH, "grouped %s matvec byte length is invalid", type_label(t));
+    rc = check_u32(rows[i], cols, type_label(t));
+    if (rc) return rc;
+    if (!outputs[i]) return fail(SI_HIP_ERR_NULL, "grouped matvec output %zu is null", i);
+    total_rows += rows[i];
+  }
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!in) return fail(SI_HIP_ERR_NULL, "grouped matvec input is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  int rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, total_rows * sizeof(float));
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+              "input copy");
+  float *dst = static_cast<float *>(ctx->stage_out);
+  size_t off = 0;
+  for (size_t i = 0; i < count; ++i) {
+    rc = dispatch_matvec(ctx, weights[i]->ggml_type, weights[i]->data(),
+                         static_cast<const float *>(ctx->stage_in), dst + off, (uint32_t)rows[i],
+                         (uint32_t)cols, 1);
+    if (rc) return rc;
+    off += rows[i];
+  }
+  off = 0;
+  for (size_t i = 0; i < count; ++i) {
+    SIHIP_CHECK(hipMemcpyAsync(outputs[i], dst + off, rows[i] * sizeof(float), hipMemcpyDeviceToHost,
+                               ctx->stream),
+                "output copy");
+    off += rows[i];
+  }
+  rc = wait_stream(ctx, "grouped quantized matvec command");
+  if (rc) return rc;
+  return ok();
+}
+
+// ---- fused gate/up ----------------------------------------------------------
+int si_hip_q4_k_fused_gate_up(si_hip_context *ctx, const uint8_t *gate, size_t gate_len,
+                              const uint8_t *up, size_t up_len, size_t rows, size_t cols,
+                              const float *in, size_t in_len, float *out) {
+  if (rows == 0 || cols == 0 || cols % 256 != 0 || in_len != cols)
+    return fail(SI_HIP_ERR_DIMENSIONS, "Q4_K fused gate/up dimensions are invalid");
+  size_t blocks, expected;
+  if (!checked_mul(rows, cols / 256, &blocks))
+    return fail(SI_HIP_ERR_OVERFLOW, "Q4_K fused gate/up block count overflows");
+  if (!checked_mul(blocks, 144, &expected))
+    return fail(SI_HIP_ERR_OVERFLOW, "Q4_K fused gate/up byte length overflows");
+  if (gate_len != expected || up_len != expected)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "Q4_K fused gate/up byte length is invalid");
+  int rc = check_u32(rows, cols, "Q4_K fused gate/up");
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!gate || !up || !in || !out) return fail(SI_HIP_ERR_NULL, "Q4_K fused gate/up buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, 2 * expected);
+  if (rc) return rc;
+  uint8_t *dw = static_cast<uint8_t *>(ctx->stage_weights);
+  SIHIP_CHECK(hipMemcpyAsync(dw, gate, expected, hipMemcpyHostToDevice, ctx->stream), "gate copy");
+  SIHIP_CHECK(hipMemcpyAsync(dw + expected, up, expected, hipMemcpyHostToDevice, ctx->stream), "up copy");
+  rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, rows * sizeof(float));
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+              "input copy");
+  rc = dispatch_gate_up(ctx, dw, dw + expected, static_cast<const float *>(ctx->stage_in),
+                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols);
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+              "output copy");
+  rc = wait_stream(ctx, "Q4_K fused gate/up command");
+  if (rc) return rc;
+  return ok();
+}
+
+namespace {
+int validate_gate_up_weights(const si_hip_quant_weight *g, const si_hip_quant_weight *u, size_t rows,
+                             size_t cols, size_t in_len, const char *invalid, const char *overflow,
+                             const char *bad_len) {
+  if (!g || !u) return fail(SI_HIP_ERR_NULL, "gate/up weight handle is null");
+  if (g->ggml_type != SI_HIP_GGML_TYPE_Q4_K || u->ggml_type != SI_HIP_GGML_TYPE_Q4_K ||
+      g->bytes != u->bytes || rows == 0 || cols == 0 || cols % 256 != 0 || in_len != cols)
+    return fail(SI_HIP_ERR_DIMENSIONS, "%s", invalid);
+  size_t blocks, expected;
+  if (!checked_mul(rows, cols / 256, &blocks) || !checked_mul(blocks, 144, &expected))
+    return fail(SI_HIP_ERR_OVERFLOW, "%s", overflow);
+  if (g->bytes != (uint64_t)expected) return fail(SI_HIP_ERR_BYTE_LENGTH, "%s", bad_len);
+  return check_u32(rows, cols, "Q4_K fused gate/up");
+}
+}  // namespace
+
+int si_hip_q4_k_fused_gate_up_weights(si_hip_context *ctx, const si_hip_quant_weight *g,
+                                      const si_hip_quant_weight *u, size_t rows, size_t cols,
+                                      const float *in, size_t in_len, float *out) {
+  int rc = validate_gate_up_weights(g, u, rows, cols, in_len,
+                                    "retained Q4_K fused gate/up dimensions are invalid",
+                                    "retained Q4_K fused gate/up byte length overflows",
+                                    "retained Q4_K fused gate/up byte length is invalid");
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!in || !out) return fail(SI_HIP_ERR_NULL, "Q4_K fused gate/up buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, rows * sizeof(float));
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+              "input copy");
+  rc = dispatch_gate_up(ctx, g->data(), u->data(), static_cast<const float *>(ctx->stage_in),
+                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols);
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+              "output copy");
+  rc = wait_stream(ctx, "retained Q4_K fused gate/up command");
+  if (rc) return rc;
+  return ok();
+}
+
+namespace {
+int validate_mlp(const si_hip_quant_weight *g, const si_hip_quant_weight *u,
+                 const si_hip_quant_weight *d, size_t gate_rows, size_t cols, size_t down_rows,
+                 size_t in_len) {
+  if (!g || !u || !d) return fail(SI_HIP_ERR_NULL, "fused MLP weight handle is null");
+  if (g->ggml_type != SI_HIP_GGML_TYPE_Q4_K || u->ggml_type != SI_HIP_GGML_TYPE_Q4_K ||
+      g->bytes != u->bytes || gate_rows == 0 || cols == 0 || down_rows == 0 || cols % 256 != 0 ||
+      in_len != cols)
+    return fail(SI_HIP_ERR_DIMENSIONS, "fused quantized MLP dimensions are invalid");
+  size_t blocks, gate_bytes;
+  if (!checked_mul(gate_rows, cols / 256, &blocks) || !checked_mul(blocks, 144, &gate_bytes))
+    return fail(SI_HIP_ERR_OVERFLOW, "fused quantized MLP gate byte length overflows");
+  if (g->bytes != (uint64_t)gate_bytes)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "fused quantized MLP gate byte length is invalid");
+  const size_t down_block = block_bytes_of(d->ggml_type);
+  if (down_block == 0) return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported fused quantized MLP down type");
+  if (gate_rows % 256 != 0)
+    return fail(SI_HIP_ERR_DIMENSIONS, "fused quantized MLP down columns are invalid");
+  size_t down_bytes;
+  if (!checked_mul(down_rows, gate_rows / 256, &blocks) || !checked_mul(blocks, down_block, &down_bytes))
+    return fail(SI_HIP_ERR_OVERFLOW, "fused quantized MLP down byte length overflows");
+  if (d->bytes != (uint64_t)down_bytes)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "fused quantized MLP down byte length is invalid");
+  int rc = check_u32(gate_rows, cols, "fused quantized MLP");
+  if (rc) return rc;
+  return check_u32(down_rows, gate_rows, "fused quantized MLP");
+}
+}  // namespace
+
+int si_hip_gguf_quant_fused_mlp_weights(si_hip_context *ctx, const si_hip_quant_weight *g,
+                                        const si_hip_quant_weight *u, const si_hip_quant_weight *d,
+                                        size_t gate_rows, size_t cols, size_t down_rows,
+                                        const float *in, size_t in_len, float *out) {
+  int rc = validate_mlp(g, u, d, gate_rows, cols, down_rows, in_len);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!in || !out) return fail(SI_HIP_ERR_NULL, "fused MLP buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_aux, &ctx->stage_aux_bytes, gate_rows * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, down_rows * sizeof(float));
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+              "input copy");
+  float *hidden = static_cast<float *>(ctx->stage_aux);
+  rc = dispatch_gate_up(ctx, g->data(), u->data(), static_cast<const float *>(ctx->stage_in), hidden,
+                        (uint32_t)gate_rows, (uint32_t)cols);
+  if (rc) return rc;
+  rc = dispatch_matvec(ctx, d->ggml_type, d->data(), hidden, static_cast<float *>(ctx->stage_out),
+                       (uint32_t)down_rows, (uint32_t)gate_rows, 1);
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, down_rows * sizeof(float), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "output copy");
+  char what[64];
+  snprintf(what, sizeof what, "fused MLP %s command", type_label(d->ggml_type));
+  rc = wait_stream(ctx, what);
+  if (rc) return rc;
+  return ok();
+}
+
+// ---- embedding --------------------------------------------------------------
+int si_hip_q4_k_embedding_row(si_hip_context *ctx, const uint8_t *row, size_t row_len, size_t cols,
+                              float *out) {
+  if (cols == 0 || cols % 256 != 0) return fail(SI_HIP_ERR_DIMENSIONS, "Q4_K embedding dimension is invalid");
+  if (row_len != cols / 256 * 144) return fail(SI_HIP_ERR_BYTE_LENGTH, "Q4_K embedding row byte length is invalid");
+  if (cols > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "embedding dimension exceeds HIP limits");
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!row || !out) return fail(SI_HIP_ERR_NULL, "Q4_K embedding buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const uint8_t *dev = nullptr;
+  int rc = stage_weights(ctx, row, row_len, &dev);
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, cols * sizeof(float));
+  if (rc) return rc;
+  hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, dev, nullptr,
+                                       static_cast<float *>(ctx->stage_out), 1, (uint32_t)cols, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "embedding launch");
+  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, cols * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+              "output copy");
+  rc = wait_stream(ctx, "Q4_K embedding command");
+  if (rc) return rc;
+  return ok();
+}
+
+namespace {
+int validate_embedding_table(const si_hip_quant_weight *t, size_t cols, size_t rows) {
+  if (!t) return fail(SI_HIP_ERR_NULL, "embedding table handle is null");
+  if (t->ggml_type != SI_HIP_GGML_TYPE_Q4_K)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "Q4_K embedding requires a rank-2 Q4_K tensor");
+  if (cols == 0 || cols % 256 != 0) return fail(SI_HIP_ERR_DIMENSIONS, "Q4_K embedding token id or dimension is invalid");
+  size_t row_bytes = cols / 256 * 144, total;
+  if (!checked_mul(rows, row_bytes, &total)) return fail(SI_HIP_ERR_OVERFLOW, "Q4_K embedding row offset overflows");
+  if (total > t->bytes) return fail(SI_HIP_ERR_BYTE_LENGTH, "Q4_K embedding tensor payload is shorter than its shape");
+  if (cols > UINT32_MAX || rows > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "embedding dimension exceeds HIP limits");
+  return SI_HIP_OK;
+}
+}  // namespace
+
+int si_hip_q4_k_embedding_tokens(si_hip_context *ctx, const si_hip_quant_weight *t, size_t cols,
+                                 size_t rows, const uint32_t *ids, size_t n, float *out) {
+  int rc = validate_embedding_table(t, cols, rows);
+  if (rc) return rc;
+  if (n == 0) return fail(SI_HIP_ERR_DIMENSIONS, "Q4_K embedding needs at least one token id");
+  if (!ids) return fail(SI_HIP_ERR_NULL, "token id buffer is null");
+  for (size_t i = 0; i < n; ++i)
+    if (ids[i] >= rows) return fail(SI_HIP_ERR_RANGE, "Q4_K embedding token id or dimension is invalid");
+  if (n > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "too many token ids");
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!out) return fail(SI_HIP_ERR_NULL, "Q4_K embedding output is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, n * sizeof(uint32_t));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, n * cols * sizeof(float));
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream),
+              "token id copy");
+  hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, t->data(),
+                                       static_cast<const uint32_t *>(ctx->stage_in),
+                                       static_cast<float *>(ctx->stage_out), (uint32_t)n, (uint32_t)cols,
+                                       ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "embedding launch");
+  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, n * cols * sizeof(float), hipMemcpyDeviceToHost,
+                             ctx->stream),
+              "output copy");
+  rc = wait_stream(ctx, "Q4_K embedding command");
+  if (rc) return rc;
+  return ok();
+}
+
+int si_hip_q4_k_embedding_tensor(si_hip_context *ctx, const si_hip_quant_weight *t, size_t cols,
+                                 size_t rows, size_t token_id, float *out) {
+  int rc = validate_embedding_table(t, cols, rows);
+  if (rc) return rc;
+  if (token_id >= rows) return fail(SI_HIP_ERR_RANGE, "Q4_K embedding token id or dimension is invalid");
+  const uint32_t id = (uint32_t)token_id;
+  return si_hip_q4_k_embedding_tokens(ctx, t, cols, rows, &id, 1, out);
+}
+
+// ---- matmul many ----------------------------------------------------------
+namespace {
+int validate_many(uint32_t type, size_t weight_len, size_t rows, size_t cols, size_t batch,
+                  size_t inputs_len, bool retained) {
+  if (batch == 0 || batch > SI_HIP_MAX_BATCH || rows == 0 || cols == 0 || cols % 256 != 0)
+    return fail(batch == 0 || batch > SI_HIP_MAX_BATCH ? SI_HIP_ERR_BATCH : SI_HIP_ERR_DIMENSIONS,
+                retained ? "batched retained quantized dimensions are invalid"
+                         : "batched quantized matvec dimensions are invalid");
+  size_t want;
+  if (!checked_mul(batch, cols, &want) || inputs_len != want)
+    return fail(SI_HIP_ERR_DIMENSIONS, retained ? "batched retained quantized input length is invalid"
+                                                : "batched quantized input length is invalid");
+  const size_t bb = block_bytes_of(type);
+  if (bb == 0)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, retained ? "unsupported retained batched quantized type"
+                                                      : "unsupported batched quantized weight type");
+  size_t blocks, expected;
+  if (!checked_mul(rows, cols / 256, &blocks) || !checked_mul(blocks, bb, &expected))
+    return fail(SI_HIP_ERR_OVERFLOW, retained ? "retained batched weight byte length overflows"
+                                              : "batched quantized weight byte length overflows");
+  if (weight_len != expected)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, retained ? "retained batched weight byte length is invalid"
+                                                 : "batched quantized weight byte length is invalid");
+  size_t out_elems;
+  if (!checked_mul(batch, rows, &out_elems))
+    return fail(SI_HIP_ERR_OVERFLOW, "batched quantized output dimensions overflow");
+  return check_u32(rows, cols, "batched");
+}
+}  // namespace
+
+int si_hip_gguf_quant_matmul_many_bytes(si_hip_context *ctx, uint32_t type, const uint8_t *wb,
+                                        size_t wl, size_t rows, size_t cols, size_t batch,
+                                        const float *inputs, size_t inputs_len, float *outputs) {
+  int rc = validate_many(type, wl, rows, cols, batch, inputs_len, false);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!wb || !inputs || !outputs) return fail(SI_HIP_ERR_NULL, "batched matvec buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const uint8_t *dev_w = nullptr;
+  rc = stage_weights(ctx, wb, wl, &dev_w);
+  if (rc) return rc;
+  return run_matvec_host(ctx, type, dev_w, rows, cols, batch, inputs, outputs,
+                         "batched quantized matvec command");
+}
+
+int si_hip_gguf_quant_matmul_many_weight(si_hip_context *ctx, const si_hip_quant_weight *w,
+                                         size_t rows, size_t cols, size_t batch,
+                                         const float *inputs, size_t inputs_len, float *outputs) {
+  int rc = check_weight(w, "batched");
+  if (rc) return rc;
+  rc = validate_many(w->ggml_type, (size_t)w->bytes, rows, cols, batch, inputs_len, true);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!inputs || !outputs) return fail(SI_HIP_ERR_NULL, "batched matvec buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  return run_matvec_host(ctx, w->ggml_type, w->data(), rows, cols, batch, inputs, outputs,
+                         "retained batched quantized matvec command");
+}
+
+// ---- head + argmax ------------------------------------------------------------
+namespace {
+int validate_head(const si_hip_quant_weight *w, size_t rows, size_t cols, size_t in_len, uint32_t rule) {
+  int rc = check_weight(w, "output head");
+  if (rc) return rc;
+  if (block_bytes_of(w->ggml_type) == 0)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported output head quantized type");
+  const char *label = type_label(w->ggml_type);
+  if (rows == 0 || cols == 0 || cols % 256 != 0 || in_len != cols)
+    return fail(SI_HIP_ERR_DIMENSIONS, "%s output head dimensions are invalid", label);
+  size_t expected;
+  rc = expected_weight_bytes(rows, cols, block_bytes_of(w->ggml_type), label, &expected);
+  if (rc) return rc;
+  if ((uint64_t)expected != w->bytes)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "%s output head byte length is invalid", label);
+  if (rule != SI_HIP_ARGMAX_LAST_FINITE && rule != SI_HIP_ARGMAX_FIRST_GREATER)
+    return fail(SI_HIP_ERR_RANGE, "unknown argmax tie rule %u", rule);
+  return check_u32(rows, cols, label);
+}
+}  // namespace
+
+int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_quant_weight *w,
+                                           size_t rows, size_t cols, const float *in, size_t in_len,
+                                           uint32_t rule, uint32_t *token, float *logits) {
+  int rc = validate_head(w, rows, cols, in_len, rule);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!in || !token) return fail(SI_HIP_ERR_NULL, "output head buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const uint32_t parts = sihip::argmax_partials((uint32_t)rows);
+  rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, rows * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_aux, &ctx->stage_aux_bytes, (parts + 1) * sizeof(uint64_t));
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+              "input copy");
+  float *d_logits = static_cast<float *>(ctx->stage_out);
+  uint64_t *aux = static_cast<uint64_t *>(ctx->stage_aux);
+  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), static_cast<const float *>(ctx->stage_in),
+                       d_logits, (uint32_t)rows, (uint32_t)cols, 1);
+  if (rc) return rc;
+  hipError_t e = sihip::launch_argmax(d_logits, (uint32_t)rows, rule, aux + 1, aux, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "argmax launch");
+  uint64_t packed = 0;
+  SIHIP_CHECK(hipMemcpyAsync(&packed, aux, sizeof packed, hipMemcpyDeviceToHost, ctx->stream), "argmax copy");
+  if (logits)
+    SIHIP_CHECK(hipMemcpyAsync(logits, d_logits, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+                "logits copy");
+  rc = wait_stream(ctx, "output head argmax command");
+  if (rc) return rc;
+  if (packed == 0) {
+    if (rule == SI_HIP_ARGMAX_LAST_FINITE) return fail(SI_HIP_ERR_NO_FINITE, "logits contain no finite values");
+    *token = 0;
+  } else {
+    *token = sihip::argmax_candidate_index(packed, rule);
+  }
+  return ok();
+}
+
+// ---- dequantisation -----------------------------------------------------------
+int si_hip_dequantize(si_hip_context *ctx, uint32_t type, const uint8_t *bytes, size_t len,
+                      size_t elements, float *out) {
+  const size_t bb = block_bytes_of(type);
+  if (bb == 0) return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported quantized type %u", type);
+  const char *label = type_label(type);
+  if (elements == 0 || elements % 256 != 0)
+    return fail(SI_HIP_ERR_DIMENSIONS, "%s element count must be a non-zero multiple of 256", label);
+  size_t expected;
+  if (!checked_mul(elements / 256, bb, &expected)) return fail(SI_HIP_ERR_OVERFLOW, "%s byte count overflows", label);
+  if (len != expected)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "%s data has %zu bytes; expected %zu", label, len, expected);
+  if (elements / 256 > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "%s block count exceeds HIP limits", label);
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!bytes || !out) return fail(SI_HIP_ERR_NULL, "dequantize buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const uint8_t *dev = nullptr;
+  int rc = stage_weights(ctx, bytes, len, &dev);
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, elements * sizeof(float));
+  if (rc) return rc;
+  // treat the blocks as one row-major [blocks x 256] matrix
+  hipError_t e = sihip::launch_dequant(type, dev, nullptr, static_cast<float *>(ctx->stage_out),
+                                       (uint32_t)(elements / 256), 256, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "dequantize launch");
+  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, elements * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+              "output copy");
+  rc = wait_stream(ctx, "dequantize command");
+  if (rc) return rc;
+  return ok();
+}
+
+// ---- device-resident API --------------------------------------------------------
+int si_hip_device_alloc(si_hip_context *ctx, size_t bytes, void **p) {
+  if (!ctx || !p) return fail(SI_HIP_ERR_NULL, "device_alloc argument is null");
+  *p = nullptr;
+  if (bytes == 0) return fail(SI_HIP_ERR_DIMENSIONS, "device_alloc of zero bytes");
+  if (hipMalloc(p, bytes) != hipSuccess) {
+    *p = nullptr;
+    return fail(SI_HIP_ERR_OUT_OF_MEMORY, "HIP could not allocate %zu bytes", bytes);
+  }
+  ctx->tel->note_alloc(bytes);
+  return ok();
+}
+
+int si_hip_device_free(si_hip_context *ctx, void *p) {
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!p) return ok();
+  size_t bytes = 0;
+  void *base = nullptr;
+  if (hipMemGetAddressRange((hipDeviceptr_t *)&base, &bytes, (hipDeviceptr_t)p) == hipSuccess)
+    ctx->tel->note_free(bytes);
+  SIHIP_CHECK(hipFree(p), "free");
+  return ok();
+}
+
+int si_hip_copy_to_device(si_hip_context *ctx, void *dst, const void *src, size_t bytes) {
+  if (!ctx || !dst || !src) return fail(SI_HIP_ERR_NULL, "copy argument is null");
+  SIHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "copy to device");
+  SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "copy to device");
+  return ok();
+}
+
+int si_hip_copy_from_device(si_hip_context *ctx, void *dst, const void *src, size_t bytes) {
+  if (!ctx || !dst || !src) return fail(SI_HIP_ERR_NULL, "copy argument is null");
+  SIHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "copy from device");
+  SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "copy from device");
+  return ok();
+}
+
+int si_hip_synchronize(si_hip_context *ctx) {
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  int rc = wait_stream(ctx, "synchronize");
+  if (rc) return rc;
+  return ok();
+}
+
+namespace {
+int validate_device_matvec(const si_hip_quant_weight *w, size_t rows, size_t cols, size_t batch) {
+  int rc = check_weight(w, "device matvec");
+  if (rc) return rc;
+  rc = validate_many(w->ggml_type, (size_t)w->bytes, rows, cols, batch, batch * cols, true);
+  return rc;
+}
+}  // namespace
+
+int si_hip_quant_matvec_device(si_hip_context *ctx, const si_hip_quant_weight *w, size_t rows,
+                               size_t cols, const float *d_in, float *d_out) {
+  int rc = validate_device_matvec(w, rows, cols, 1);
+  if (rc) return rc;
+  if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matvec argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, 1);
+  if (rc) return rc;
+  ctx->async_submitted.fetch_add(1);
+  return ok();
+}
+
+int si_hip_quant_matvec_device_repeat(si_hip_context *ctx, const si_hip_quant_weight *const *ws,
+                                      size_t n, size_t rows, size_t cols, const float *d_in,
+                                      float *d_out, size_t iters) {
+  if (!ws || n == 0) return fail(SI_HIP_ERR_NULL, "repeat needs at least one weight");
+  for (size_t i = 0; i < n; ++i) {
+    int rc = validate_device_matvec(ws[i], rows, cols, 1);
+    if (rc) return rc;
+    if (ws[i]->ggml_type != ws[0]->ggml_type)
+      return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "repeat weights must share one type");
+  }
+  if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matvec argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  for (size_t i = 0; i < iters; ++i) {
+    const si_hip_quant_weight *w = ws[i % n];
+    int rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, 1);
+    if (rc) return rc;
+  }
+  ctx->async_submitted.fetch_add(iters);
+  return ok();
+}
+
+int si_hip_q4_k_fused_gate_up_device(si_hip_context *ctx, const si_hip_quant_weight *g,
+                                     const si_hip_quant_weight *u, size_t rows, size_t cols,
+                                     const float *d_in, float *d_out) {
+  int rc = validate_gate_up_weights(g, u, rows, cols, cols,
+                                    "retained Q4_K fused gate/up dimensions are invalid",
+                                    "retained Q4_K fused gate/up byte length overflows",
+                                    "retained Q4_K fused gate/up byte length is invalid");
+  if (rc) return rc;
+  if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device gate/up argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  rc = dispatch_gate_up(ctx, g->data(), u->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols);
+  if (rc) return rc;
+  ctx->async_submitted.fetch_add(1);
+  return ok();
+}
+
+int si_hip_fused_mlp_device(si_hip_context *ctx, const si_hip_quant_weight *g,
+                            const si_hip_quant_weight *u, const si_hip_quant_weight *d,
+                            size_t gate_rows, size_t cols, size_t down_rows, const float *d_in,
+                            float *d_hidden, float *d_out) {
+  int rc = validate_mlp(g, u, d, gate_rows, cols, down_rows, cols);
+  if (rc) return rc;
+  if (!ctx || !d_in || !d_hidden || !d_out) return fail(SI_HIP_ERR_NULL, "device MLP argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  rc = dispatch_gate_up(ctx, g->data(), u->data(), d_in, d_hidden, (uint32_t)gate_rows, (uint32_t)cols);
+  if (rc) return rc;
+  rc = dispatch_matvec(ctx, d->ggml_type, d->data(), d_hidden, d_out, (uint32_t)down_rows,
+                       (uint32_t)gate_rows, 1);
+  if (rc) return rc;
+  ctx->async_submitted.fetch_add(1);
+  return ok();
+}
+
+int si_hip_matmul_many_device(si_hip_context *ctx, const si_hip_quant_weight *w, size_t rows,
+                              size_t cols, size_t batch, const float *d_in, float *d_out) {
+  int rc = validate_device_matvec(w, rows, cols, batch);
+  if (rc) return rc;
+  if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matmul argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols,
+                       (uint32_t)batch);
+  if (rc) return rc;
+  ctx->async_submitted.fetch_add(1);
+  return ok();
+}
+
+int si_hip_matvec_argmax_device(si_hip_context *ctx, const si_hip_quant_weight *w, size_t rows,
+                                size_t cols, const float *d_in, uint32_t rule, float *d_logits,
+                                uint64_t *d_result) {
+  int rc = validate_head(w, rows, cols, cols, rule);
+  if (rc) return rc;
+  if (!ctx || !d_in || !d_logits || !d_result) return fail(SI_HIP_ERR_NULL, "device head argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  const uint32_t parts = sihip::argmax_partials((uint32_t)rows);
+  rc = grow(ctx, &ctx->stage_aux, &ctx->stage_aux_bytes, parts * sizeof(uint64_t));
+  if (rc) return rc;
+  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_logits, (uint32_t)rows, (uint32_t)cols, 1);
+  if (rc) return rc;
+  hipError_t e = sihip::launch_argmax(d_logits, (uint32_t)rows, rule,
+                                      static_cast<uint64_t *>(ctx->stage_aux), d_result, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "argmax launch");
+  ctx->async_submitted.fetch_add(1);
+  return ok();
+}
+
+uint32_t si_hip_argmax_result_index(uint64_t packed, uint32_t rule) {
+  return sihip::argmax_candidate_index(packed, rule);
+}
+
+int si_hip_embedding_device(si_hip_context *ctx, const si_hip_quant_weight *t, size_t cols,
+                            size_t rows, const uint32_t *d_ids, size_t n, float *d_out) {
+  int rc = validate_embedding_table(t, cols, rows);
+  if (rc) return rc;
+  if (n == 0 || n > UINT32_MAX) return fail(SI_HIP_ERR_DIMENSIONS, "embedding token count is invalid");
+  if (!ctx || !d_ids || !d_out) return fail(SI_HIP_ERR_NULL, "device embedding argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, t->data(), d_ids, d_out, (uint32_t)n,
+                                       (uint32_t)cols, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "embedding launch");
+  ctx->async_submitted.fetch_add(1);
+  return ok();
+}
+
+int si_hip_event_record(si_hip_context *ctx, uint32_t slot) {
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (slot >= 16) return fail(SI_HIP_ERR_RANGE, "event slot %u out of range", slot);
+  SIHIP_CHECK(hipEventRecord(ctx->events[slot], ctx->stream), "event record");
+  return ok();
+}
+
+int si_hip_event_elapsed_ms(si_hip_context *ctx, uint32_t a, uint32_t b, float *ms) {
+  if (!ctx || !ms) return fail(SI_HIP_ERR_NULL, "event argument is null");
+  if (a >= 16 || b >= 16) return fail(SI_HIP_ERR_RANGE, "event slot out of range");
+  SIHIP_CHECK(hipEventSynchronize(ctx->events[b]), "event synchronize");
+  SIHIP_CHECK(hipEventElapsedTime(ms, ctx->events[a], ctx->events[b]), "event elapsed");
+  return ok();
+}
+
+int si_hip_set_kernel_policy(si_hip_context *ctx, uint32_t policy) {
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (policy != SI_HIP_KERNEL_AUTO && policy != SI_HIP_KERNEL_GENERIC)
+    return fail(SI_HIP_ERR_RANGE, "unknown kernel policy %u", policy);
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  ctx->policy = policy;
+  return ok();
+}
+
+uint64_t si_hip_current_allocated_bytes(const si_hip_context *ctx) {
+  return ctx ? ctx->tel->allocated.load() : 0;
+}
+uint64_t si_hip_peak_allocated_bytes(const si_hip_context *ctx) {
+  return ctx ? ctx->tel->peak_allocated.load() : 0;
+}
+uint64_t si_hip_peak_active_weight_bytes(const si_hip_context *ctx) {
+  return ctx ? ctx->tel->peak_active_weights.load() : 0;
+}
+void si_hip_reset_peaks(si_hip_context *ctx) {
+  if (!ctx) return;
+  ctx->tel->peak_allocated.store(ctx->tel->allocated.load());
+  ctx->tel->peak_active_weights.store(ctx->tel->active_weights.load());
+}
+int si_hip_get_command_stats(const si_hip_context *ctx, si_hip_command_stats *out) {
+  if (!ctx || !out) return fail(SI_HIP_ERR_NULL, "command stats argument is null");
+  out->submitted = ctx->submitted.load();
+  out->async_submitted = ctx->async_submitted.load();
+  out->waited = ctx->waited.load();
+  out->wait_nanos = ctx->wait_nanos.load();
+  return ok();
+}
+
+}  // extern "C"

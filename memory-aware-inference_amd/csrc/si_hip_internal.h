@@ -1,0 +1,57 @@
+// Internal launch interface between the C ABI (api.cpp) and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace sihip {
+
+// silu(g) * u exactly as src/runtime.rs:4296-4298 / metal.rs:585 write it.
+__host__ __device__ __forceinline__ float silu_times(float g, float u) {
+  return g / (1.0f + expf(-g)) * u;
+}
+
+// Greedy-argmax tie rules.
+enum ArgmaxRule : uint32_t {
+  kArgmaxLastFinite = 0,     // runtime.rs:4301-4309 (finite, total order, last max)
+  kArgmaxFirstGreater = 1,   // qwen35_runtime.rs:2237-2244 (strict '>', first max)
+};
+
+// Packed (order key, index) candidate: larger is better; 0 = no candidate.
+__host__ __device__ __forceinline__ uint64_t argmax_candidate(float v, uint32_t index,
+                                                              uint32_t rule) {
+  uint32_t bits;
+  if (rule == kArgmaxFirstGreater) {
+    if (v != v || v == -__builtin_huge_valf()) return 0;  // never beats -inf
+    v = v + 0.0f;                                         // -0 == +0 under '>'
+  } else {
+    if (!__builtin_isfinite(v)) return 0;
+  }
+  __builtin_memcpy(&bits, &v, 4);
+  const int32_t key = (int32_t)bits ^ (int32_t)((uint32_t)((int32_t)bits >> 31) >> 1);
+  const uint32_t ukey = (uint32_t)key ^ 0x80000000u;
+  const uint32_t tie = rule == kArgmaxFirstGreater ? 0xffffffffu - index : index;
+  return ((uint64_t)ukey << 32) | tie;
+}
+
+__host__ __device__ __forceinline__ uint32_t argmax_candidate_index(uint64_t c, uint32_t rule) {
+  const uint32_t lo = (uint32_t)c;
+  return rule == kArgmaxFirstGreater ? 0xffffffffu - lo : lo;
+}
+
+// kernels_generic.hip
+hipError_t launch_matvec_generic(uint32_t type, const uint8_t* w, const float* x, float* y,
+                                 uint32_t rows, uint32_t cols, uint32_t batch, hipStream_t s);
+hipError_t launch_fused_gate_up_generic(const uint8_t* gate, const uint8_t* up, const float* x,
+                                        float* h, uint32_t rows, uint32_t cols, hipStream_t s);
+hipError_t launch_dequant(uint32_t type, const uint8_t* w, const uint32_t* row_index, float* out,
+                          uint32_t out_rows, uint32_t cols, hipStream_t s);
+
+// kernels_argmax.hip: two-stage max-loc over n logits.  `partials` must hold
+// argmax_partials(n) entries; the winner lands in *result (packed candidate).
+uint32_t argmax_partials(uint32_t n);
+hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t rule, uint64_t* partials,
+                         uint64_t* result, hipStream_t s);
+
+}  // namespace sihip

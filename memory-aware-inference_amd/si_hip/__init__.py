@@ -1,0 +1,487 @@
+"""Python binding of the gfx950 K-quant C ABI (include/si_hip.h).
+
+`HipContext` mirrors the K-quant methods of super-inference's `MetalContext`
+(src/metal.rs:3354-5015) with the same names and argument meaning; a
+non-zero status from the C ABI raises `HipError` carrying the message the
+reference would return as `Err(String)`.
+
+The library must have been built (memory-aware-inference_amd/build.py);
+there is no CPU fallback: a missing library raises at load time.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import re
+from pathlib import Path
+from typing import Iterable, Sequence
+
+import numpy as np
+
+_HERE = Path(__file__).resolve().parent
+LIB_PATH = _HERE / "libsi_hip.so"
+INCLUDE_DIR = _HERE.parent.parent / "include"
+
+GGML_TYPE_Q4_K = 12
+GGML_TYPE_Q5_K = 13
+GGML_TYPE_Q6_K = 14
+BLOCK_BYTES = {GGML_TYPE_Q4_K: 144, GGML_TYPE_Q5_K: 176, GGML_TYPE_Q6_K: 210}
+ARGMAX_LAST_FINITE = 0
+ARGMAX_FIRST_GREATER = 1
+KERNEL_AUTO = 0
+KERNEL_GENERIC = 1
+MAX_BATCH = 16
+
+STATUS = {
+    0: "SI_HIP_OK", -1: "SI_HIP_ERR_NULL", -2: "SI_HIP_ERR_DIMENSIONS",
+    -3: "SI_HIP_ERR_BYTE_LENGTH", -4: "SI_HIP_ERR_OVERFLOW",
+    -5: "SI_HIP_ERR_UNSUPPORTED_TYPE", -6: "SI_HIP_ERR_BATCH", -7: "SI_HIP_ERR_RANGE",
+    -8: "SI_HIP_ERR_NO_FINITE", -9: "SI_HIP_ERR_DEVICE", -10: "SI_HIP_ERR_OUT_OF_MEMORY",
+    -11: "SI_HIP_ERR_EMPTY",
+}
+
+
+class HipError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{STATUS.get(status, status)}: {message}")
+        self.status = status
+        self.message = message
+
+
+class CommandStats(C.Structure):
+    _fields_ = [("submitted", C.c_uint64), ("async_submitted", C.c_uint64),
+                ("waited", C.c_uint64), ("wait_nanos", C.c_uint64)]
+
+
+_P = C.c_void_p
+_SZ = C.c_size_t
+_U32 = C.c_uint32
+_U64 = C.c_uint64
+_I = C.c_int
+_FP = C.POINTER(C.c_float)
+_BP = C.POINTER(C.c_uint8)
+_U32P = C.POINTER(C.c_uint32)
+
+# name -> (restype, argtypes)
+_SIGS = {
+    "si_hip_last_error": (C.c_char_p, []),
+    "si_hip_status_name": (C.c_char_p, [_I]),
+    "si_hip_abi_version": (_U32, []),
+    "si_hip_context_new": (_I, [_I, C.POINTER(_P)]),
+    "si_hip_context_free": (None, [_P]),
+    "si_hip_upload_quant_weight_private": (_I, [_P, _BP, _SZ, _U32, C.POINTER(_P)]),
+    "si_hip_bind_quant_weight_mapped": (_I, [_P, _BP, _SZ, _U32, C.POINTER(_P)]),
+    "si_hip_quant_weight_view": (_I, [_P, _U64, _U64, _U32, C.POINTER(_P)]),
+    "si_hip_quant_weight_free": (None, [_P]),
+    "si_hip_quant_weight_byte_len": (_U64, [_P]),
+    "si_hip_quant_weight_ggml_type": (_U32, [_P]),
+    "si_hip_quant_weight_is_mapped": (_I, [_P]),
+    "si_hip_quant_weight_device_ptr": (_P, [_P]),
+    "si_hip_q4_k_matvec": (_I, [_P, _BP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_q5_k_matvec": (_I, [_P, _BP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_q6_k_matvec": (_I, [_P, _BP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_gguf_quant_matvec_bytes": (_I, [_P, _U32, _BP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_gguf_quant_matvec_weight": (_I, [_P, _P, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_gguf_quant_matvec_tensor_rows": (_I, [_P, _P, _SZ, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_gguf_quant_matvec_many_weights": (
+        _I, [_P, C.POINTER(_P), C.POINTER(_SZ), _SZ, _SZ, _FP, _SZ, C.POINTER(_FP)]),
+    "si_hip_q4_k_fused_gate_up": (_I, [_P, _BP, _SZ, _BP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_q4_k_fused_gate_up_weights": (_I, [_P, _P, _P, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_gguf_quant_fused_mlp_weights": (_I, [_P, _P, _P, _P, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_q4_k_embedding_row": (_I, [_P, _BP, _SZ, _SZ, _FP]),
+    "si_hip_q4_k_embedding_tensor": (_I, [_P, _P, _SZ, _SZ, _SZ, _FP]),
+    "si_hip_q4_k_embedding_tokens": (_I, [_P, _P, _SZ, _SZ, _U32P, _SZ, _FP]),
+    "si_hip_gguf_quant_matmul_many_bytes": (_I, [_P, _U32, _BP, _SZ, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_gguf_quant_matmul_many_weight": (_I, [_P, _P, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_gguf_quant_matvec_argmax_weight": (_I, [_P, _P, _SZ, _SZ, _FP, _SZ, _U32, _U32P, _FP]),
+    "si_hip_dequantize": (_I, [_P, _U32, _BP, _SZ, _SZ, _FP]),
+    "si_hip_device_alloc": (_I, [_P, _SZ, C.POINTER(_P)]),
+    "si_hip_device_free": (_I, [_P, _P]),
+    "si_hip_copy_to_device": (_I, [_P, _P, _P, _SZ]),
+    "si_hip_copy_from_device": (_I, [_P, _P, _P, _SZ]),
+    "si_hip_synchronize": (_I, [_P]),
+    "si_hip_quant_matvec_device": (_I, [_P, _P, _SZ, _SZ, _P, _P]),
+    "si_hip_q4_k_fused_gate_up_device": (_I, [_P, _P, _P, _SZ, _SZ, _P, _P]),
+    "si_hip_fused_mlp_device": (_I, [_P, _P, _P, _P, _SZ, _SZ, _SZ, _P, _P, _P]),
+    "si_hip_matmul_many_device": (_I, [_P, _P, _SZ, _SZ, _SZ, _P, _P]),
+    "si_hip_matvec_argmax_device": (_I, [_P, _P, _SZ, _SZ, _P, _U32, _P, _P]),
+    "si_hip_argmax_result_index": (_U32, [_U64, _U32]),
+    "si_hip_embedding_device": (_I, [_P, _P, _SZ, _SZ, _P, _SZ, _P]),
+    "si_hip_event_record": (_I, [_P, _U32]),
+    "si_hip_event_elapsed_ms": (_I, [_P, _U32, _U32, C.POINTER(C.c_float)]),
+    "si_hip_quant_matvec_device_repeat": (_I, [_P, C.POINTER(_P), _SZ, _SZ, _SZ, _P, _P, _SZ]),
+    "si_hip_set_kernel_policy": (_I, [_P, _U32]),
+    "si_hip_current_allocated_bytes": (_U64, [_P]),
+    "si_hip_peak_allocated_bytes": (_U64, [_P]),
+    "si_hip_peak_active_weight_bytes": (_U64, [_P]),
+    "si_hip_reset_peaks": (None, [_P]),
+    "si_hip_get_command_stats": (_I, [_P, C.POINTER(CommandStats)]),
+    # si_hip_synth.h
+    "si_hip_synth_blocks": (_I, [_U32, _U64, _U64, _SZ, _BP, _SZ, _I]),
+    "si_hip_synth_normal_f32": (_I, [_U64, _U64, _SZ, C.c_float, _FP]),
+    "si_hip_synth_token_ids": (_I, [_U64, _SZ, _U32, _U32P]),
+    "si_hip_synth_f32_to_f16": (C.c_uint16, [C.c_float]),
+}
+
+_lib = None
+
+
+def lib() -> C.CDLL:
+    """Load libsi_hip.so (raises if it has not been built)."""
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with "
+                "`python memory-aware-inference_amd/build.py` (no CPU fallback exists)")
+        handle = C.CDLL(str(LIB_PATH))
+        for name, (res, args) in _SIGS.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+def header_symbols() -> list[str]:
+    """Every function the public headers declare."""
+    names = []
+    for h in sorted(INCLUDE_DIR.glob("*.h")):
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names += re.findall(r"\b(si_hip_\w+)\s*\(", text)
+    return sorted(set(names))
+
+
+def last_error() -> str:
+    return lib().si_hip_last_error().decode()
+
+
+def _check(status: int) -> None:
+    if status != 0:
+        raise HipError(status, last_error())
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(_FP)
+
+
+def _u8(b) -> np.ndarray:
+    if isinstance(b, (bytes, bytearray, memoryview)):
+        return np.frombuffer(b, dtype=np.uint8)
+    return np.ascontiguousarray(b, dtype=np.uint8)
+
+
+def _bp(a: np.ndarray):
+    return a.ctypes.data_as(_BP)
+
+
+# ---------------------------------------------------------------------------
+# synthetic data (host only, no GPU needed)
+
+def synth_blocks(ggml_type: int, seed: int, n_blocks: int, first_block: int = 0,
+                 threads: int = 1) -> np.ndarray:
+    out = np.empty(n_blocks * BLOCK_BYTES[ggml_type], dtype=np.uint8)
+    _check(lib().si_hip_synth_blocks(ggml_type, seed, first_block, n_blocks, _bp(out), out.size,
+                                     threads))
+    return out
+
+
+def synth_matrix(ggml_type: int, seed: int, rows: int, cols: int, threads: int = 1) -> np.ndarray:
+    return synth_blocks(ggml_type, seed, rows * (cols // 256), threads=threads)
+
+
+def synth_normal(seed: int, n: int, scale: float = 1.0, first_index: int = 0) -> np.ndarray:
+    out = np.empty(n, dtype=np.float32)
+    _check(lib().si_hip_synth_normal_f32(seed, first_index, n, scale, _fp(out)))
+    return out
+
+
+def synth_token_ids(seed: int, n: int, vocab: int) -> np.ndarray:
+    out = np.empty(n, dtype=np.uint32)
+    _check(lib().si_hip_synth_token_ids(seed, n, vocab, out.ctypes.data_as(_U32P)))
+    return out
+
+
+def f32_to_f16_bits(v: float) -> int:
+    return int(lib().si_hip_synth_f32_to_f16(v))
+
+
+# ---------------------------------------------------------------------------
+
+class QuantWeight:
+    """Owning handle of HBM-resident packed blocks (QuantWeight, metal.rs:1840)."""
+
+    def __init__(self, ctx: "HipContext", handle: int, parent: "QuantWeight | None" = None):
+        self._ctx = ctx
+        self._h = C.c_void_p(handle)
+        self._parent = parent
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def byte_len(self) -> int:
+        return int(lib().si_hip_quant_weight_byte_len(self._h))
+
+    def ggml_type(self) -> int:
+        return int(lib().si_hip_quant_weight_ggml_type(self._h))
+
+    def is_mapped(self) -> bool:
+        return bool(lib().si_hip_quant_weight_is_mapped(self._h))
+
+    def device_ptr(self) -> int:
+        return int(lib().si_hip_quant_weight_device_ptr(self._h) or 0)
+
+    def view(self, offset: int, nbytes: int, ggml_type: int) -> "QuantWeight":
+        out = C.c_void_p()
+        _check(lib().si_hip_quant_weight_view(self._h, offset, nbytes, ggml_type, C.byref(out)))
+        return QuantWeight(self._ctx, out.value, parent=self)
+
+    def free(self) -> None:
+        if self._h:
+            lib().si_hip_quant_weight_free(self._h)
+            self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HipContext:
+    """K-quant surface of MetalContext on one MI355X GPU."""
+
+    def __init__(self, device: int = 0):
+        out = C.c_void_p()
+        _check(lib().si_hip_context_new(device, C.byref(out)))
+        self._h = out
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    def close(self) -> None:
+        if self._h:
+            lib().si_hip_context_free(self._h)
+            self._h = C.c_void_p()
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def set_kernel_policy(self, policy: int) -> None:
+        _check(lib().si_hip_set_kernel_policy(self._h, policy))
+
+    # ---- weights
+    def upload_quant_weight_private(self, weight_bytes, ggml_type: int) -> QuantWeight:
+        b = _u8(weight_bytes)
+        out = C.c_void_p()
+        _check(lib().si_hip_upload_quant_weight_private(self._h, _bp(b), b.size, ggml_type,
+                                                        C.byref(out)))
+        return QuantWeight(self, out.value)
+
+    def bind_quant_weight_mapped(self, weight_bytes, ggml_type: int) -> QuantWeight:
+        b = _u8(weight_bytes)
+        out = C.c_void_p()
+        _check(lib().si_hip_bind_quant_weight_mapped(self._h, _bp(b), b.size, ggml_type,
+                                                     C.byref(out)))
+        return QuantWeight(self, out.value)
+
+    # ---- matvec
+    def _typed(self, fn, weight_bytes, rows, columns, input) -> np.ndarray:
+        b, x = _u8(weight_bytes), _f32(input)
+        y = np.empty(rows, dtype=np.float32)
+        _check(fn(self._h, _bp(b), b.size, rows, columns, _fp(x), x.size, _fp(y)))
+        return y
+
+    def q4_k_matvec(self, weight_bytes, rows: int, columns: int, input) -> np.ndarray:
+        return self._typed(lib().si_hip_q4_k_matvec, weight_bytes, rows, columns, input)
+
+    def q5_k_matvec(self, weight_bytes, rows: int, columns: int, input) -> np.ndarray:
+        return self._typed(lib().si_hip_q5_k_matvec, weight_bytes, rows, columns, input)
+
+    def q6_k_matvec(self, weight_bytes, rows: int, columns: int, input) -> np.ndarray:
+        return self._typed(lib().si_hip_q6_k_matvec, weight_bytes, rows, columns, input)
+
+    def gguf_quant_matvec_bytes(self, ggml_type: int, weight_bytes, rows: int, columns: int,
+                                input) -> np.ndarray:
+        b, x = _u8(weight_bytes), _f32(input)
+        y = np.empty(rows, dtype=np.float32)
+        _check(lib().si_hip_gguf_quant_matvec_bytes(self._h, ggml_type, _bp(b), b.size, rows,
+                                                    columns, _fp(x), x.size, _fp(y)))
+        return y
+
+    def gguf_quant_matvec_weight(self, weight: QuantWeight, rows: int, columns: int,
+                                 input) -> np.ndarray:
+        x = _f32(input)
+        y = np.empty(rows, dtype=np.float32)
+        _check(lib().si_hip_gguf_quant_matvec_weight(self._h, weight.handle, rows, columns,
+                                                     _fp(x), x.size, _fp(y)))
+        return y
+
+    def gguf_quant_matvec_tensor_rows(self, tensor: QuantWeight, shape: Sequence[int],
+                                      row_start: int, row_count: int, input) -> np.ndarray:
+        x = _f32(input)
+        y = np.empty(max(row_count, 1), dtype=np.float32)
+        _check(lib().si_hip_gguf_quant_matvec_tensor_rows(
+            self._h, tensor.handle, shape[0], shape[1], row_start, row_count, _fp(x), x.size,
+            _fp(y)))
+        return y[:row_count]
+
+    def gguf_quant_matvec_many_weights(self, weights: Sequence[QuantWeight],
+                                       rows: Sequence[int], columns: int, input) -> list:
+        x = _f32(input)
+        n = len(weights)
+        outs = [np.empty(r, dtype=np.float32) for r in rows]
+        harr = (C.c_void_p * n)(*[w.handle.value for w in weights])
+        rarr = (C.c_size_t * n)(*rows)
+        oarr = (_FP * n)(*[_fp(o) for o in outs])
+        _check(lib().si_hip_gguf_quant_matvec_many_weights(self._h, harr, rarr, n, columns,
+                                                           _fp(x), x.size, oarr))
+        return outs
+
+    # ---- fused SwiGLU
+    def q4_k_fused_gate_up(self, gate_bytes, up_bytes, rows: int, columns: int,
+                           input) -> np.ndarray:
+        g, u, x = _u8(gate_bytes), _u8(up_bytes), _f32(input)
+        y = np.empty(rows, dtype=np.float32)
+        _check(lib().si_hip_q4_k_fused_gate_up(self._h, _bp(g), g.size, _bp(u), u.size, rows,
+                                               columns, _fp(x), x.size, _fp(y)))
+        return y
+
+    def q4_k_fused_gate_up_weights(self, gate: QuantWeight, up: QuantWeight, rows: int,
+                                   columns: int, input) -> np.ndarray:
+        x = _f32(input)
+        y = np.empty(rows, dtype=np.float32)
+        _check(lib().si_hip_q4_k_fused_gate_up_weights(self._h, gate.handle, up.handle, rows,
+                                                       columns, _fp(x), x.size, _fp(y)))
+        return y
+
+    def gguf_quant_fused_mlp_weights(self, gate: QuantWeight, up: QuantWeight,
+                                     down: QuantWeight, gate_rows: int, columns: int,
+                                     down_rows: int, input) -> np.ndarray:
+        x = _f32(input)
+        y = np.empty(down_rows, dtype=np.float32)
+        _check(lib().si_hip_gguf_quant_fused_mlp_weights(
+            self._h, gate.handle, up.handle, down.handle, gate_rows, columns, down_rows, _fp(x),
+            x.size, _fp(y)))
+        return y
+
+    # ---- embedding
+    def q4_k_embedding_row(self, row_bytes, columns: int) -> np.ndarray:
+        b = _u8(row_bytes)
+        y = np.empty(max(columns, 1), dtype=np.float32)
+        _check(lib().si_hip_q4_k_embedding_row(self._h, _bp(b), b.size, columns, _fp(y)))
+        return y[:columns]
+
+    def q4_k_embedding_tensor(self, table: QuantWeight, shape: Sequence[int],
+                              token_id: int) -> np.ndarray:
+        y = np.empty(max(shape[0], 1), dtype=np.float32)
+        _check(lib().si_hip_q4_k_embedding_tensor(self._h, table.handle, shape[0], shape[1],
+                                                  token_id, _fp(y)))
+        return y[:shape[0]]
+
+    def q4_k_embedding_tokens(self, table: QuantWeight, shape: Sequence[int],
+                              token_ids) -> np.ndarray:
+        ids = np.ascontiguousarray(token_ids, dtype=np.uint32)
+        y = np.empty((max(ids.size, 1), shape[0]), dtype=np.float32)
+        _check(lib().si_hip_q4_k_embedding_tokens(self._h, table.handle, shape[0], shape[1],
+                                                  ids.ctypes.data_as(_U32P), ids.size, _fp(y)))
+        return y[:ids.size]
+
+    # ---- multi-token verify (the reference's Vec<Vec<f32>>, batch-major)
+    def gguf_quant_matmul_many_bytes(self, ggml_type: int, weight_bytes, rows: int, columns: int,
+                                     batch: int, inputs) -> list:
+        b, x = _u8(weight_bytes), _f32(inputs).reshape(-1)
+        y = np.empty(max(batch, 1) * rows, dtype=np.float32)
+        _check(lib().si_hip_gguf_quant_matmul_many_bytes(self._h, ggml_type, _bp(b), b.size, rows,
+                                                         columns, batch, _fp(x), x.size, _fp(y)))
+        return [y[i * rows:(i + 1) * rows] for i in range(batch)]
+
+    def gguf_quant_matmul_many_weight(self, weight: QuantWeight, rows: int, columns: int,
+                                      batch: int, inputs) -> list:
+        x = _f32(inputs).reshape(-1)
+        y = np.empty(max(batch, 1) * rows, dtype=np.float32)
+        _check(lib().si_hip_gguf_quant_matmul_many_weight(self._h, weight.handle, rows, columns,
+                                                          batch, _fp(x), x.size, _fp(y)))
+        return [y[i * rows:(i + 1) * rows] for i in range(batch)]
+
+    # ---- head + argmax
+    def gguf_quant_matvec_argmax_weight(self, head: QuantWeight, rows: int, columns: int, input,
+                                        rule: int = ARGMAX_LAST_FINITE,
+                                        want_logits: bool = True):
+        x = _f32(input)
+        tok = C.c_uint32()
+        logits = np.empty(rows, dtype=np.float32) if want_logits else None
+        _check(lib().si_hip_gguf_quant_matvec_argmax_weight(
+            self._h, head.handle, rows, columns, _fp(x), x.size, rule, C.byref(tok),
+            _fp(logits) if logits is not None else None))
+        return int(tok.value), logits
+
+    def dequantize(self, ggml_type: int, data, elements: int) -> np.ndarray:
+        b = _u8(data)
+        y = np.empty(max(elements, 1), dtype=np.float32)
+        _check(lib().si_hip_dequantize(self._h, ggml_type, _bp(b), b.size, elements, _fp(y)))
+        return y[:elements]
+
+    # ---- device-resident plumbing
+    def device_alloc(self, nbytes: int) -> int:
+        p = C.c_void_p()
+        _check(lib().si_hip_device_alloc(self._h, nbytes, C.byref(p)))
+        return p.value
+
+    def device_free(self, ptr: int) -> None:
+        _check(lib().si_hip_device_free(self._h, C.c_void_p(ptr)))
+
+    def to_device(self, ptr: int, arr: np.ndarray) -> None:
+        a = np.ascontiguousarray(arr)
+        _check(lib().si_hip_copy_to_device(self._h, C.c_void_p(ptr), a.ctypes.data_as(_P),
+                                           a.nbytes))
+
+    def from_device(self, ptr: int, shape, dtype=np.float32) -> np.ndarray:
+        out = np.empty(shape, dtype=dtype)
+        _check(lib().si_hip_copy_from_device(self._h, out.ctypes.data_as(_P), C.c_void_p(ptr),
+                                             out.nbytes))
+        return out
+
+    def synchronize(self) -> None:
+        _check(lib().si_hip_synchronize(self._h))
+
+    def event_record(self, slot: int) -> None:
+        _check(lib().si_hip_event_record(self._h, slot))
+
+    def event_elapsed_ms(self, a: int, b: int) -> float:
+        ms = C.c_float()
+        _check(lib().si_hip_event_elapsed_ms(self._h, a, b, C.byref(ms)))
+        return float(ms.value)
+
+    # ---- telemetry
+    def current_allocated_bytes(self) -> int:
+        return int(lib().si_hip_current_allocated_bytes(self._h))
+
+    def peak_allocated_bytes(self) -> int:
+        return int(lib().si_hip_peak_allocated_bytes(self._h))
+
+    def peak_active_weight_bytes(self) -> int:
+        return int(lib().si_hip_peak_active_weight_bytes(self._h))
+
+    def reset_peaks(self) -> None:
+        lib().si_hip_reset_peaks(self._h)
+
+    def command_stats(self) -> dict:
+        s = CommandStats()
+        _check(lib().si_hip_get_command_stats(self._h, C.byref(s)))
+        return {k: int(getattr(s, k)) for k, _ in CommandStats._fields_}
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

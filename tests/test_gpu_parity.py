@@ -1,0 +1,432 @@
+"""GPU parity: the HIP path against the CPU oracle, through the C ABI.
+
+Bars: dequantisation bit-exact with quant.rs; every
+f32 dot within 2e-5 * sum|w*x| of the f64 value of the exact products;
+greedy argmax identical.  Tests that restate the reference's own Metal tests
+(src/metal.rs:7445-7602) keep their inputs and tolerances.
+"""
+import json
+import struct
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import si_hip
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+DOT_TOL = 2e-5          # relative to sum |w*x|
+POLICIES = [si_hip.KERNEL_AUTO, si_hip.KERNEL_GENERIC]
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def same_bits(a, b):
+    a, b = np.asarray(a, np.float32), np.asarray(b, np.float32)
+    nan = np.isnan(a) & np.isnan(b)
+    return bool(np.all(nan | (a.view(np.uint32) == b.view(np.uint32))))
+
+
+def assert_dot_close(y, y64, absdot, tol=DOT_TOL, what=""):
+    err = np.abs(y.astype(np.float64) - y64)
+    bound = tol * absdot + 1e-30
+    worst = np.max(err / bound)
+    assert worst <= 1.0, f"{what}: worst error {worst:.3f}x of {tol} * sum|w*x|"
+    return worst
+
+
+@pytest.fixture(params=POLICIES, ids=["auto", "generic"])
+def ctx(request, hip_ctx):
+    hip_ctx.set_kernel_policy(request.param)
+    yield hip_ctx
+    hip_ctx.set_kernel_policy(si_hip.KERNEL_AUTO)
+
+
+# ---- dequantisation: bit-exact ------------------------------------------------
+@pytest.mark.parametrize("t,name", [(12, "q4_k"), (13, "q5_k"), (14, "q6_k")])
+def test_dequantize_fixtures_bit_exact(hip_ctx, t, name):
+    log(f"dequant fixtures {name}")
+    fx = json.loads((GOLDEN / f"blocks_{name}.json").read_text())
+    data = bytes.fromhex(fx["bytes"])
+    got = hip_ctx.dequantize(t, data, fx["n_blocks"] * 256)
+    exp = np.array(fx["expected_bits"], dtype=np.uint32).view(np.float32)
+    assert same_bits(got, exp)
+
+
+def test_dequantize_reference_kats(hip_ctx):
+    kats = json.loads((GOLDEN / "quant_kats.json").read_text())
+    for k in kats["kats"]:
+        got = hip_ctx.dequantize(k["ggml_type"], bytes.fromhex(k["bytes"]), k["elements"])
+        assert np.array_equal(got, np.array(k["expected"], np.float32)), k["name"]
+    for r in kats["rejections"]:
+        with pytest.raises(si_hip.HipError):
+            hip_ctx.dequantize(r["ggml_type"], bytes(r["byte_len"]), r["elements"])
+
+
+@pytest.mark.parametrize("t", [12, 13, 14])
+def test_dequantize_random_blocks_bit_exact(hip_ctx, t):
+    log(f"dequant random type {t}")
+    data = si_hip.synth_blocks(t, seed=900 + t, n_blocks=4096)
+    got = hip_ctx.dequantize(t, data, 4096 * 256)
+    assert same_bits(got, O.dequantize(t, data, 4096 * 256))
+    # fully random bytes (NaN/inf d included)
+    raw = np.random.default_rng(t).integers(0, 256, 1024 * si_hip.BLOCK_BYTES[t], dtype=np.uint8)
+    assert same_bits(hip_ctx.dequantize(t, raw, 1024 * 256), O.dequantize(t, raw, 1024 * 256))
+
+
+# ---- matvec ---------------------------------------------------------------------
+SHAPES = [(1, 256), (7, 512), (64, 1024), (300, 5120), (1024, 5120), (129, 17408)]
+
+
+@pytest.mark.parametrize("t", [12, 13, 14])
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_matvec_within_tolerance(ctx, t, rows, cols):
+    log(f"matvec t={t} {rows}x{cols}")
+    w = si_hip.synth_matrix(t, seed=rows * 31 + cols + t, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(rows + 7 * t, cols)
+    _, y64, ab = O.matvec(t, w, rows, cols, x, threads=8)
+    y = ctx.gguf_quant_matvec_bytes(t, w, rows, cols, x)
+    assert_dot_close(y, y64, ab, what=f"type {t} {rows}x{cols}")
+    weight = ctx.upload_quant_weight_private(w, t)
+    y2 = ctx.gguf_quant_matvec_weight(weight, rows, cols, x)
+    assert np.array_equal(y, y2)
+
+
+@pytest.mark.parametrize("rows,cols", [(17408, 5120), (5120, 5120), (5120, 17408), (1024, 5120)])
+def test_q4_k_baseline_shapes(hip_ctx, rows, cols):
+    log(f"q4_k baseline shape {rows}x{cols}")
+    w = si_hip.synth_matrix(12, seed=2024, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(5, cols)
+    _, y64, ab = O.matvec(12, w, rows, cols, x, threads=8)
+    weight = hip_ctx.upload_quant_weight_private(w, 12)
+    y = hip_ctx.gguf_quant_matvec_weight(weight, rows, cols, x)
+    worst = assert_dot_close(y, y64, ab, what=f"{rows}x{cols}")
+    log(f"  worst error / bound = {worst:.4f}")
+
+
+def test_matvec_cancellation_heavy_blocks(ctx):
+    # blocks where d*sc*q and dmin*m nearly cancel: all nibbles equal, m chosen
+    # so that w is small against its two terms
+    rows, cols = 16, 2048
+    rng = np.random.default_rng(11)
+    blocks = []
+    for r in range(rows * cols // 256):
+        b = bytearray(144)
+        b[0:2] = struct.pack("<e", 0.01 + 0.001 * (r % 5))
+        b[2:4] = struct.pack("<e", 0.01 + 0.001 * (r % 5))
+        sc = [int(v) for v in rng.integers(20, 64, 8)]
+        q = int(rng.integers(1, 16))
+        mn = [min(63, s * q // 4) for s in sc]
+        import numpy_ref
+        b[4:16] = numpy_ref.encode_k4_scales(sc, mn)
+        b[16:] = bytes([(q | (q << 4))] * 128)
+        # sprinkle different nibbles so rows are not all-constant
+        for i in rng.integers(0, 128, 12):
+            b[16 + int(i)] = int(rng.integers(0, 256))
+        blocks.append(bytes(b))
+    w = b"".join(blocks)
+    x = si_hip.synth_normal(99, cols)
+    _, y64, ab = O.matvec(12, w, rows, cols, x)
+    y = ctx.q4_k_matvec(w, rows, cols, x)
+    assert_dot_close(y, y64, ab, what="cancellation")
+
+
+# restatement of metal.rs:7445-7494 (q4_k_matvec_kernel_matches_cpu_reference)
+def test_reference_q4_k_matvec_test(ctx):
+    rows, cols = 2, 512
+    w = bytearray(rows * 2 * 144)
+    for row in range(rows):
+        for bi in range(2):
+            s = (row * 2 + bi) * 144
+            w[s:s + 2] = struct.pack("<H", 0x3C00)
+            for i in range(12):
+                w[s + 4 + i] = (i * 13 + 7) & 0xFF
+            for i in range(128):
+                w[s + 16 + i] = 0x10 if (i + row + bi) % 3 == 0 else 0x21
+    x = np.array([((i % 11) - 5.0) / 3.0 for i in range(cols)], np.float32)
+    expected, _, _ = O.matvec(12, bytes(w), rows, cols, x)
+    got = ctx.q4_k_matvec(bytes(w), rows, cols, x)
+    assert np.all(np.abs(got - expected) < 1e-4)
+
+
+# restatement of metal.rs:7565-7602 (q5_and_q6_k_matvec_kernels_match_cpu_reference)
+def test_reference_q5_q6_matvec_test(ctx):
+    x = np.array([((i % 13) - 6.0) / 5.0 for i in range(256)], np.float32)
+    q5 = bytearray(176)
+    q5[0:2] = struct.pack("<H", 0x3C00)
+    q5[4:16] = bytes([1] * 12)
+    q5[16:48] = bytes([0xFF] * 32)
+    q5[48:] = bytes([0x10] * 128)
+    e5, _, _ = O.matvec(13, bytes(q5), 1, 256, x)
+    assert abs(ctx.q5_k_matvec(bytes(q5), 1, 256, x)[0] - e5[0]) < 1e-4
+    q6 = bytearray(210)
+    q6[208:210] = struct.pack("<H", 0x3C00)
+    q6[:128] = bytes([0x21] * 128)
+    q6[128:192] = bytes([0xE4] * 64)
+    q6[192:208] = bytes([1] * 16)
+    e6, _, _ = O.matvec(14, bytes(q6), 1, 256, x)
+    assert abs(ctx.q6_k_matvec(bytes(q6), 1, 256, x)[0] - e6[0]) < 1e-4
+
+
+# ---- fused SwiGLU -----------------------------------------------------------------
+def silu64(g):
+    return g / (1.0 + np.exp(-g))
+
+
+def gate_up_bound(g64, ag, u64, au):
+    sig = 1.0 / (1.0 + np.exp(-g64))
+    dsilu = np.abs(sig * (1.0 + g64 * (1.0 - sig)))
+    return DOT_TOL * (dsilu * ag * np.abs(u64) + np.abs(silu64(g64)) * au) \
+        + 4e-7 * np.abs(silu64(g64) * u64) + 1e-30
+
+
+# restatement of metal.rs:7498-7540
+def test_reference_fused_gate_up_test(ctx):
+    rows, cols = 2, 256
+    gate = bytearray(rows * 144)
+    up = bytearray(rows * 144)
+    for row in range(rows):
+        s = row * 144
+        gate[s:s + 2] = struct.pack("<H", 0x3C00)
+        up[s:s + 2] = struct.pack("<H", 0x3800)
+        gate[s + 4:s + 16] = bytes([7] * 12)
+        up[s + 4:s + 16] = bytes([11] * 12)
+        gate[s + 16:s + 144] = bytes([0x21] * 128)
+        up[s + 16:s + 144] = bytes([0x12] * 128)
+    x = np.array([((i % 17) - 8.0) / 5.0 for i in range(cols)], np.float32)
+    g, _, _ = O.matvec(12, bytes(gate), rows, cols, x)
+    u, _, _ = O.matvec(12, bytes(up), rows, cols, x)
+    expected = np.array([O.silu(float(a)) * b for a, b in zip(g, u)], np.float32)
+    got = ctx.q4_k_fused_gate_up(bytes(gate), bytes(up), rows, cols, x)
+    assert np.all(np.abs(got - expected) < 1e-4)
+
+
+@pytest.mark.parametrize("rows,cols", [(64, 1024), (1000, 5120), (17408, 5120)])
+def test_fused_gate_up_within_tolerance(ctx, rows, cols):
+    log(f"gate/up {rows}x{cols}")
+    gw = si_hip.synth_matrix(12, seed=501, rows=rows, cols=cols, threads=8)
+    uw = si_hip.synth_matrix(12, seed=502, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(503, cols, scale=0.1)
+    _, g64, ag = O.matvec(12, gw, rows, cols, x, threads=8)
+    _, u64, au = O.matvec(12, uw, rows, cols, x, threads=8)
+    g = ctx.upload_quant_weight_private(gw, 12)
+    u = ctx.upload_quant_weight_private(uw, 12)
+    h = ctx.q4_k_fused_gate_up_weights(g, u, rows, cols, x)
+    ref = silu64(g64) * u64
+    err = np.abs(h.astype(np.float64) - ref)
+    assert np.all(err <= gate_up_bound(g64, ag, u64, au))
+
+
+def test_fused_mlp_q6_down(ctx):
+    gate_rows, cols, down_rows = 2048, 1024, 512
+    log("fused mlp")
+    gw = si_hip.synth_matrix(12, seed=601, rows=gate_rows, cols=cols, threads=8)
+    uw = si_hip.synth_matrix(12, seed=602, rows=gate_rows, cols=cols, threads=8)
+    dw = si_hip.synth_matrix(14, seed=603, rows=down_rows, cols=gate_rows, threads=8)
+    x = si_hip.synth_normal(604, cols, scale=0.1)
+    _, g64, ag = O.matvec(12, gw, gate_rows, cols, x, threads=8)
+    _, u64, au = O.matvec(12, uw, gate_rows, cols, x, threads=8)
+    h64 = silu64(g64) * u64
+    hb = gate_up_bound(g64, ag, u64, au)
+    wd = O.dequantize(14, dw, down_rows * gate_rows).reshape(down_rows, gate_rows).astype(np.float64)
+    y64 = wd @ h64
+    bound = DOT_TOL * (np.abs(wd) @ np.abs(h64)) + np.abs(wd) @ hb + 1e-30
+    G = ctx.upload_quant_weight_private(gw, 12)
+    U = ctx.upload_quant_weight_private(uw, 12)
+    D = ctx.upload_quant_weight_private(dw, 14)
+    y = ctx.gguf_quant_fused_mlp_weights(G, U, D, gate_rows, cols, down_rows, x)
+    assert np.all(np.abs(y - y64) <= bound)
+
+
+# ---- embedding ----------------------------------------------------------------------
+# restatement of metal.rs:7544-7561 (bit-exact here: it is a dequantisation)
+def test_reference_embedding_row_test(ctx):
+    row = bytearray(144)
+    row[0:2] = struct.pack("<H", 0x3C00)
+    row[4:16] = bytes([7, 19, 31, 43, 55, 67, 79, 91, 103, 115, 127, 139])
+    row[16:] = bytes([0x21] * 128)
+    got = ctx.q4_k_embedding_row(bytes(row), 256)
+    assert same_bits(got, O.dequantize(12, bytes(row), 256))
+
+
+def test_embedding_tokens_bit_exact(hip_ctx):
+    vocab, cols = 4099, 5120
+    table = si_hip.synth_matrix(12, seed=700, rows=vocab, cols=cols, threads=8)
+    T = hip_ctx.upload_quant_weight_private(table, 12)
+    ids = si_hip.synth_token_ids(701, 64, vocab)
+    ids[0], ids[1] = 0, vocab - 1
+    got = hip_ctx.q4_k_embedding_tokens(T, (cols, vocab), ids)
+    rb = cols // 256 * 144
+    for i, t in enumerate(ids):
+        exp = O.dequantize(12, table[t * rb:(t + 1) * rb], cols)
+        assert same_bits(got[i], exp)
+    one = hip_ctx.q4_k_embedding_tensor(T, (cols, vocab), int(ids[5]))
+    assert same_bits(one, got[5])
+    with pytest.raises(si_hip.HipError) as e:
+        hip_ctx.q4_k_embedding_tensor(T, (cols, vocab), vocab)
+    assert e.value.status == -7
+
+
+# ---- multi-token verify --------------------------------------------------------------
+@pytest.mark.parametrize("t", [12, 13, 14])
+@pytest.mark.parametrize("batch", [1, 2, 4, 8, 16])
+def test_matmul_many(ctx, t, batch):
+    rows, cols = 512, 5120
+    log(f"matmul_many t={t} batch={batch}")
+    w = si_hip.synth_matrix(t, seed=800 + t, rows=rows, cols=cols, threads=8)
+    X = si_hip.synth_normal(801, batch * cols).reshape(batch, cols)
+    W = ctx.upload_quant_weight_private(w, t)
+    if batch <= 8:
+        outs = ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    else:
+        outs = ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(batch):
+        _, y64, ab = O.matvec(t, w, rows, cols, X[b], threads=8)
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+
+
+def test_matmul_many_bytes_matches_weight(hip_ctx):
+    rows, cols, batch = 96, 1024, 3
+    w = si_hip.synth_matrix(13, seed=9, rows=rows, cols=cols)
+    X = si_hip.synth_normal(10, batch * cols)
+    a = hip_ctx.gguf_quant_matmul_many_bytes(13, w, rows, cols, batch, X)
+    W = hip_ctx.upload_quant_weight_private(w, 13)
+    b = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for i in range(batch):
+        assert np.array_equal(a[i], b[i])
+
+
+# ---- output head + argmax -----------------------------------------------------------
+@pytest.mark.parametrize("t", [12, 14])
+def test_head_argmax_matches_oracle(ctx, t):
+    rows, cols = 20011, 5120
+    log(f"head argmax t={t}")
+    w = si_hip.synth_matrix(t, seed=1100 + t, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(1101, cols)
+    y32, y64, ab = O.matvec(t, w, rows, cols, x, threads=8)
+    H = ctx.upload_quant_weight_private(w, t)
+    tok, logits = ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, x)
+    assert_dot_close(logits, y64, ab, what="head logits")
+    order = np.argsort(y64)
+    top, second = order[-1], order[-2]
+    margin = y64[top] - y64[second]
+    bound = DOT_TOL * (ab[top] + ab[second])
+    log(f"  top-2 margin {margin:.6g} vs error bound {bound:.3g}")
+    assert margin > bound
+    assert tok == top == O.argmax_last_finite(y32) == O.argmax_last_finite(logits)
+    tok2, _ = ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, x, rule=si_hip.ARGMAX_FIRST_GREATER,
+                                                  want_logits=False)
+    assert tok2 == tok
+
+
+def test_head_argmax_tie_rules(hip_ctx):
+    # identical rows -> identical logits -> ties decided by the rule
+    rows, cols = 4096 + 5, 256
+    base = si_hip.synth_matrix(12, seed=1200, rows=rows, cols=cols)
+    blocks = base.reshape(rows, 144).copy()
+    # row 17: d = 1, dmin = 0, every scale and nibble at its maximum, so with
+    # x = 1 its logit (63*15*256) dominates every random row (d ~ 0.02)
+    blocks[17, 0:2] = np.frombuffer(struct.pack("<H", 0x3C00), np.uint8)
+    blocks[17, 2:4] = 0
+    blocks[17, 4:] = 0xFF
+    blocks[1000] = blocks[17]
+    blocks[3000] = blocks[17]
+    x = np.ones(cols, np.float32)
+    H = hip_ctx.upload_quant_weight_private(blocks.tobytes(), 12)
+    _, logits = hip_ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, x)
+    assert logits[17] == logits[1000] == logits[3000] == logits.max()
+    last, _ = hip_ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, x, rule=si_hip.ARGMAX_LAST_FINITE)
+    first, _ = hip_ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, x, rule=si_hip.ARGMAX_FIRST_GREATER)
+    assert (first, last) == (17, 3000)
+    assert last == O.argmax_last_finite(logits)
+    assert first == O.argmax_first_greater(logits)
+
+
+def test_head_argmax_no_finite_logits(hip_ctx):
+    # d = +inf with nonzero scales makes every logit non-finite
+    rows, cols = 3, 256
+    b = bytearray(si_hip.synth_matrix(12, seed=3, rows=rows, cols=cols).tobytes())
+    for r in range(rows):
+        b[r * 144:r * 144 + 2] = struct.pack("<H", 0x7C00)
+        b[r * 144 + 4:r * 144 + 16] = bytes([0x3F] * 12)
+    H = hip_ctx.upload_quant_weight_private(bytes(b), 12)
+    x = np.ones(cols, np.float32)
+    with pytest.raises(si_hip.HipError) as e:
+        hip_ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, x)
+    assert e.value.status == -8
+    tok, _ = hip_ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, x, rule=si_hip.ARGMAX_FIRST_GREATER)
+    assert tok == O.argmax_first_greater(np.full(rows, np.nan, np.float32))
+
+
+# ---- tensor rows, grouped submission, views, telemetry ---------------------------------
+def test_tensor_rows_and_views(hip_ctx):
+    rows, cols = 300, 1024
+    w = si_hip.synth_matrix(14, seed=1300, rows=rows, cols=cols)
+    x = si_hip.synth_normal(1301, cols)
+    T = hip_ctx.upload_quant_weight_private(w, 14)
+    full = hip_ctx.gguf_quant_matvec_weight(T, rows, cols, x)
+    part = hip_ctx.gguf_quant_matvec_tensor_rows(T, (cols, rows), 37, 100, x)
+    assert np.array_equal(part, full[37:137])
+    with pytest.raises(si_hip.HipError) as e:
+        hip_ctx.gguf_quant_matvec_tensor_rows(T, (cols, rows), 250, 51, x)
+    assert e.value.status == -7 and e.value.message == "Q6_K row range is invalid"
+    rb = cols // 256 * 210
+    V = T.view(37 * rb, 100 * rb, 14)
+    assert np.array_equal(hip_ctx.gguf_quant_matvec_weight(V, 100, cols, x), full[37:137])
+    with pytest.raises(si_hip.HipError):
+        T.view(0, rows * rb + 1, 14)
+
+
+def test_grouped_matvecs_share_one_submission(hip_ctx):
+    cols = 2048
+    x = si_hip.synth_normal(1400, cols)
+    specs = [(12, 64), (13, 33), (14, 100)]
+    ws, raws = [], []
+    for i, (t, r) in enumerate(specs):
+        raw = si_hip.synth_matrix(t, seed=1401 + i, rows=r, cols=cols)
+        raws.append(raw)
+        ws.append(hip_ctx.upload_quant_weight_private(raw, t))
+    before = hip_ctx.command_stats()
+    outs = hip_ctx.gguf_quant_matvec_many_weights(ws, [r for _, r in specs], cols, x)
+    after = hip_ctx.command_stats()
+    assert after["waited"] - before["waited"] == 1
+    for (t, r), raw, y in zip(specs, raws, outs):
+        assert np.array_equal(y, hip_ctx.gguf_quant_matvec_weight(ws[specs.index((t, r))], r, cols, x))
+
+
+def test_telemetry_counts_weights(hip_ctx):
+    hip_ctx.reset_peaks()
+    base = hip_ctx.current_allocated_bytes()
+    w = si_hip.synth_matrix(12, seed=1500, rows=128, cols=1024)
+    W = hip_ctx.upload_quant_weight_private(w, 12)
+    assert hip_ctx.current_allocated_bytes() == base + w.size
+    assert hip_ctx.peak_active_weight_bytes() >= w.size
+    M = hip_ctx.bind_quant_weight_mapped(w, 12)
+    assert M.is_mapped() and not W.is_mapped()
+    assert W.byte_len() == w.size and W.ggml_type() == 12
+    W.free()
+    M.free()
+    assert hip_ctx.current_allocated_bytes() == base
+
+
+def test_retained_errors_with_context(hip_ctx):
+    w = si_hip.synth_matrix(12, seed=1600, rows=8, cols=512)
+    W = hip_ctx.upload_quant_weight_private(w, 12)
+    x = np.zeros(512, np.float32)
+    with pytest.raises(si_hip.HipError) as e:
+        hip_ctx.gguf_quant_matvec_weight(W, 9, 512, x)
+    assert e.value.message == "Q4_K retained matvec byte length is invalid"
+    with pytest.raises(si_hip.HipError) as e:
+        hip_ctx.q4_k_fused_gate_up_weights(W, W, 8, 512, x[:256])
+    assert e.value.message == "retained Q4_K fused gate/up dimensions are invalid"
+    D = hip_ctx.upload_quant_weight_private(si_hip.synth_matrix(13, seed=1, rows=4, cols=256), 13)
+    with pytest.raises(si_hip.HipError) as e:
+        hip_ctx.gguf_quant_fused_mlp_weights(W, D, D, 8, 512, 4, x)
+    assert e.value.message == "fused quantized MLP dimensions are invalid"
