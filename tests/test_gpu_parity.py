@@ -430,3 +430,24 @@ def test_retained_errors_with_context(hip_ctx):
     with pytest.raises(si_hip.HipError) as e:
         hip_ctx.gguf_quant_fused_mlp_weights(W, D, D, 8, 512, 4, x)
     assert e.value.message == "fused quantized MLP dimensions are invalid"
+
+
+# ---- kernel structure probes ---------------------------------------------------------
+@pytest.mark.parametrize("t", [12, 13, 14])
+def test_matvec_unit_vectors_pick_each_column(hip_ctx, t):
+    """x = e_k makes y[r] the dequantised weight w[r, k]: every column of every
+    row must be read from the right place by the tuned kernels."""
+    rows, cols = 67, 512
+    w = si_hip.synth_matrix(t, seed=1700 + t, rows=rows, cols=cols)
+    dq = O.dequantize(t, w, rows * cols).reshape(rows, cols)
+    W = hip_ctx.upload_quant_weight_private(w, t)
+    X = np.eye(cols, dtype=np.float32)
+    bad = []
+    for k in range(cols):
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, X[k])
+        err = np.abs(y - dq[:, k])
+        tol = 2e-5 * np.abs(dq[:, k]) + 1e-6
+        if np.any(err > tol):
+            bad.append((k, int(np.argmax(err - tol)), float(y[np.argmax(err - tol)]),
+                        float(dq[np.argmax(err - tol), k])))
+    assert bad == [], f"{len(bad)} columns wrong, first: {bad[:8]}"
