@@ -1,0 +1,572 @@
+// Q4_K matvec on the gfx950 matrix cores (replaces si_q4_k_matvec* for one
+// input vector, src/metal.rs:310-494).
+//
+// The dot of a 32-weight unit, sum_i q_i * x_i with q_i in 0..15, is done as
+// an exact integer product on v_mfma_i32_16x16x64_i8:
+//
+//  * Activations.  Each 256-element block b of x is written in fixed point,
+//    x_i = X_i * 2^(e_b - 30) with |X_i| <= 2^30 (e_b from the block's largest
+//    |x|), and X_i = sum_d D_d * 256^d in four signed byte digits (|D| <= 128,
+//    the top one <= 64).  Rounding x to X costs at most 2^-31 of the block's
+//    largest activation.
+//  * Weights.  A 16-byte piece of qs masked with 0x0f (or shifted by 4 first)
+//    is 16 int8 weights.
+//  * Units stay apart.  Lane l of the B operand is row l % 16 of a 16-row
+//    tile; lane group g = l / 16 supplies the qs bytes [32g, 32g + 32) of the
+//    block, i.e. units 2g (low nibbles) and 2g + 1 (high nibbles).  Rows
+//    4g..4g+3 of the A operand hold the four digits of the activations that
+//    meet group g's weights and are zero elsewhere, so output rows 4g + d are
+//    digit d of group g's unit sums, and they land in lane group g -- the
+//    lanes that hold that unit's scale and min.
+//
+// Per block and lane: C_e, C_o (4 digits each) from four MFMAs; T_d = sc_e *
+// C_e[d] + sc_o * C_o[d] in integers (|T_d| < 2^23, exact in f32); y += d *
+// (sum_d T_d * 256^d) * 2^(e_b-30) - dmin * (m_e * X_e + m_o * X_o), X_u the
+// f32 sum of unit u's activations.  The factored form rounds differently
+// from the per-weight w * x of quant.rs; the result stays within the 2e-5 *
+// sum|w*x| bar.  Blocks whose activations are not finite or reach 2^100 take
+// an exact per-weight f32 path instead, so NaN/Inf propagate as in the
+// reference.
+//
+// Data path.  One persistent workgroup of WAVES waves per CU.  At start it
+// turns all of x into digit images in LDS (1 KB per block, plus unit sums and
+// exponents) while each wave's first stage of weights is already in flight.
+// The workgroup owns the 16-row tiles G, G + gridDim.x, ...; their (tile,
+// stage) pairs, a stage being four blocks (16 rows x 576 bytes), go to the
+// waves round-robin, so every wave streams its own sequence of stages.
+// Weights arrive by 16-byte buffer->LDS copies in piece-major order (LDS
+// byte 16 (16 q + r) is piece q of row r), so every read is a conflict-free
+// 16-lane sweep; a wave's next stage is in flight while it computes.  Only
+// the 16 lanes whose A rows carry digits read images (exec-masked; the other
+// lanes hold zeros for the whole kernel).  A wave leaves its stage's 16 row
+// partials in an LDS slot of the tile and counts them with an LDS atomic; the
+// wave that completes the tile sums the partials in stage order and stores
+// the rows, so results do not depend on timing.  LDS is only touched through
+// inline asm and the one barrier is a bare s_barrier: the compiler neither
+// counts nor orders buffer->LDS copies, and a fence would drain them.
+#include "kquant_device.h"
+#include "si_hip_tuned.h"
+
+#include <cstdlib>
+
+namespace sihip {
+namespace {
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kBufferWord3 = 0x00020000;  // raw dword access (CDNA buffer descriptor)
+constexpr int kFixBits = 30;
+constexpr uint32_t kStageBytes = 16u * 4u * kQ4Bytes;  // 9216
+constexpr uint32_t kLdsBytes = 163840u;
+constexpr int kBadBlock = 0x40000000;  // exponent slot of a block taking the exact path
+
+constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+
+// LDS map of one workgroup (byte offsets): per-wave stage buffers, digit
+// images of all blocks (plus 4 KB that dead blocks of a short last stage
+// may read), unit sums [block][unit], exponents [block], then a ring of
+// `slots` tile slots: [slot][stage][16 rows] f32 partials, and per slot a
+// completion count and the tile index it currently belongs to.
+struct Layout {
+  uint32_t img, xsum, expo, part, cnt, owner, total;
+};
+__host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
+                                            uint32_t slots) {
+  Layout l{};
+  const uint32_t nstages = (nb + 3u) / 4u;
+  l.img = waves * depth * kStageBytes;
+  l.xsum = l.img + nb * 1024u + 4096u;
+  l.expo = l.xsum + nb * 32u + 128u;
+  l.part = l.expo + ((nb * 4u + 15u) & ~15u) + 16u;
+  l.cnt = l.part + slots * nstages * 64u;
+  l.owner = l.cnt + slots * 4u;
+  l.total = l.owner + slots * 4u;
+  return l;
+}
+
+// Lanes whose A rows carry digits: lane 16 g + n with n / 4 == g.
+constexpr uint64_t kActiveLanes = 0xF0000F0000F0000Full;
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x15f;
+
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ void lds_write_b128(uint32_t addr, u32x4 v) {
+  asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_write_b32(uint32_t addr, uint32_t v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+// LDS atomic add; returns the previous value.
+__device__ __forceinline__ uint32_t lds_add_rtn(uint32_t addr, uint32_t v) {
+  uint32_t old;
+  asm volatile("ds_add_rtn_u32 %0, %1, %2\ns_waitcnt lgkmcnt(0)" : "=&v"(old) : "v"(addr), "v"(v) : "memory");
+  return old;
+}
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// The caller waits (lgkmcnt) in an asm that takes the value as an operand.
+__device__ __forceinline__ uint32_t lds_read_b32_nowait(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1" : "=&v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// Four 16-byte reads at addr + STRIDE * t, t = 0..3.
+template <int STRIDE, typename V>
+__device__ __forceinline__ void lds_read4(uint32_t addr, V (&a)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n"
+      "ds_read_b128 %1, %4 offset:%5\n"
+      "ds_read_b128 %2, %4 offset:%6\n"
+      "ds_read_b128 %3, %4 offset:%7\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3])
+      : "v"(addr), "i"(STRIDE), "i"(2 * STRIDE), "i"(3 * STRIDE)
+      : "memory");
+}
+
+// The lane's header and two qs pieces of the four blocks of a stage buffer:
+// header of block b at hb + 2304 b, qs pieces at qb + 2304 b (+256).
+__device__ __forceinline__ void lds_read_weights(uint32_t hb, uint32_t qb, u32x4 (&v)[12]) {
+  asm volatile(
+      "ds_read_b128 %0, %12\n"
+      "ds_read_b128 %1, %13\n"
+      "ds_read_b128 %2, %13 offset:256\n"
+      "ds_read_b128 %3, %12 offset:2304\n"
+      "ds_read_b128 %4, %13 offset:2304\n"
+      "ds_read_b128 %5, %13 offset:2560\n"
+      "ds_read_b128 %6, %12 offset:4608\n"
+      "ds_read_b128 %7, %13 offset:4608\n"
+      "ds_read_b128 %8, %13 offset:4864\n"
+      "ds_read_b128 %9, %12 offset:6912\n"
+      "ds_read_b128 %10, %13 offset:6912\n"
+      "ds_read_b128 %11, %13 offset:7168\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+        "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11])
+      : "v"(hb), "v"(qb)
+      : "memory");
+}
+
+// Unit sums of the lane's two units in the four blocks (xb + 32 b) and the
+// four block exponents (eb).
+__device__ __forceinline__ void lds_read_sums(uint32_t xb, uint32_t eb, u32x2 (&xs)[4], i32x4& ex) {
+  asm volatile(
+      "ds_read_b64 %0, %5\n"
+      "ds_read_b64 %1, %5 offset:32\n"
+      "ds_read_b64 %2, %5 offset:64\n"
+      "ds_read_b64 %3, %5 offset:96\n"
+      "ds_read_b128 %4, %6\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(xs[0]), "=&v"(xs[1]), "=&v"(xs[2]), "=&v"(xs[3]), "=&v"(ex)
+      : "v"(xb), "v"(eb)
+      : "memory");
+}
+
+// The 16 A images of a stage (block b, MFMA t at addr + 1024 b + 256 t),
+// read only by the lanes in `mask`; the other lanes keep their registers.
+__device__ __forceinline__ void lds_read_images(uint32_t addr, uint64_t mask, i32x4 (&a)[16]) {
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %[sv], exec\n"
+      "s_mov_b64 exec, %[m]\n"
+      "ds_read_b128 %0, %[ad]\n"
+      "ds_read_b128 %1, %[ad] offset:256\n"
+      "ds_read_b128 %2, %[ad] offset:512\n"
+      "ds_read_b128 %3, %[ad] offset:768\n"
+      "ds_read_b128 %4, %[ad] offset:1024\n"
+      "ds_read_b128 %5, %[ad] offset:1280\n"
+      "ds_read_b128 %6, %[ad] offset:1536\n"
+      "ds_read_b128 %7, %[ad] offset:1792\n"
+      "ds_read_b128 %8, %[ad] offset:2048\n"
+      "ds_read_b128 %9, %[ad] offset:2304\n"
+      "ds_read_b128 %10, %[ad] offset:2560\n"
+      "ds_read_b128 %11, %[ad] offset:2816\n"
+      "ds_read_b128 %12, %[ad] offset:3072\n"
+      "ds_read_b128 %13, %[ad] offset:3328\n"
+      "ds_read_b128 %14, %[ad] offset:3584\n"
+      "ds_read_b128 %15, %[ad] offset:3840\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      "s_mov_b64 exec, %[sv]"
+      : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]),
+        "+v"(a[7]), "+v"(a[8]), "+v"(a[9]), "+v"(a[10]), "+v"(a[11]), "+v"(a[12]), "+v"(a[13]),
+        "+v"(a[14]), "+v"(a[15]), [sv] "=&s"(saved)
+      : [ad] "v"(addr), [m] "s"(mask)
+      : "memory");
+}
+
+// Byte digits of four elements' biased values (X + 0x80808080): byte d of
+// each element gathered into one word, then flipped to signed (b - 128).
+__device__ __forceinline__ void transpose_digits(uint32_t u0, uint32_t u1, uint32_t u2,
+                                                 uint32_t u3, uint32_t (&out)[4]) {
+  // v_perm_b32 selector bytes 0..3 pick from the second source, 4..7 the first
+  const uint32_t lo01 = __builtin_amdgcn_perm(u1, u0, 0x05010400u);  // u0.b0 u1.b0 u0.b1 u1.b1
+  const uint32_t hi01 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);  // u0.b2 u1.b2 u0.b3 u1.b3
+  const uint32_t lo23 = __builtin_amdgcn_perm(u3, u2, 0x05010400u);
+  const uint32_t hi23 = __builtin_amdgcn_perm(u3, u2, 0x07030602u);
+  out[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+  out[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+  out[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
+  out[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u) ^ 0x80808080u;
+}
+
+__device__ __forceinline__ i32x4 low_nibbles(const u32x4& q) {
+  return i32x4{(int)(q[0] & 0x0f0f0f0fu), (int)(q[1] & 0x0f0f0f0fu), (int)(q[2] & 0x0f0f0f0fu),
+               (int)(q[3] & 0x0f0f0f0fu)};
+}
+__device__ __forceinline__ i32x4 high_nibbles(const u32x4& q) {
+  return i32x4{(int)((q[0] >> 4) & 0x0f0f0f0fu), (int)((q[1] >> 4) & 0x0f0f0f0fu),
+               (int)((q[2] >> 4) & 0x0f0f0f0fu), (int)((q[3] >> 4) & 0x0f0f0f0fu)};
+}
+
+// Exact per-weight f32 dot of 16 nibbles (low or high half of each byte of q)
+// with 16 activations.
+__device__ __forceinline__ float exact_dot16(const u32x4& q, int shift, float d1, float m1,
+                                             const float* __restrict__ xs, float acc) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t nib = (q[j >> 2] >> (8 * (j & 3) + shift)) & 0x0fu;
+    acc = fmaf(k4_value_exact(d1, m1, nib), xs[j], acc);
+  }
+  return acc;
+}
+
+// Sum over the four 16-lane groups, ((g0 + g1) + (g2 + g3)), in every lane.
+__device__ __forceinline__ float sum_lane_groups(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+
+// Fast-path dot of one block for one lane: row n's units 2 grp, 2 grp + 1.
+__device__ __forceinline__ float block_terms(const u32x4& h, const u32x4& qa, const u32x4& qb,
+                                             const i32x4& a0, const i32x4& a1, const i32x4& a2,
+                                             const i32x4& a3, u32x2 xs, int eb, bool hi_units,
+                                             int bsh) {
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  const uint32_t scw = hi_units ? sc47 : sc03;
+  const uint32_t mnw = hi_units ? mn47 : mn03;
+  const int sce = (int)((scw >> bsh) & 0xffu), sco = (int)((scw >> (bsh + 8)) & 0xffu);
+  const uint32_t mne = (mnw >> bsh) & 0xffu, mno = (mnw >> (bsh + 8)) & 0xffu;
+  const i32x4 zero = {0, 0, 0, 0};
+  i32x4 ce = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, low_nibbles(qa), zero, 0, 0, 0);
+  i32x4 co = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, high_nibbles(qa), zero, 0, 0, 0);
+  ce = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, low_nibbles(qb), ce, 0, 0, 0);
+  co = __builtin_amdgcn_mfma_i32_16x16x64_i8(a3, high_nibbles(qb), co, 0, 0, 0);
+  const int t0 = __mul24(sce, ce[0]) + __mul24(sco, co[0]);
+  const int t1 = __mul24(sce, ce[1]) + __mul24(sco, co[1]);
+  const int t2 = __mul24(sce, ce[2]) + __mul24(sco, co[2]);
+  const int t3 = __mul24(sce, ce[3]) + __mul24(sco, co[3]);
+  const float tc =
+      fmaf(fmaf(fmaf((float)t3, 256.0f, (float)t2), 256.0f, (float)t1), 256.0f, (float)t0);
+  const float d = half_bits_to_float(h[0] & 0xffffu);
+  const float dmin = half_bits_to_float(h[0] >> 16);
+  const float um = fmaf((float)mne, __uint_as_float(xs[0]), (float)mno * __uint_as_float(xs[1]));
+  return __builtin_amdgcn_ldexpf(d * tc, eb) - dmin * um;
+}
+
+// Exact per-weight path of one block (activations not finite or >= 2^100).
+__device__ __forceinline__ float block_exact(const u32x4& h, const u32x4& qa, const u32x4& qb,
+                                             bool hi_units, int bsh, const float* __restrict__ xs) {
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  const uint32_t scw = hi_units ? sc47 : sc03;
+  const uint32_t mnw = hi_units ? mn47 : mn03;
+  const uint32_t sce = (scw >> bsh) & 0xffu, sco = (scw >> (bsh + 8)) & 0xffu;
+  const uint32_t mne = (mnw >> bsh) & 0xffu, mno = (mnw >> (bsh + 8)) & 0xffu;
+  const float d = half_bits_to_float(h[0] & 0xffffu);
+  const float dmin = half_bits_to_float(h[0] >> 16);
+  const float d1e = __fmul_rn(d, (float)sce), m1e = __fmul_rn(dmin, (float)mne);
+  const float d1o = __fmul_rn(d, (float)sco), m1o = __fmul_rn(dmin, (float)mno);
+  float acc = exact_dot16(qa, 0, d1e, m1e, xs, 0.0f);
+  acc = exact_dot16(qb, 0, d1e, m1e, xs + 16, acc);
+  acc = exact_dot16(qa, 4, d1o, m1o, xs + 32, acc);
+  return exact_dot16(qb, 4, d1o, m1o, xs + 48, acc);
+}
+
+template <int WAVES, int DEPTH>
+__global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y, uint32_t rows,
+                                                              uint32_t nb, uint32_t slots) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const Layout L = layout(WAVES, DEPTH, nb, slots);
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t grp = lane >> 4, n = lane & 15u;
+  const uint32_t row_bytes = nb * kQ4Bytes;
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t nstages = (nb + 3u) / 4u;
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
+
+  // 1. x into the image area, natural order (block b at img + 1024 b): pass
+  //    j of wave v copies blocks 4 (v + WAVES j) .. +3, one per instruction.
+  const uint32_t npass = (nb + 4u * WAVES - 1u) / (4u * WAVES);
+  {
+    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<float*>(x), 0, (int)(nb * 1024u), kBufferWord3);
+    for (uint32_t j = 0; j < npass; ++j) {
+      const uint32_t b0 = 4u * (wave + WAVES * j);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint32_t b = b0 + i;
+        if (b < nb)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(smem + L.img + 1024u * b), 16,
+                                                    1024u * b + 16u * lane, 0, 0, 0);
+      }
+    }
+  }
+
+  // 2. this wave's pairs p = wave, wave + WAVES, ... of the workgroup's tiles
+  //    (pair p = stage p % nstages of local tile p / nstages), and the copies
+  //    of its first DEPTH, pair j of the wave into buffer j % DEPTH.  Piece
+  //    c = 64 i + lane of a stage is piece c / 16 of row c % 16's 576 bytes.
+  const uint32_t my_tiles =
+      blockIdx.x < ntiles ? (ntiles - 1u - blockIdx.x) / gridDim.x + 1u : 0u;
+  const uint32_t npairs = my_tiles * nstages;
+  const uint32_t voff = n * row_bytes + 16u * grp;
+  const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
+  auto issue = [&](uint32_t j) {
+    const uint32_t p = wave + j * WAVES;
+    const uint32_t lt = p / nstages, st = p - lt * nstages;
+    const uint32_t row0 = (blockIdx.x + lt * gridDim.x) * 16u;
+    const uint32_t nrows = min(16u, rows - row0);
+    const uint8_t* sb = w + (size_t)row0 * row_bytes + 576u * st;
+    // the descriptor ends at the tile's last row: pieces past it read zero
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - 576u * st), kBufferWord3);
+    uint8_t* dst = wstage + (j % DEPTH) * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < 9; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * i), 16,
+                                                voff + 64u * i, 0, 0, 0);
+  };
+#pragma unroll
+  for (int j = 0; j < DEPTH; ++j)
+    if ((uint32_t)j < my_pairs) issue(j);
+
+  // 3. ring slots, then (once the x copies have landed) digit images, unit
+  //    sums and exponents
+  for (uint32_t k = threadIdx.x; k < slots; k += WAVES * 64u) {
+    lds_write_b32(sbase + L.cnt + 4u * k, 0u);
+    lds_write_b32(sbase + L.owner + 4u * k, k);
+  }
+  // the stage copies were issued after x's and complete in order
+  const uint32_t early = min((uint32_t)DEPTH, my_pairs);
+  if (early >= 3u)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(27));
+  else if (early == 2u)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(18));
+  else if (early == 1u)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(9));
+  else
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  for (uint32_t j = 0; j < npass; ++j) {
+    if (4u * (wave + WAVES * j) >= nb) break;
+    // lane (grp, n): elements 16n..16n+15 of block pb
+    const uint32_t pb = 4u * (wave + WAVES * j) + grp;
+    const uint32_t pbc = pb < nb ? pb : nb - 1u;  // lanes past K redo the last block, unstored
+    u32x4 xq[4];
+    lds_read4<16>(sbase + L.img + 1024u * pbc + 64u * n, xq);
+    float xv[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xv[4 * k + c] = __uint_as_float(xq[k][c]);
+    float amax = 0.0f, xsum = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float av = fabsf(xv[k]);
+      amax = fmaxf(amax, av);
+      bad |= !(av < 0x1p100f);
+      xsum += xv[k];
+    }
+    amax = fmaxf(amax, dpp<kRowShr1>(amax));
+    amax = fmaxf(amax, dpp<kRowShr2>(amax));
+    amax = fmaxf(amax, dpp<kRowShr4>(amax));
+    amax = fmaxf(amax, dpp<kRowShr8>(amax));
+    amax = dpp<kRowBcast15>(amax);
+    const int e = __builtin_amdgcn_frexp_expf(amax);  // amax < 2^e; 0 for amax == 0
+    uint32_t u[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      u[k] = (uint32_t)__float2int_rn(__builtin_amdgcn_ldexpf(xv[k], kFixBits - e)) + 0x80808080u;
+    uint32_t dg[4][4];  // [element quad][digit]
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      transpose_digits(u[4 * k], u[4 * k + 1], u[4 * k + 2], u[4 * k + 3], dg[k]);
+    // image of (block, t, A row m = 4p + d) at 1024 block + 256 t + 16 m; this
+    // lane's elements are those of t = n % 4, p = n / 4 (all lanes have read)
+    const uint32_t ib = sbase + L.img + 1024u * pbc + 256u * (n & 3u) + 64u * (n >> 2);
+    const bool store = pb < nb;
+    if (store) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        lds_write_b128(ib + 16u * d, u32x4{dg[0][d], dg[1][d], dg[2][d], dg[3][d]});
+    }
+    xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit n / 2
+    if (store && (n & 1u))
+      lds_write_b32(sbase + L.xsum + 32u * pb + 4u * (n >> 1), __float_as_uint(xsum));
+    const bool bad_blk = (__builtin_amdgcn_ballot_w64(bad) >> (16u * grp)) & 0xffffull;
+    if (store && n == 0u)
+      lds_write_b32(sbase + L.expo + 4u * pb, (uint32_t)(bad_blk ? kBadBlock : e - kFixBits));
+  }
+  lds_wait();
+  __builtin_amdgcn_s_barrier();
+
+  // 4. the wave's pairs
+  const bool hi_units = grp >= 2u;       // units 4..7 use the packed upper scales
+  const int bsh = 16 * (int)(grp & 1u);  // byte of unit 2 grp within its scale word
+  const uint32_t hb0 = sbase + wave * DEPTH * kStageBytes + 16u * n;
+  const uint32_t qb0 = hb0 + 256u + 512u * grp;
+  i32x4 A[16];
+#pragma unroll
+  for (int t = 0; t < 16; ++t) A[t] = i32x4{0, 0, 0, 0};
+  for (uint32_t j = 0; j < my_pairs; ++j) {
+    const uint32_t p = wave + j * WAVES;
+    const uint32_t lt = p / nstages, s = p - lt * nstages;
+    const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
+    if (DEPTH >= 3 && later >= 2u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(18));
+    else if (DEPTH >= 2 && later >= 1u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(9));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    const uint32_t buf = (j % DEPTH) * kStageBytes;
+    u32x4 v[12];
+    lds_read_weights(hb0 + buf, qb0 + buf, v);
+    if (j + DEPTH < my_pairs) issue(j + DEPTH);  // the buffer just read is free again
+    lds_read_images(sbase + L.img + 4096u * s + 16u * n, kActiveLanes, A);
+    u32x2 xs[4];
+    i32x4 ex;
+    lds_read_sums(sbase + L.xsum + 128u * s + 8u * grp, sbase + L.expo + 16u * s, xs, ex);
+    const uint32_t nlive = min(4u, nb - 4u * s);
+    float part[4];
+    bool bad_any = false;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
+      const bool use = (uint32_t)b < nlive;
+      bad_any |= use && eb == kBadBlock;
+      const float c = block_terms(v[3 * b], v[3 * b + 1], v[3 * b + 2], A[4 * b], A[4 * b + 1],
+                                  A[4 * b + 2], A[4 * b + 3], xs[b], eb, hi_units, bsh);
+      part[b] = (use && eb != kBadBlock) ? c : 0.0f;
+    }
+    if (bad_any) {
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        if ((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock)
+          part[b] = block_exact(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh,
+                                x + 256u * (4u * s + b) + 64u * grp);
+    }
+    const float rowsum = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
+
+    // hand the 16 row partials to the tile's slot (waiting while an earlier
+    // tile still holds it), count them, and let the last stage finish the tile
+    const uint32_t slot = lt % slots;
+    for (uint32_t spin = 0; lds_read_b32(sbase + L.owner + 4u * slot) != lt && spin < (1u << 24);
+         ++spin)
+      __builtin_amdgcn_s_sleep(1);
+    if (grp == 0u)
+      lds_write_b32(sbase + L.part + 64u * (slot * nstages + s) + 4u * n, __float_as_uint(rowsum));
+    const uint32_t done = uniform(lds_add_rtn(sbase + L.cnt + 4u * slot, lane == 0u ? 1u : 0u));
+    if (done == nstages - 1u) {
+      float sum = 0.0f;
+      for (uint32_t st = 0; st < nstages; ++st)
+        sum += __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * nstages + st) + 4u * n));
+      const uint32_t row = (blockIdx.x + lt * gridDim.x) * 16u + n;
+      if (grp == 0u && row < rows) y[row] = sum;
+      if (lane == 0u) {
+        lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
+        lds_write_b32(sbase + L.owner + 4u * slot, lt + slots);
+      }
+    }
+  }
+}
+
+int env_int(const char* name, int fallback) {
+  const char* v = std::getenv(name);
+  return v ? std::atoi(v) : fallback;
+}
+
+int cu_count() {
+  static int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      n = 256;
+    return n;
+  }();
+  return cus;
+}
+
+template <int W, int D>
+bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+               hipStream_t s, hipError_t* err) {
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t grid = min(ntiles, (uint32_t)cu_count());
+  const uint32_t nstages = (nb + 3u) / 4u;
+  const uint32_t per_wg = (ntiles + grid - 1u) / grid;
+  // enough slots for every wave to be a few tiles ahead, within 8 KB
+  uint32_t slots = min(per_wg, max(4u, (2u * W * D + nstages - 1u) / nstages + 2u));
+  while (slots > 2u && slots * nstages * 64u > 8192u) --slots;
+  const uint32_t lds = layout(W, D, nb, slots).total;
+  if (lds > kLdsBytes) return false;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
+  if (attr != hipSuccess) {
+    *err = attr;
+    return true;
+  }
+  hipLaunchKernelGGL((q4k_matvec_mfma<W, D>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows, nb,
+                     slots);
+  *err = hipGetLastError();
+  return true;
+}
+
+}  // namespace
+
+bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, hipStream_t s, hipError_t* err) {
+  const uint32_t nb = cols / kBlockElems;
+  if (nb == 0 || (uint64_t)nb * kQ4Bytes * 16u > 0x7fffffffu || nb * 1024u > 0x7fffffffu)
+    return false;
+  static const int cfg = env_int("SI_HIP_Q4K_MFMA_CFG", 0);
+  switch (cfg) {
+    case 1: return launch_wd<12, 1>(w, x, y, rows, nb, s, err);
+    case 2: return launch_wd<8, 1>(w, x, y, rows, nb, s, err);
+    case 3: return launch_wd<4, 3>(w, x, y, rows, nb, s, err);
+    case 4: return launch_wd<4, 2>(w, x, y, rows, nb, s, err);
+    case 5: return launch_wd<8, 2>(w, x, y, rows, nb, s, err);
+    default: break;
+  }
+  return launch_wd<12, 1>(w, x, y, rows, nb, s, err) || launch_wd<8, 1>(w, x, y, rows, nb, s, err) ||
+         launch_wd<4, 1>(w, x, y, rows, nb, s, err);
+}
+
+}  // namespace sihip

@@ -299,6 +299,8 @@ int device_cu_count() {
 bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float* y, uint32_t rows,
                          uint32_t cols, uint32_t batch, hipStream_t s, hipError_t* err) {
   if (type != kTypeQ4K || batch != 1) return false;
+  static const int mode = env_int("SI_HIP_Q4K_MODE", 0);
+  if (mode == 0 && launch_q4k_matvec_mfma(w, x, y, rows, cols, s, err)) return true;
   const uint32_t nb = cols / kBlockElems;
   const uint32_t nstages = (nb + 3) / 4;
   // offsets inside one 16-row tile are 32-bit

@@ -1,4 +1,4 @@
-// Tuned gfx950 kernels (kernels_tuned.hip).  Each launcher returns false when
+// Tuned gfx950 kernels (kernels_tuned.hip, kernels_q4k_mfma.hip).  Each launcher returns false when
 // the shape is outside what the tuned kernel handles; the caller then uses
 // the generic kernels.  When it returns true, *err holds the launch status.
 #pragma once
@@ -10,6 +10,9 @@ namespace sihip {
 
 bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float* y, uint32_t rows,
                          uint32_t cols, uint32_t batch, hipStream_t s, hipError_t* err);
+// Q4_K, one vector, K <= 8192, on the matrix cores.
+bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, hipStream_t s, hipError_t* err);
 bool launch_fused_gate_up_tuned(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
                                 uint32_t rows, uint32_t cols, hipStream_t s, hipError_t* err);
 
