@@ -30,6 +30,9 @@ sys.path.insert(0, str(REPO / "memory-aware-inference_amd"))
 import si_hip  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+# HBM bytes per launch of the headline kernel from the two rocprofv3 --pmc
+# passes (FETCH_SIZE, WRITE_SIZE) scaled by a copy of known size
+TRAFFIC_PROFILE = REPO / "profiles" / "q4k_matvec_mfma_17408x5120_traffic.md"
 METRIC = "Q4_K matvec achieved HBM GB/s (% of peak) + µs/call at 17408×5120, batch 1"
 NCOPIES = 8
 
@@ -77,6 +80,16 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
             "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def profiled_traffic() -> int | None:
+    try:
+        for line in TRAFFIC_PROFILE.read_text().splitlines():
+            if line.startswith("traffic_bytes_per_launch:"):
+                return int(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(rows: int, cols: int, budget_s: float = 10.0) -> dict:
     """Reference CPU path (oracle restatement of quant.rs + host dot), 1 thread."""
     sys.path.insert(0, str(REPO / "tests"))
@@ -120,6 +133,9 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time the batch-1 shape sweep")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also time device-to-device copies of the matrix size (the yardstick "
+                         "that scales HBM traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
@@ -149,8 +165,27 @@ def main() -> int:
                    "cols": cols, "batch": 1, "weight_copies": NCOPIES,
                    "bytes_per_call": head["bytes_per_call"]},
         "roofline": {"bound": "hbm", "achieved": head["gb_per_s"], "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": head["frac_of_peak"], "traffic": None},
+                     "unit": "GB/s", "frac": head["frac_of_peak"],
+                     "traffic": profiled_traffic()},
     }
+    if args.copy_probe:
+        nbytes = head["bytes_per_call"]
+        src, dst = ctx.device_alloc(nbytes), ctx.device_alloc(nbytes)
+        for _ in range(args.warmup):
+            ctx.device_copy(dst, src, nbytes)
+        ctx.synchronize()
+        ctx.event_record(0)
+        for _ in range(args.steps):
+            ctx.device_copy(dst, src, nbytes)
+        ctx.event_record(1)
+        ms = ctx.event_elapsed_ms(0, 1)
+        ctx.synchronize()
+        ctx.device_free(src)
+        ctx.device_free(dst)
+        us = ms * 1000.0 / args.steps
+        out["copy_probe"] = {"bytes_read_per_copy": nbytes, "us_per_copy": round(us, 3),
+                             "gb_per_s_read": round(nbytes / (us * 1e-6) / 1e9, 1)}
+        log(f"  copy probe {nbytes} B: {us:.3f} us")
     if args.sweep:
         sweep = []
         for r, c in ((5120, 5120), (17408, 5120), (5120, 17408), (1024, 5120)):

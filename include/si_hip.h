@@ -211,6 +211,11 @@ int si_hip_copy_to_device(si_hip_context *ctx, void *device_dst, const void *hos
                           size_t bytes);
 int si_hip_copy_from_device(si_hip_context *ctx, void *host_dst, const void *device_src,
                             size_t bytes);
+/* Device-to-device copy on the compute stream (asynchronous).  Plumbing with
+ * no counterpart in metal.rs; the benchmark uses it as the plain-copy yardstick
+ * for HBM traffic counters. */
+int si_hip_copy_device(si_hip_context *ctx, void *device_dst, const void *device_src,
+                       size_t bytes);
 int si_hip_synchronize(si_hip_context *ctx);
 int si_hip_quant_matvec_device(si_hip_context *ctx, const si_hip_quant_weight *weight,
                                size_t rows, size_t columns, const float *d_input,

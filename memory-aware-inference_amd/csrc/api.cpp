@@ -974,6 +974,12 @@ int si_hip_copy_from_device(si_hip_context *ctx, void *dst, const void *src, siz
   return ok();
 }
 
+int si_hip_copy_device(si_hip_context *ctx, void *dst, const void *src, size_t bytes) {
+  if (!ctx || !dst || !src) return fail(SI_HIP_ERR_NULL, "copy argument is null");
+  SIHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream), "device copy");
+  return ok();
+}
+
 int si_hip_synchronize(si_hip_context *ctx) {
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   int rc = wait_stream(ctx, "synchronize");

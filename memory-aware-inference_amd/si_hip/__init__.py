@@ -99,6 +99,7 @@ _SIGS = {
     "si_hip_device_free": (_I, [_P, _P]),
     "si_hip_copy_to_device": (_I, [_P, _P, _P, _SZ]),
     "si_hip_copy_from_device": (_I, [_P, _P, _P, _SZ]),
+    "si_hip_copy_device": (_I, [_P, _P, _P, _SZ]),
     "si_hip_synchronize": (_I, [_P]),
     "si_hip_quant_matvec_device": (_I, [_P, _P, _SZ, _SZ, _P, _P]),
     "si_hip_q4_k_fused_gate_up_device": (_I, [_P, _P, _P, _SZ, _SZ, _P, _P]),
@@ -436,6 +437,9 @@ class HipContext:
         p = C.c_void_p()
         _check(lib().si_hip_device_alloc(self._h, nbytes, C.byref(p)))
         return p.value
+
+    def device_copy(self, dst: int, src: int, nbytes: int) -> None:
+        _check(lib().si_hip_copy_device(self._h, C.c_void_p(dst), C.c_void_p(src), nbytes))
 
     def device_free(self, ptr: int) -> None:
         _check(lib().si_hip_device_free(self._h, C.c_void_p(ptr)))

@@ -19,7 +19,9 @@
  *
  * Pinning (how each function is checked, see tests/test_oracle.py):
  *   kq_f16_to_f32        exhaustive 65,536 patterns vs numpy float16->float32
- *   kq_get_scale_min     exhaustive over every byte value it reads
+ *   kq_get_scale_min     round trip through an independent 6-bit packer
+ *                        (random scale/min sets), hand-worked byte values
+ *                        for j >= 4, exhaustive over the two bytes j < 4 reads
  *   kq_dequantize_q*_k   the four quant.rs known-answer tests (committed
  *                        fixtures) + an independent numpy restatement,
  *                        bit-for-bit on random blocks + committed random
