@@ -80,6 +80,155 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
             "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
+def _timed(ctx, fn, steps: int, warmup: int) -> float:
+    """Average ms per call of fn(i) enqueued back to back on the compute stream."""
+    for i in range(warmup):
+        fn(i)
+    ctx.synchronize()
+    ctx.event_record(0)
+    for i in range(steps):
+        fn(i)
+    ctx.event_record(1)
+    ms = ctx.event_elapsed_ms(0, 1)
+    ctx.synchronize()
+    return ms / steps
+
+
+def _rate(nbytes: int, ms: float) -> dict:
+    us = ms * 1000.0
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"bytes_per_call": nbytes, "us_per_call": round(us, 3), "gb_per_s": round(gbs, 1),
+            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def run_configs(ctx, steps: int, warmup: int) -> dict:
+    """BASELINE configs 2-5 on the HBM-resident device path (synthetic data)."""
+    import ctypes as C
+    lib = si_hip.lib()
+    Q4, Q5, Q6 = si_hip.GGML_TYPE_Q4_K, si_hip.GGML_TYPE_Q5_K, si_hip.GGML_TYPE_Q6_K
+    res: dict = {}
+
+    def upload(t, seed, rows, cols):
+        w = si_hip.synth_matrix(t, seed=seed, rows=rows, cols=cols, threads=16)
+        h = ctx.upload_quant_weight_private(w, t)
+        del w
+        return h
+
+    def dev_f32(values):
+        a = np.ascontiguousarray(values, dtype=np.float32)
+        p = ctx.device_alloc(a.nbytes)
+        ctx.to_device(p, a)
+        return p
+
+    def bpc(t, rows, cols):
+        return rows * (cols // 256) * si_hip.BLOCK_BYTES[t]
+
+    # config 3: fused SwiGLU (gate/up Q4_K 17408x5120, down Q6_K 5120x17408), 3 copies
+    log("configs: fused SwiGLU MLP")
+    N, K = 17408, 5120
+    mlp = [(upload(Q4, 300 + c, N, K), upload(Q4, 310 + c, N, K), upload(Q6, 320 + c, K, N))
+           for c in range(3)]
+    x = dev_f32(si_hip.synth_normal(301, K) * np.float32(0.1))
+    h = ctx.device_alloc(N * 4)
+    y = ctx.device_alloc(K * 4)
+    gu_ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_q4_k_fused_gate_up_device(
+        ctx.handle, mlp[i % 3][0].handle, mlp[i % 3][1].handle, N, K, C.c_void_p(x),
+        C.c_void_p(h))), steps, warmup)
+    mlp_ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_fused_mlp_device(
+        ctx.handle, mlp[i % 3][0].handle, mlp[i % 3][1].handle, mlp[i % 3][2].handle, N, K, K,
+        C.c_void_p(x), C.c_void_p(h), C.c_void_p(y))), steps, warmup)
+    res["fused_gate_up_q4k_17408x5120"] = _rate(2 * bpc(Q4, N, K), gu_ms)
+    res["fused_mlp_q4k_gate_up_q6k_down"] = _rate(2 * bpc(Q4, N, K) + bpc(Q6, K, N), mlp_ms)
+    for g, u, d in mlp:
+        g.free(); u.free(); d.free()
+    for p in (x, h, y):
+        ctx.device_free(p)
+
+    # config 4: Q5_K 5120x5120, Q6_K head 151936x5120 + argmax, Q4_K embedding of 64 ids
+    log("configs: Q5_K matvec, Q6_K head + argmax, Q4_K embedding")
+    q5 = [upload(Q5, 400 + c, K, K) for c in range(8)]
+    x = dev_f32(si_hip.synth_normal(401, K))
+    y = ctx.device_alloc(K * 4)
+    ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_quant_matvec_device(
+        ctx.handle, q5[i % 8].handle, K, K, C.c_void_p(x), C.c_void_p(y))), steps, warmup)
+    res["q5k_matvec_5120x5120"] = _rate(bpc(Q5, K, K), ms)
+    for w in q5:
+        w.free()
+    V = 151936
+    head = upload(Q6, 410, V, K)
+    logits = ctx.device_alloc(V * 4)
+    packed = ctx.device_alloc(8)
+    ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_matvec_argmax_device(
+        ctx.handle, head.handle, V, K, C.c_void_p(x), 0, C.c_void_p(logits),
+        C.c_void_p(packed))), max(steps // 4, 10), max(warmup // 4, 2))
+    res["q6k_head_argmax_151936x5120"] = _rate(bpc(Q6, V, K), ms)
+    head.free()
+    ctx.device_free(logits); ctx.device_free(packed)
+    table = upload(Q4, 420, V, K)
+    ids = ctx.device_alloc(64 * 4)
+    ctx.to_device(ids, si_hip.synth_token_ids(421, 64, V).astype(np.uint32))
+    emb = ctx.device_alloc(64 * K * 4)
+    ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_embedding_device(
+        ctx.handle, table.handle, K, V, C.c_void_p(ids), 64, C.c_void_p(emb))), steps, warmup)
+    res["q4k_embedding_64_tokens"] = _rate(64 * bpc(Q4, 1, K), ms)
+    table.free()
+    for p in (ids, emb, x, y):
+        ctx.device_free(p)
+
+    # config 5: matmul-many M in {1,2,4,8,16} on Q4_K 17408x5120, 8 copies
+    log("configs: multi-token verify")
+    ws = [upload(Q4, 500 + c, N, K) for c in range(8)]
+    X = dev_f32(si_hip.synth_normal(501, 16 * K))
+    Y = ctx.device_alloc(16 * N * 4)
+    many = {}
+    for m in (1, 2, 4, 8, 16):
+        ms = _timed(ctx, lambda i, m=m: si_hip._check(lib.si_hip_matmul_many_device(
+            ctx.handle, ws[i % 8].handle, N, K, m, C.c_void_p(X), C.c_void_p(Y))), steps, warmup)
+        r = _rate(bpc(Q4, N, K), ms)
+        r["tflop_per_s"] = round(2.0 * m * N * K / (ms * 1e-3) / 1e12, 3)
+        many[f"M{m}"] = r
+    res["matmul_many_q4k_17408x5120"] = many
+    for w in ws:
+        w.free()
+    ctx.device_free(X); ctx.device_free(Y)
+
+    # config 5b: 64 synthetic 27B-class layers streamed once per token
+    log("configs: 64-layer aggregate")
+    layer_shapes = [(Q4, 16384, 5120), (Q4, 5120, 6144), (Q4, 17408, 5120), (Q4, 17408, 5120),
+                    (Q6, 5120, 17408)]
+    host = [si_hip.synth_matrix(t, seed=600 + i, rows=r, cols=c, threads=16)
+            for i, (t, r, c) in enumerate(layer_shapes)]
+    layers = [[ctx.upload_quant_weight_private(hb, t) for hb, (t, _, _) in zip(host, layer_shapes)]
+              for _ in range(64)]
+    del host
+    xin = dev_f32(si_hip.synth_normal(601, 17408))
+    ybuf = ctx.device_alloc(17408 * 4)
+    hbuf = ctx.device_alloc(17408 * 4)
+    layer_bytes = sum(bpc(t, r, c) for t, r, c in layer_shapes)
+
+    def token(_i):
+        for L in layers:
+            si_hip._check(lib.si_hip_quant_matvec_device(ctx.handle, L[0].handle, 16384, 5120,
+                                                         C.c_void_p(xin), C.c_void_p(ybuf)))
+            si_hip._check(lib.si_hip_quant_matvec_device(ctx.handle, L[1].handle, 5120, 6144,
+                                                         C.c_void_p(xin), C.c_void_p(ybuf)))
+            si_hip._check(lib.si_hip_fused_mlp_device(ctx.handle, L[2].handle, L[3].handle,
+                                                      L[4].handle, 17408, 5120, 5120,
+                                                      C.c_void_p(xin), C.c_void_p(hbuf),
+                                                      C.c_void_p(ybuf)))
+    ms = _timed(ctx, token, 5, 1)
+    agg = _rate(64 * layer_bytes, ms)
+    agg["layers"] = 64
+    agg["per_layer"] = "qkv Q4_K 16384x5120, o Q4_K 5120x6144, gate/up Q4_K 17408x5120 fused, down Q6_K 5120x17408"
+    res["aggregate_64_layers"] = agg
+    for L in layers:
+        for w in L:
+            w.free()
+    for p in (xin, ybuf, hbuf):
+        ctx.device_free(p)
+    return res
+
+
 def profiled_traffic() -> int | None:
     try:
         for line in TRAFFIC_PROFILE.read_text().splitlines():
@@ -133,6 +282,9 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time the batch-1 shape sweep")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--configs", action="store_true",
+                    help="also time BASELINE configs 3-5 (fused MLP, Q5_K, Q6_K head + argmax, "
+                         "embedding, matmul-many, 64-layer aggregate)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time device-to-device copies of the matrix size (the yardstick "
                          "that scales HBM traffic counters)")
@@ -193,6 +345,8 @@ def main() -> int:
             log(f"  sweep {r}x{c}: {res['us_per_call']} us, {res['gb_per_s']} GB/s")
             sweep.append(res)
         out["sweep"] = sweep
+    if args.configs:
+        out["configs"] = run_configs(ctx, args.steps, args.warmup)
     ctx.close()
     if not args.no_cpu:
         log("timing the CPU baseline")

@@ -41,10 +41,14 @@
 // lanes hold zeros for the whole kernel).  A wave leaves its stage's 16 row
 // partials in an LDS slot of the tile and counts them with an LDS atomic; the
 // wave that completes the tile sums the partials in stage order and stores
-// the rows, so results do not depend on timing.  LDS is only touched through
+// the rows, so results do not depend on timing.  With MATS = 2 (fused SwiGLU
+// gate/up, replacing si_q4_k_fused_gate_up, metal.rs:498-587) a tile's pairs
+// cover the stages of both matrices, which share the activation images, and
+// the finishing wave stores silu(gate) * up.  LDS is only touched through
 // inline asm and the one barrier is a bare s_barrier: the compiler neither
 // counts nor orders buffer->LDS copies, and a fence would drain them.
 #include "kquant_device.h"
+#include "si_hip_internal.h"
 #include "si_hip_tuned.h"
 
 #include <cstdlib>
@@ -74,9 +78,9 @@ struct Layout {
   uint32_t img, xsum, expo, part, cnt, owner, total;
 };
 __host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
-                                            uint32_t slots) {
+                                            uint32_t slots, uint32_t mats) {
   Layout l{};
-  const uint32_t nstages = (nb + 3u) / 4u;
+  const uint32_t nstages = (nb + 3u) / 4u * mats;  // partials per tile
   l.img = waves * depth * kStageBytes;
   l.xsum = l.img + nb * 1024u + 4096u;
   l.expo = l.xsum + nb * 32u + 128u;
@@ -306,19 +310,21 @@ __device__ __forceinline__ float block_exact(const u32x4& h, const u32x4& qa, co
   return exact_dot16(qb, 4, d1o, m1o, xs + 48, acc);
 }
 
-template <int WAVES, int DEPTH>
+template <int WAVES, int DEPTH, int MATS>
 __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __restrict__ w,
+                                                              const uint8_t* __restrict__ w2,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
                                                               uint32_t nb, uint32_t slots) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const Layout L = layout(WAVES, DEPTH, nb, slots);
+  const Layout L = layout(WAVES, DEPTH, nb, slots, MATS);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t grp = lane >> 4, n = lane & 15u;
   const uint32_t row_bytes = nb * kQ4Bytes;
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = (nb + 3u) / 4u;
+  const uint32_t tstages = MATS * nstages;  // pairs (and partials) per tile
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
   uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
 
@@ -341,20 +347,22 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   }
 
   // 2. this wave's pairs p = wave, wave + WAVES, ... of the workgroup's tiles
-  //    (pair p = stage p % nstages of local tile p / nstages), and the copies
+  //    (pair p = partial p % tstages of local tile p / tstages; partial r is
+  //    stage r % nstages of matrix r / nstages), and the copies
   //    of its first DEPTH, pair j of the wave into buffer j % DEPTH.  Piece
   //    c = 64 i + lane of a stage is piece c / 16 of row c % 16's 576 bytes.
   const uint32_t my_tiles =
       blockIdx.x < ntiles ? (ntiles - 1u - blockIdx.x) / gridDim.x + 1u : 0u;
-  const uint32_t npairs = my_tiles * nstages;
+  const uint32_t npairs = my_tiles * tstages;
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
   auto issue = [&](uint32_t j) {
     const uint32_t p = wave + j * WAVES;
-    const uint32_t lt = p / nstages, st = p - lt * nstages;
+    const uint32_t lt = p / tstages, r = p - lt * tstages;
+    const uint32_t mat = MATS > 1 && r >= nstages ? 1u : 0u, st = r - mat * nstages;
     const uint32_t row0 = (blockIdx.x + lt * gridDim.x) * 16u;
     const uint32_t nrows = min(16u, rows - row0);
-    const uint8_t* sb = w + (size_t)row0 * row_bytes + 576u * st;
+    const uint8_t* sb = (mat ? w2 : w) + (size_t)row0 * row_bytes + 576u * st;
     // the descriptor ends at the tile's last row: pieces past it read zero
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - 576u * st), kBufferWord3);
@@ -448,7 +456,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   for (int t = 0; t < 16; ++t) A[t] = i32x4{0, 0, 0, 0};
   for (uint32_t j = 0; j < my_pairs; ++j) {
     const uint32_t p = wave + j * WAVES;
-    const uint32_t lt = p / nstages, s = p - lt * nstages;
+    const uint32_t lt = p / tstages, r = p - lt * tstages;
+    const uint32_t s = MATS > 1 && r >= nstages ? r - nstages : r;  // stage
     const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
     if (DEPTH >= 3 && later >= 2u)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(18));
@@ -492,14 +501,20 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
          ++spin)
       __builtin_amdgcn_s_sleep(1);
     if (grp == 0u)
-      lds_write_b32(sbase + L.part + 64u * (slot * nstages + s) + 4u * n, __float_as_uint(rowsum));
-    const uint32_t done = uniform(lds_add_rtn(sbase + L.cnt + 4u * slot, lane == 0u ? 1u : 0u));
-    if (done == nstages - 1u) {
-      float sum = 0.0f;
+      lds_write_b32(sbase + L.part + 64u * (slot * tstages + r) + 4u * n, __float_as_uint(rowsum));
+    uint32_t old = 0u;
+    if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);  // one lane: no serialised atomics
+    const uint32_t done = __builtin_amdgcn_readlane(old, 0);
+    if (done == tstages - 1u) {
+      float sum = 0.0f, sum2 = 0.0f;
       for (uint32_t st = 0; st < nstages; ++st)
-        sum += __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * nstages + st) + 4u * n));
+        sum += __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * tstages + st) + 4u * n));
+      if (MATS > 1)
+        for (uint32_t st = nstages; st < tstages; ++st)
+          sum2 += __uint_as_float(
+              lds_read_b32(sbase + L.part + 64u * (slot * tstages + st) + 4u * n));
       const uint32_t row = (blockIdx.x + lt * gridDim.x) * 16u + n;
-      if (grp == 0u && row < rows) y[row] = sum;
+      if (grp == 0u && row < rows) y[row] = MATS > 1 ? silu_times(sum, sum2) : sum;
       if (lane == 0u) {
         lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
         lds_write_b32(sbase + L.owner + 4u * slot, lt + slots);
@@ -524,49 +539,61 @@ int cu_count() {
   return cus;
 }
 
-template <int W, int D>
-bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
-               hipStream_t s, hipError_t* err) {
+template <int W, int D, int M>
+bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, uint32_t rows,
+               uint32_t nb, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t grid = min(ntiles, (uint32_t)cu_count());
-  const uint32_t nstages = (nb + 3u) / 4u;
+  const uint32_t tstages = (nb + 3u) / 4u * M;
   const uint32_t per_wg = (ntiles + grid - 1u) / grid;
   // enough slots for every wave to be a few tiles ahead, within 8 KB
-  uint32_t slots = min(per_wg, max(4u, (2u * W * D + nstages - 1u) / nstages + 2u));
-  while (slots > 2u && slots * nstages * 64u > 8192u) --slots;
-  const uint32_t lds = layout(W, D, nb, slots).total;
+  uint32_t slots = min(per_wg, max(4u, (2u * W * D + tstages - 1u) / tstages + 2u));
+  while (slots > 2u && slots * tstages * 64u > 8192u) --slots;
+  const uint32_t lds = layout(W, D, nb, slots, M).total;
   if (lds > kLdsBytes) return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D>),
+      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q4k_matvec_mfma<W, D>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows, nb,
-                     slots);
+  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M>), dim3(grid), dim3(W * 64), lds, s, w, w2, x, y,
+                     rows, nb, slots);
   *err = hipGetLastError();
   return true;
+}
+
+bool shape_ok(uint32_t cols) {
+  const uint32_t nb = cols / kBlockElems;
+  return nb != 0 && (uint64_t)nb * kQ4Bytes * 16u <= 0x7fffffffu && nb * 1024u <= 0x7fffffffu;
 }
 
 }  // namespace
 
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, hipStream_t s, hipError_t* err) {
+  if (!shape_ok(cols)) return false;
   const uint32_t nb = cols / kBlockElems;
-  if (nb == 0 || (uint64_t)nb * kQ4Bytes * 16u > 0x7fffffffu || nb * 1024u > 0x7fffffffu)
-    return false;
   static const int cfg = env_int("SI_HIP_Q4K_MFMA_CFG", 0);
   switch (cfg) {
-    case 1: return launch_wd<12, 1>(w, x, y, rows, nb, s, err);
-    case 2: return launch_wd<8, 1>(w, x, y, rows, nb, s, err);
-    case 3: return launch_wd<4, 3>(w, x, y, rows, nb, s, err);
-    case 4: return launch_wd<4, 2>(w, x, y, rows, nb, s, err);
-    case 5: return launch_wd<8, 2>(w, x, y, rows, nb, s, err);
+    case 1: return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, s, err);
+    case 2: return launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, s, err);
+    case 3: return launch_wd<4, 3, 1>(w, nullptr, x, y, rows, nb, s, err);
     default: break;
   }
-  return launch_wd<12, 1>(w, x, y, rows, nb, s, err) || launch_wd<8, 1>(w, x, y, rows, nb, s, err) ||
-         launch_wd<4, 1>(w, x, y, rows, nb, s, err);
+  return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, s, err) ||
+         launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, s, err) ||
+         launch_wd<4, 1, 1>(w, nullptr, x, y, rows, nb, s, err);
+}
+
+bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
+                             uint32_t rows, uint32_t cols, hipStream_t s, hipError_t* err) {
+  if (!shape_ok(cols)) return false;
+  const uint32_t nb = cols / kBlockElems;
+  return launch_wd<12, 1, 2>(gate, up, x, h, rows, nb, s, err) ||
+         launch_wd<8, 1, 2>(gate, up, x, h, rows, nb, s, err) ||
+         launch_wd<4, 1, 2>(gate, up, x, h, rows, nb, s, err);
 }
 
 }  // namespace sihip

@@ -335,9 +335,9 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
   return true;
 }
 
-bool launch_fused_gate_up_tuned(const uint8_t*, const uint8_t*, const float*, float*, uint32_t,
-                                uint32_t, hipStream_t, hipError_t*) {
-  return false;
+bool launch_fused_gate_up_tuned(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
+                                uint32_t rows, uint32_t cols, hipStream_t s, hipError_t* err) {
+  return launch_q4k_gate_up_mfma(gate, up, x, h, rows, cols, s, err);
 }
 
 }  // namespace sihip

@@ -13,6 +13,9 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
 // Q4_K, one vector, K <= 8192, on the matrix cores.
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, hipStream_t s, hipError_t* err);
+// Fused SwiGLU gate/up (both Q4_K) on the matrix cores: h = silu(gate.x) * (up.x).
+bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
+                             uint32_t rows, uint32_t cols, hipStream_t s, hipError_t* err);
 bool launch_fused_gate_up_tuned(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
                                 uint32_t rows, uint32_t cols, hipStream_t s, hipError_t* err);
 
