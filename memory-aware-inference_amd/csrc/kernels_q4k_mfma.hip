@@ -47,101 +47,20 @@
 // the finishing wave stores silu(gate) * up.  LDS is only touched through
 // inline asm and the one barrier is a bare s_barrier: the compiler neither
 // counts nor orders buffer->LDS copies, and a fence would drain them.
-#include "kquant_device.h"
-#include "si_hip_internal.h"
+#include "mfma_common.h"
 #include "si_hip_tuned.h"
-
-#include <cstdlib>
 
 namespace sihip {
 namespace {
 
-typedef __attribute__((address_space(3))) void lds_void;
-typedef int i32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+using namespace mfma;
 
-constexpr int kBufferWord3 = 0x00020000;  // raw dword access (CDNA buffer descriptor)
-constexpr int kFixBits = 30;
-constexpr uint32_t kStageBytes = 16u * 4u * kQ4Bytes;  // 9216
-constexpr uint32_t kLdsBytes = 163840u;
-constexpr int kBadBlock = 0x40000000;  // exponent slot of a block taking the exact path
+constexpr uint32_t kStageBytes = 16u * 4u * kQ4Bytes;  // 9216: 16 rows x 4 blocks
 
-constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
-
-// LDS map of one workgroup (byte offsets): per-wave stage buffers, digit
-// images of all blocks (plus 4 KB that dead blocks of a short last stage
-// may read), unit sums [block][unit], exponents [block], then a ring of
-// `slots` tile slots: [slot][stage][16 rows] f32 partials, and per slot a
-// completion count and the tile index it currently belongs to.
-struct Layout {
-  uint32_t img, xsum, expo, part, cnt, owner, total;
-};
+// LDS map (make_layout): 4-block stages, 32 bytes of unit sums per block.
 __host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
                                             uint32_t slots, uint32_t mats) {
-  Layout l{};
-  const uint32_t nstages = (nb + 3u) / 4u * mats;  // partials per tile
-  l.img = waves * depth * kStageBytes;
-  l.xsum = l.img + nb * 1024u + 4096u;
-  l.expo = l.xsum + nb * 32u + 128u;
-  l.part = l.expo + ((nb * 4u + 15u) & ~15u) + 16u;
-  l.cnt = l.part + slots * nstages * 64u;
-  l.owner = l.cnt + slots * 4u;
-  l.total = l.owner + slots * 4u;
-  return l;
-}
-
-// Lanes whose A rows carry digits: lane 16 g + n with n / 4 == g.
-constexpr uint64_t kActiveLanes = 0xF0000F0000F0000Full;
-
-__device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
-
-template <int CTRL>
-__device__ __forceinline__ float dpp(float v) {
-  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
-}
-constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
-constexpr int kRowBcast15 = 0x15f;
-
-__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-__device__ __forceinline__ void lds_write_b128(uint32_t addr, u32x4 v) {
-  asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v) : "memory");
-}
-__device__ __forceinline__ void lds_write_b32(uint32_t addr, uint32_t v) {
-  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
-}
-// LDS atomic add; returns the previous value.
-__device__ __forceinline__ uint32_t lds_add_rtn(uint32_t addr, uint32_t v) {
-  uint32_t old;
-  asm volatile("ds_add_rtn_u32 %0, %1, %2\ns_waitcnt lgkmcnt(0)" : "=&v"(old) : "v"(addr), "v"(v) : "memory");
-  return old;
-}
-__device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
-  uint32_t v;
-  asm volatile("ds_read_b32 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
-  return v;
-}
-
-// The caller waits (lgkmcnt) in an asm that takes the value as an operand.
-__device__ __forceinline__ uint32_t lds_read_b32_nowait(uint32_t addr) {
-  uint32_t v;
-  asm volatile("ds_read_b32 %0, %1" : "=&v"(v) : "v"(addr) : "memory");
-  return v;
-}
-
-// Four 16-byte reads at addr + STRIDE * t, t = 0..3.
-template <int STRIDE, typename V>
-__device__ __forceinline__ void lds_read4(uint32_t addr, V (&a)[4]) {
-  asm volatile(
-      "ds_read_b128 %0, %4\n"
-      "ds_read_b128 %1, %4 offset:%5\n"
-      "ds_read_b128 %2, %4 offset:%6\n"
-      "ds_read_b128 %3, %4 offset:%7\n"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3])
-      : "v"(addr), "i"(STRIDE), "i"(2 * STRIDE), "i"(3 * STRIDE)
-      : "memory");
+  return make_layout(kStageBytes, 4u, 32u, waves, depth, nb, slots, mats);
 }
 
 // The lane's header and two qs pieces of the four blocks of a stage buffer:
@@ -214,21 +133,6 @@ __device__ __forceinline__ void lds_read_images(uint32_t addr, uint64_t mask, i3
       : "memory");
 }
 
-// Byte digits of four elements' biased values (X + 0x80808080): byte d of
-// each element gathered into one word, then flipped to signed (b - 128).
-__device__ __forceinline__ void transpose_digits(uint32_t u0, uint32_t u1, uint32_t u2,
-                                                 uint32_t u3, uint32_t (&out)[4]) {
-  // v_perm_b32 selector bytes 0..3 pick from the second source, 4..7 the first
-  const uint32_t lo01 = __builtin_amdgcn_perm(u1, u0, 0x05010400u);  // u0.b0 u1.b0 u0.b1 u1.b1
-  const uint32_t hi01 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);  // u0.b2 u1.b2 u0.b3 u1.b3
-  const uint32_t lo23 = __builtin_amdgcn_perm(u3, u2, 0x05010400u);
-  const uint32_t hi23 = __builtin_amdgcn_perm(u3, u2, 0x07030602u);
-  out[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
-  out[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
-  out[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
-  out[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u) ^ 0x80808080u;
-}
-
 __device__ __forceinline__ i32x4 low_nibbles(const u32x4& q) {
   return i32x4{(int)(q[0] & 0x0f0f0f0fu), (int)(q[1] & 0x0f0f0f0fu), (int)(q[2] & 0x0f0f0f0fu),
                (int)(q[3] & 0x0f0f0f0fu)};
@@ -249,15 +153,6 @@ __device__ __forceinline__ float exact_dot16(const u32x4& q, int shift, float d1
   }
   return acc;
 }
-
-// Sum over the four 16-lane groups, ((g0 + g1) + (g2 + g3)), in every lane.
-__device__ __forceinline__ float sum_lane_groups(float v) {
-  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
-  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
-  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
-}
-
 
 // Fast-path dot of one block for one lane: row n's units 2 grp, 2 grp + 1.
 __device__ __forceinline__ float block_terms(const u32x4& h, const u32x4& qa, const u32x4& qb,
@@ -328,23 +223,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
   uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
 
-  // 1. x into the image area, natural order (block b at img + 1024 b): pass
-  //    j of wave v copies blocks 4 (v + WAVES j) .. +3, one per instruction.
-  const uint32_t npass = (nb + 4u * WAVES - 1u) / (4u * WAVES);
-  {
-    const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<float*>(x), 0, (int)(nb * 1024u), kBufferWord3);
-    for (uint32_t j = 0; j < npass; ++j) {
-      const uint32_t b0 = 4u * (wave + WAVES * j);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const uint32_t b = b0 + i;
-        if (b < nb)
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(smem + L.img + 1024u * b), 16,
-                                                    1024u * b + 16u * lane, 0, 0, 0);
-      }
-    }
-  }
+  // 1. x into the image area, natural order (block b at img + 1024 b)
+  copy_x<WAVES>(smem, L.img, x, nb, wave, lane);
 
   // 2. this wave's pairs p = wave, wave + WAVES, ... of the workgroup's tiles
   //    (pair p = partial p % tstages of local tile p / tstages; partial r is
@@ -378,10 +258,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
 
   // 3. ring slots, then (once the x copies have landed) digit images, unit
   //    sums and exponents
-  for (uint32_t k = threadIdx.x; k < slots; k += WAVES * 64u) {
-    lds_write_b32(sbase + L.cnt + 4u * k, 0u);
-    lds_write_b32(sbase + L.owner + 4u * k, k);
-  }
+  init_slots<WAVES>(sbase, L, slots);
   // the stage copies were issued after x's and complete in order
   const uint32_t early = min((uint32_t)DEPTH, my_pairs);
   if (early >= 3u)
@@ -392,57 +269,9 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(9));
   else
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-  for (uint32_t j = 0; j < npass; ++j) {
-    if (4u * (wave + WAVES * j) >= nb) break;
-    // lane (grp, n): elements 16n..16n+15 of block pb
-    const uint32_t pb = 4u * (wave + WAVES * j) + grp;
-    const uint32_t pbc = pb < nb ? pb : nb - 1u;  // lanes past K redo the last block, unstored
-    u32x4 xq[4];
-    lds_read4<16>(sbase + L.img + 1024u * pbc + 64u * n, xq);
-    float xv[16];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int c = 0; c < 4; ++c) xv[4 * k + c] = __uint_as_float(xq[k][c]);
-    float amax = 0.0f, xsum = 0.0f;
-    bool bad = false;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float av = fabsf(xv[k]);
-      amax = fmaxf(amax, av);
-      bad |= !(av < 0x1p100f);
-      xsum += xv[k];
-    }
-    amax = fmaxf(amax, dpp<kRowShr1>(amax));
-    amax = fmaxf(amax, dpp<kRowShr2>(amax));
-    amax = fmaxf(amax, dpp<kRowShr4>(amax));
-    amax = fmaxf(amax, dpp<kRowShr8>(amax));
-    amax = dpp<kRowBcast15>(amax);
-    const int e = __builtin_amdgcn_frexp_expf(amax);  // amax < 2^e; 0 for amax == 0
-    uint32_t u[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k)
-      u[k] = (uint32_t)__float2int_rn(__builtin_amdgcn_ldexpf(xv[k], kFixBits - e)) + 0x80808080u;
-    uint32_t dg[4][4];  // [element quad][digit]
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      transpose_digits(u[4 * k], u[4 * k + 1], u[4 * k + 2], u[4 * k + 3], dg[k]);
-    // image of (block, t, A row m = 4p + d) at 1024 block + 256 t + 16 m; this
-    // lane's elements are those of t = n % 4, p = n / 4 (all lanes have read)
-    const uint32_t ib = sbase + L.img + 1024u * pbc + 256u * (n & 3u) + 64u * (n >> 2);
-    const bool store = pb < nb;
-    if (store) {
-#pragma unroll
-      for (int d = 0; d < 4; ++d)
-        lds_write_b128(ib + 16u * d, u32x4{dg[0][d], dg[1][d], dg[2][d], dg[3][d]});
-    }
-    xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit n / 2
-    if (store && (n & 1u))
-      lds_write_b32(sbase + L.xsum + 32u * pb + 4u * (n >> 1), __float_as_uint(xsum));
-    const bool bad_blk = (__builtin_amdgcn_ballot_w64(bad) >> (16u * grp)) & 0xffffull;
-    if (store && n == 0u)
-      lds_write_b32(sbase + L.expo + 4u * pb, (uint32_t)(bad_blk ? kBadBlock : e - kFixBits));
-  }
+  // chunk c = 4 p + t: units 2p, 2p + 1 of lane group p, MFMA t
+  build_images<WAVES>(sbase, L, nb, wave, grp, n,
+                      [](uint32_t c) { return 256u * (c & 3u) + 64u * (c >> 2); });
   lds_wait();
   __builtin_amdgcn_s_barrier();
 
@@ -494,49 +323,10 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     }
     const float rowsum = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
 
-    // hand the 16 row partials to the tile's slot (waiting while an earlier
-    // tile still holds it), count them, and let the last stage finish the tile
-    const uint32_t slot = lt % slots;
-    for (uint32_t spin = 0; lds_read_b32(sbase + L.owner + 4u * slot) != lt && spin < (1u << 24);
-         ++spin)
-      __builtin_amdgcn_s_sleep(1);
-    if (grp == 0u)
-      lds_write_b32(sbase + L.part + 64u * (slot * tstages + r) + 4u * n, __float_as_uint(rowsum));
-    uint32_t old = 0u;
-    if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);  // one lane: no serialised atomics
-    const uint32_t done = __builtin_amdgcn_readlane(old, 0);
-    if (done == tstages - 1u) {
-      float sum = 0.0f, sum2 = 0.0f;
-      for (uint32_t st = 0; st < nstages; ++st)
-        sum += __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * tstages + st) + 4u * n));
-      if (MATS > 1)
-        for (uint32_t st = nstages; st < tstages; ++st)
-          sum2 += __uint_as_float(
-              lds_read_b32(sbase + L.part + 64u * (slot * tstages + st) + 4u * n));
-      const uint32_t row = (blockIdx.x + lt * gridDim.x) * 16u + n;
-      if (grp == 0u && row < rows) y[row] = MATS > 1 ? silu_times(sum, sum2) : sum;
-      if (lane == 0u) {
-        lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
-        lds_write_b32(sbase + L.owner + 4u * slot, lt + slots);
-      }
-    }
+    // hand the 16 row partials to the tile's slot; the last stage finishes it
+    hand_off<MATS>(sbase, L, slots, lt, r, nstages, rowsum, lane,
+                   (blockIdx.x + lt * gridDim.x) * 16u + n, rows, y);
   }
-}
-
-int env_int(const char* name, int fallback) {
-  const char* v = std::getenv(name);
-  return v ? std::atoi(v) : fallback;
-}
-
-int cu_count() {
-  static int cus = [] {
-    int dev = 0, n = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
-      n = 256;
-    return n;
-  }();
-  return cus;
 }
 
 template <int W, int D, int M>
@@ -545,10 +335,7 @@ bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, ui
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t grid = min(ntiles, (uint32_t)cu_count());
   const uint32_t tstages = (nb + 3u) / 4u * M;
-  const uint32_t per_wg = (ntiles + grid - 1u) / grid;
-  // enough slots for every wave to be a few tiles ahead, within 8 KB
-  uint32_t slots = min(per_wg, max(4u, (2u * W * D + tstages - 1u) / tstages + 2u));
-  while (slots > 2u && slots * tstages * 64u > 8192u) --slots;
+  const uint32_t slots = ring_slots(W, D, (ntiles + grid - 1u) / grid, tstages);
   const uint32_t lds = layout(W, D, nb, slots, M).total;
   if (lds > kLdsBytes) return false;
   static const hipError_t attr = hipFuncSetAttribute(

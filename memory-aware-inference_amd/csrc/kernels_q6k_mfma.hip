@@ -1,0 +1,360 @@
+// Q6_K matvec on the gfx950 matrix cores (replaces si_q6_k_matvec* for one
+// input vector, src/metal.rs:895-1081; the output head of the greedy decode
+// and the MLP down projection).
+//
+// Weights.  quant.rs:145-171 decodes half h (128 elements) of a block from
+// ql[64h .. 64h + 64), qh[32h .. 32h + 32) and scales[8h .. 8h + 8): element
+// 128h + 32t + l (t = 0..3, l = 0..31) is (6-bit q) - 32 with scale
+// 8h + 2t + l / 16.  Lane group g = 2h + s of the B operand owns l in
+// [16s, 16s + 16) of half h for all four t: its 16-byte pieces are ql at
+// 64h + 16s (low nibbles: t = 0, high: t = 2), ql at 64h + 32 + 16s (t = 1, 3)
+// and qh at 128 + 32h + 16s (two bits per t), and MFMA t of a block gets one
+// scale per lane.  The MFMA takes the unsigned q (0..63); a second MFMA of the
+// same image with every weight byte -32 adds the offset, so each lane's digit
+// sums C_t[d] = sum (q - 32) D_d are exact integers.
+//
+// Per block and lane: T_d = sum_t sc_t * C_t[d] in integers, y += d * (sum_d
+// T_d * 256^d) * 2^(e_b - 30) (the digit images of the activations are built
+// as for Q4_K).  Blocks whose activations are not finite or reach 2^100 take
+// an exact per-weight f32 path (w = (d * sc) * (q - 32), quant.rs rounding).
+//
+// Data path.  Blocks are 210 bytes, so they are not 16-byte aligned; with an
+// even block count nb every row and every stage of two blocks (420 bytes)
+// starts on a 4-byte boundary, which the 16-byte buffer->LDS copies need (odd
+// nb is left to the generic kernel).  Each row's 420 bytes of a stage arrive
+// with 27 copies in piece-major order, piece q of row r at LDS byte
+// 16 (16 q + r), so every read is a conflict-free 16-lane sweep.  Pieces 0..25
+// are bytes 16 q .. 16 q + 15; piece 26 is bytes 404..419, so no copy runs
+// past the stage (a copy that crosses the end of its buffer descriptor reads
+// as zero in full).  The second block of a stage starts 2 bytes into piece
+// 13: its chunks are read as two pieces and realigned with v_alignbyte.
+// Scheduling, the LDS slot ring and the finishing wave are the Q4_K
+// kernel's (mfma_common.h).
+#include "mfma_common.h"
+#include "si_hip_tuned.h"
+
+namespace sihip {
+namespace {
+
+using namespace mfma;
+
+constexpr uint32_t kStageRowBytes = 2u * kQ6Bytes;     // 420: two blocks of one row
+constexpr uint32_t kRowPieces = 27u;                   // pieces per row and stage
+constexpr uint32_t kLastPiece = kStageRowBytes - 16u;  // 404: start of piece 26
+constexpr uint32_t kCopies = 7u;                       // 7 x 64 lanes >= 16 rows x 27 pieces
+constexpr uint32_t kStageBytes = kCopies * 1024u;      // 7168
+static_assert(16u * (kRowPieces - 1u) <= kStageRowBytes && kLastPiece % 4u == 0u,
+              "pieces 0..25 and 26 lie inside the stage, 4-byte aligned");
+static_assert(16u * kRowPieces <= kCopies * 64u, "copies cover every piece");
+
+__host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
+                                            uint32_t slots) {
+  return make_layout(kStageBytes, 2u, 0u, waves, depth, nb, slots, 1u);
+}
+
+// The lane's 13 pieces of a stage buffer (piece q of row n at 256 q + 16 n;
+// qa = piece 4h + s, qh = piece 8 + 2h + s, sc = piece 12 of the lane's row):
+//   v0 ql chunk A, v1 ql chunk B (piece +2), v2 qh chunk, v3 scales,
+//   v4 piece 13 (d of block 0) -- block 0;
+//   v5,v6 / v7,v8 / v9,v10 the same chunks of block 1 (13 pieces later, two
+//   pieces each), v11 piece 25 (stage bytes 400..415), v12 piece 26 (bytes
+//   404..419) -- its scales and d, block 1.
+__device__ __forceinline__ void lds_read_stage(uint32_t qa, uint32_t qh, uint32_t sc,
+                                               u32x4 (&v)[13]) {
+  asm volatile(
+      "ds_read_b128 %0, %13\n"
+      "ds_read_b128 %1, %13 offset:512\n"
+      "ds_read_b128 %2, %14\n"
+      "ds_read_b128 %3, %15\n"
+      "ds_read_b128 %4, %15 offset:256\n"
+      "ds_read_b128 %5, %13 offset:3328\n"
+      "ds_read_b128 %6, %13 offset:3584\n"
+      "ds_read_b128 %7, %13 offset:3840\n"
+      "ds_read_b128 %8, %13 offset:4096\n"
+      "ds_read_b128 %9, %14 offset:3328\n"
+      "ds_read_b128 %10, %14 offset:3584\n"
+      "ds_read_b128 %11, %15 offset:3328\n"
+      "ds_read_b128 %12, %15 offset:3584\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+        "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+        "=&v"(v[12])
+      : "v"(qa), "v"(qh), "v"(sc)
+      : "memory");
+}
+
+// The 8 A images of a stage (block b, MFMA t at addr + 1024 b + 256 t), read
+// only by the lanes in `mask`; the other lanes keep their (zero) registers.
+__device__ __forceinline__ void lds_read_images(uint32_t addr, uint64_t mask, i32x4 (&a)[8]) {
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %[sv], exec\n"
+      "s_mov_b64 exec, %[m]\n"
+      "ds_read_b128 %0, %[ad]\n"
+      "ds_read_b128 %1, %[ad] offset:256\n"
+      "ds_read_b128 %2, %[ad] offset:512\n"
+      "ds_read_b128 %3, %[ad] offset:768\n"
+      "ds_read_b128 %4, %[ad] offset:1024\n"
+      "ds_read_b128 %5, %[ad] offset:1280\n"
+      "ds_read_b128 %6, %[ad] offset:1536\n"
+      "ds_read_b128 %7, %[ad] offset:1792\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      "s_mov_b64 exec, %[sv]"
+      : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]),
+        "+v"(a[7]), [sv] "=&s"(saved)
+      : [ad] "v"(addr), [m] "s"(mask)
+      : "memory");
+}
+
+__device__ __forceinline__ u32x2 lds_read_b64(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// Signed byte of w at bit offset `bit` (an int8 scale).
+__device__ __forceinline__ int scale_at(uint32_t w, uint32_t bit) {
+  return (int)__builtin_amdgcn_sbfe((int)w, bit, 8u);
+}
+
+// The 16 bytes that start 2 bytes into piece lo (and end in piece hi).
+__device__ __forceinline__ u32x4 skip2(const u32x4& lo, const u32x4& hi) {
+  return u32x4{__builtin_amdgcn_alignbyte(lo[1], lo[0], 2), __builtin_amdgcn_alignbyte(lo[2], lo[1], 2),
+               __builtin_amdgcn_alignbyte(lo[3], lo[2], 2), __builtin_amdgcn_alignbyte(hi[0], lo[3], 2)};
+}
+
+// Unsigned 6-bit weights (0..63) of the lane's four sets t from its ql chunks
+// a (l), b (l + 32) and qh chunk h (quant.rs:155-159).
+__device__ __forceinline__ void q6_sets(const u32x4& a, const u32x4& b, const u32x4& h,
+                                        i32x4 (&q)[4]) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    q[0][k] = (int)((a[k] & 0x0f0f0f0fu) | ((h[k] << 4) & 0x30303030u));
+    q[1][k] = (int)((b[k] & 0x0f0f0f0fu) | ((h[k] << 2) & 0x30303030u));
+    q[2][k] = (int)(((a[k] >> 4) & 0x0f0f0f0fu) | (h[k] & 0x30303030u));
+    q[3][k] = (int)(((b[k] >> 4) & 0x0f0f0f0fu) | ((h[k] >> 2) & 0x30303030u));
+  }
+}
+
+// Fast-path dot of one block for one lane.
+__device__ __forceinline__ float block_terms(const i32x4 (&q)[4], const int (&sc)[4], float d,
+                                             const i32x4& a0, const i32x4& a1, const i32x4& a2,
+                                             const i32x4& a3, int eb) {
+  const i32x4 zero = {0, 0, 0, 0};
+  const int m32 = (int)0xe0e0e0e0u;  // -32 in every byte
+  const i32x4 neg32 = {m32, m32, m32, m32};
+  i32x4 c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, q[0], zero, 0, 0, 0);
+  i32x4 c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, q[1], zero, 0, 0, 0);
+  i32x4 c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, q[2], zero, 0, 0, 0);
+  i32x4 c3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a3, q[3], zero, 0, 0, 0);
+  c0 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, neg32, c0, 0, 0, 0);
+  c1 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, neg32, c1, 0, 0, 0);
+  c2 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, neg32, c2, 0, 0, 0);
+  c3 = __builtin_amdgcn_mfma_i32_16x16x64_i8(a3, neg32, c3, 0, 0, 0);
+  int t[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k)
+    t[k] = __mul24(sc[0], c0[k]) + __mul24(sc[1], c1[k]) + __mul24(sc[2], c2[k]) +
+           __mul24(sc[3], c3[k]);
+  const float tc =
+      fmaf(fmaf(fmaf((float)t[3], 256.0f, (float)t[2]), 256.0f, (float)t[1]), 256.0f, (float)t[0]);
+  return __builtin_amdgcn_ldexpf(d * tc, eb);
+}
+
+// Exact per-weight path of one block: xs = x of the block + 128 h + 16 s.
+__device__ __forceinline__ float block_exact(const i32x4 (&q)[4], const int (&sc)[4], float d,
+                                             const float* __restrict__ xs) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int qv = (int)(((uint32_t)q[t][i >> 2] >> (8 * (i & 3))) & 0xffu) - 32;
+      acc = fmaf(k6_value_exact(d, sc[t], qv), xs[32 * t + i], acc);
+    }
+  }
+  return acc;
+}
+
+template <int WAVES, int DEPTH>
+__global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y, uint32_t rows,
+                                                              uint32_t nb, uint32_t slots) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const Layout L = layout(WAVES, DEPTH, nb, slots);
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t grp = lane >> 4, n = lane & 15u;
+  const uint32_t half = grp >> 1, sub = grp & 1u;
+  const uint32_t row_bytes = nb * kQ6Bytes;
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t nstages = (nb + 1u) / 2u;
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
+
+  // 1. x into the image area, natural order (block b at img + 1024 b)
+  copy_x<WAVES>(smem, L.img, x, nb, wave, lane);
+
+  // 2. this wave's pairs p = wave, wave + WAVES, ... of the workgroup's tiles
+  //    (pair p = stage p % nstages of local tile p / nstages) and the copies
+  //    of its first DEPTH, pair j into buffer j % DEPTH.  Copy i, lane l moves
+  //    piece 4 i + l / 16 of row l % 16; the 16 lanes whose piece would be the
+  //    28th re-read the 27th (same addresses, no extra traffic).  All copies
+  //    lie inside the stage's 420 bytes of their row.
+  const uint32_t my_tiles =
+      blockIdx.x < ntiles ? (ntiles - 1u - blockIdx.x) / gridDim.x + 1u : 0u;
+  const uint32_t npairs = my_tiles * nstages;
+  const uint32_t voff = n * row_bytes + 16u * grp;
+  const uint32_t voff_last = n * row_bytes + (grp < 2u ? 16u * (24u + grp) : kLastPiece);
+  const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
+  auto issue = [&](uint32_t j) {
+    const uint32_t p = wave + j * WAVES;
+    const uint32_t lt = p / nstages, st = p - lt * nstages;
+    const uint32_t row0 = (blockIdx.x + lt * gridDim.x) * 16u;
+    const uint32_t nrows = min(16u, rows - row0);
+    const uint8_t* sb = w + (size_t)row0 * row_bytes + kStageRowBytes * st;
+    // the descriptor ends at the tile's last row: pieces past it read zero
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - kStageRowBytes * st),
+        kBufferWord3);
+    uint8_t* dst = wstage + (j % DEPTH) * kStageBytes;
+#pragma unroll
+    for (int i = 0; i < (int)kCopies - 1; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * i), 16,
+                                                voff + 64u * i, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * (kCopies - 1)), 16,
+                                              voff_last, 0, 0, 0);
+  };
+#pragma unroll
+  for (int j = 0; j < DEPTH; ++j)
+    if ((uint32_t)j < my_pairs) issue(j);
+
+  // 3. ring slots, then (once the x copies have landed) digit images and
+  //    exponents
+  init_slots<WAVES>(sbase, L, slots);
+  // the stage copies were issued after x's and complete in order
+  const uint32_t early = min((uint32_t)DEPTH, my_pairs);
+  if (early >= 3u)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * kCopies));
+  else if (early == 2u)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kCopies));
+  else if (early == 1u)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies));
+  else
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  // chunk c = 8 h + 2 t + s: MFMA t of lane group 2 h + s
+  build_images<WAVES>(sbase, L, nb, wave, grp, n, [](uint32_t c) {
+    return 256u * ((c >> 1) & 3u) + 64u * (2u * (c >> 3) + (c & 1u));
+  });
+  lds_wait();
+  __builtin_amdgcn_s_barrier();
+
+  // 4. the wave's pairs
+  const bool upper = half != 0u;  // lane groups 2, 3: scales 8..15
+  const uint32_t base = sbase + wave * DEPTH * kStageBytes + 16u * n;
+  const uint32_t qa0 = base + 256u * (4u * half + sub);
+  const uint32_t qh0 = base + 256u * (8u + 2u * half + sub);
+  const uint32_t sc0 = base + 256u * 12u;
+  const uint32_t sb_lo = 8u * sub, sb_hi = 8u * sub + 16u;  // bit offsets of the lane's scales
+  i32x4 A[8];
+#pragma unroll
+  for (int t = 0; t < 8; ++t) A[t] = i32x4{0, 0, 0, 0};
+  for (uint32_t j = 0; j < my_pairs; ++j) {
+    const uint32_t p = wave + j * WAVES;
+    const uint32_t lt = p / nstages, st = p - lt * nstages;
+    const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
+    if (DEPTH >= 3 && later >= 2u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kCopies));
+    else if (DEPTH >= 2 && later >= 1u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    const uint32_t buf = (j % DEPTH) * kStageBytes;
+    u32x4 v[13];
+    lds_read_stage(qa0 + buf, qh0 + buf, sc0 + buf, v);
+    if (j + DEPTH < my_pairs) issue(j + DEPTH);  // the buffer just read is free again
+    lds_read_images(sbase + L.img + 2048u * st + 16u * n, kActiveLanes, A);
+    const u32x2 ex = lds_read_b64(sbase + L.expo + 8u * st);
+    const int e0 = __builtin_amdgcn_readfirstlane(ex[0]);
+    const int e1 = __builtin_amdgcn_readfirstlane(ex[1]);
+
+    // block 0: scales[8h + s + 2t] = bytes s, s + 2 of words 2h, 2h + 1 of v3
+    i32x4 q0[4];
+    q6_sets(v[0], v[1], v[2], q0);
+    const uint32_t w0 = upper ? v[3][2] : v[3][0], w1 = upper ? v[3][3] : v[3][1];
+    const int sc_0[4] = {scale_at(w0, sb_lo), scale_at(w0, sb_hi), scale_at(w1, sb_lo),
+                         scale_at(w1, sb_hi)};
+    const float d0 = half_bits_to_float(v[4][0] & 0xffffu);
+    // block 1: its scale j < 14 is byte 2 + j of piece 25; scales 14, 15 and
+    // d are the last word of piece 26
+    i32x4 q1[4];
+    q6_sets(skip2(v[5], v[6]), skip2(v[7], v[8]), skip2(v[9], v[10]), q1);
+    const uint32_t u0 = upper ? v[11][2] : v[11][0], u1 = upper ? v[11][3] : v[11][1];
+    const uint32_t u2 = upper ? v[12][3] : v[11][2];
+    const int sc_1[4] = {scale_at(u0, sb_hi), scale_at(u1, sb_lo), scale_at(u1, sb_hi),
+                         scale_at(u2, sb_lo)};
+    const float d1 = half_bits_to_float(v[12][3] >> 16);
+
+    const float c0 = block_terms(q0, sc_0, d0, A[0], A[1], A[2], A[3], e0);
+    const float c1 = block_terms(q1, sc_1, d1, A[4], A[5], A[6], A[7], e1);
+    float part0 = e0 != kBadBlock ? c0 : 0.0f;
+    float part1 = e1 != kBadBlock ? c1 : 0.0f;
+    if (e0 == kBadBlock || e1 == kBadBlock) {
+      const float* xb = x + 512u * st + 128u * half + 16u * sub;
+      if (e0 == kBadBlock) part0 = block_exact(q0, sc_0, d0, xb);
+      if (e1 == kBadBlock) part1 = block_exact(q1, sc_1, d1, xb + 256);
+    }
+    const float rowsum = sum_lane_groups(part0 + part1);
+
+    // hand the 16 row partials to the tile's slot; the last stage finishes it
+    hand_off<1>(sbase, L, slots, lt, st, nstages, rowsum, lane,
+                (blockIdx.x + lt * gridDim.x) * 16u + n, rows, y);
+  }
+}
+
+template <int W, int D>
+bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+               hipStream_t s, hipError_t* err) {
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t grid = min(ntiles, (uint32_t)cu_count());
+  const uint32_t nstages = (nb + 1u) / 2u;
+  const uint32_t slots = ring_slots(W, D, (ntiles + grid - 1u) / grid, nstages);
+  const uint32_t lds = layout(W, D, nb, slots).total;
+  if (lds > kLdsBytes) return false;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
+  if (attr != hipSuccess) {
+    *err = attr;
+    return true;
+  }
+  hipLaunchKernelGGL((q6k_matvec_mfma<W, D>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
+                     nb, slots);
+  *err = hipGetLastError();
+  return true;
+}
+
+}  // namespace
+
+bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, hipStream_t s, hipError_t* err) {
+  const uint32_t nb = cols / kBlockElems;
+  // even nb (4-byte aligned rows and stages); in-tile offsets (16 rows) and
+  // the descriptor sizes are 32-bit
+  if (nb == 0 || (nb & 1u) || rows == 0 || (uint64_t)nb * kQ6Bytes * 16u > 0x7fffffffu ||
+      (uint64_t)nb * 1024u > 0x7fffffffu)
+    return false;
+  static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
+  switch (cfg) {
+    case 1: return launch_wd<12, 1>(w, x, y, rows, nb, s, err);
+    case 2: return launch_wd<8, 2>(w, x, y, rows, nb, s, err);
+    case 3: return launch_wd<8, 1>(w, x, y, rows, nb, s, err);
+    case 4: return launch_wd<6, 2>(w, x, y, rows, nb, s, err);
+    default: break;
+  }
+  return launch_wd<12, 1>(w, x, y, rows, nb, s, err) || launch_wd<10, 1>(w, x, y, rows, nb, s, err) ||
+         launch_wd<8, 1>(w, x, y, rows, nb, s, err) || launch_wd<4, 1>(w, x, y, rows, nb, s, err);
+}
+
+}  // namespace sihip

@@ -298,8 +298,23 @@ int device_cu_count() {
 
 bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float* y, uint32_t rows,
                          uint32_t cols, uint32_t batch, hipStream_t s, hipError_t* err) {
-  if (type != kTypeQ4K || batch != 1) return false;
+  if (batch == 0) return false;
   static const int mode = env_int("SI_HIP_Q4K_MODE", 0);
+  const bool q4_mfma = type == kTypeQ4K && mode == 0;
+  if (type == kTypeQ6K || (q4_mfma && batch > 1)) {
+    // several candidates (batch-major x and y, metal.rs:1104-1126): one
+    // matrix-core matvec per candidate, each bit-identical to its M = 1 call
+    for (uint32_t b = 0; b < batch; ++b) {
+      const float* xb = x + (size_t)b * cols;
+      float* yb = y + (size_t)b * rows;
+      const bool ok = type == kTypeQ6K ? launch_q6k_matvec_mfma(w, xb, yb, rows, cols, s, err)
+                                       : launch_q4k_matvec_mfma(w, xb, yb, rows, cols, s, err);
+      if (!ok) return b == 0 ? false : (*err = hipErrorInvalidValue, true);
+      if (*err != hipSuccess) return true;
+    }
+    return true;
+  }
+  if (type != kTypeQ4K || batch != 1) return false;
   if (mode == 0 && launch_q4k_matvec_mfma(w, x, y, rows, cols, s, err)) return true;
   const uint32_t nb = cols / kBlockElems;
   const uint32_t nstages = (nb + 3) / 4;

@@ -1,0 +1,295 @@
+// Building blocks shared by the K-quant matvec kernels that run on the gfx950
+// int8 matrix cores (kernels_q4k_mfma.hip, kernels_q6k_mfma.hip).
+//
+// Activations.  Each 256-element block b of x is written in fixed point,
+// x_i = X_i * 2^(e_b - 30) with |X_i| <= 2^30 (e_b from the block's largest
+// |x|), and X_i = sum_d D_d * 256^d in four signed byte digits.  For every
+// 16-element chunk of a block the workgroup keeps an A-operand "image" of
+// v_mfma_i32_16x16x64_i8 in LDS: A rows 4 p + d hold digit d of the chunk
+// that meets lane group p's weights and every other row is zero, so the
+// product with a B operand whose lane (p, n) holds 16 int8 weights of tile row
+// n returns, in lane (p, n), the four digit sums of that lane's own chunk.
+// Which chunk goes to which (MFMA, lane group) slot depends on how a format
+// lays its weights out; build_images takes that map as a template argument.
+//
+// Workgroup protocol.  One persistent workgroup per CU walks (tile, stage)
+// pairs; a wave leaves each stage's 16 row partials in an LDS slot of its tile
+// and counts them with an LDS atomic; the wave that completes the tile sums
+// the partials in stage order (results do not depend on timing).  LDS is
+// touched only through inline asm and the one barrier is a bare s_barrier:
+// the compiler neither counts nor orders buffer->LDS copies, and a fence
+// would drain them.
+#pragma once
+
+#include "kquant_device.h"
+#include "si_hip_internal.h"
+
+#include <cstdlib>
+
+namespace sihip {
+namespace mfma {
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kBufferWord3 = 0x00020000;  // raw dword access (CDNA buffer descriptor)
+constexpr int kFixBits = 30;
+constexpr uint32_t kLdsBytes = 163840u;
+constexpr int kBadBlock = 0x40000000;  // exponent slot of a block taking the exact path
+
+constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
+
+// LDS map of one workgroup (byte offsets): per-wave stage buffers, digit
+// images of all blocks (plus 4 KB that dead blocks of a short last stage
+// may read), unit sums [block][unit] (formats that need them), exponents
+// [block], then a ring of `slots` tile slots: [slot][partial][16 rows] f32
+// partials, and per slot a completion count and the tile index it currently
+// belongs to.
+struct Layout {
+  uint32_t img, xsum, expo, part, cnt, owner, total;
+};
+__host__ __device__ constexpr Layout make_layout(uint32_t stage_bytes, uint32_t stage_blocks,
+                                                 uint32_t xsum_per_block, uint32_t waves,
+                                                 uint32_t depth, uint32_t nb, uint32_t slots,
+                                                 uint32_t mats) {
+  Layout l{};
+  const uint32_t partials = (nb + stage_blocks - 1u) / stage_blocks * mats;  // per tile
+  l.img = waves * depth * stage_bytes;
+  l.xsum = l.img + nb * 1024u + 4096u;
+  l.expo = l.xsum + (xsum_per_block ? nb * xsum_per_block + 128u : 0u);
+  l.part = l.expo + ((nb * 4u + 15u) & ~15u) + 16u;
+  l.cnt = l.part + slots * partials * 64u;
+  l.owner = l.cnt + slots * 4u;
+  l.total = l.owner + slots * 4u;
+  return l;
+}
+
+// Lanes whose A rows carry digits: lane 16 g + n with n / 4 == g.
+constexpr uint64_t kActiveLanes = 0xF0000F0000F0000Full;
+
+__device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
+}
+constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kRowBcast15 = 0x15f;
+
+__device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ void lds_write_b128(uint32_t addr, u32x4 v) {
+  asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+__device__ __forceinline__ void lds_write_b32(uint32_t addr, uint32_t v) {
+  asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
+// LDS atomic add; returns the previous value.
+__device__ __forceinline__ uint32_t lds_add_rtn(uint32_t addr, uint32_t v) {
+  uint32_t old;
+  asm volatile("ds_add_rtn_u32 %0, %1, %2\ns_waitcnt lgkmcnt(0)" : "=&v"(old) : "v"(addr), "v"(v) : "memory");
+  return old;
+}
+__device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_b32 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// Four 16-byte reads at addr + STRIDE * t, t = 0..3.
+template <int STRIDE, typename V>
+__device__ __forceinline__ void lds_read4(uint32_t addr, V (&a)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %4\n"
+      "ds_read_b128 %1, %4 offset:%5\n"
+      "ds_read_b128 %2, %4 offset:%6\n"
+      "ds_read_b128 %3, %4 offset:%7\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3])
+      : "v"(addr), "i"(STRIDE), "i"(2 * STRIDE), "i"(3 * STRIDE)
+      : "memory");
+}
+
+// Byte digits of four elements' biased values (X + 0x80808080): byte d of
+// each element gathered into one word, then flipped to signed (b - 128).
+__device__ __forceinline__ void transpose_digits(uint32_t u0, uint32_t u1, uint32_t u2,
+                                                 uint32_t u3, uint32_t (&out)[4]) {
+  // v_perm_b32 selector bytes 0..3 pick from the second source, 4..7 the first
+  const uint32_t lo01 = __builtin_amdgcn_perm(u1, u0, 0x05010400u);  // u0.b0 u1.b0 u0.b1 u1.b1
+  const uint32_t hi01 = __builtin_amdgcn_perm(u1, u0, 0x07030602u);  // u0.b2 u1.b2 u0.b3 u1.b3
+  const uint32_t lo23 = __builtin_amdgcn_perm(u3, u2, 0x05010400u);
+  const uint32_t hi23 = __builtin_amdgcn_perm(u3, u2, 0x07030602u);
+  out[0] = __builtin_amdgcn_perm(lo23, lo01, 0x05040100u) ^ 0x80808080u;
+  out[1] = __builtin_amdgcn_perm(lo23, lo01, 0x07060302u) ^ 0x80808080u;
+  out[2] = __builtin_amdgcn_perm(hi23, hi01, 0x05040100u) ^ 0x80808080u;
+  out[3] = __builtin_amdgcn_perm(hi23, hi01, 0x07060302u) ^ 0x80808080u;
+}
+
+// Sum over the four 16-lane groups, ((g0 + g1) + (g2 + g3)), in every lane.
+__device__ __forceinline__ float sum_lane_groups(float v) {
+  auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Copy of x (nb blocks of 256 f32) into the image area in natural order
+// (block b at img + 1024 b): pass j of wave v copies blocks 4 (v + WAVES j)
+// .. +3, one 64-lane 16-byte copy each.
+template <int WAVES>
+__device__ __forceinline__ void copy_x(uint8_t* smem, uint32_t img, const float* x, uint32_t nb,
+                                       uint32_t wave, uint32_t lane) {
+  const uint32_t npass = (nb + 4u * WAVES - 1u) / (4u * WAVES);
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(x), 0, (int)(nb * 1024u), kBufferWord3);
+  for (uint32_t j = 0; j < npass; ++j) {
+    const uint32_t b0 = 4u * (wave + WAVES * j);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t b = b0 + i;
+      if (b < nb)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(smem + img + 1024u * b), 16,
+                                                  1024u * b + 16u * lane, 0, 0, 0);
+    }
+  }
+}
+
+// Turns the copied blocks into digit images in place, plus exponents and,
+// when L.xsum < L.expo, the f32 sums of each 32-element unit.  The caller has
+// waited for the copies.  CHUNK_SLOT(c) gives the byte offset, inside the
+// block's 1 KB, of the A row 4 p (digit 0) of MFMA t that holds chunk c
+// (elements 16 c .. 16 c + 15): 256 t + 64 p.  A block whose activations are
+// not all finite and below 2^100 gets exponent kBadBlock.
+template <int WAVES, typename ChunkSlot>
+__device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, uint32_t nb,
+                                             uint32_t wave, uint32_t grp, uint32_t n,
+                                             ChunkSlot chunk_slot) {
+  const uint32_t npass = (nb + 4u * WAVES - 1u) / (4u * WAVES);
+  const bool want_sums = L.xsum < L.expo;
+  for (uint32_t j = 0; j < npass; ++j) {
+    if (4u * (wave + WAVES * j) >= nb) break;
+    // lane (grp, n): elements 16n..16n+15 of block pb
+    const uint32_t pb = 4u * (wave + WAVES * j) + grp;
+    const uint32_t pbc = pb < nb ? pb : nb - 1u;  // lanes past K redo the last block, unstored
+    u32x4 xq[4];
+    lds_read4<16>(sbase + L.img + 1024u * pbc + 64u * n, xq);
+    float xv[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xv[4 * k + c] = __uint_as_float(xq[k][c]);
+    float amax = 0.0f, xsum = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float av = fabsf(xv[k]);
+      amax = fmaxf(amax, av);
+      bad |= !(av < 0x1p100f);
+      xsum += xv[k];
+    }
+    amax = fmaxf(amax, dpp<kRowShr1>(amax));
+    amax = fmaxf(amax, dpp<kRowShr2>(amax));
+    amax = fmaxf(amax, dpp<kRowShr4>(amax));
+    amax = fmaxf(amax, dpp<kRowShr8>(amax));
+    amax = dpp<kRowBcast15>(amax);
+    const int e = __builtin_amdgcn_frexp_expf(amax);  // amax < 2^e; 0 for amax == 0
+    uint32_t u[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      u[k] = (uint32_t)__float2int_rn(__builtin_amdgcn_ldexpf(xv[k], kFixBits - e)) + 0x80808080u;
+    uint32_t dg[4][4];  // [element quad][digit]
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      transpose_digits(u[4 * k], u[4 * k + 1], u[4 * k + 2], u[4 * k + 3], dg[k]);
+    // all lanes of the group have read the block before any lane writes it
+    const uint32_t ib = sbase + L.img + 1024u * pbc + chunk_slot(n);
+    const bool store = pb < nb;
+    if (store) {
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+        lds_write_b128(ib + 16u * d, u32x4{dg[0][d], dg[1][d], dg[2][d], dg[3][d]});
+    }
+    if (want_sums) {
+      xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit n / 2
+      if (store && (n & 1u))
+        lds_write_b32(sbase + L.xsum + 32u * pb + 4u * (n >> 1), __float_as_uint(xsum));
+    }
+    const bool bad_blk = (__builtin_amdgcn_ballot_w64(bad) >> (16u * grp)) & 0xffffull;
+    if (store && n == 0u)
+      lds_write_b32(sbase + L.expo + 4u * pb, (uint32_t)(bad_blk ? kBadBlock : e - kFixBits));
+  }
+}
+
+// Slot ring set-up: every slot empty and owned by local tile == its index.
+template <int WAVES>
+__device__ __forceinline__ void init_slots(uint32_t sbase, const Layout& L, uint32_t slots) {
+  for (uint32_t k = threadIdx.x; k < slots; k += WAVES * 64u) {
+    lds_write_b32(sbase + L.cnt + 4u * k, 0u);
+    lds_write_b32(sbase + L.owner + 4u * k, k);
+  }
+}
+
+// Hands partial r (of `tparts` per tile) of local tile lt to the tile's slot,
+// waiting while an earlier tile still holds it, and lets the wave that
+// completes the tile store it: y[row] = sum of partials 0..nparts-1 (in that
+// order), or with MATS == 2 silu(first nparts) * (second nparts).
+template <int MATS>
+__device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32_t slots,
+                                         uint32_t lt, uint32_t r, uint32_t nparts, float rowsum,
+                                         uint32_t lane, uint32_t row, uint32_t rows,
+                                         float* __restrict__ y) {
+  const uint32_t grp = lane >> 4, n = lane & 15u;
+  const uint32_t tparts = MATS * nparts;
+  const uint32_t slot = lt % slots;
+  for (uint32_t spin = 0; lds_read_b32(sbase + L.owner + 4u * slot) != lt && spin < (1u << 24);
+       ++spin)
+    __builtin_amdgcn_s_sleep(1);
+  if (grp == 0u)
+    lds_write_b32(sbase + L.part + 64u * (slot * tparts + r) + 4u * n, __float_as_uint(rowsum));
+  uint32_t old = 0u;
+  if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);  // one lane: no serialised atomics
+  const uint32_t done = __builtin_amdgcn_readlane(old, 0);
+  if (done == tparts - 1u) {
+    float sum = 0.0f, sum2 = 0.0f;
+    for (uint32_t st = 0; st < nparts; ++st)
+      sum += __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * tparts + st) + 4u * n));
+    if (MATS > 1)
+      for (uint32_t st = nparts; st < tparts; ++st)
+        sum2 += __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * tparts + st) + 4u * n));
+    if (grp == 0u && row < rows) y[row] = MATS > 1 ? silu_times(sum, sum2) : sum;
+    if (lane == 0u) {
+      lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
+      lds_write_b32(sbase + L.owner + 4u * slot, lt + slots);
+    }
+  }
+}
+
+// Slots of the ring: enough for every wave to be a few tiles ahead, within
+// 8 KB of partials.
+inline uint32_t ring_slots(uint32_t waves, uint32_t depth, uint32_t tiles_per_wg,
+                           uint32_t tparts) {
+  uint32_t slots = min(tiles_per_wg, max(4u, (2u * waves * depth + tparts - 1u) / tparts + 2u));
+  while (slots > 2u && slots * tparts * 64u > 8192u) --slots;
+  return slots;
+}
+
+inline int env_int(const char* name, int fallback) {
+  const char* v = std::getenv(name);
+  return v ? std::atoi(v) : fallback;
+}
+
+inline int cu_count() {
+  static int cus = [] {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      n = 256;
+    return n;
+  }();
+  return cus;
+}
+
+}  // namespace mfma
+}  // namespace sihip

@@ -1,4 +1,4 @@
-// Tuned gfx950 kernels (kernels_tuned.hip, kernels_q4k_mfma.hip).  Each launcher returns false when
+// Tuned gfx950 kernels (kernels_tuned.hip, kernels_q4k_mfma.hip, kernels_q6k_mfma.hip).  Each launcher returns false when
 // the shape is outside what the tuned kernel handles; the caller then uses
 // the generic kernels.  When it returns true, *err holds the launch status.
 #pragma once
@@ -12,6 +12,9 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
                          uint32_t cols, uint32_t batch, hipStream_t s, hipError_t* err);
 // Q4_K, one vector, K <= 8192, on the matrix cores.
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, hipStream_t s, hipError_t* err);
+// Q6_K, one vector, on the matrix cores.
+bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, hipStream_t s, hipError_t* err);
 // Fused SwiGLU gate/up (both Q4_K) on the matrix cores: h = silu(gate.x) * (up.x).
 bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float* x, float* h,

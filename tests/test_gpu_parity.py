@@ -83,8 +83,9 @@ def test_dequantize_random_blocks_bit_exact(hip_ctx, t):
 
 # ---- matvec ---------------------------------------------------------------------
 # K from one block to past the tuned kernels' register-resident limit (32768)
-SHAPES = [(1, 256), (7, 512), (64, 1024), (300, 5120), (1024, 5120), (33, 9216),
-          (129, 17408), (17, 27648), (5, 33024)]
+# (odd block counts leave the matrix-core kernels a half-empty last stage)
+SHAPES = [(1, 256), (7, 512), (64, 1024), (40, 2304), (300, 5120), (48, 5376), (1024, 5120),
+          (33, 9216), (129, 17408), (17, 27648), (5, 33024)]
 
 
 @pytest.mark.parametrize("t", [12, 13, 14])
@@ -111,6 +112,53 @@ def test_q4_k_baseline_shapes(hip_ctx, rows, cols):
     y = hip_ctx.gguf_quant_matvec_weight(weight, rows, cols, x)
     worst = assert_dot_close(y, y64, ab, what=f"{rows}x{cols}")
     log(f"  worst error / bound = {worst:.4f}")
+
+
+# the Q6_K output head (Qwen-style vocabulary) and MLP down projection
+@pytest.mark.parametrize("rows,cols", [(5120, 17408), (151936, 5120)])
+def test_q6_k_baseline_shapes(hip_ctx, rows, cols):
+    log(f"q6_k baseline shape {rows}x{cols}")
+    w = si_hip.synth_matrix(14, seed=2025, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(6, cols)
+    _, y64, ab = O.matvec(14, w, rows, cols, x, threads=8)
+    weight = hip_ctx.upload_quant_weight_private(w, 14)
+    y = hip_ctx.gguf_quant_matvec_weight(weight, rows, cols, x)
+    worst = assert_dot_close(y, y64, ab, what=f"{rows}x{cols}")
+    log(f"  worst error / bound = {worst:.4f}")
+
+
+def _category(v):
+    v = np.asarray(v, np.float64)
+    return np.where(np.isnan(v), 3, np.where(np.isposinf(v), 1, np.where(np.isneginf(v), 2, 0)))
+
+
+@pytest.mark.parametrize("t", [12, 13, 14])
+def test_matvec_nonfinite_and_huge_activations(ctx, t):
+    """Blocks whose activations are not finite, or so large that a fixed-point
+    form would overflow, or subnormal, must give what per-weight f32 products
+    give: +-inf / NaN rows exactly where the reference has them, and finite rows
+    within the usual bound."""
+    rows, cols = 48, 2304
+    log(f"non-finite activations t={t}")
+    w = si_hip.synth_matrix(t, seed=1900 + t, rows=rows, cols=cols)
+    W = ctx.upload_quant_weight_private(w, t)
+    base = si_hip.synth_normal(1901, cols)
+    # huge (>= 2^100) values in one block, subnormal and zero blocks elsewhere
+    x = base.copy()
+    x[600:620] = np.float32(3e30)
+    x[621] = np.float32(-2.5e33)
+    x[1024:1280] = np.float32(1e-41)
+    x[1280:1536] = 0.0
+    _, y64, ab = O.matvec(t, w, rows, cols, x)
+    y = ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+    assert_dot_close(y, y64, ab, what="huge/subnormal activations")
+    # one infinite activation: the sign of w[r, k] decides +inf / -inf, w == 0 gives NaN
+    for k, v in [(300, np.inf), (1800, -np.inf), (5, np.nan)]:
+        x = base.copy()
+        x[k] = v
+        y32, _, _ = O.matvec(t, w, rows, cols, x)
+        y = ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        assert np.array_equal(_category(y), _category(y32)), f"x[{k}] = {v}"
 
 
 def test_matvec_cancellation_heavy_blocks(ctx):
