@@ -134,6 +134,8 @@ struct si_hip_context {
   size_t stage_weights_bytes = 0;
   void *stage_aux = nullptr;
   size_t stage_aux_bytes = 0;
+  // cross-workgroup combine area of the matrix-core kernels (kept zeroed)
+  sihip::Workspace ws;
   hipEvent_t events[16] = {};
   // telemetry
   std::shared_ptr<Telemetry> tel = std::make_shared<Telemetry>();
@@ -200,7 +202,7 @@ int dispatch_matvec(si_hip_context *ctx, uint32_t type, const uint8_t *w, const 
   hipError_t e = hipErrorInvalidValue;
   bool done = false;
   if (ctx->policy == SI_HIP_KERNEL_AUTO) {
-    done = sihip::launch_matvec_tuned(type, w, x, y, rows, cols, batch, ctx->stream, &e);
+    done = sihip::launch_matvec_tuned(type, w, x, y, rows, cols, batch, ctx->ws, ctx->stream, &e);
   }
   if (!done) e = sihip::launch_matvec_generic(type, w, x, y, rows, cols, batch, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "matvec launch");
@@ -212,7 +214,7 @@ int dispatch_gate_up(si_hip_context *ctx, const uint8_t *g, const uint8_t *u, co
   hipError_t e = hipErrorInvalidValue;
   bool done = false;
   if (ctx->policy == SI_HIP_KERNEL_AUTO) {
-    done = sihip::launch_fused_gate_up_tuned(g, u, x, h, rows, cols, ctx->stream, &e);
+    done = sihip::launch_fused_gate_up_tuned(g, u, x, h, rows, cols, ctx->ws, ctx->stream, &e);
   }
   if (!done) e = sihip::launch_fused_gate_up_generic(g, u, x, h, rows, cols, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "fused gate/up launch");
@@ -362,6 +364,25 @@ int si_hip_context_new(int device_ordinal, si_hip_context **out) {
   SIHIP_CHECK(hipStreamCreateWithFlags(&ctx->stream, hipStreamNonBlocking), "stream create");
   SIHIP_CHECK(hipStreamCreateWithFlags(&ctx->upload_stream, hipStreamNonBlocking), "stream create");
   for (auto &ev : ctx->events) SIHIP_CHECK(hipEventCreate(&ev), "event create");
+  {
+    void *p = nullptr;
+    if (hipMalloc(&p, sihip::kWorkspaceBytes) != hipSuccess)
+      return fail(SI_HIP_ERR_OUT_OF_MEMORY, "HIP could not allocate the %zu-byte workspace",
+                  sihip::kWorkspaceBytes);
+    ctx->ws.ptr = p;
+    ctx->ws.bytes = sihip::kWorkspaceBytes;
+    ctx->tel->note_alloc(sihip::kWorkspaceBytes);
+    // counters zero, entries empty; set on the context's own (non-blocking)
+    // stream before any kernel
+    SIHIP_CHECK(hipMemsetAsync(p, 0, sihip::kWorkspaceCounterBytes, ctx->stream),
+                "workspace clear");
+    SIHIP_CHECK(hipMemsetD32Async(static_cast<uint8_t *>(p) + sihip::kWorkspaceCounterBytes,
+                                  (int)sihip::kWorkspaceEmpty,
+                                  (sihip::kWorkspaceBytes - sihip::kWorkspaceCounterBytes) / 4,
+                                  ctx->stream),
+                "workspace clear");
+    SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "workspace clear");
+  }
   *out = ctx.release();
   return ok();
 }
@@ -370,10 +391,10 @@ void si_hip_context_free(si_hip_context *ctx) {
   if (!ctx) return;
   (void)hipSetDevice(ctx->device);
   if (ctx->stream) (void)hipStreamSynchronize(ctx->stream);
-  for (void *p : {ctx->stage_in, ctx->stage_out, ctx->stage_weights, ctx->stage_aux})
+  for (void *p : {ctx->stage_in, ctx->stage_out, ctx->stage_weights, ctx->stage_aux, ctx->ws.ptr})
     if (p) (void)hipFree(p);
   ctx->tel->note_free(ctx->stage_in_bytes + ctx->stage_out_bytes + ctx->stage_weights_bytes +
-                      ctx->stage_aux_bytes);
+                      ctx->stage_aux_bytes + ctx->ws.bytes);
   for (auto &ev : ctx->events)
     if (ev) (void)hipEventDestroy(ev);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

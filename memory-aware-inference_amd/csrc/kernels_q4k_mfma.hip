@@ -210,9 +210,11 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
                                                               const uint8_t* __restrict__ w2,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
-                                                              uint32_t nb, uint32_t slots) {
+                                                              uint32_t nb, uint32_t slots,
+                                                              void* __restrict__ wsp, uint32_t split) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const Layout L = layout(WAVES, DEPTH, nb, slots, MATS);
+  const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t grp = lane >> 4, n = lane & 15u;
@@ -226,21 +228,19 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   // 1. x into the image area, natural order (block b at img + 1024 b)
   copy_x<WAVES>(smem, L.img, x, nb, wave, lane);
 
-  // 2. this wave's pairs p = wave, wave + WAVES, ... of the workgroup's tiles
-  //    (pair p = partial p % tstages of local tile p / tstages; partial r is
-  //    stage r % nstages of matrix r / nstages), and the copies
-  //    of its first DEPTH, pair j of the wave into buffer j % DEPTH.  Piece
+  // 2. this wave's pairs k = wave, wave + WAVES, ... of the workgroup's pairs
+  //    (pair_at: a tile and its partial r, r being stage r % nstages of
+  //    matrix r / nstages), and the copies of its first DEPTH, pair j of the
+  //    wave into buffer j % DEPTH.  Piece
   //    c = 64 i + lane of a stage is piece c / 16 of row c % 16's 576 bytes.
-  const uint32_t my_tiles =
-      blockIdx.x < ntiles ? (ntiles - 1u - blockIdx.x) / gridDim.x + 1u : 0u;
-  const uint32_t npairs = my_tiles * tstages;
+  const Sched sc = make_sched(ntiles, tstages, split != 0u, WAVES, slots);
+  const uint32_t npairs = sc.npairs;
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
   auto issue = [&](uint32_t j) {
-    const uint32_t p = wave + j * WAVES;
-    const uint32_t lt = p / tstages, r = p - lt * tstages;
-    const uint32_t mat = MATS > 1 && r >= nstages ? 1u : 0u, st = r - mat * nstages;
-    const uint32_t row0 = (blockIdx.x + lt * gridDim.x) * 16u;
+    const Pair pr = pair_at(sc, wave + j * WAVES, tstages);
+    const uint32_t mat = MATS > 1 && pr.r >= nstages ? 1u : 0u, st = pr.r - mat * nstages;
+    const uint32_t row0 = pr.tile * 16u;
     const uint32_t nrows = min(16u, rows - row0);
     const uint8_t* sb = (mat ? w2 : w) + (size_t)row0 * row_bytes + 576u * st;
     // the descriptor ends at the tile's last row: pieces past it read zero
@@ -284,9 +284,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
 #pragma unroll
   for (int t = 0; t < 16; ++t) A[t] = i32x4{0, 0, 0, 0};
   for (uint32_t j = 0; j < my_pairs; ++j) {
-    const uint32_t p = wave + j * WAVES;
-    const uint32_t lt = p / tstages, r = p - lt * tstages;
-    const uint32_t s = MATS > 1 && r >= nstages ? r - nstages : r;  // stage
+    const Pair pr = pair_at(sc, wave + j * WAVES, tstages);
+    const uint32_t s = MATS > 1 && pr.r >= nstages ? pr.r - nstages : pr.r;  // stage
     const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
     if (DEPTH >= 3 && later >= 2u)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(18));
@@ -324,18 +323,18 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     const float rowsum = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
-    hand_off<MATS>(sbase, L, slots, lt, r, nstages, rowsum, lane,
-                   (blockIdx.x + lt * gridDim.x) * 16u + n, rows, y);
+    hand_off<MATS>(sbase, L, slots, sc, pr, nstages, rowsum, lane, rows, y, ws);
   }
 }
 
 template <int W, int D, int M>
 bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, uint32_t rows,
-               uint32_t nb, hipStream_t s, hipError_t* err) {
+               uint32_t nb, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
-  const uint32_t grid = min(ntiles, (uint32_t)cu_count());
   const uint32_t tstages = (nb + 3u) / 4u * M;
-  const uint32_t slots = ring_slots(W, D, (ntiles + grid - 1u) / grid, tstages);
+  const LaunchShape ls = launch_shape(ntiles, tstages, W, ws.bytes, M);
+  const uint32_t grid = ls.groups;
+  const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, tstages);
   const uint32_t lds = layout(W, D, nb, slots, M).total;
   if (lds > kLdsBytes) return false;
   static const hipError_t attr = hipFuncSetAttribute(
@@ -346,41 +345,44 @@ bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, ui
     return true;
   }
   hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M>), dim3(grid), dim3(W * 64), lds, s, w, w2, x, y,
-                     rows, nb, slots);
+                     rows, nb, slots, ws.ptr, ls.split ? 1u : 0u);
   *err = hipGetLastError();
   return true;
 }
 
-bool shape_ok(uint32_t cols) {
+bool shape_ok(uint32_t rows, uint32_t cols, uint32_t mats) {
   const uint32_t nb = cols / kBlockElems;
-  return nb != 0 && (uint64_t)nb * kQ4Bytes * 16u <= 0x7fffffffu && nb * 1024u <= 0x7fffffffu;
+  const uint64_t pairs = (uint64_t)((rows + 15u) / 16u) * ((nb + 3u) / 4u) * mats;
+  return rows != 0 && nb != 0 && (uint64_t)nb * kQ4Bytes * 16u <= 0x7fffffffu &&
+         (uint64_t)nb * 1024u <= 0x7fffffffu && pairs <= 0xffffffffu;
 }
 
 }  // namespace
 
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
-                            uint32_t cols, hipStream_t s, hipError_t* err) {
-  if (!shape_ok(cols)) return false;
+                            uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  if (!shape_ok(rows, cols, 1u)) return false;
   const uint32_t nb = cols / kBlockElems;
   static const int cfg = env_int("SI_HIP_Q4K_MFMA_CFG", 0);
   switch (cfg) {
-    case 1: return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, s, err);
-    case 2: return launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, s, err);
-    case 3: return launch_wd<4, 3, 1>(w, nullptr, x, y, rows, nb, s, err);
+    case 1: return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
+    case 2: return launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
+    case 3: return launch_wd<4, 3, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
     default: break;
   }
-  return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, s, err) ||
-         launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, s, err) ||
-         launch_wd<4, 1, 1>(w, nullptr, x, y, rows, nb, s, err);
+  return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err) ||
+         launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err) ||
+         launch_wd<4, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
 }
 
 bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
-                             uint32_t rows, uint32_t cols, hipStream_t s, hipError_t* err) {
-  if (!shape_ok(cols)) return false;
+                             uint32_t rows, uint32_t cols, const Workspace& ws, hipStream_t s,
+                             hipError_t* err) {
+  if (!shape_ok(rows, cols, 2u)) return false;
   const uint32_t nb = cols / kBlockElems;
-  return launch_wd<12, 1, 2>(gate, up, x, h, rows, nb, s, err) ||
-         launch_wd<8, 1, 2>(gate, up, x, h, rows, nb, s, err) ||
-         launch_wd<4, 1, 2>(gate, up, x, h, rows, nb, s, err);
+  return launch_wd<12, 1, 2>(gate, up, x, h, rows, nb, ws, s, err) ||
+         launch_wd<8, 1, 2>(gate, up, x, h, rows, nb, ws, s, err) ||
+         launch_wd<4, 1, 2>(gate, up, x, h, rows, nb, ws, s, err);
 }
 
 }  // namespace sihip

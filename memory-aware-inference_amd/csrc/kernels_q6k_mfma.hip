@@ -180,9 +180,11 @@ template <int WAVES, int DEPTH>
 __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
-                                                              uint32_t nb, uint32_t slots) {
+                                                              uint32_t nb, uint32_t slots,
+                                                              void* __restrict__ wsp, uint32_t split) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const Layout L = layout(WAVES, DEPTH, nb, slots);
+  const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t grp = lane >> 4, n = lane & 15u;
@@ -196,22 +198,21 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   // 1. x into the image area, natural order (block b at img + 1024 b)
   copy_x<WAVES>(smem, L.img, x, nb, wave, lane);
 
-  // 2. this wave's pairs p = wave, wave + WAVES, ... of the workgroup's tiles
-  //    (pair p = stage p % nstages of local tile p / nstages) and the copies
-  //    of its first DEPTH, pair j into buffer j % DEPTH.  Copy i, lane l moves
+  // 2. this wave's pairs k = wave, wave + WAVES, ... of the workgroup's pairs
+  //    (pair_at: a tile and its stage) and the copies of its first DEPTH, pair
+  //    j into buffer j % DEPTH.  Copy i, lane l moves
   //    piece 4 i + l / 16 of row l % 16; the 16 lanes whose piece would be the
   //    28th re-read the 27th (same addresses, no extra traffic).  All copies
   //    lie inside the stage's 420 bytes of their row.
-  const uint32_t my_tiles =
-      blockIdx.x < ntiles ? (ntiles - 1u - blockIdx.x) / gridDim.x + 1u : 0u;
-  const uint32_t npairs = my_tiles * nstages;
+  const Sched sc = make_sched(ntiles, nstages, split != 0u, WAVES, slots);
+  const uint32_t npairs = sc.npairs;
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t voff_last = n * row_bytes + (grp < 2u ? 16u * (24u + grp) : kLastPiece);
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
   auto issue = [&](uint32_t j) {
-    const uint32_t p = wave + j * WAVES;
-    const uint32_t lt = p / nstages, st = p - lt * nstages;
-    const uint32_t row0 = (blockIdx.x + lt * gridDim.x) * 16u;
+    const Pair pr = pair_at(sc, wave + j * WAVES, nstages);
+    const uint32_t st = pr.r;
+    const uint32_t row0 = pr.tile * 16u;
     const uint32_t nrows = min(16u, rows - row0);
     const uint8_t* sb = w + (size_t)row0 * row_bytes + kStageRowBytes * st;
     // the descriptor ends at the tile's last row: pieces past it read zero
@@ -261,8 +262,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
 #pragma unroll
   for (int t = 0; t < 8; ++t) A[t] = i32x4{0, 0, 0, 0};
   for (uint32_t j = 0; j < my_pairs; ++j) {
-    const uint32_t p = wave + j * WAVES;
-    const uint32_t lt = p / nstages, st = p - lt * nstages;
+    const Pair pr = pair_at(sc, wave + j * WAVES, nstages);
+    const uint32_t st = pr.r;
     const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
     if (DEPTH >= 3 && later >= 2u)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kCopies));
@@ -308,18 +309,18 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     const float rowsum = sum_lane_groups(part0 + part1);
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
-    hand_off<1>(sbase, L, slots, lt, st, nstages, rowsum, lane,
-                (blockIdx.x + lt * gridDim.x) * 16u + n, rows, y);
+    hand_off<1>(sbase, L, slots, sc, pr, nstages, rowsum, lane, rows, y, ws);
   }
 }
 
 template <int W, int D>
 bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
-               hipStream_t s, hipError_t* err) {
+               const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
-  const uint32_t grid = min(ntiles, (uint32_t)cu_count());
   const uint32_t nstages = (nb + 1u) / 2u;
-  const uint32_t slots = ring_slots(W, D, (ntiles + grid - 1u) / grid, nstages);
+  const LaunchShape ls = launch_shape(ntiles, nstages, W, ws.bytes, 1u);
+  const uint32_t grid = ls.groups;
+  const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, nstages);
   const uint32_t lds = layout(W, D, nb, slots).total;
   if (lds > kLdsBytes) return false;
   static const hipError_t attr = hipFuncSetAttribute(
@@ -330,7 +331,7 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
     return true;
   }
   hipLaunchKernelGGL((q6k_matvec_mfma<W, D>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
-                     nb, slots);
+                     nb, slots, ws.ptr, ls.split ? 1u : 0u);
   *err = hipGetLastError();
   return true;
 }
@@ -338,23 +339,24 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
 }  // namespace
 
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
-                            uint32_t cols, hipStream_t s, hipError_t* err) {
+                            uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t nb = cols / kBlockElems;
   // even nb (4-byte aligned rows and stages); in-tile offsets (16 rows) and
   // the descriptor sizes are 32-bit
   if (nb == 0 || (nb & 1u) || rows == 0 || (uint64_t)nb * kQ6Bytes * 16u > 0x7fffffffu ||
-      (uint64_t)nb * 1024u > 0x7fffffffu)
+      (uint64_t)nb * 1024u > 0x7fffffffu ||
+      (uint64_t)((rows + 15u) / 16u) * (nb / 2u) > 0xffffffffu)
     return false;
   static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
   switch (cfg) {
-    case 1: return launch_wd<12, 1>(w, x, y, rows, nb, s, err);
-    case 2: return launch_wd<8, 2>(w, x, y, rows, nb, s, err);
-    case 3: return launch_wd<8, 1>(w, x, y, rows, nb, s, err);
-    case 4: return launch_wd<6, 2>(w, x, y, rows, nb, s, err);
+    case 1: return launch_wd<12, 1>(w, x, y, rows, nb, ws, s, err);
+    case 2: return launch_wd<8, 2>(w, x, y, rows, nb, ws, s, err);
+    case 3: return launch_wd<8, 1>(w, x, y, rows, nb, ws, s, err);
+    case 4: return launch_wd<6, 2>(w, x, y, rows, nb, ws, s, err);
     default: break;
   }
-  return launch_wd<12, 1>(w, x, y, rows, nb, s, err) || launch_wd<10, 1>(w, x, y, rows, nb, s, err) ||
-         launch_wd<8, 1>(w, x, y, rows, nb, s, err) || launch_wd<4, 1>(w, x, y, rows, nb, s, err);
+  return launch_wd<12, 1>(w, x, y, rows, nb, ws, s, err) || launch_wd<10, 1>(w, x, y, rows, nb, ws, s, err) ||
+         launch_wd<8, 1>(w, x, y, rows, nb, ws, s, err) || launch_wd<4, 1>(w, x, y, rows, nb, ws, s, err);
 }
 
 }  // namespace sihip

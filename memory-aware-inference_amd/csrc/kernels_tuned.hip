@@ -297,7 +297,8 @@ int device_cu_count() {
 }  // namespace
 
 bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float* y, uint32_t rows,
-                         uint32_t cols, uint32_t batch, hipStream_t s, hipError_t* err) {
+                         uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
+                         hipError_t* err) {
   if (batch == 0) return false;
   static const int mode = env_int("SI_HIP_Q4K_MODE", 0);
   const bool q4_mfma = type == kTypeQ4K && mode == 0;
@@ -307,15 +308,15 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
     for (uint32_t b = 0; b < batch; ++b) {
       const float* xb = x + (size_t)b * cols;
       float* yb = y + (size_t)b * rows;
-      const bool ok = type == kTypeQ6K ? launch_q6k_matvec_mfma(w, xb, yb, rows, cols, s, err)
-                                       : launch_q4k_matvec_mfma(w, xb, yb, rows, cols, s, err);
+      const bool ok = type == kTypeQ6K ? launch_q6k_matvec_mfma(w, xb, yb, rows, cols, ws, s, err)
+                                       : launch_q4k_matvec_mfma(w, xb, yb, rows, cols, ws, s, err);
       if (!ok) return b == 0 ? false : (*err = hipErrorInvalidValue, true);
       if (*err != hipSuccess) return true;
     }
     return true;
   }
   if (type != kTypeQ4K || batch != 1) return false;
-  if (mode == 0 && launch_q4k_matvec_mfma(w, x, y, rows, cols, s, err)) return true;
+  if (mode == 0 && launch_q4k_matvec_mfma(w, x, y, rows, cols, ws, s, err)) return true;
   const uint32_t nb = cols / kBlockElems;
   const uint32_t nstages = (nb + 3) / 4;
   // offsets inside one 16-row tile are 32-bit
@@ -351,8 +352,9 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
 }
 
 bool launch_fused_gate_up_tuned(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
-                                uint32_t rows, uint32_t cols, hipStream_t s, hipError_t* err) {
-  return launch_q4k_gate_up_mfma(gate, up, x, h, rows, cols, s, err);
+                                uint32_t rows, uint32_t cols, const Workspace& ws, hipStream_t s,
+                                hipError_t* err) {
+  return launch_q4k_gate_up_mfma(gate, up, x, h, rows, cols, ws, s, err);
 }
 
 }  // namespace sihip

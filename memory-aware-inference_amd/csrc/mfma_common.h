@@ -12,10 +12,11 @@
 // Which chunk goes to which (MFMA, lane group) slot depends on how a format
 // lays its weights out; build_images takes that map as a template argument.
 //
-// Workgroup protocol.  One persistent workgroup per CU walks (tile, stage)
-// pairs; a wave leaves each stage's 16 row partials in an LDS slot of its tile
-// and counts them with an LDS atomic; the wave that completes the tile sums
-// the partials in stage order (results do not depend on timing).  LDS is
+// Workgroup protocol.  One persistent workgroup per CU walks a contiguous
+// range of (tile, stage) pairs; a wave leaves each stage's 16 row partials in
+// an LDS slot of its tile and counts them with an LDS atomic; the wave that
+// completes the workgroup's share of a tile sums the partials in stage order
+// (results do not depend on timing).  LDS is
 // touched only through inline asm and the one barrier is a bare s_barrier:
 // the compiler neither counts nor orders buffer->LDS copies, and a fence
 // would drain them.
@@ -231,48 +232,219 @@ __device__ __forceinline__ void init_slots(uint32_t sbase, const Layout& L, uint
   }
 }
 
-// Hands partial r (of `tparts` per tile) of local tile lt to the tile's slot,
-// waiting while an earlier tile still holds it, and lets the wave that
-// completes the tile store it: y[row] = sum of partials 0..nparts-1 (in that
-// order), or with MATS == 2 silu(first nparts) * (second nparts).
+// Work split.  With G workgroups and T tiles of S partials each, workgroup g
+// owns the whole tiles g, g + G, ...  When that leaves some workgroups a
+// round of pairs more than others (rounds = pairs / waves, rounded up), the
+// launch "splits": workgroup g keeps q = T / G whole tiles g, g + G, ...,
+// g + (q - 1) G, and the L = (T - q G) S pairs of the leftover tiles are cut
+// into G contiguous ranges, so every workgroup gets the same number of pairs
+// to within one.  A leftover tile whose pairs fall into two or more ranges is
+// "split": each of its workgroups sums its own partials, publishes them in a
+// small global workspace and counts them on the tile's global counter; the
+// workgroup that completes the count adds the published sums in workgroup
+// order and stores the rows (deterministic for a given grid).  That exchange
+// costs a wave a few microseconds of waiting, so the leftover pairs go to the
+// last waves of the first round -- waves with a pair less than the others --
+// when the ring has a slot for every tile of the workgroup (tiles are then
+// not taken in slot order), and first otherwise.
+struct Sched {
+  uint32_t a, b;        // [a, b): this workgroup's leftover pairs
+  uint32_t lpairs;      // L
+  uint32_t split_base;  // first leftover tile, q G
+  uint32_t nsplit;      // leftover tiles this workgroup touches
+  uint32_t whole0, nwhole, wstride;  // whole tiles whole0 + wstride t, t < nwhole
+  uint32_t ngroups;
+  uint32_t npairs;      // this workgroup's pairs
+  uint32_t slack0;      // > 0: leftover pairs at positions slack0 .. slack0 + nl - 1
+};
+__device__ __forceinline__ uint32_t range_start(uint32_t g, uint32_t npairs, uint32_t ngroups) {
+  return (uint32_t)((uint64_t)g * npairs / ngroups);
+}
+// The workgroup whose range holds pair p.
+__device__ __forceinline__ uint32_t range_of(uint32_t p, uint32_t npairs, uint32_t ngroups) {
+  return (uint32_t)(((uint64_t)(p + 1u) * ngroups - 1u) / npairs);
+}
+__device__ __forceinline__ Sched make_sched(uint32_t ntiles, uint32_t tparts, bool split,
+                                            uint32_t waves, uint32_t slots) {
+  Sched s;
+  const uint32_t G = gridDim.x, g = blockIdx.x;
+  s.ngroups = G;
+  s.whole0 = g;
+  s.wstride = G;
+  s.slack0 = 0u;
+  if (!split) {
+    s.split_base = ntiles;
+    s.lpairs = 0u;
+    s.a = s.b = 0u;
+    s.nwhole = g < ntiles ? (ntiles - 1u - g) / G + 1u : 0u;
+  } else {
+    s.nwhole = ntiles / G;
+    s.split_base = s.nwhole * G;
+    s.lpairs = (ntiles - s.split_base) * tparts;
+    s.a = range_start(g, s.lpairs, G);
+    s.b = range_start(g + 1u, s.lpairs, G);
+  }
+  s.nsplit = s.b > s.a ? (s.b - 1u) / tparts - s.a / tparts + 1u : 0u;
+  s.npairs = (s.b - s.a) + s.nwhole * tparts;
+  const uint32_t nl = s.b - s.a, last = s.npairs % waves;
+  if (nl > 0u && nl < waves && s.npairs > waves && last != 0u && last <= waves - nl &&
+      s.nsplit + s.nwhole <= slots)
+    s.slack0 = waves - nl;
+  return s;
+}
+// The workgroup's pair k: tile, partial r, local tile index lt (its ring
+// slot is lt % slots) and the workgroup's share [lo, hi) of that tile's
+// partials.
+struct Pair {
+  uint32_t tile, r, lt, lo, hi;
+};
+__device__ __forceinline__ Pair pair_at(const Sched& s, uint32_t k, uint32_t tparts) {
+  Pair p;
+  const uint32_t nl = s.b - s.a;
+  bool split;
+  uint32_t ks;  // index among the leftover pairs, or nl + index among the whole-tile pairs
+  if (s.slack0) {
+    split = k >= s.slack0 && k < s.slack0 + nl;
+    ks = split ? k - s.slack0 : (k < s.slack0 ? k + nl : k);
+  } else {
+    split = k < nl;
+    ks = k;
+  }
+  if (split) {
+    const uint32_t lp = s.a + ks, t = lp / tparts;
+    p.tile = s.split_base + t;
+    p.r = lp - t * tparts;
+    p.lt = t - s.a / tparts;
+    p.lo = max(s.a, t * tparts) - t * tparts;
+    p.hi = min(s.b, (t + 1u) * tparts) - t * tparts;
+  } else {
+    const uint32_t kk = ks - nl, t = kk / tparts;
+    p.tile = s.whole0 + s.wstride * t;
+    p.r = kk - t * tparts;
+    p.lt = s.nsplit + t;
+    p.lo = 0u;
+    p.hi = tparts;
+  }
+  return p;
+}
+
+// Global workspace of split tiles: one counter per tile at the start (a fixed
+// region, so launches of any grid size find their counters at zero), then per
+// workgroup two entries (its first and its last tile) of MATS x 16 row sums.
+// An entry that holds no sum holds kPartEmpty, a signalling-NaN pattern that
+// no arithmetic result can have (results of operations are quiet NaNs).
+struct SplitWs {
+  float* part;
+  uint32_t* cnt;
+};
+constexpr size_t kCounterBytes = kWorkspaceCounterBytes;
+constexpr uint32_t kPartEmpty = kWorkspaceEmpty;
+__host__ __device__ constexpr bool split_ws_fits(size_t ws_bytes, uint32_t ngroups,
+                                                 uint32_t ntiles, uint32_t mats) {
+  return (size_t)ntiles * 4u <= kCounterBytes &&
+         kCounterBytes + (size_t)ngroups * 2u * mats * 64u <= ws_bytes;
+}
+__host__ __device__ inline SplitWs split_ws(void* base) {
+  SplitWs w;
+  w.cnt = static_cast<uint32_t*>(base);
+  w.part = reinterpret_cast<float*>(static_cast<uint8_t*>(base) + kCounterBytes);
+  return w;
+}
+
+// Device-coherent (sc1) word accesses: each XCD has its own L2, and these
+// bypass it for the few words workgroups exchange.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float load_coherent(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Takes a published sum, waiting (bounded) until its store has landed, and
+// marks the entry empty again.
+__device__ __forceinline__ float take_part(float* p) {
+  float v = load_coherent(p);
+  for (uint32_t spin = 0; __float_as_uint(v) == kPartEmpty && spin < (1u << 22); ++spin) {
+    __builtin_amdgcn_s_sleep(1);
+    v = load_coherent(p);
+  }
+  return v;
+}
+
+// Hands partial pr.r (of tparts = MATS * nparts per tile) of tile pr.tile to
+// the tile's LDS slot, waiting while an earlier tile still holds it.  The wave
+// that completes the workgroup's share of the tile sums that share in partial
+// order and stores the rows -- y[row] = sum, or with MATS == 2 silu(sum of
+// partials < nparts) * (sum of the rest) -- or, for a split tile, publishes
+// the sums and, if it completes the tile, combines all shares.
 template <int MATS>
 __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32_t slots,
-                                         uint32_t lt, uint32_t r, uint32_t nparts, float rowsum,
-                                         uint32_t lane, uint32_t row, uint32_t rows,
-                                         float* __restrict__ y) {
+                                         const Sched& sc, const Pair& pr, uint32_t nparts,
+                                         float rowsum, uint32_t lane, uint32_t rows,
+                                         float* __restrict__ y, SplitWs ws) {
   const uint32_t grp = lane >> 4, n = lane & 15u;
   const uint32_t tparts = MATS * nparts;
-  const uint32_t slot = lt % slots;
-  for (uint32_t spin = 0; lds_read_b32(sbase + L.owner + 4u * slot) != lt && spin < (1u << 24);
-       ++spin)
+  const uint32_t slot = pr.lt % slots;
+  for (uint32_t spin = 0;
+       lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
     __builtin_amdgcn_s_sleep(1);
   if (grp == 0u)
-    lds_write_b32(sbase + L.part + 64u * (slot * tparts + r) + 4u * n, __float_as_uint(rowsum));
+    lds_write_b32(sbase + L.part + 64u * (slot * tparts + pr.r) + 4u * n, __float_as_uint(rowsum));
   uint32_t old = 0u;
   if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);  // one lane: no serialised atomics
   const uint32_t done = __builtin_amdgcn_readlane(old, 0);
-  if (done == tparts - 1u) {
-    float sum = 0.0f, sum2 = 0.0f;
-    for (uint32_t st = 0; st < nparts; ++st)
-      sum += __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * tparts + st) + 4u * n));
-    if (MATS > 1)
-      for (uint32_t st = nparts; st < tparts; ++st)
-        sum2 += __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * tparts + st) + 4u * n));
+  if (done != pr.hi - pr.lo - 1u) return;
+  float sum = 0.0f, sum2 = 0.0f;
+  for (uint32_t st = pr.lo; st < pr.hi; ++st) {
+    const float v =
+        __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * tparts + st) + 4u * n));
+    if (MATS == 1 || st < nparts)
+      sum += v;
+    else
+      sum2 += v;
+  }
+  const uint32_t row = pr.tile * 16u + n;
+  if (pr.lo == 0u && pr.hi == tparts) {
     if (grp == 0u && row < rows) y[row] = MATS > 1 ? silu_times(sum, sum2) : sum;
-    if (lane == 0u) {
-      lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
-      lds_write_b32(sbase + L.owner + 4u * slot, lt + slots);
+  } else {
+    // Publish the share's sums, then count the share; no fence orders the
+    // two: the workgroup that completes the count waits for each entry to
+    // leave the empty state.  Only read-modify-write atomics touch the counter.
+    const uint32_t t = pr.tile - sc.split_base;  // leftover tile index
+    const uint32_t e = 2u * blockIdx.x + (t == sc.a / tparts ? 0u : 1u);
+    if (grp == 0u) {
+      store_coherent(ws.part + (e * MATS) * 16u + n, sum);
+      if (MATS > 1) store_coherent(ws.part + (e * MATS + 1u) * 16u + n, sum2);
+    }
+    uint32_t before = 0u;
+    if (lane == 0u)
+      before = __hip_atomic_fetch_add(ws.cnt + t, pr.hi - pr.lo, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+    before = __builtin_amdgcn_readlane(before, 0);
+    if (before + (pr.hi - pr.lo) == tparts) {
+      const uint32_t g0 = range_of(t * tparts, sc.lpairs, sc.ngroups);
+      const uint32_t g1 = range_of(t * tparts + tparts - 1u, sc.lpairs, sc.ngroups);
+      float g = 0.0f, u = 0.0f;
+      if (grp == 0u) {
+        for (uint32_t wg = g0; wg <= g1; ++wg) {
+          const uint32_t wa = range_start(wg, sc.lpairs, sc.ngroups);
+          if (wa == range_start(wg + 1u, sc.lpairs, sc.ngroups)) continue;  // no leftover pairs
+          const uint32_t t0 = wa / tparts;
+          float* pe = ws.part + (2u * wg + (t == t0 ? 0u : 1u)) * MATS * 16u + n;
+          g += take_part(pe);
+          if (MATS > 1) u += take_part(pe + 16u);
+          store_coherent(pe, __uint_as_float(kPartEmpty));
+          if (MATS > 1) store_coherent(pe + 16u, __uint_as_float(kPartEmpty));
+        }
+        if (row < rows) y[row] = MATS > 1 ? silu_times(g, u) : g;
+      }
+      if (lane == 0u)
+        (void)__hip_atomic_exchange(ws.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-}
-
-// Slots of the ring: enough for every wave to be a few tiles ahead, within
-// 8 KB of partials.
-inline uint32_t ring_slots(uint32_t waves, uint32_t depth, uint32_t tiles_per_wg,
-                           uint32_t tparts) {
-  uint32_t slots = min(tiles_per_wg, max(4u, (2u * waves * depth + tparts - 1u) / tparts + 2u));
-  while (slots > 2u && slots * tparts * 64u > 8192u) --slots;
-  return slots;
+  if (lane == 0u) {
+    lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
+    lds_write_b32(sbase + L.owner + 4u * slot, pr.lt + slots);
+  }
 }
 
 inline int env_int(const char* name, int fallback) {
@@ -289,6 +461,42 @@ inline int cu_count() {
     return n;
   }();
   return cus;
+}
+
+// Workgroups of a launch: one per CU, fewer when there are fewer pairs.
+// Launch shape of a matrix-core matvec: workgroups, whether tiles are split
+// (fewer rounds of pairs per wave than with whole tiles), and the most tiles
+// one workgroup touches.
+struct LaunchShape {
+  uint32_t groups;
+  bool split;
+  uint32_t tiles_per_group;
+};
+inline LaunchShape launch_shape(uint32_t ntiles, uint32_t tparts, uint32_t waves,
+                                size_t ws_bytes, uint32_t mats) {
+  LaunchShape ls;
+  const uint32_t cus = (uint32_t)cu_count();
+  const uint32_t g0 = min(ntiles, cus);
+  const uint64_t rounds0 = ((uint64_t)(ntiles + g0 - 1u) / g0 * tparts + waves - 1u) / waves;
+  const uint32_t g1 = (uint32_t)min((uint64_t)cus, (uint64_t)ntiles * tparts);
+  const uint32_t q = ntiles / g1;
+  const uint64_t lpairs = (uint64_t)(ntiles - q * g1) * tparts;
+  const uint64_t most = (uint64_t)q * tparts + (lpairs + g1 - 1u) / g1;
+  const uint64_t rounds1 = (most + waves - 1u) / waves;
+  ls.split = rounds1 < rounds0 && split_ws_fits(ws_bytes, g1, ntiles, mats);
+  ls.groups = ls.split ? g1 : g0;
+  ls.tiles_per_group = ls.split ? q + (uint32_t)(((lpairs + g1 - 1u) / g1 + tparts - 1u) / tparts) + 1u
+                                : (ntiles + g0 - 1u) / g0;
+  return ls;
+}
+
+// Slots of the ring: enough for every wave to be a few tiles ahead, within
+// 8 KB of partials.
+inline uint32_t ring_slots(uint32_t waves, uint32_t depth, uint32_t tiles_per_wg,
+                           uint32_t tparts) {
+  uint32_t slots = min(tiles_per_wg, max(4u, (2u * waves * depth + tparts - 1u) / tparts + 2u));
+  while (slots > 2u && slots * tparts * 64u > 8192u) --slots;
+  return slots;
 }
 
 }  // namespace mfma

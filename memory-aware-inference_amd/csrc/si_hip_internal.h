@@ -7,6 +7,19 @@
 
 namespace sihip {
 
+// Device memory a context lends to the kernels that combine partial sums
+// across workgroups: kWorkspaceCounterBytes of zeroed counters, then entries
+// that hold kWorkspaceEmpty when unused.  The kernels leave it in that state.
+struct Workspace {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+constexpr size_t kWorkspaceBytes = size_t(2) << 20;
+constexpr size_t kWorkspaceCounterBytes = size_t(1) << 20;
+// a signalling-NaN pattern: no arithmetic result has it (results of
+// operations are quiet NaNs)
+constexpr uint32_t kWorkspaceEmpty = 0x7fbadbadu;
+
 // silu(g) * u exactly as src/runtime.rs:4296-4298 / metal.rs:585 write it.
 __host__ __device__ __forceinline__ float silu_times(float g, float u) {
   return g / (1.0f + expf(-g)) * u;

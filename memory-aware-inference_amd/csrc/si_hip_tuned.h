@@ -6,20 +6,25 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "si_hip_internal.h"
+
 namespace sihip {
 
 bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float* y, uint32_t rows,
-                         uint32_t cols, uint32_t batch, hipStream_t s, hipError_t* err);
+                         uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
+                         hipError_t* err);
 // Q4_K, one vector, K <= 8192, on the matrix cores.
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
-                            uint32_t cols, hipStream_t s, hipError_t* err);
+                            uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
 // Q6_K, one vector, on the matrix cores.
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
-                            uint32_t cols, hipStream_t s, hipError_t* err);
+                            uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
 // Fused SwiGLU gate/up (both Q4_K) on the matrix cores: h = silu(gate.x) * (up.x).
 bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
-                             uint32_t rows, uint32_t cols, hipStream_t s, hipError_t* err);
+                             uint32_t rows, uint32_t cols, const Workspace& ws, hipStream_t s,
+                             hipError_t* err);
 bool launch_fused_gate_up_tuned(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
-                                uint32_t rows, uint32_t cols, hipStream_t s, hipError_t* err);
+                                uint32_t rows, uint32_t cols, const Workspace& ws, hipStream_t s,
+                                hipError_t* err);
 
 }  // namespace sihip

@@ -161,6 +161,23 @@ def test_matvec_nonfinite_and_huge_activations(ctx, t):
         assert np.array_equal(_category(y), _category(y32)), f"x[{k}] = {v}"
 
 
+def test_split_tiles_across_grid_sizes(hip_ctx):
+    """Launches with large, then small grids, with and without split tiles:
+    tiles whose partials span several workgroups are combined through per-tile
+    counters and entries that every launch must find reset, whatever the
+    previous launch's grid was."""
+    cases = [(12, 17408, 5120), (14, 160, 17408), (12, 1600, 17408), (14, 48, 17408),
+             (12, 160, 17408), (14, 300, 5120), (12, 48, 17408), (12, 1024, 5120),
+             (14, 5120, 17408), (12, 40, 2304), (14, 16, 512)]
+    for t, rows, cols in cases * 2:
+        w = si_hip.synth_matrix(t, seed=rows + cols + t, rows=rows, cols=cols, threads=8)
+        x = si_hip.synth_normal(rows ^ cols, cols)
+        _, y64, ab = O.matvec(t, w, rows, cols, x, threads=8)
+        W = hip_ctx.upload_quant_weight_private(w, t)
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        assert_dot_close(y, y64, ab, what=f"type {t} {rows}x{cols}")
+
+
 def test_matvec_cancellation_heavy_blocks(ctx):
     # blocks where d*sc*q and dmin*m nearly cancel: all nibbles equal, m chosen
     # so that w is small against its two terms
@@ -258,7 +275,7 @@ def test_reference_fused_gate_up_test(ctx):
     assert np.all(np.abs(got - expected) < 1e-4)
 
 
-@pytest.mark.parametrize("rows,cols", [(64, 1024), (1000, 5120), (17408, 5120)])
+@pytest.mark.parametrize("rows,cols", [(64, 1024), (1000, 5120), (160, 17408), (17408, 5120)])
 def test_fused_gate_up_within_tolerance(ctx, rows, cols):
     log(f"gate/up {rows}x{cols}")
     gw = si_hip.synth_matrix(12, seed=501, rows=rows, cols=cols, threads=8)
