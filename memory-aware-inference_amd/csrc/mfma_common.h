@@ -162,7 +162,8 @@ __device__ __forceinline__ void copy_x(uint8_t* smem, uint32_t img, const float*
 // waited for the copies.  CHUNK_SLOT(c) gives the byte offset, inside the
 // block's 1 KB, of the A row 4 p (digit 0) of MFMA t that holds chunk c
 // (elements 16 c .. 16 c + 15): 256 t + 64 p.  A block whose activations are
-// not all finite and below 2^100 gets exponent kBadBlock.
+// not all finite and below 2^100, or that has a non-zero 16-element chunk more
+// than 2^13 below its largest activation, gets exponent kBadBlock.
 template <int WAVES, typename ChunkSlot>
 __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, uint32_t nb,
                                              uint32_t wave, uint32_t grp, uint32_t n,
@@ -190,11 +191,16 @@ __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, ui
       bad |= !(av < 0x1p100f);
       xsum += xv[k];
     }
+    const float cmax = amax;  // this lane's 16-element chunk
     amax = fmaxf(amax, dpp<kRowShr1>(amax));
     amax = fmaxf(amax, dpp<kRowShr2>(amax));
     amax = fmaxf(amax, dpp<kRowShr4>(amax));
     amax = fmaxf(amax, dpp<kRowShr8>(amax));
     amax = dpp<kRowBcast15>(amax);
+    // A chunk far below the block's largest activation would keep too few
+    // significant bits in the block's fixed point; such blocks (outliers
+    // next to small activations) take the exact path too.
+    bad |= cmax > 0.0f && cmax < amax * 0x1p-13f;
     const int e = __builtin_amdgcn_frexp_expf(amax);  // amax < 2^e; 0 for amax == 0
     uint32_t u[16];
 #pragma unroll

@@ -161,6 +161,35 @@ def test_matvec_nonfinite_and_huge_activations(ctx, t):
         assert np.array_equal(_category(y), _category(y32)), f"x[{k}] = {v}"
 
 
+def test_matvec_outlier_activations_on_zero_weights(ctx):
+    """Massive activations whose Q6_K weights are exactly zero (q = 32): the
+    dot is then carried by the ordinary activations alone, which must keep
+    full precision next to the outlier (quant.rs:155-169 decoding)."""
+    rows, cols = 64, 2048
+    w = bytearray(si_hip.synth_matrix(14, seed=1950, rows=rows, cols=cols))
+    nb = cols // 256
+    outliers = [3, 300, 777, 1100, 2047]
+    for r in range(rows):
+        for k in outliers:
+            blk, e = divmod(k, 256)
+            h, rem = divmod(e, 128)
+            t, l = divmod(rem, 32)
+            base = (r * nb + blk) * 210
+            qi = base + 64 * h + l + 32 * (t & 1)
+            w[qi] &= 0xF0 if (t >> 1) == 0 else 0x0F           # nibble 0
+            hi = base + 128 + 32 * h + l
+            w[hi] = (w[hi] & ~(3 << (2 * t)) & 0xFF) | (2 << (2 * t))  # high bits 2 -> q = 32
+    w = bytes(w)
+    dq = O.dequantize(14, w, rows * cols).reshape(rows, cols)
+    assert np.all(dq[:, outliers] == 0.0)
+    x = si_hip.synth_normal(1951, cols)
+    x[outliers] = np.float32(1e6)
+    _, y64, ab = O.matvec(14, w, rows, cols, x)
+    W = ctx.upload_quant_weight_private(w, 14)
+    y = ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+    assert_dot_close(y, y64, ab, what="outliers on zero weights")
+
+
 def test_split_tiles_across_grid_sizes(hip_ctx):
     """Launches with large, then small grids, with and without split tiles:
     tiles whose partials span several workgroups are combined through per-tile
