@@ -59,8 +59,8 @@ constexpr uint32_t kStageBytes = 16u * 4u * kQ4Bytes;  // 9216: 16 rows x 4 bloc
 
 // LDS map (make_layout): 4-block stages, 32 bytes of unit sums per block.
 __host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
-                                            uint32_t slots, uint32_t mats) {
-  return make_layout(kStageBytes, 4u, 32u, waves, depth, nb, slots, mats);
+                                            uint32_t slots, uint32_t mats, uint32_t ntok = 1u) {
+  return make_layout(kStageBytes, 4u, 32u, waves, depth, nb, slots, mats, ntok);
 }
 
 // The lane's header and two qs pieces of the four blocks of a stage buffer:
@@ -154,34 +154,60 @@ __device__ __forceinline__ float exact_dot16(const u32x4& q, int shift, float d1
   return acc;
 }
 
-// Fast-path dot of one block for one lane: row n's units 2 grp, 2 grp + 1.
-__device__ __forceinline__ float block_terms(const u32x4& h, const u32x4& qa, const u32x4& qb,
-                                             const i32x4& a0, const i32x4& a1, const i32x4& a2,
-                                             const i32x4& a3, u32x2 xs, int eb, bool hi_units,
-                                             int bsh) {
+// One block of one lane's row, decoded once for every activation vector:
+// B operands (low/high nibbles of its two qs pieces), the 6-bit scales and
+// mins of units 2 grp, 2 grp + 1, d and dmin.
+struct BlockQ4 {
+  i32x4 la, ha, lb, hb;
+  int sce, sco;
+  float mne, mno, d, dmin;
+};
+__device__ __forceinline__ BlockQ4 decode_q4(const u32x4& h, const u32x4& qa, const u32x4& qb,
+                                             bool hi_units, int bsh) {
+  BlockQ4 w;
   const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
   const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
   const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
   const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
   const uint32_t scw = hi_units ? sc47 : sc03;
   const uint32_t mnw = hi_units ? mn47 : mn03;
-  const int sce = (int)((scw >> bsh) & 0xffu), sco = (int)((scw >> (bsh + 8)) & 0xffu);
-  const uint32_t mne = (mnw >> bsh) & 0xffu, mno = (mnw >> (bsh + 8)) & 0xffu;
+  w.sce = (int)((scw >> bsh) & 0xffu);
+  w.sco = (int)((scw >> (bsh + 8)) & 0xffu);
+  w.mne = (float)((mnw >> bsh) & 0xffu);
+  w.mno = (float)((mnw >> (bsh + 8)) & 0xffu);
+  w.la = low_nibbles(qa);
+  w.ha = high_nibbles(qa);
+  w.lb = low_nibbles(qb);
+  w.hb = high_nibbles(qb);
+  w.d = half_bits_to_float(h[0] & 0xffffu);
+  w.dmin = half_bits_to_float(h[0] >> 16);
+  return w;
+}
+
+// Fast-path dot of one decoded block with one activation vector's images.
+__device__ __forceinline__ float block_dot(const BlockQ4& w, const i32x4& a0, const i32x4& a1,
+                                           const i32x4& a2, const i32x4& a3, u32x2 xs, int eb) {
   const i32x4 zero = {0, 0, 0, 0};
-  i32x4 ce = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, low_nibbles(qa), zero, 0, 0, 0);
-  i32x4 co = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, high_nibbles(qa), zero, 0, 0, 0);
-  ce = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, low_nibbles(qb), ce, 0, 0, 0);
-  co = __builtin_amdgcn_mfma_i32_16x16x64_i8(a3, high_nibbles(qb), co, 0, 0, 0);
-  const int t0 = __mul24(sce, ce[0]) + __mul24(sco, co[0]);
-  const int t1 = __mul24(sce, ce[1]) + __mul24(sco, co[1]);
-  const int t2 = __mul24(sce, ce[2]) + __mul24(sco, co[2]);
-  const int t3 = __mul24(sce, ce[3]) + __mul24(sco, co[3]);
+  i32x4 ce = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w.la, zero, 0, 0, 0);
+  i32x4 co = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, w.ha, zero, 0, 0, 0);
+  ce = __builtin_amdgcn_mfma_i32_16x16x64_i8(a1, w.lb, ce, 0, 0, 0);
+  co = __builtin_amdgcn_mfma_i32_16x16x64_i8(a3, w.hb, co, 0, 0, 0);
+  const int t0 = __mul24(w.sce, ce[0]) + __mul24(w.sco, co[0]);
+  const int t1 = __mul24(w.sce, ce[1]) + __mul24(w.sco, co[1]);
+  const int t2 = __mul24(w.sce, ce[2]) + __mul24(w.sco, co[2]);
+  const int t3 = __mul24(w.sce, ce[3]) + __mul24(w.sco, co[3]);
   const float tc =
       fmaf(fmaf(fmaf((float)t3, 256.0f, (float)t2), 256.0f, (float)t1), 256.0f, (float)t0);
-  const float d = half_bits_to_float(h[0] & 0xffffu);
-  const float dmin = half_bits_to_float(h[0] >> 16);
-  const float um = fmaf((float)mne, __uint_as_float(xs[0]), (float)mno * __uint_as_float(xs[1]));
-  return __builtin_amdgcn_ldexpf(d * tc, eb) - dmin * um;
+  const float um = fmaf(w.mne, __uint_as_float(xs[0]), w.mno * __uint_as_float(xs[1]));
+  return __builtin_amdgcn_ldexpf(w.d * tc, eb) - w.dmin * um;
+}
+
+// Fast-path dot of one block for one lane: row n's units 2 grp, 2 grp + 1.
+__device__ __forceinline__ float block_terms(const u32x4& h, const u32x4& qa, const u32x4& qb,
+                                             const i32x4& a0, const i32x4& a1, const i32x4& a2,
+                                             const i32x4& a3, u32x2 xs, int eb, bool hi_units,
+                                             int bsh) {
+  return block_dot(decode_q4(h, qa, qb, hi_units, bsh), a0, a1, a2, a3, xs, eb);
 }
 
 // Exact per-weight path of one block (activations not finite or >= 2^100).
@@ -205,7 +231,7 @@ __device__ __forceinline__ float block_exact(const u32x4& h, const u32x4& qa, co
   return exact_dot16(qb, 4, d1o, m1o, xs + 48, acc);
 }
 
-template <int WAVES, int DEPTH, int MATS>
+template <int WAVES, int DEPTH, int MATS, int NTOK>
 __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const uint8_t* __restrict__ w2,
                                                               const float* __restrict__ x,
@@ -213,7 +239,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
                                                               uint32_t nb, uint32_t slots,
                                                               void* __restrict__ wsp, uint32_t split) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  const Layout L = layout(WAVES, DEPTH, nb, slots, MATS);
+  static_assert(NTOK == 1 || MATS == 1, "several activation vectors: one matrix");
+  const Layout L = layout(WAVES, DEPTH, nb, slots, MATS, NTOK);
   const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
@@ -225,8 +252,12 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
   uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
 
-  // 1. x into the image area, natural order (block b at img + 1024 b)
-  copy_x<WAVES>(smem, L.img, x, nb, wave, lane);
+  // 1. x into the image area, natural order (block b at img + 1024 b; vector
+  //    t of NTOK at img + t img_stride)
+#pragma unroll
+  for (int t = 0; t < NTOK; ++t)
+    copy_x<WAVES>(smem, L.img + t * L.img_stride, x + (size_t)t * nb * kBlockElems, nb, wave,
+                  lane);
 
   // 2. this wave's pairs k = wave, wave + WAVES, ... of the workgroup's pairs
   //    (pair_at: a tile and its partial r, r being stage r % nstages of
@@ -270,8 +301,10 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   else
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   // chunk c = 4 p + t: units 2p, 2p + 1 of lane group p, MFMA t
-  build_images<WAVES>(sbase, L, nb, wave, grp, n,
-                      [](uint32_t c) { return 256u * (c & 3u) + 64u * (c >> 2); });
+#pragma unroll
+  for (int t = 0; t < NTOK; ++t)
+    build_images<WAVES>(sbase, L, nb, wave, grp, n,
+                        [](uint32_t c) { return 256u * (c & 3u) + 64u * (c >> 2); }, t);
   lds_wait();
   __builtin_amdgcn_s_barrier();
 
@@ -297,11 +330,49 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     u32x4 v[12];
     lds_read_weights(hb0 + buf, qb0 + buf, v);
     if (j + DEPTH < my_pairs) issue(j + DEPTH);  // the buffer just read is free again
+    const uint32_t nlive = min(4u, nb - 4u * s);
+    if constexpr (NTOK > 1) {
+      // the stage's weights are decoded once and meet every vector in turn
+      BlockQ4 bw[4];
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        bw[b] = decode_q4(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh);
+      float rs[NTOK];
+#pragma unroll
+      for (int t = 0; t < NTOK; ++t) {
+        lds_read_images(sbase + L.img + t * L.img_stride + 4096u * s + 16u * n, kActiveLanes, A);
+        u32x2 xs[4];
+        i32x4 ex;
+        lds_read_sums(sbase + L.xsum + t * L.xsum_stride + 128u * s + 8u * grp,
+                      sbase + L.expo + t * L.expo_stride + 16u * s, xs, ex);
+        float part[4];
+        bool bad_any = false;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+          const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
+          const bool use = (uint32_t)b < nlive;
+          bad_any |= use && eb == kBadBlock;
+          const float c = block_dot(bw[b], A[4 * b], A[4 * b + 1], A[4 * b + 2], A[4 * b + 3],
+                                    xs[b], eb);
+          part[b] = (use && eb != kBadBlock) ? c : 0.0f;
+        }
+        if (bad_any) {
+#pragma unroll
+          for (int b = 0; b < 4; ++b)
+            if ((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock)
+              part[b] = block_exact(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh,
+                                    x + (size_t)t * nb * kBlockElems + 256u * (4u * s + b) +
+                                        64u * grp);
+        }
+        rs[t] = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
+      }
+      hand_off_tokens<NTOK>(sbase, L, slots, pr, tstages, rs, lane, rows, y);
+      continue;
+    }
     lds_read_images(sbase + L.img + 4096u * s + 16u * n, kActiveLanes, A);
     u32x2 xs[4];
     i32x4 ex;
     lds_read_sums(sbase + L.xsum + 128u * s + 8u * grp, sbase + L.expo + 16u * s, xs, ex);
-    const uint32_t nlive = min(4u, nb - 4u * s);
     float part[4];
     bool bad_any = false;
 #pragma unroll
@@ -327,27 +398,37 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   }
 }
 
-template <int W, int D, int M>
+template <int W, int D, int M, int NT = 1>
 bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, uint32_t rows,
                uint32_t nb, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t tstages = (nb + 3u) / 4u * M;
-  const LaunchShape ls = launch_shape(ntiles, tstages, W, ws.bytes, M);
+  // several vectors: whole tiles only
+  const LaunchShape ls = launch_shape(ntiles, tstages, W, NT == 1 ? ws.bytes : 0u, M);
   const uint32_t grid = ls.groups;
   const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, tstages);
-  const uint32_t lds = layout(W, D, nb, slots, M).total;
+  const uint32_t lds = layout(W, D, nb, slots, M, NT).total;
   if (lds > kLdsBytes) return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M>),
+      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M>), dim3(grid), dim3(W * 64), lds, s, w, w2, x, y,
-                     rows, nb, slots, ws.ptr, ls.split ? 1u : 0u);
+  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT>), dim3(grid), dim3(W * 64), lds, s, w, w2, x,
+                     y, rows, nb, slots, ws.ptr, ls.split ? 1u : 0u);
   *err = hipGetLastError();
   return true;
+}
+
+// NT activation vectors (batch-major x and y) in one pass over the weights.
+template <int NT>
+bool launch_tokens(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+                   const Workspace& ws, hipStream_t s, hipError_t* err) {
+  return launch_wd<8, 1, 1, NT>(w, nullptr, x, y, rows, nb, ws, s, err) ||
+         launch_wd<6, 1, 1, NT>(w, nullptr, x, y, rows, nb, ws, s, err) ||
+         launch_wd<4, 1, 1, NT>(w, nullptr, x, y, rows, nb, ws, s, err);
 }
 
 bool shape_ok(uint32_t rows, uint32_t cols, uint32_t mats) {
@@ -373,6 +454,35 @@ bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
   return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err) ||
          launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err) ||
          launch_wd<4, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
+}
+
+bool launch_q4k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
+                            hipError_t* err) {
+  if (batch < 2 || !shape_ok(rows, cols, 1u)) return false;
+  const uint32_t nb = cols / kBlockElems;
+  // up to four vectors per pass over the weights (their activation images
+  // share the LDS with the stage buffers)
+  for (uint32_t b = 0; b < batch;) {
+    const uint32_t nt = min(4u, batch - b);
+    const float* xb = x + (size_t)b * cols;
+    float* yb = y + (size_t)b * rows;
+    bool ok;
+    switch (nt) {
+      case 4: ok = launch_tokens<4>(w, xb, yb, rows, nb, ws, s, err); break;
+      case 3: ok = launch_tokens<3>(w, xb, yb, rows, nb, ws, s, err); break;
+      case 2: ok = launch_tokens<2>(w, xb, yb, rows, nb, ws, s, err); break;
+      default: ok = launch_q4k_matvec_mfma(w, xb, yb, rows, cols, ws, s, err); break;
+    }
+    if (!ok) {
+      if (b == 0) return false;
+      *err = hipErrorInvalidValue;
+      return true;
+    }
+    if (*err != hipSuccess) return true;
+    b += nt;
+  }
+  return true;
 }
 
 bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float* x, float* h,

@@ -302,6 +302,10 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
   if (batch == 0) return false;
   static const int mode = env_int("SI_HIP_Q4K_MODE", 0);
   const bool q4_mfma = type == kTypeQ4K && mode == 0;
+  static const int tokens_per_pass = env_int("SI_HIP_Q4K_BATCH_PASS", 1);
+  if (q4_mfma && batch > 1 && tokens_per_pass &&
+      launch_q4k_matmul_mfma(w, x, y, rows, cols, batch, ws, s, err))
+    return true;
   if (type == kTypeQ6K || (q4_mfma && batch > 1)) {
     // several candidates (batch-major x and y, metal.rs:1104-1126): one
     // matrix-core matvec per candidate, each bit-identical to its M = 1 call

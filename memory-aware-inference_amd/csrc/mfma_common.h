@@ -42,26 +42,31 @@ constexpr int kBadBlock = 0x40000000;  // exponent slot of a block taking the ex
 
 constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
 
-// LDS map of one workgroup (byte offsets): per-wave stage buffers, digit
-// images of all blocks (plus 4 KB that dead blocks of a short last stage
-// may read), unit sums [block][unit] (formats that need them), exponents
-// [block], then a ring of `slots` tile slots: [slot][partial][16 rows] f32
-// partials, and per slot a completion count and the tile index it currently
-// belongs to.
+// LDS map of one workgroup (byte offsets): per-wave stage buffers; for each
+// of ntok activation vectors the digit images of all its blocks (a further
+// 4 KB after the last one, which dead blocks of a short last stage may
+// read), its unit sums [block][unit] (formats that need them) and its
+// exponents [block]; then a ring of `slots` tile slots: [slot][partial]
+// [token][16 rows] f32 partials, and per slot a completion count and the tile
+// index it currently belongs to.
 struct Layout {
   uint32_t img, xsum, expo, part, cnt, owner, total;
+  uint32_t img_stride, xsum_stride, expo_stride;  // per activation vector
 };
 __host__ __device__ constexpr Layout make_layout(uint32_t stage_bytes, uint32_t stage_blocks,
                                                  uint32_t xsum_per_block, uint32_t waves,
                                                  uint32_t depth, uint32_t nb, uint32_t slots,
-                                                 uint32_t mats) {
+                                                 uint32_t mats, uint32_t ntok = 1u) {
   Layout l{};
   const uint32_t partials = (nb + stage_blocks - 1u) / stage_blocks * mats;  // per tile
+  l.img_stride = nb * 1024u;
+  l.xsum_stride = nb * xsum_per_block;
+  l.expo_stride = (nb * 4u + 15u) & ~15u;
   l.img = waves * depth * stage_bytes;
-  l.xsum = l.img + nb * 1024u + 4096u;
-  l.expo = l.xsum + (xsum_per_block ? nb * xsum_per_block + 128u : 0u);
-  l.part = l.expo + ((nb * 4u + 15u) & ~15u) + 16u;
-  l.cnt = l.part + slots * partials * 64u;
+  l.xsum = l.img + ntok * l.img_stride + 4096u;
+  l.expo = l.xsum + (xsum_per_block ? ntok * l.xsum_stride + 128u : 0u);
+  l.part = l.expo + ntok * l.expo_stride + 16u;
+  l.cnt = l.part + slots * partials * 64u * ntok;
   l.owner = l.cnt + slots * 4u;
   l.total = l.owner + slots * 4u;
   return l;
@@ -157,8 +162,9 @@ __device__ __forceinline__ void copy_x(uint8_t* smem, uint32_t img, const float*
   }
 }
 
-// Turns the copied blocks into digit images in place, plus exponents and,
-// when L.xsum < L.expo, the f32 sums of each 32-element unit.  The caller has
+// Turns the copied blocks of activation vector `tok` into digit images in
+// place, plus exponents and, when the layout keeps them, the f32 sums of each
+// 32-element unit.  The caller has
 // waited for the copies.  CHUNK_SLOT(c) gives the byte offset, inside the
 // block's 1 KB, of the A row 4 p (digit 0) of MFMA t that holds chunk c
 // (elements 16 c .. 16 c + 15): 256 t + 64 p.  A block whose activations are
@@ -167,16 +173,19 @@ __device__ __forceinline__ void copy_x(uint8_t* smem, uint32_t img, const float*
 template <int WAVES, typename ChunkSlot>
 __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, uint32_t nb,
                                              uint32_t wave, uint32_t grp, uint32_t n,
-                                             ChunkSlot chunk_slot) {
+                                             ChunkSlot chunk_slot, uint32_t tok = 0u) {
   const uint32_t npass = (nb + 4u * WAVES - 1u) / (4u * WAVES);
-  const bool want_sums = L.xsum < L.expo;
+  const bool want_sums = L.xsum_stride != 0u;
+  const uint32_t img = L.img + tok * L.img_stride;
+  const uint32_t xsb = L.xsum + tok * L.xsum_stride;
+  const uint32_t exb = L.expo + tok * L.expo_stride;
   for (uint32_t j = 0; j < npass; ++j) {
     if (4u * (wave + WAVES * j) >= nb) break;
     // lane (grp, n): elements 16n..16n+15 of block pb
     const uint32_t pb = 4u * (wave + WAVES * j) + grp;
     const uint32_t pbc = pb < nb ? pb : nb - 1u;  // lanes past K redo the last block, unstored
     u32x4 xq[4];
-    lds_read4<16>(sbase + L.img + 1024u * pbc + 64u * n, xq);
+    lds_read4<16>(sbase + img + 1024u * pbc + 64u * n, xq);
     float xv[16];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -211,7 +220,7 @@ __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, ui
     for (int k = 0; k < 4; ++k)
       transpose_digits(u[4 * k], u[4 * k + 1], u[4 * k + 2], u[4 * k + 3], dg[k]);
     // all lanes of the group have read the block before any lane writes it
-    const uint32_t ib = sbase + L.img + 1024u * pbc + chunk_slot(n);
+    const uint32_t ib = sbase + img + 1024u * pbc + chunk_slot(n);
     const bool store = pb < nb;
     if (store) {
 #pragma unroll
@@ -221,11 +230,11 @@ __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, ui
     if (want_sums) {
       xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit n / 2
       if (store && (n & 1u))
-        lds_write_b32(sbase + L.xsum + 32u * pb + 4u * (n >> 1), __float_as_uint(xsum));
+        lds_write_b32(sbase + xsb + 32u * pb + 4u * (n >> 1), __float_as_uint(xsum));
     }
     const bool bad_blk = (__builtin_amdgcn_ballot_w64(bad) >> (16u * grp)) & 0xffffull;
     if (store && n == 0u)
-      lds_write_b32(sbase + L.expo + 4u * pb, (uint32_t)(bad_blk ? kBadBlock : e - kFixBits));
+      lds_write_b32(sbase + exb + 4u * pb, (uint32_t)(bad_blk ? kBadBlock : e - kFixBits));
   }
 }
 
@@ -494,6 +503,43 @@ inline LaunchShape launch_shape(uint32_t ntiles, uint32_t tparts, uint32_t waves
   ls.tiles_per_group = ls.split ? q + (uint32_t)(((lpairs + g1 - 1u) / g1 + tparts - 1u) / tparts) + 1u
                                 : (ntiles + g0 - 1u) / g0;
   return ls;
+}
+
+// hand_off for NTOK activation vectors at once, whole tiles only: partial r
+// of the tile holds 16 rows x NTOK sums; the finishing wave stores
+// y[tok * rows + row] for every token.
+template <int NTOK>
+__device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L, uint32_t slots,
+                                                const Pair& pr, uint32_t tparts,
+                                                const float (&rowsum)[NTOK], uint32_t lane,
+                                                uint32_t rows, float* __restrict__ y) {
+  const uint32_t grp = lane >> 4, n = lane & 15u;
+  const uint32_t slot = pr.lt % slots;
+  for (uint32_t spin = 0;
+       lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
+    __builtin_amdgcn_s_sleep(1);
+  const uint32_t base = sbase + L.part + 64u * NTOK * (slot * tparts + pr.r) + 4u * n;
+  if (grp == 0u) {
+#pragma unroll
+    for (int t = 0; t < NTOK; ++t) lds_write_b32(base + 64u * t, __float_as_uint(rowsum[t]));
+  }
+  uint32_t old = 0u;
+  if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);
+  const uint32_t done = __builtin_amdgcn_readlane(old, 0);
+  if (done != tparts - 1u) return;
+  // lane group g stores tokens g, g + 4, ...
+  const uint32_t row = pr.tile * 16u + n;
+  for (uint32_t t = grp; t < (uint32_t)NTOK; t += 4u) {
+    float sum = 0.0f;
+    for (uint32_t st = 0; st < tparts; ++st)
+      sum += __uint_as_float(
+          lds_read_b32(sbase + L.part + 64u * NTOK * (slot * tparts + st) + 64u * t + 4u * n));
+    if (row < rows) y[(size_t)t * rows + row] = sum;
+  }
+  if (lane == 0u) {
+    lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
+    lds_write_b32(sbase + L.owner + 4u * slot, pr.lt + slots);
+  }
 }
 
 // Slots of the ring: enough for every wave to be a few tiles ahead, within

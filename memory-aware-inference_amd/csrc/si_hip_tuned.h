@@ -16,6 +16,11 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
 // Q4_K, one vector, K <= 8192, on the matrix cores.
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
+// Q4_K, batch >= 2 vectors (batch-major x and y): up to four per pass over the
+// weights, which are decoded once per pass.
+bool launch_q4k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
+                            hipError_t* err);
 // Q6_K, one vector, on the matrix cores.
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);

@@ -388,6 +388,22 @@ def test_matmul_many(ctx, t, batch):
         assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
 
 
+def test_matmul_many_baseline_shape(hip_ctx):
+    """M = 6 candidates on the 17408 x 5120 Q4_K matrix: one pass over the
+    weights for four vectors and one for two; each candidate matches its own
+    reference and the batch is deterministic."""
+    rows, cols, batch = 17408, 5120, 6
+    w = si_hip.synth_matrix(12, seed=2026, rows=rows, cols=cols, threads=8)
+    X = si_hip.synth_normal(2027, batch * cols).reshape(batch, cols)
+    W = hip_ctx.upload_quant_weight_private(w, 12)
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    again = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(batch):
+        _, y64, ab = O.matvec(12, w, rows, cols, X[b], threads=8)
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+        assert np.array_equal(outs[b], again[b])
+
+
 def test_matmul_many_bytes_matches_weight(hip_ctx):
     rows, cols, batch = 96, 1024, 3
     w = si_hip.synth_matrix(13, seed=9, rows=rows, cols=cols)
