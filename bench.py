@@ -42,7 +42,7 @@ def log(msg: str) -> None:
 
 
 def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: int,
-                copies: int = NCOPIES, seed: int = 17) -> dict:
+                copies: int = NCOPIES, seed: int = 17, detail: bool = False) -> dict:
     nbytes = rows * (cols // 256) * si_hip.BLOCK_BYTES[ggml_type]
     weights = []
     for c in range(copies):
@@ -69,15 +69,55 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
     ctx.event_record(1)
     ms = ctx.event_elapsed_ms(0, 1)
     ctx.synchronize()
+    extra = {}
+    if detail:
+        extra = call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, steps)
     ctx.device_free(d_x)
     ctx.device_free(d_y)
     for w in weights:
         w.free()
     us = ms * 1000.0 / steps
     gbs = nbytes / (us * 1e-6) / 1e9
-    return {"rows": rows, "cols": cols, "ggml_type": ggml_type, "bytes_per_call": nbytes,
-            "us_per_call": round(us, 3), "gb_per_s": round(gbs, 1),
-            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    out = {"rows": rows, "cols": cols, "ggml_type": ggml_type, "bytes_per_call": nbytes,
+           "us_per_call": round(us, 3), "gb_per_s": round(gbs, 1),
+           "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+    out.update(extra)
+    return out
+
+
+def call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, samples: int) -> dict:
+    """Per-call device time of isolated calls (events around each call, the
+    stream drained in between: p10/p50/p90), and host wall time per call of
+    the synchronous host-pointer API (x copied in, y copied out, one wait)."""
+    import ctypes as C
+    per = []
+    copies = len(weights)
+    for i in range(samples):
+        one = (C.c_void_p * 1)(harr[i % copies])
+        ctx.event_record(2)
+        rc = lib.si_hip_quant_matvec_device_repeat(ctx.handle, one, 1, rows, cols,
+                                                   C.c_void_p(d_x), C.c_void_p(d_y), 1)
+        if rc:
+            raise si_hip.HipError(rc, si_hip.last_error())
+        ctx.event_record(3)
+        ctx.synchronize()
+        per.append(ctx.event_elapsed_ms(2, 3) * 1000.0)
+    per = np.array(per)
+    n_wall = max(20, samples // 2)
+    for i in range(5):
+        ctx.gguf_quant_matvec_weight(weights[i % copies], rows, cols, x)
+    t0 = time.perf_counter()
+    for i in range(n_wall):
+        ctx.gguf_quant_matvec_weight(weights[i % copies], rows, cols, x)
+    wall = (time.perf_counter() - t0) / n_wall * 1e6
+    return {"isolated_call_us": {"p10": round(float(np.percentile(per, 10)), 3),
+                                 "p50": round(float(np.percentile(per, 50)), 3),
+                                 "p90": round(float(np.percentile(per, 90)), 3),
+                                 "samples": samples},
+            "host_wall_us_per_call": round(wall, 2),
+            "host_wall_note": "synchronous C-ABI call with host x and y (H2D copy of x, "
+                              "kernel, D2H copy of y, stream wait), averaged over "
+                              f"{n_wall} calls"}
 
 
 def _timed(ctx, fn, steps: int, warmup: int) -> float:
@@ -101,8 +141,12 @@ def _rate(nbytes: int, ms: float) -> dict:
             "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def run_configs(ctx, steps: int, warmup: int) -> dict:
-    """BASELINE configs 2-5 on the HBM-resident device path (synthetic data)."""
+CONFIG_NAMES = ("mlp", "q5k", "head", "embedding", "many", "aggregate")
+
+
+def run_configs(ctx, steps: int, warmup: int, only=CONFIG_NAMES) -> dict:
+    """BASELINE configs 3-5 on the HBM-resident device path (synthetic data);
+    `only` picks some of CONFIG_NAMES."""
     import ctypes as C
     lib = si_hip.lib()
     Q4, Q5, Q6 = si_hip.GGML_TYPE_Q4_K, si_hip.GGML_TYPE_Q5_K, si_hip.GGML_TYPE_Q6_K
@@ -123,9 +167,24 @@ def run_configs(ctx, steps: int, warmup: int) -> dict:
     def bpc(t, rows, cols):
         return rows * (cols // 256) * si_hip.BLOCK_BYTES[t]
 
+    N, K = 17408, 5120
+    if "mlp" in only:
+        res.update(_config_mlp(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K))
+    if {"q5k", "head", "embedding"} & set(only):
+        res.update(_config_mixed(ctx, lib, upload, dev_f32, bpc, steps, warmup, K, only))
+    if "many" in only:
+        res.update(_config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K))
+    if "aggregate" in only:
+        res.update(_config_aggregate(ctx, lib, dev_f32, bpc))
+    return res
+
+
+def _config_mlp(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
+    import ctypes as C
+    Q4, Q6 = si_hip.GGML_TYPE_Q4_K, si_hip.GGML_TYPE_Q6_K
+    res = {}
     # config 3: fused SwiGLU (gate/up Q4_K 17408x5120, down Q6_K 5120x17408), 3 copies
     log("configs: fused SwiGLU MLP")
-    N, K = 17408, 5120
     mlp = [(upload(Q4, 300 + c, N, K), upload(Q4, 310 + c, N, K), upload(Q6, 320 + c, K, N))
            for c in range(3)]
     x = dev_f32(si_hip.synth_normal(301, K) * np.float32(0.1))
@@ -143,38 +202,54 @@ def run_configs(ctx, steps: int, warmup: int) -> dict:
         g.free(); u.free(); d.free()
     for p in (x, h, y):
         ctx.device_free(p)
+    return res
 
+
+def _config_mixed(ctx, lib, upload, dev_f32, bpc, steps, warmup, K, only) -> dict:
+    import ctypes as C
+    Q4, Q5, Q6 = si_hip.GGML_TYPE_Q4_K, si_hip.GGML_TYPE_Q5_K, si_hip.GGML_TYPE_Q6_K
+    res = {}
     # config 4: Q5_K 5120x5120, Q6_K head 151936x5120 + argmax, Q4_K embedding of 64 ids
     log("configs: Q5_K matvec, Q6_K head + argmax, Q4_K embedding")
-    q5 = [upload(Q5, 400 + c, K, K) for c in range(8)]
     x = dev_f32(si_hip.synth_normal(401, K))
     y = ctx.device_alloc(K * 4)
-    ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_quant_matvec_device(
-        ctx.handle, q5[i % 8].handle, K, K, C.c_void_p(x), C.c_void_p(y))), steps, warmup)
-    res["q5k_matvec_5120x5120"] = _rate(bpc(Q5, K, K), ms)
-    for w in q5:
-        w.free()
+    if "q5k" in only:
+        q5 = [upload(Q5, 400 + c, K, K) for c in range(8)]
+        ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_quant_matvec_device(
+            ctx.handle, q5[i % 8].handle, K, K, C.c_void_p(x), C.c_void_p(y))), steps, warmup)
+        res["q5k_matvec_5120x5120"] = _rate(bpc(Q5, K, K), ms)
+        for w in q5:
+            w.free()
     V = 151936
-    head = upload(Q6, 410, V, K)
-    logits = ctx.device_alloc(V * 4)
-    packed = ctx.device_alloc(8)
-    ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_matvec_argmax_device(
-        ctx.handle, head.handle, V, K, C.c_void_p(x), 0, C.c_void_p(logits),
-        C.c_void_p(packed))), max(steps // 4, 10), max(warmup // 4, 2))
-    res["q6k_head_argmax_151936x5120"] = _rate(bpc(Q6, V, K), ms)
-    head.free()
-    ctx.device_free(logits); ctx.device_free(packed)
-    table = upload(Q4, 420, V, K)
-    ids = ctx.device_alloc(64 * 4)
-    ctx.to_device(ids, si_hip.synth_token_ids(421, 64, V).astype(np.uint32))
-    emb = ctx.device_alloc(64 * K * 4)
-    ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_embedding_device(
-        ctx.handle, table.handle, K, V, C.c_void_p(ids), 64, C.c_void_p(emb))), steps, warmup)
-    res["q4k_embedding_64_tokens"] = _rate(64 * bpc(Q4, 1, K), ms)
-    table.free()
-    for p in (ids, emb, x, y):
+    if "head" in only:
+        head = upload(Q6, 410, V, K)
+        logits = ctx.device_alloc(V * 4)
+        packed = ctx.device_alloc(8)
+        ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_matvec_argmax_device(
+            ctx.handle, head.handle, V, K, C.c_void_p(x), 0, C.c_void_p(logits),
+            C.c_void_p(packed))), max(steps // 4, 10), max(warmup // 4, 2))
+        res["q6k_head_argmax_151936x5120"] = _rate(bpc(Q6, V, K), ms)
+        head.free()
+        ctx.device_free(logits); ctx.device_free(packed)
+    if "embedding" in only:
+        table = upload(Q4, 420, V, K)
+        ids = ctx.device_alloc(64 * 4)
+        ctx.to_device(ids, si_hip.synth_token_ids(421, 64, V).astype(np.uint32))
+        emb = ctx.device_alloc(64 * K * 4)
+        ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_embedding_device(
+            ctx.handle, table.handle, K, V, C.c_void_p(ids), 64, C.c_void_p(emb))), steps, warmup)
+        res["q4k_embedding_64_tokens"] = _rate(64 * bpc(Q4, 1, K), ms)
+        table.free()
+        ctx.device_free(ids); ctx.device_free(emb)
+    for p in (x, y):
         ctx.device_free(p)
+    return res
 
+
+def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
+    import ctypes as C
+    Q4 = si_hip.GGML_TYPE_Q4_K
+    res = {}
     # config 5: matmul-many M in {1,2,4,8,16} on Q4_K 17408x5120, 8 copies
     log("configs: multi-token verify")
     ws = [upload(Q4, 500 + c, N, K) for c in range(8)]
@@ -191,7 +266,13 @@ def run_configs(ctx, steps: int, warmup: int) -> dict:
     for w in ws:
         w.free()
     ctx.device_free(X); ctx.device_free(Y)
+    return res
 
+
+def _config_aggregate(ctx, lib, dev_f32, bpc) -> dict:
+    import ctypes as C
+    Q4, Q6 = si_hip.GGML_TYPE_Q4_K, si_hip.GGML_TYPE_Q6_K
+    res = {}
     # config 5b: 64 synthetic 27B-class layers streamed once per token
     log("configs: 64-layer aggregate")
     layer_shapes = [(Q4, 16384, 5120), (Q4, 5120, 6144), (Q4, 17408, 5120), (Q4, 17408, 5120),
@@ -239,8 +320,9 @@ def profiled_traffic() -> int | None:
     return None
 
 
-def cpu_baseline(rows: int, cols: int, budget_s: float = 10.0) -> dict:
-    """Reference CPU path (oracle restatement of quant.rs + host dot), 1 thread."""
+def cpu_baseline(rows: int, cols: int, budget_s: float = 10.0, threads: int = 1) -> dict:
+    """Reference CPU path (oracle restatement of quant.rs + host dot) on
+    `threads` host threads (rows split between them; results identical)."""
     sys.path.insert(0, str(REPO / "tests"))
     import oracle_lib  # the checker library; only this leg of the benchmark uses it
     w = si_hip.synth_matrix(12, seed=99, rows=rows, cols=cols, threads=16)
@@ -254,7 +336,7 @@ def cpu_baseline(rows: int, cols: int, budget_s: float = 10.0) -> dict:
     calls = 0
     t0 = time.perf_counter()
     while True:
-        rc = lib.kq_matvec_ref(12, bp, w.size, rows, cols, xp, yp, None, None, 1)
+        rc = lib.kq_matvec_ref(12, bp, w.size, rows, cols, xp, yp, None, None, threads)
         assert rc == 0
         calls += 1
         if time.perf_counter() - t0 >= budget_s:
@@ -268,7 +350,7 @@ def cpu_baseline(rows: int, cols: int, budget_s: float = 10.0) -> dict:
                 break
     except OSError:
         pass
-    return {"value": round(w.size / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+    return {"value": round(w.size / dt / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "us_per_call": round(dt * 1e6, 1),
             "sample": f"{calls} full Q4_K {rows}x{cols} calls (quant.rs dequant + sequential f32 "
                       f"dot), oracle/kquant_ref.c -O2 -ffp-contract=off, {model}"}
@@ -282,9 +364,9 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time the batch-1 shape sweep")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--configs", action="store_true",
-                    help="also time BASELINE configs 3-5 (fused MLP, Q5_K, Q6_K head + argmax, "
-                         "embedding, matmul-many, 64-layer aggregate)")
+    ap.add_argument("--configs", nargs="?", const=",".join(CONFIG_NAMES), default=None,
+                    help="also time BASELINE configs 3-5: a comma list of "
+                         f"{','.join(CONFIG_NAMES)} (default: all)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time device-to-device copies of the matrix size (the yardstick "
                          "that scales HBM traffic counters)")
@@ -297,7 +379,7 @@ def main() -> int:
     ctx = si_hip.HipContext(0)
     rows, cols = 17408, 5120
     log(f"timing Q4_K {rows}x{cols}, {args.steps} steps, {NCOPIES} resident copies")
-    head = time_matvec(ctx, 12, rows, cols, args.steps, args.warmup)
+    head = time_matvec(ctx, 12, rows, cols, args.steps, args.warmup, detail=True)
     log(f"  {head['us_per_call']} us/call, {head['gb_per_s']} GB/s")
     out = {
         "metric": METRIC,
@@ -319,6 +401,9 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": head["gb_per_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": head["frac_of_peak"],
                      "traffic": profiled_traffic()},
+        "isolated_call_us": head["isolated_call_us"],
+        "host_wall_us_per_call": head["host_wall_us_per_call"],
+        "host_wall_note": head["host_wall_note"],
     }
     if args.copy_probe:
         nbytes = head["bytes_per_call"]
@@ -346,11 +431,21 @@ def main() -> int:
             sweep.append(res)
         out["sweep"] = sweep
     if args.configs:
-        out["configs"] = run_configs(ctx, args.steps, args.warmup)
+        only = tuple(c for c in args.configs.split(",") if c)
+        bad = [c for c in only if c not in CONFIG_NAMES]
+        if bad:
+            print(f"unknown config(s) {bad}; choose from {CONFIG_NAMES}", file=sys.stderr)
+            return 2
+        out["configs"] = run_configs(ctx, args.steps, args.warmup, only)
     ctx.close()
     if not args.no_cpu:
         log("timing the CPU baseline")
         out["cpu_baseline"] = cpu_baseline(rows, cols, args.cpu_seconds)
+        # all host cores the box gives this process (rows split between threads)
+        cores = min(int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1)),
+                    os.cpu_count() or 1, 64)
+        log(f"timing the CPU baseline on {cores} threads")
+        out["cpu_baseline_all_cores"] = cpu_baseline(rows, cols, args.cpu_seconds, threads=cores)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -893,12 +893,11 @@ int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_qua
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!in || !token) return fail(SI_HIP_ERR_NULL, "output head buffer is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
-  const uint32_t parts = sihip::argmax_partials((uint32_t)rows);
   rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, rows * sizeof(float));
   if (rc) return rc;
-  rc = grow(ctx, &ctx->stage_aux, &ctx->stage_aux_bytes, (parts + 1) * sizeof(uint64_t));
+  rc = grow(ctx, &ctx->stage_aux, &ctx->stage_aux_bytes, sizeof(uint64_t));
   if (rc) return rc;
   SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
               "input copy");
@@ -907,7 +906,7 @@ int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_qua
   rc = dispatch_matvec(ctx, w->ggml_type, w->data(), static_cast<const float *>(ctx->stage_in),
                        d_logits, (uint32_t)rows, (uint32_t)cols, 1);
   if (rc) return rc;
-  hipError_t e = sihip::launch_argmax(d_logits, (uint32_t)rows, rule, aux + 1, aux, ctx->stream);
+  hipError_t e = sihip::launch_argmax(d_logits, (uint32_t)rows, rule, ctx->ws, aux, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "argmax launch");
   uint64_t packed = 0;
   SIHIP_CHECK(hipMemcpyAsync(&packed, aux, sizeof packed, hipMemcpyDeviceToHost, ctx->stream), "argmax copy");
@@ -1103,13 +1102,9 @@ int si_hip_matvec_argmax_device(si_hip_context *ctx, const si_hip_quant_weight *
   if (rc) return rc;
   if (!ctx || !d_in || !d_logits || !d_result) return fail(SI_HIP_ERR_NULL, "device head argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
-  const uint32_t parts = sihip::argmax_partials((uint32_t)rows);
-  rc = grow(ctx, &ctx->stage_aux, &ctx->stage_aux_bytes, parts * sizeof(uint64_t));
-  if (rc) return rc;
   rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_logits, (uint32_t)rows, (uint32_t)cols, 1);
   if (rc) return rc;
-  hipError_t e = sihip::launch_argmax(d_logits, (uint32_t)rows, rule,
-                                      static_cast<uint64_t *>(ctx->stage_aux), d_result, ctx->stream);
+  hipError_t e = sihip::launch_argmax(d_logits, (uint32_t)rows, rule, ctx->ws, d_result, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "argmax launch");
   ctx->async_submitted.fetch_add(1);
   return ok();

@@ -356,7 +356,7 @@ constexpr size_t kCounterBytes = kWorkspaceCounterBytes;
 constexpr uint32_t kPartEmpty = kWorkspaceEmpty;
 __host__ __device__ constexpr bool split_ws_fits(size_t ws_bytes, uint32_t ngroups,
                                                  uint32_t ntiles, uint32_t mats) {
-  return (size_t)ntiles * 4u <= kCounterBytes &&
+  return (size_t)ntiles * 4u + 64u <= kCounterBytes &&  // the last words are the argmax's
          kCounterBytes + (size_t)ngroups * 2u * mats * 64u <= ws_bytes;
 }
 __host__ __device__ inline SplitWs split_ws(void* base) {

@@ -19,6 +19,10 @@ constexpr size_t kWorkspaceCounterBytes = size_t(1) << 20;
 // a signalling-NaN pattern: no arithmetic result has it (results of
 // operations are quiet NaNs)
 constexpr uint32_t kWorkspaceEmpty = 0x7fbadbadu;
+// the argmax reduction's counter (the last counter word) and its 256 u64
+// entries (the last 4 KB)
+constexpr size_t kWorkspaceArgmaxCounter = kWorkspaceCounterBytes - 4;
+constexpr size_t kWorkspaceArgmaxEntries = kWorkspaceBytes - 4096;
 
 // silu(g) * u exactly as src/runtime.rs:4296-4298 / metal.rs:585 write it.
 __host__ __device__ __forceinline__ float silu_times(float g, float u) {
@@ -61,10 +65,10 @@ hipError_t launch_fused_gate_up_generic(const uint8_t* gate, const uint8_t* up, 
 hipError_t launch_dequant(uint32_t type, const uint8_t* w, const uint32_t* row_index, float* out,
                           uint32_t out_rows, uint32_t cols, hipStream_t s);
 
-// kernels_argmax.hip: two-stage max-loc over n logits.  `partials` must hold
-// argmax_partials(n) entries; the winner lands in *result (packed candidate).
-uint32_t argmax_partials(uint32_t n);
-hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t rule, uint64_t* partials,
+// kernels_argmax.hip: max-loc over n < 2^31 logits in one launch, using the
+// context workspace's argmax area; the winner lands in *result (packed
+// candidate, 0 when there is none).
+hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t rule, const Workspace& ws,
                          uint64_t* result, hipStream_t s);
 
 }  // namespace sihip
