@@ -55,12 +55,17 @@ namespace {
 
 using namespace mfma;
 
-constexpr uint32_t kStageBytes = 16u * 4u * kQ4Bytes;  // 9216: 16 rows x 4 blocks
+// Block bytes of the two formats this kernel reads (QB = quant bits): 144
+// (Q4_K) and 176 (Q5_K), both multiples of 16.  A stage is 16 rows x 4 blocks.
+__host__ __device__ constexpr uint32_t block_bytes(int qb) { return qb == 5 ? kQ5Bytes : kQ4Bytes; }
+__host__ __device__ constexpr uint32_t block_pieces(int qb) { return block_bytes(qb) / 16u; }
+__host__ __device__ constexpr uint32_t stage_bytes(int qb) { return 64u * block_bytes(qb); }
 
 // LDS map (make_layout): 4-block stages, 32 bytes of unit sums per block.
 __host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
-                                            uint32_t slots, uint32_t mats, uint32_t ntok = 1u) {
-  return make_layout(kStageBytes, 4u, 32u, waves, depth, nb, slots, mats, ntok);
+                                            uint32_t slots, uint32_t mats, uint32_t ntok = 1u,
+                                            int qb = 4) {
+  return make_layout(stage_bytes(qb), 4u, 32u, waves, depth, nb, slots, mats, ntok);
 }
 
 // The lane's header and two qs pieces of the four blocks of a stage buffer:
@@ -202,14 +207,6 @@ __device__ __forceinline__ float block_dot(const BlockQ4& w, const i32x4& a0, co
   return __builtin_amdgcn_ldexpf(w.d * tc, eb) - w.dmin * um;
 }
 
-// Fast-path dot of one block for one lane: row n's units 2 grp, 2 grp + 1.
-__device__ __forceinline__ float block_terms(const u32x4& h, const u32x4& qa, const u32x4& qb,
-                                             const i32x4& a0, const i32x4& a1, const i32x4& a2,
-                                             const i32x4& a3, u32x2 xs, int eb, bool hi_units,
-                                             int bsh) {
-  return block_dot(decode_q4(h, qa, qb, hi_units, bsh), a0, a1, a2, a3, xs, eb);
-}
-
 // Exact per-weight path of one block (activations not finite or >= 2^100).
 __device__ __forceinline__ float block_exact(const u32x4& h, const u32x4& qa, const u32x4& qb,
                                              bool hi_units, int bsh, const float* __restrict__ xs) {
@@ -231,7 +228,128 @@ __device__ __forceinline__ float block_exact(const u32x4& h, const u32x4& qa, co
   return exact_dot16(qb, 4, d1o, m1o, xs + 48, acc);
 }
 
-template <int WAVES, int DEPTH, int MATS, int NTOK>
+// Q5_K (quant.rs:67-125): the lane's header, the two qh pieces and its two qs
+// pieces of the four blocks of a stage buffer -- block b's pieces start at
+// hb + 2816 b (header, qh at +256, +512) and qb + 2816 b (qs, +256).
+__device__ __forceinline__ void lds_read_weights5(uint32_t hb, uint32_t qb, u32x4 (&v)[20]) {
+  asm volatile(
+      "ds_read_b128 %0, %20\n"
+      "ds_read_b128 %1, %20 offset:256\n"
+      "ds_read_b128 %2, %20 offset:512\n"
+      "ds_read_b128 %3, %21\n"
+      "ds_read_b128 %4, %21 offset:256\n"
+      "ds_read_b128 %5, %20 offset:2816\n"
+      "ds_read_b128 %6, %20 offset:3072\n"
+      "ds_read_b128 %7, %20 offset:3328\n"
+      "ds_read_b128 %8, %21 offset:2816\n"
+      "ds_read_b128 %9, %21 offset:3072\n"
+      "ds_read_b128 %10, %20 offset:5632\n"
+      "ds_read_b128 %11, %20 offset:5888\n"
+      "ds_read_b128 %12, %20 offset:6144\n"
+      "ds_read_b128 %13, %21 offset:5632\n"
+      "ds_read_b128 %14, %21 offset:5888\n"
+      "ds_read_b128 %15, %20 offset:8448\n"
+      "ds_read_b128 %16, %20 offset:8704\n"
+      "ds_read_b128 %17, %20 offset:8960\n"
+      "ds_read_b128 %18, %21 offset:8448\n"
+      "ds_read_b128 %19, %21 offset:8704\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+        "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11]),
+        "=&v"(v[12]), "=&v"(v[13]), "=&v"(v[14]), "=&v"(v[15]), "=&v"(v[16]), "=&v"(v[17]),
+        "=&v"(v[18]), "=&v"(v[19])
+      : "v"(hb), "v"(qb)
+      : "memory");
+}
+
+// 5-bit weights of units 2 grp (low nibbles + qh bit 2 grp) and 2 grp + 1
+// (high nibbles + bit 2 grp + 1) from 16 qs bytes and the matching 16 qh
+// bytes.  rot_lo / rot_hi rotate that qh bit of every byte to bit 4
+// (v_alignbit of a word with itself is a rotate right).
+__device__ __forceinline__ void q5_operands(const u32x4& qs, const u32x4& qh, uint32_t rot_lo,
+                                            uint32_t rot_hi, i32x4& lo, i32x4& hi) {
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t tl = __builtin_amdgcn_alignbit(qh[k], qh[k], rot_lo);
+    const uint32_t th = __builtin_amdgcn_alignbit(qh[k], qh[k], rot_hi);
+    lo[k] = (int)((qs[k] & 0x0f0f0f0fu) | (tl & 0x10101010u));
+    hi[k] = (int)(((qs[k] >> 4) & 0x0f0f0f0fu) | (th & 0x10101010u));
+  }
+}
+
+__device__ __forceinline__ BlockQ4 decode_q5(const u32x4& h, const u32x4& qh0, const u32x4& qh1,
+                                             const u32x4& qa, const u32x4& qb, bool hi_units,
+                                             int bsh, uint32_t rot_lo, uint32_t rot_hi) {
+  BlockQ4 w = decode_q4(h, qa, qb, hi_units, bsh);  // scales, mins, d, dmin
+  q5_operands(qa, qh0, rot_lo, rot_hi, w.la, w.ha);
+  q5_operands(qb, qh1, rot_lo, rot_hi, w.lb, w.hb);
+  return w;
+}
+
+// Exact per-weight f32 dot of 16 weights given as bytes (0..31) with 16
+// activations.
+__device__ __forceinline__ float exact_dot16_bytes(const i32x4& q, float d1, float m1,
+                                                   const float* __restrict__ xs, float acc) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const uint32_t v = ((uint32_t)q[j >> 2] >> (8 * (j & 3))) & 0xffu;
+    acc = fmaf(k4_value_exact(d1, m1, v), xs[j], acc);
+  }
+  return acc;
+}
+
+// Exact per-weight path of one decoded Q5_K block (same element order as
+// block_exact).
+__device__ __forceinline__ float block_exact5(const BlockQ4& w, const u32x4& h, bool hi_units,
+                                              int bsh, const float* __restrict__ xs) {
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  const uint32_t scw = hi_units ? sc47 : sc03;
+  const uint32_t mnw = hi_units ? mn47 : mn03;
+  const uint32_t sce = (scw >> bsh) & 0xffu, sco = (scw >> (bsh + 8)) & 0xffu;
+  const uint32_t mne = (mnw >> bsh) & 0xffu, mno = (mnw >> (bsh + 8)) & 0xffu;
+  const float d = half_bits_to_float(h[0] & 0xffffu);
+  const float dmin = half_bits_to_float(h[0] >> 16);
+  const float d1e = __fmul_rn(d, (float)sce), m1e = __fmul_rn(dmin, (float)mne);
+  const float d1o = __fmul_rn(d, (float)sco), m1o = __fmul_rn(dmin, (float)mno);
+  float acc = exact_dot16_bytes(w.la, d1e, m1e, xs, 0.0f);
+  acc = exact_dot16_bytes(w.lb, d1e, m1e, xs + 16, acc);
+  acc = exact_dot16_bytes(w.ha, d1o, m1o, xs + 32, acc);
+  return exact_dot16_bytes(w.hb, d1o, m1o, xs + 48, acc);
+}
+
+// The weights of a stage in registers, per format: Q4_K keeps (header, qs
+// piece a, qs piece b) per block, Q5_K adds the two qh pieces.
+template <int QB>
+struct StageRegs {
+  static constexpr int kPer = QB == 5 ? 5 : 3;
+  u32x4 v[4 * kPer];
+  __device__ __forceinline__ void read(uint32_t hb, uint32_t qb) {
+    if constexpr (QB == 5)
+      lds_read_weights5(hb, qb, v);
+    else
+      lds_read_weights(hb, qb, v);
+  }
+  __device__ __forceinline__ BlockQ4 decode(int b, bool hi_units, int bsh, uint32_t rot_lo,
+                                            uint32_t rot_hi) const {
+    if constexpr (QB == 5)
+      return decode_q5(v[5 * b], v[5 * b + 1], v[5 * b + 2], v[5 * b + 3], v[5 * b + 4],
+                       hi_units, bsh, rot_lo, rot_hi);
+    else
+      return decode_q4(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh);
+  }
+  __device__ __forceinline__ float exact(int b, bool hi_units, int bsh, uint32_t rot_lo,
+                                         uint32_t rot_hi, const float* __restrict__ xs) const {
+    if constexpr (QB == 5)
+      return block_exact5(decode(b, hi_units, bsh, rot_lo, rot_hi), v[5 * b], hi_units, bsh, xs);
+    else
+      return block_exact(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh, xs);
+  }
+};
+
+template <int WAVES, int DEPTH, int MATS, int NTOK, int QB>
 __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const uint8_t* __restrict__ w2,
                                                               const float* __restrict__ x,
@@ -240,17 +358,20 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
                                                               void* __restrict__ wsp, uint32_t split) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   static_assert(NTOK == 1 || MATS == 1, "several activation vectors: one matrix");
-  const Layout L = layout(WAVES, DEPTH, nb, slots, MATS, NTOK);
+  static_assert(QB == 4 || QB == 5, "Q4_K or Q5_K");
+  constexpr uint32_t kPieces = block_pieces(QB);        // 16-byte pieces per block
+  constexpr uint32_t kStage = stage_bytes(QB);
+  const Layout L = layout(WAVES, DEPTH, nb, slots, MATS, NTOK, QB);
   const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t grp = lane >> 4, n = lane & 15u;
-  const uint32_t row_bytes = nb * kQ4Bytes;
+  const uint32_t row_bytes = nb * block_bytes(QB);
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = (nb + 3u) / 4u;
   const uint32_t tstages = MATS * nstages;  // pairs (and partials) per tile
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
-  uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
+  uint8_t* const wstage = smem + wave * DEPTH * kStage;
 
   // 1. x into the image area, natural order (block b at img + 1024 b; vector
   //    t of NTOK at img + t img_stride)
@@ -273,13 +394,14 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     const uint32_t mat = MATS > 1 && pr.r >= nstages ? 1u : 0u, st = pr.r - mat * nstages;
     const uint32_t row0 = pr.tile * 16u;
     const uint32_t nrows = min(16u, rows - row0);
-    const uint8_t* sb = (mat ? w2 : w) + (size_t)row0 * row_bytes + 576u * st;
+    const uint8_t* sb = (mat ? w2 : w) + (size_t)row0 * row_bytes + 4u * block_bytes(QB) * st;
     // the descriptor ends at the tile's last row: pieces past it read zero
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - 576u * st), kBufferWord3);
-    uint8_t* dst = wstage + (j % DEPTH) * kStageBytes;
+        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - 4u * block_bytes(QB) * st),
+        kBufferWord3);
+    uint8_t* dst = wstage + (j % DEPTH) * kStage;
 #pragma unroll
-    for (int i = 0; i < 9; ++i)
+    for (int i = 0; i < (int)kPieces; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * i), 16,
                                                 voff + 64u * i, 0, 0, 0);
   };
@@ -293,11 +415,11 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   // the stage copies were issued after x's and complete in order
   const uint32_t early = min((uint32_t)DEPTH, my_pairs);
   if (early >= 3u)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(27));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * kPieces));
   else if (early == 2u)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(18));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kPieces));
   else if (early == 1u)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(9));
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kPieces));
   else
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   // chunk c = 4 p + t: units 2p, 2p + 1 of lane group p, MFMA t
@@ -311,8 +433,11 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   // 4. the wave's pairs
   const bool hi_units = grp >= 2u;       // units 4..7 use the packed upper scales
   const int bsh = 16 * (int)(grp & 1u);  // byte of unit 2 grp within its scale word
-  const uint32_t hb0 = sbase + wave * DEPTH * kStageBytes + 16u * n;
-  const uint32_t qb0 = hb0 + 256u + 512u * grp;
+  const uint32_t hb0 = sbase + wave * DEPTH * kStage + 16u * n;
+  // qs pieces of lane group grp: Q4_K pieces 1 + 2 grp, Q5_K 3 + 2 grp
+  const uint32_t qb0 = hb0 + (QB == 5 ? 768u : 256u) + 512u * grp;
+  // Q5_K: rotations that bring qh bits 2 grp / 2 grp + 1 of each byte to bit 4
+  const uint32_t rot_lo = (28u + 2u * grp) & 31u, rot_hi = (29u + 2u * grp) & 31u;
   i32x4 A[16];
 #pragma unroll
   for (int t = 0; t < 16; ++t) A[t] = i32x4{0, 0, 0, 0};
@@ -321,14 +446,14 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     const uint32_t s = MATS > 1 && pr.r >= nstages ? pr.r - nstages : pr.r;  // stage
     const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
     if (DEPTH >= 3 && later >= 2u)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(18));
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kPieces));
     else if (DEPTH >= 2 && later >= 1u)
-      __builtin_amdgcn_s_waitcnt(waitcnt_vm(9));
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kPieces));
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    const uint32_t buf = (j % DEPTH) * kStageBytes;
-    u32x4 v[12];
-    lds_read_weights(hb0 + buf, qb0 + buf, v);
+    const uint32_t buf = (j % DEPTH) * kStage;
+    StageRegs<QB> v;
+    v.read(hb0 + buf, qb0 + buf);
     if (j + DEPTH < my_pairs) issue(j + DEPTH);  // the buffer just read is free again
     const uint32_t nlive = min(4u, nb - 4u * s);
     if constexpr (NTOK > 1) {
@@ -336,7 +461,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       BlockQ4 bw[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b)
-        bw[b] = decode_q4(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh);
+        bw[b] = v.decode(b, hi_units, bsh, rot_lo, rot_hi);
       float rs[NTOK];
 #pragma unroll
       for (int t = 0; t < NTOK; ++t) {
@@ -360,9 +485,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
 #pragma unroll
           for (int b = 0; b < 4; ++b)
             if ((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock)
-              part[b] = block_exact(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh,
-                                    x + (size_t)t * nb * kBlockElems + 256u * (4u * s + b) +
-                                        64u * grp);
+              part[b] = v.exact(b, hi_units, bsh, rot_lo, rot_hi,
+                                x + (size_t)t * nb * kBlockElems + 256u * (4u * s + b) + 64u * grp);
         }
         rs[t] = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
       }
@@ -380,16 +504,15 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
       const bool use = (uint32_t)b < nlive;
       bad_any |= use && eb == kBadBlock;
-      const float c = block_terms(v[3 * b], v[3 * b + 1], v[3 * b + 2], A[4 * b], A[4 * b + 1],
-                                  A[4 * b + 2], A[4 * b + 3], xs[b], eb, hi_units, bsh);
+      const float c = block_dot(v.decode(b, hi_units, bsh, rot_lo, rot_hi), A[4 * b],
+                                A[4 * b + 1], A[4 * b + 2], A[4 * b + 3], xs[b], eb);
       part[b] = (use && eb != kBadBlock) ? c : 0.0f;
     }
     if (bad_any) {
 #pragma unroll
       for (int b = 0; b < 4; ++b)
         if ((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock)
-          part[b] = block_exact(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh,
-                                x + 256u * (4u * s + b) + 64u * grp);
+          part[b] = v.exact(b, hi_units, bsh, rot_lo, rot_hi, x + 256u * (4u * s + b) + 64u * grp);
     }
     const float rowsum = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
 
@@ -398,7 +521,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   }
 }
 
-template <int W, int D, int M, int NT = 1>
+template <int W, int D, int M, int NT = 1, int QB = 4>
 bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, uint32_t rows,
                uint32_t nb, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
@@ -407,42 +530,81 @@ bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, ui
   const LaunchShape ls = launch_shape(ntiles, tstages, W, NT == 1 ? ws.bytes : 0u, M);
   const uint32_t grid = ls.groups;
   const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, tstages);
-  const uint32_t lds = layout(W, D, nb, slots, M, NT).total;
+  const uint32_t lds = layout(W, D, nb, slots, M, NT, QB).total;
   if (lds > kLdsBytes) return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT>),
+      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT, QB>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT>), dim3(grid), dim3(W * 64), lds, s, w, w2, x,
-                     y, rows, nb, slots, ws.ptr, ls.split ? 1u : 0u);
+  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT, QB>), dim3(grid), dim3(W * 64), lds, s, w, w2,
+                     x, y, rows, nb, slots, ws.ptr, ls.split ? 1u : 0u);
   *err = hipGetLastError();
   return true;
 }
 
 // NT activation vectors (batch-major x and y) in one pass over the weights.
-template <int NT>
+template <int NT, int QB>
 bool launch_tokens(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                    const Workspace& ws, hipStream_t s, hipError_t* err) {
-  return launch_wd<8, 1, 1, NT>(w, nullptr, x, y, rows, nb, ws, s, err) ||
-         launch_wd<6, 1, 1, NT>(w, nullptr, x, y, rows, nb, ws, s, err) ||
-         launch_wd<4, 1, 1, NT>(w, nullptr, x, y, rows, nb, ws, s, err);
+  return launch_wd<8, 1, 1, NT, QB>(w, nullptr, x, y, rows, nb, ws, s, err) ||
+         launch_wd<6, 1, 1, NT, QB>(w, nullptr, x, y, rows, nb, ws, s, err) ||
+         launch_wd<4, 1, 1, NT, QB>(w, nullptr, x, y, rows, nb, ws, s, err);
 }
 
-bool shape_ok(uint32_t rows, uint32_t cols, uint32_t mats) {
+bool shape_ok(uint32_t rows, uint32_t cols, uint32_t mats, int qb) {
   const uint32_t nb = cols / kBlockElems;
   const uint64_t pairs = (uint64_t)((rows + 15u) / 16u) * ((nb + 3u) / 4u) * mats;
-  return rows != 0 && nb != 0 && (uint64_t)nb * kQ4Bytes * 16u <= 0x7fffffffu &&
+  return rows != 0 && nb != 0 && (uint64_t)nb * block_bytes(qb) * 16u <= 0x7fffffffu &&
          (uint64_t)nb * 1024u <= 0x7fffffffu && pairs <= 0xffffffffu;
+}
+
+// One vector, Q5_K (8 waves: its 20 weight pieces per stage leave too few
+// registers for 12).
+bool launch_q5k_one(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+                    const Workspace& ws, hipStream_t s, hipError_t* err) {
+  return launch_wd<8, 1, 1, 1, 5>(w, nullptr, x, y, rows, nb, ws, s, err) ||
+         launch_wd<4, 1, 1, 1, 5>(w, nullptr, x, y, rows, nb, ws, s, err);
+}
+
+// batch >= 2 vectors, up to four per pass over the weights (their activation
+// images share the LDS with the stage buffers)
+template <int QB>
+bool matmul_passes(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t cols,
+                   uint32_t batch, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  const uint32_t nb = cols / kBlockElems;
+  for (uint32_t b = 0; b < batch;) {
+    const uint32_t nt = min(4u, batch - b);
+    const float* xb = x + (size_t)b * cols;
+    float* yb = y + (size_t)b * rows;
+    bool ok;
+    switch (nt) {
+      case 4: ok = launch_tokens<4, QB>(w, xb, yb, rows, nb, ws, s, err); break;
+      case 3: ok = launch_tokens<3, QB>(w, xb, yb, rows, nb, ws, s, err); break;
+      case 2: ok = launch_tokens<2, QB>(w, xb, yb, rows, nb, ws, s, err); break;
+      default:
+        ok = QB == 5 ? launch_q5k_one(w, xb, yb, rows, nb, ws, s, err)
+                     : launch_q4k_matvec_mfma(w, xb, yb, rows, cols, ws, s, err);
+        break;
+    }
+    if (!ok) {
+      if (b == 0) return false;
+      *err = hipErrorInvalidValue;
+      return true;
+    }
+    if (*err != hipSuccess) return true;
+    b += nt;
+  }
+  return true;
 }
 
 }  // namespace
 
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
-  if (!shape_ok(rows, cols, 1u)) return false;
+  if (!shape_ok(rows, cols, 1u, 4)) return false;
   const uint32_t nb = cols / kBlockElems;
   static const int cfg = env_int("SI_HIP_Q4K_MFMA_CFG", 0);
   switch (cfg) {
@@ -456,39 +618,30 @@ bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
          launch_wd<4, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
 }
 
+bool launch_q5k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  if (!shape_ok(rows, cols, 1u, 5)) return false;
+  return launch_q5k_one(w, x, y, rows, cols / kBlockElems, ws, s, err);
+}
+
 bool launch_q4k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
                             hipError_t* err) {
-  if (batch < 2 || !shape_ok(rows, cols, 1u)) return false;
-  const uint32_t nb = cols / kBlockElems;
-  // up to four vectors per pass over the weights (their activation images
-  // share the LDS with the stage buffers)
-  for (uint32_t b = 0; b < batch;) {
-    const uint32_t nt = min(4u, batch - b);
-    const float* xb = x + (size_t)b * cols;
-    float* yb = y + (size_t)b * rows;
-    bool ok;
-    switch (nt) {
-      case 4: ok = launch_tokens<4>(w, xb, yb, rows, nb, ws, s, err); break;
-      case 3: ok = launch_tokens<3>(w, xb, yb, rows, nb, ws, s, err); break;
-      case 2: ok = launch_tokens<2>(w, xb, yb, rows, nb, ws, s, err); break;
-      default: ok = launch_q4k_matvec_mfma(w, xb, yb, rows, cols, ws, s, err); break;
-    }
-    if (!ok) {
-      if (b == 0) return false;
-      *err = hipErrorInvalidValue;
-      return true;
-    }
-    if (*err != hipSuccess) return true;
-    b += nt;
-  }
-  return true;
+  if (batch < 2 || !shape_ok(rows, cols, 1u, 4)) return false;
+  return matmul_passes<4>(w, x, y, rows, cols, batch, ws, s, err);
+}
+
+bool launch_q5k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
+                            hipError_t* err) {
+  if (batch < 2 || !shape_ok(rows, cols, 1u, 5)) return false;
+  return matmul_passes<5>(w, x, y, rows, cols, batch, ws, s, err);
 }
 
 bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
                              uint32_t rows, uint32_t cols, const Workspace& ws, hipStream_t s,
                              hipError_t* err) {
-  if (!shape_ok(rows, cols, 2u)) return false;
+  if (!shape_ok(rows, cols, 2u, 4)) return false;
   const uint32_t nb = cols / kBlockElems;
   return launch_wd<12, 1, 2>(gate, up, x, h, rows, nb, ws, s, err) ||
          launch_wd<8, 1, 2>(gate, up, x, h, rows, nb, ws, s, err) ||

@@ -480,8 +480,8 @@ inline int cu_count() {
 
 // Workgroups of a launch: one per CU, fewer when there are fewer pairs.
 // Launch shape of a matrix-core matvec: workgroups, whether tiles are split
-// (fewer rounds of pairs per wave than with whole tiles), and the most tiles
-// one workgroup touches.
+// (fewer rounds of pairs per wave than with whole tiles, in a launch of at
+// least three rounds), and the most tiles one workgroup touches.
 struct LaunchShape {
   uint32_t groups;
   bool split;
@@ -498,7 +498,9 @@ inline LaunchShape launch_shape(uint32_t ntiles, uint32_t tparts, uint32_t waves
   const uint64_t lpairs = (uint64_t)(ntiles - q * g1) * tparts;
   const uint64_t most = (uint64_t)q * tparts + (lpairs + g1 - 1u) / g1;
   const uint64_t rounds1 = (most + waves - 1u) / waves;
-  ls.split = rounds1 < rounds0 && split_ws_fits(ws_bytes, g1, ntiles, mats);
+  // the cross-workgroup exchange costs about a round in a short launch, so
+  // split only launches of three or more rounds
+  ls.split = rounds1 < rounds0 && rounds0 >= 3u && split_ws_fits(ws_bytes, g1, ntiles, mats);
   ls.groups = ls.split ? g1 : g0;
   ls.tiles_per_group = ls.split ? q + (uint32_t)(((lpairs + g1 - 1u) / g1 + tparts - 1u) / tparts) + 1u
                                 : (ntiles + g0 - 1u) / g0;

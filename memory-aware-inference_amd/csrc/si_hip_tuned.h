@@ -21,6 +21,13 @@ bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
 bool launch_q4k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
                             hipError_t* err);
+// Q5_K, one vector / batch >= 2 vectors, on the matrix cores (the Q4_K kernel
+// reading 176-byte blocks).
+bool launch_q5k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
+bool launch_q5k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
+                            hipError_t* err);
 // Q6_K, one vector, on the matrix cores.
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
