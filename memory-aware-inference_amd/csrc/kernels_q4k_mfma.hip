@@ -558,7 +558,8 @@ bool shape_ok(uint32_t rows, uint32_t cols, uint32_t mats, int qb) {
   const uint32_t nb = cols / kBlockElems;
   const uint64_t pairs = (uint64_t)((rows + 15u) / 16u) * ((nb + 3u) / 4u) * mats;
   return rows != 0 && nb != 0 && (uint64_t)nb * block_bytes(qb) * 16u <= 0x7fffffffu &&
-         (uint64_t)nb * 1024u <= 0x7fffffffu && pairs <= 0xffffffffu;
+         (uint64_t)nb * 1024u <= 0x7fffffffu && pairs <= 0xffffffffu &&
+         quotients_fit((rows + 15u) / 16u, (nb + 3u) / 4u * mats);
 }
 
 // One vector, Q5_K (8 waves: its 20 weight pieces per stage leave too few
@@ -611,6 +612,7 @@ bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
     case 1: return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
     case 2: return launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
     case 3: return launch_wd<4, 3, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
+    case 4: return launch_wd<5, 3, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
     default: break;
   }
   return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err) ||

@@ -345,7 +345,8 @@ bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
   // the descriptor sizes are 32-bit
   if (nb == 0 || (nb & 1u) || rows == 0 || (uint64_t)nb * kQ6Bytes * 16u > 0x7fffffffu ||
       (uint64_t)nb * 1024u > 0x7fffffffu ||
-      (uint64_t)((rows + 15u) / 16u) * (nb / 2u) > 0xffffffffu)
+      (uint64_t)((rows + 15u) / 16u) * (nb / 2u) > 0xffffffffu ||
+      !quotients_fit((rows + 15u) / 16u, nb / 2u))
     return false;
   static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
   switch (cfg) {

@@ -247,6 +247,19 @@ __device__ __forceinline__ void init_slots(uint32_t sbase, const Layout& L, uint
   }
 }
 
+// Division by a launch constant d as a multiply-high: m = ceil(2^32 / d) (0
+// for d = 1) gives floor(x / d) exactly whenever x * d < 2^32, which the host
+// guarantees for every quotient taken this way (pair and tile indices).
+struct FastDiv {
+  uint32_t d, m;
+};
+__device__ __forceinline__ FastDiv make_div(uint32_t d) {
+  return FastDiv{d, d > 1u ? 0xffffffffu / d + 1u : 0u};
+}
+__device__ __forceinline__ uint32_t quo(uint32_t x, const FastDiv& f) {
+  return f.m ? __umulhi(x, f.m) : x;
+}
+
 // Work split.  With G workgroups and T tiles of S partials each, workgroup g
 // owns the whole tiles g, g + G, ...  When that leaves some workgroups a
 // round of pairs more than others (rounds = pairs / waves, rounded up), the
@@ -271,6 +284,8 @@ struct Sched {
   uint32_t ngroups;
   uint32_t npairs;      // this workgroup's pairs
   uint32_t slack0;      // > 0: leftover pairs at positions slack0 .. slack0 + nl - 1
+  FastDiv by_parts, by_slots;
+  uint32_t t_a;         // first leftover tile index (a / parts)
 };
 __device__ __forceinline__ uint32_t range_start(uint32_t g, uint32_t npairs, uint32_t ngroups) {
   return (uint32_t)((uint64_t)g * npairs / ngroups);
@@ -283,6 +298,8 @@ __device__ __forceinline__ Sched make_sched(uint32_t ntiles, uint32_t tparts, bo
                                             uint32_t waves, uint32_t slots) {
   Sched s;
   const uint32_t G = gridDim.x, g = blockIdx.x;
+  s.by_parts = make_div(tparts);
+  s.by_slots = make_div(slots);
   s.ngroups = G;
   s.whole0 = g;
   s.wstride = G;
@@ -299,7 +316,8 @@ __device__ __forceinline__ Sched make_sched(uint32_t ntiles, uint32_t tparts, bo
     s.a = range_start(g, s.lpairs, G);
     s.b = range_start(g + 1u, s.lpairs, G);
   }
-  s.nsplit = s.b > s.a ? (s.b - 1u) / tparts - s.a / tparts + 1u : 0u;
+  s.t_a = s.a / tparts;
+  s.nsplit = s.b > s.a ? (s.b - 1u) / tparts - s.t_a + 1u : 0u;
   s.npairs = (s.b - s.a) + s.nwhole * tparts;
   const uint32_t nl = s.b - s.a, last = s.npairs % waves;
   if (nl > 0u && nl < waves && s.npairs > waves && last != 0u && last <= waves - nl &&
@@ -326,14 +344,14 @@ __device__ __forceinline__ Pair pair_at(const Sched& s, uint32_t k, uint32_t tpa
     ks = k;
   }
   if (split) {
-    const uint32_t lp = s.a + ks, t = lp / tparts;
+    const uint32_t lp = s.a + ks, t = quo(lp, s.by_parts);
     p.tile = s.split_base + t;
     p.r = lp - t * tparts;
-    p.lt = t - s.a / tparts;
+    p.lt = t - s.t_a;
     p.lo = max(s.a, t * tparts) - t * tparts;
     p.hi = min(s.b, (t + 1u) * tparts) - t * tparts;
   } else {
-    const uint32_t kk = ks - nl, t = kk / tparts;
+    const uint32_t kk = ks - nl, t = quo(kk, s.by_parts);
     p.tile = s.whole0 + s.wstride * t;
     p.r = kk - t * tparts;
     p.lt = s.nsplit + t;
@@ -398,7 +416,7 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
                                          float* __restrict__ y, SplitWs ws) {
   const uint32_t grp = lane >> 4, n = lane & 15u;
   const uint32_t tparts = MATS * nparts;
-  const uint32_t slot = pr.lt % slots;
+  const uint32_t slot = pr.lt - quo(pr.lt, sc.by_slots) * slots;
   for (uint32_t spin = 0;
        lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
     __builtin_amdgcn_s_sleep(1);
@@ -425,7 +443,7 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
     // two: the workgroup that completes the count waits for each entry to
     // leave the empty state.  Only read-modify-write atomics touch the counter.
     const uint32_t t = pr.tile - sc.split_base;  // leftover tile index
-    const uint32_t e = 2u * blockIdx.x + (t == sc.a / tparts ? 0u : 1u);
+    const uint32_t e = 2u * blockIdx.x + (t == sc.t_a ? 0u : 1u);
     if (grp == 0u) {
       store_coherent(ws.part + (e * MATS) * 16u + n, sum);
       if (MATS > 1) store_coherent(ws.part + (e * MATS + 1u) * 16u + n, sum2);
@@ -487,6 +505,15 @@ struct LaunchShape {
   bool split;
   uint32_t tiles_per_group;
 };
+// Pair and tile indices divided with FastDiv stay below ntiles * tparts and
+// the ring's tile count below ntiles; the kernels need those times their
+// divisor below 2^32.
+inline bool quotients_fit(uint32_t ntiles, uint32_t tparts) {
+  // ring slots are at most 8192 / 64 = 128
+  return (uint64_t)ntiles * tparts * tparts < (1ull << 32) &&
+         (uint64_t)ntiles * 128u < (1ull << 32);
+}
+
 inline LaunchShape launch_shape(uint32_t ntiles, uint32_t tparts, uint32_t waves,
                                 size_t ws_bytes, uint32_t mats) {
   LaunchShape ls;
@@ -516,7 +543,7 @@ __device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L,
                                                 const float (&rowsum)[NTOK], uint32_t lane,
                                                 uint32_t rows, float* __restrict__ y) {
   const uint32_t grp = lane >> 4, n = lane & 15u;
-  const uint32_t slot = pr.lt % slots;
+  const uint32_t slot = pr.lt % slots;  // (no Sched here; a few tokens' work per pair)
   for (uint32_t spin = 0;
        lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
     __builtin_amdgcn_s_sleep(1);
