@@ -31,7 +31,7 @@
 // Data path.  One persistent workgroup of WAVES waves per CU.  At start it
 // turns all of x into digit images in LDS (1 KB per block, plus unit sums and
 // exponents) while each wave's first stage of weights is already in flight.
-// The workgroup owns the 16-row tiles G, G + gridDim.x, ...; their (tile,
+// Workgroup g of G owns the 16-row tiles g, g + G, ...; their (tile,
 // stage) pairs, a stage being four blocks (16 rows x 576 bytes), go to the
 // waves round-robin, so every wave streams its own sequence of stages.
 // Weights arrive by 16-byte buffer->LDS copies in piece-major order (LDS
@@ -354,11 +354,12 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
                                                               const uint8_t* __restrict__ w2,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
-                                                              uint32_t nb, uint32_t slots,
-                                                              void* __restrict__ wsp, uint32_t split) {
+                                                              uint32_t nb, void* __restrict__ wsp,
+                                                              SchedArgs sa) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   static_assert(NTOK == 1 || MATS == 1, "several activation vectors: one matrix");
   static_assert(QB == 4 || QB == 5, "Q4_K or Q5_K");
+  const uint32_t slots = sa.packed & 0xffu;
   constexpr uint32_t kPieces = block_pieces(QB);        // 16-byte pieces per block
   constexpr uint32_t kStage = stage_bytes(QB);
   const Layout L = layout(WAVES, DEPTH, nb, slots, MATS, NTOK, QB);
@@ -385,7 +386,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   //    matrix r / nstages), and the copies of its first DEPTH, pair j of the
   //    wave into buffer j % DEPTH.  Piece
   //    c = 64 i + lane of a stage is piece c / 16 of row c % 16's 576 bytes.
-  const Sched sc = make_sched(ntiles, tstages, split != 0u, WAVES, slots);
+  const Sched sc = make_sched(ntiles, tstages, WAVES, sa);
   const uint32_t npairs = sc.npairs;
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
@@ -490,7 +491,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
         }
         rs[t] = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
       }
-      hand_off_tokens<NTOK>(sbase, L, slots, pr, tstages, rs, lane, rows, y);
+      hand_off_tokens<NTOK>(sbase, L, sc.by_slots, pr, tstages, rs, lane, rows, y);
       continue;
     }
     lds_read_images(sbase + L.img + 4096u * s + 16u * n, kActiveLanes, A);
@@ -517,7 +518,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     const float rowsum = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
-    hand_off<MATS>(sbase, L, slots, sc, pr, nstages, rowsum, lane, rows, y, ws);
+    hand_off<MATS>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws);
   }
 }
 
@@ -531,7 +532,8 @@ bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, ui
   const uint32_t grid = ls.groups;
   const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, tstages);
   const uint32_t lds = layout(W, D, nb, slots, M, NT, QB).total;
-  if (lds > kLdsBytes) return false;
+  SchedArgs sa;
+  if (lds > kLdsBytes || !make_sched_args(ntiles, tstages, slots, ls, &sa)) return false;
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT, QB>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
@@ -540,7 +542,7 @@ bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, ui
     return true;
   }
   hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT, QB>), dim3(grid), dim3(W * 64), lds, s, w, w2,
-                     x, y, rows, nb, slots, ws.ptr, ls.split ? 1u : 0u);
+                     x, y, rows, nb, ws.ptr, sa);
   *err = hipGetLastError();
   return true;
 }
@@ -645,8 +647,16 @@ bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float
                              hipError_t* err) {
   if (!shape_ok(rows, cols, 2u, 4)) return false;
   const uint32_t nb = cols / kBlockElems;
-  return launch_wd<12, 1, 2>(gate, up, x, h, rows, nb, ws, s, err) ||
-         launch_wd<8, 1, 2>(gate, up, x, h, rows, nb, ws, s, err) ||
+  static const int cfg = env_int("SI_HIP_GATE_UP_MFMA_CFG", 0);
+  switch (cfg) {
+    case 1: return launch_wd<12, 1, 2>(gate, up, x, h, rows, nb, ws, s, err);
+    case 2: return launch_wd<8, 1, 2>(gate, up, x, h, rows, nb, ws, s, err);
+    case 3: return launch_wd<10, 1, 2>(gate, up, x, h, rows, nb, ws, s, err);
+    default: break;
+  }
+  // 8 waves: as fast as 12 here, and 12 leave the two-matrix kernel too few
+  // registers (it spills)
+  return launch_wd<8, 1, 2>(gate, up, x, h, rows, nb, ws, s, err) ||
          launch_wd<4, 1, 2>(gate, up, x, h, rows, nb, ws, s, err);
 }
 

@@ -180,9 +180,10 @@ template <int WAVES, int DEPTH>
 __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
-                                                              uint32_t nb, uint32_t slots,
-                                                              void* __restrict__ wsp, uint32_t split) {
+                                                              uint32_t nb, void* __restrict__ wsp,
+                                                              SchedArgs sa) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const uint32_t slots = sa.packed & 0xffu;
   const Layout L = layout(WAVES, DEPTH, nb, slots);
   const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
@@ -204,7 +205,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   //    piece 4 i + l / 16 of row l % 16; the 16 lanes whose piece would be the
   //    28th re-read the 27th (same addresses, no extra traffic).  All copies
   //    lie inside the stage's 420 bytes of their row.
-  const Sched sc = make_sched(ntiles, nstages, split != 0u, WAVES, slots);
+  const Sched sc = make_sched(ntiles, nstages, WAVES, sa);
   const uint32_t npairs = sc.npairs;
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t voff_last = n * row_bytes + (grp < 2u ? 16u * (24u + grp) : kLastPiece);
@@ -309,7 +310,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     const float rowsum = sum_lane_groups(part0 + part1);
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
-    hand_off<1>(sbase, L, slots, sc, pr, nstages, rowsum, lane, rows, y, ws);
+    hand_off<1>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws);
   }
 }
 
@@ -322,7 +323,8 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
   const uint32_t grid = ls.groups;
   const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, nstages);
   const uint32_t lds = layout(W, D, nb, slots).total;
-  if (lds > kLdsBytes) return false;
+  SchedArgs sa;
+  if (lds > kLdsBytes || !make_sched_args(ntiles, nstages, slots, ls, &sa)) return false;
   static const hipError_t attr = hipFuncSetAttribute(
       reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
@@ -331,7 +333,7 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
     return true;
   }
   hipLaunchKernelGGL((q6k_matvec_mfma<W, D>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
-                     nb, slots, ws.ptr, ls.split ? 1u : 0u);
+                     nb, ws.ptr, sa);
   *err = hipGetLastError();
   return true;
 }

@@ -249,16 +249,29 @@ __device__ __forceinline__ void init_slots(uint32_t sbase, const Layout& L, uint
 
 // Division by a launch constant d as a multiply-high: m = ceil(2^32 / d) (0
 // for d = 1) gives floor(x / d) exactly whenever x * d < 2^32, which the host
-// guarantees for every quotient taken this way (pair and tile indices).
+// guarantees for every quotient taken this way (pair, tile and range
+// indices).  The constants come from the host: the GPU has no integer divide,
+// and the dozen dependent instructions of each software division cost a
+// workgroup a noticeable part of a microsecond before its first weight copy.
 struct FastDiv {
   uint32_t d, m;
 };
-__device__ __forceinline__ FastDiv make_div(uint32_t d) {
-  return FastDiv{d, d > 1u ? 0xffffffffu / d + 1u : 0u};
+__host__ __device__ constexpr uint32_t div_magic(uint32_t d) {
+  return d > 1u ? 0xffffffffu / d + 1u : 0u;
 }
 __device__ __forceinline__ uint32_t quo(uint32_t x, const FastDiv& f) {
   return f.m ? __umulhi(x, f.m) : x;
 }
+
+// The launch constants of the work split below, one kernel argument: the ring
+// slot count (bits 0-7), the split flag (bit 8) and the workgroup count G
+// (bits 16-31), then the division constants of G, the partials per tile and
+// the slot count.  Kept to 16 bytes so a kernel's arguments stay within the
+// first 64-byte line of its argument block (one memory round trip).
+struct SchedArgs {
+  uint32_t packed;
+  uint32_t m_groups, m_parts, m_slots;
+};
 
 // Work split.  With G workgroups and T tiles of S partials each, workgroup g
 // owns the whole tiles g, g + G, ...  When that leaves some workgroups a
@@ -280,44 +293,60 @@ struct Sched {
   uint32_t lpairs;      // L
   uint32_t split_base;  // first leftover tile, q G
   uint32_t nsplit;      // leftover tiles this workgroup touches
-  uint32_t whole0, nwhole, wstride;  // whole tiles whole0 + wstride t, t < nwhole
-  uint32_t ngroups;
+  uint32_t nwhole;      // whole tiles g + G t, t < nwhole (g = blockIdx.x)
+  uint32_t groups;      // G
   uint32_t npairs;      // this workgroup's pairs
   uint32_t slack0;      // > 0: leftover pairs at positions slack0 .. slack0 + nl - 1
   FastDiv by_parts, by_slots;
   uint32_t t_a;         // first leftover tile index (a / parts)
 };
-__device__ __forceinline__ uint32_t range_start(uint32_t g, uint32_t npairs, uint32_t ngroups) {
-  return (uint32_t)((uint64_t)g * npairs / ngroups);
+// First leftover pair of workgroup g: floor(g L / G).
+__device__ __forceinline__ uint32_t range_start(uint32_t g, uint32_t lpairs,
+                                                const FastDiv& by_groups) {
+  return quo(g * lpairs, by_groups);
 }
-// The workgroup whose range holds pair p.
-__device__ __forceinline__ uint32_t range_of(uint32_t p, uint32_t npairs, uint32_t ngroups) {
-  return (uint32_t)(((uint64_t)(p + 1u) * ngroups - 1u) / npairs);
+// (the division constant of G is taken from the kernel argument where it is
+// needed rather than kept in the schedule, which would hold a scalar register
+// through the whole kernel)
+__device__ __forceinline__ uint32_t range_start(const Sched& s, const SchedArgs& sa, uint32_t g) {
+  return range_start(g, s.lpairs, FastDiv{s.groups, sa.m_groups});
 }
-__device__ __forceinline__ Sched make_sched(uint32_t ntiles, uint32_t tparts, bool split,
-                                            uint32_t waves, uint32_t slots) {
+// The workgroup whose range holds leftover pair p (p < L), i.e. the g with
+// range_start(g) <= p < range_start(g + 1): p G / L in floating point (with
+// the approximate reciprocal) is within one or two of it, and the loops
+// settle the rest.
+__device__ __forceinline__ uint32_t range_of(const Sched& s, const SchedArgs& sa, uint32_t p) {
+  const uint32_t G = s.groups;
+  uint32_t g = min((uint32_t)((float)p * (float)G * __builtin_amdgcn_rcpf((float)s.lpairs)), G - 1u);
+  while (g > 0u && range_start(s, sa, g) > p) --g;
+  while (g + 1u < G && range_start(s, sa, g + 1u) <= p) ++g;
+  return g;
+}
+__device__ __forceinline__ Sched make_sched(uint32_t ntiles, uint32_t tparts, uint32_t waves,
+                                            const SchedArgs& sa) {
   Sched s;
-  const uint32_t G = gridDim.x, g = blockIdx.x;
-  s.by_parts = make_div(tparts);
-  s.by_slots = make_div(slots);
-  s.ngroups = G;
-  s.whole0 = g;
-  s.wstride = G;
+  const uint32_t G = sa.packed >> 16, g = blockIdx.x, slots = sa.packed & 0xffu;
+  const bool split = (sa.packed & 0x100u) != 0u;
+  const FastDiv by_parts{tparts, sa.m_parts}, by_groups{G, sa.m_groups};
+  // (plain locals first: the struct is filled in once at the end)
+  const uint32_t nwhole = split ? quo(ntiles, by_groups)
+                                : (g < ntiles ? quo(ntiles - 1u - g, by_groups) + 1u : 0u);
+  const uint32_t split_base = split ? nwhole * G : ntiles;
+  const uint32_t lpairs = split ? (ntiles - split_base) * tparts : 0u;
+  const uint32_t a = split ? range_start(g, lpairs, by_groups) : 0u;
+  const uint32_t b = split ? range_start(g + 1u, lpairs, by_groups) : 0u;
+  const uint32_t t_a = quo(a, by_parts);
+  s.by_parts = by_parts;
+  s.by_slots = FastDiv{slots, sa.m_slots};
+  s.groups = G;
   s.slack0 = 0u;
-  if (!split) {
-    s.split_base = ntiles;
-    s.lpairs = 0u;
-    s.a = s.b = 0u;
-    s.nwhole = g < ntiles ? (ntiles - 1u - g) / G + 1u : 0u;
-  } else {
-    s.nwhole = ntiles / G;
-    s.split_base = s.nwhole * G;
-    s.lpairs = (ntiles - s.split_base) * tparts;
-    s.a = range_start(g, s.lpairs, G);
-    s.b = range_start(g + 1u, s.lpairs, G);
-  }
-  s.t_a = s.a / tparts;
-  s.nsplit = s.b > s.a ? (s.b - 1u) / tparts - s.t_a + 1u : 0u;
+  s.nwhole = nwhole;
+  s.split_base = split_base;
+  s.lpairs = lpairs;
+  s.a = a;
+  s.b = b;
+  s.t_a = t_a;
+  s.nsplit = b > a ? quo(b - 1u, by_parts) - t_a + 1u : 0u;
   s.npairs = (s.b - s.a) + s.nwhole * tparts;
   const uint32_t nl = s.b - s.a, last = s.npairs % waves;
   if (nl > 0u && nl < waves && s.npairs > waves && last != 0u && last <= waves - nl &&
@@ -352,7 +381,7 @@ __device__ __forceinline__ Pair pair_at(const Sched& s, uint32_t k, uint32_t tpa
     p.hi = min(s.b, (t + 1u) * tparts) - t * tparts;
   } else {
     const uint32_t kk = ks - nl, t = quo(kk, s.by_parts);
-    p.tile = s.whole0 + s.wstride * t;
+    p.tile = blockIdx.x + s.groups * t;
     p.r = kk - t * tparts;
     p.lt = s.nsplit + t;
     p.lo = 0u;
@@ -411,7 +440,8 @@ __device__ __forceinline__ float take_part(float* p) {
 // the sums and, if it completes the tile, combines all shares.
 template <int MATS>
 __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32_t slots,
-                                         const Sched& sc, const Pair& pr, uint32_t nparts,
+                                         const Sched& sc, const SchedArgs& sa, const Pair& pr,
+                                         uint32_t nparts,
                                          float rowsum, uint32_t lane, uint32_t rows,
                                          float* __restrict__ y, SplitWs ws) {
   const uint32_t grp = lane >> 4, n = lane & 15u;
@@ -454,14 +484,14 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
                                       __HIP_MEMORY_SCOPE_AGENT);
     before = __builtin_amdgcn_readlane(before, 0);
     if (before + (pr.hi - pr.lo) == tparts) {
-      const uint32_t g0 = range_of(t * tparts, sc.lpairs, sc.ngroups);
-      const uint32_t g1 = range_of(t * tparts + tparts - 1u, sc.lpairs, sc.ngroups);
+      const uint32_t g0 = range_of(sc, sa, t * tparts);
+      const uint32_t g1 = range_of(sc, sa, t * tparts + tparts - 1u);
       float g = 0.0f, u = 0.0f;
       if (grp == 0u) {
         for (uint32_t wg = g0; wg <= g1; ++wg) {
-          const uint32_t wa = range_start(wg, sc.lpairs, sc.ngroups);
-          if (wa == range_start(wg + 1u, sc.lpairs, sc.ngroups)) continue;  // no leftover pairs
-          const uint32_t t0 = wa / tparts;
+          const uint32_t wa = range_start(sc, sa, wg);
+          if (wa == range_start(sc, sa, wg + 1u)) continue;  // no leftover pairs
+          const uint32_t t0 = quo(wa, sc.by_parts);
           float* pe = ws.part + (2u * wg + (t == t0 ? 0u : 1u)) * MATS * 16u + n;
           g += take_part(pe);
           if (MATS > 1) u += take_part(pe + 16u);
@@ -538,12 +568,14 @@ inline LaunchShape launch_shape(uint32_t ntiles, uint32_t tparts, uint32_t waves
 // of the tile holds 16 rows x NTOK sums; the finishing wave stores
 // y[tok * rows + row] for every token.
 template <int NTOK>
-__device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L, uint32_t slots,
-                                                const Pair& pr, uint32_t tparts,
-                                                const float (&rowsum)[NTOK], uint32_t lane,
-                                                uint32_t rows, float* __restrict__ y) {
+__device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L,
+                                                const FastDiv& by_slots, const Pair& pr,
+                                                uint32_t tparts, const float (&rowsum)[NTOK],
+                                                uint32_t lane, uint32_t rows,
+                                                float* __restrict__ y) {
   const uint32_t grp = lane >> 4, n = lane & 15u;
-  const uint32_t slot = pr.lt % slots;  // (no Sched here; a few tokens' work per pair)
+  const uint32_t slots = by_slots.d;
+  const uint32_t slot = pr.lt - quo(pr.lt, by_slots) * slots;
   for (uint32_t spin = 0;
        lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
     __builtin_amdgcn_s_sleep(1);
@@ -569,6 +601,25 @@ __device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L,
     lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
     lds_write_b32(sbase + L.owner + 4u * slot, pr.lt + slots);
   }
+}
+
+// The schedule constants of a launch, or false when a multiply-high quotient
+// of the schedule could be inexact (x * d >= 2^32 for some quotient taken) or
+// the counts do not fit their fields.
+inline bool make_sched_args(uint32_t ntiles, uint32_t tparts, uint32_t slots,
+                            const LaunchShape& ls, SchedArgs* out) {
+  const uint64_t G = ls.groups;
+  if (G == 0u || G > 0xffffu || slots == 0u || slots > 0xffu) return false;
+  if ((uint64_t)ntiles * G >= (1ull << 32)) return false;  // tile / G quotients
+  if (ls.split) {
+    const uint64_t lpairs = (uint64_t)(ntiles - ntiles / ls.groups * ls.groups) * tparts;
+    if (lpairs * G * G >= (1ull << 32)) return false;  // range starts: (g + 1) L / G
+  }
+  out->packed = (uint32_t)(G << 16) | (ls.split ? 0x100u : 0u) | slots;
+  out->m_groups = div_magic((uint32_t)G);
+  out->m_parts = div_magic(tparts);
+  out->m_slots = div_magic(slots);
+  return true;
 }
 
 // Slots of the ring: enough for every wave to be a few tiles ahead, within
