@@ -69,9 +69,11 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
     ctx.event_record(1)
     ms = ctx.event_elapsed_ms(0, 1)
     ctx.synchronize()
-    extra = {}
+    graph_ms = time_graph_repeat(ctx, lib, harr, copies, rows, cols, d_x, d_y, steps, warmup)
+    extra = {"graph_us_per_call": round(graph_ms * 1000.0, 3),
+             "graph_gb_per_s": round(nbytes / (graph_ms * 1e-3) / 1e9, 1)}
     if detail:
-        extra = call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, steps)
+        extra.update(call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, steps))
     ctx.device_free(d_x)
     ctx.device_free(d_y)
     for w in weights:
@@ -83,6 +85,38 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
     out.update(extra)
     return out
+
+
+GRAPH_CALLS = int(os.environ.get("SI_BENCH_GRAPH_CALLS", "64"))
+
+
+def time_graph_repeat(ctx, lib, harr, copies, rows, cols, d_x, d_y, steps: int,
+                      warmup: int) -> float:
+    """Average ms per matvec when GRAPH_CALLS calls (cycling through the
+    resident copies) are recorded once into a HIP graph (si_hip_capture_begin/
+    end) and the graph is replayed back to back: the launch overhead per kernel
+    of a captured decode step rather than of separate host launches."""
+    import ctypes as C
+    ctx.capture_begin()
+    per_graph = copies * max(1, GRAPH_CALLS // copies)
+    rc = lib.si_hip_quant_matvec_device_repeat(ctx.handle, harr, copies, rows, cols,
+                                               C.c_void_p(d_x), C.c_void_p(d_y), per_graph)
+    graph = ctx.capture_end()
+    if rc:
+        graph.free()
+        raise si_hip.HipError(rc, si_hip.last_error())
+    reps = max(1, steps // per_graph)
+    for _ in range(max(1, warmup // per_graph)):
+        graph.launch()
+    ctx.synchronize()
+    ctx.event_record(0)
+    for _ in range(reps):
+        graph.launch()
+    ctx.event_record(1)
+    ms = ctx.event_elapsed_ms(0, 1)
+    ctx.synchronize()
+    graph.free()
+    return ms / (reps * per_graph)
 
 
 def call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, samples: int) -> dict:
@@ -401,6 +435,8 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": head["gb_per_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": head["frac_of_peak"],
                      "traffic": profiled_traffic()},
+        "graph_us_per_call": head["graph_us_per_call"],
+        "graph_gb_per_s": head["graph_gb_per_s"],
         "isolated_call_us": head["isolated_call_us"],
         "host_wall_us_per_call": head["host_wall_us_per_call"],
         "host_wall_note": head["host_wall_note"],

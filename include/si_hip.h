@@ -51,6 +51,7 @@ extern "C" {
 #define SI_HIP_ERR_DEVICE (-9)            /* HIP runtime or launch failure */
 #define SI_HIP_ERR_OUT_OF_MEMORY (-10)
 #define SI_HIP_ERR_EMPTY (-11)            /* empty weight upload */
+#define SI_HIP_ERR_STATE (-12)            /* graph capture already open / not open */
 
 #define SI_HIP_GGML_TYPE_Q4_K 12u
 #define SI_HIP_GGML_TYPE_Q5_K 13u
@@ -252,6 +253,24 @@ int si_hip_quant_matvec_device_repeat(si_hip_context *ctx,
                                       const si_hip_quant_weight *const *weights,
                                       size_t n_weights, size_t rows, size_t columns,
                                       const float *d_input, float *d_output, size_t iterations);
+
+/* ---- captured submission (HIP graphs) ------------------------------------
+ * No counterpart in the reference: every Metal call there commits its command
+ * buffer and waits (metal.rs:2320-2337).  For callers that repeat the same
+ * device-resident work -- a decode step's projections, the 64-layer streaming
+ * aggregate -- the *_device calls (and si_hip_copy_device) made between
+ * si_hip_capture_begin and si_hip_capture_end are recorded instead of run, and
+ * si_hip_graph_launch replays them on the compute stream with less launch
+ * overhead per kernel.  The other calls keep running immediately while a
+ * capture is open.  One capture per context at a time; record from one
+ * thread.  A graph reads the weights and device buffers it was recorded with:
+ * keep them alive while it may run. */
+typedef struct si_hip_graph si_hip_graph;
+int si_hip_capture_begin(si_hip_context *ctx);
+int si_hip_capture_end(si_hip_context *ctx, si_hip_graph **out_graph);
+int si_hip_graph_launch(si_hip_context *ctx, const si_hip_graph *graph);
+uint64_t si_hip_graph_calls(const si_hip_graph *graph);  /* device calls recorded */
+void si_hip_graph_free(si_hip_graph *graph);
 
 /* ---- kernel selection (the reference picks variants via SI_QK_* env) --- */
 #define SI_HIP_KERNEL_AUTO 0u     /* tuned gfx950 kernels where they apply */

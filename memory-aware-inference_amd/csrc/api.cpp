@@ -137,6 +137,11 @@ struct si_hip_context {
   // cross-workgroup combine area of the matrix-core kernels (kept zeroed)
   sihip::Workspace ws;
   hipEvent_t events[16] = {};
+  // graph capture: while `capturing`, the *_device calls go to capture_stream,
+  // where HIP records them instead of running them
+  hipStream_t capture_stream = nullptr;
+  bool capturing = false;
+  uint64_t captured_calls = 0;
   // telemetry
   std::shared_ptr<Telemetry> tel = std::make_shared<Telemetry>();
   std::atomic<uint64_t> submitted{0}, async_submitted{0}, waited{0}, wait_nanos{0};
@@ -151,6 +156,13 @@ struct si_hip_quant_weight {
   bool mapped = false;
   bool owner = false;  // counts toward active weight bytes
   const uint8_t *data() const { return static_cast<const uint8_t *>(buffer->ptr) + offset; }
+};
+
+struct si_hip_graph {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+  int device = 0;
+  uint64_t calls = 0;  // device calls recorded
 };
 
 namespace {
@@ -198,27 +210,34 @@ int wait_stream(si_hip_context *ctx, const char *what) {
 // ---------------------------------------------------------------------------
 // Kernel dispatch.
 int dispatch_matvec(si_hip_context *ctx, uint32_t type, const uint8_t *w, const float *x,
-                    float *y, uint32_t rows, uint32_t cols, uint32_t batch) {
+                    float *y, uint32_t rows, uint32_t cols, uint32_t batch,
+                    hipStream_t stream) {
   hipError_t e = hipErrorInvalidValue;
   bool done = false;
   if (ctx->policy == SI_HIP_KERNEL_AUTO) {
-    done = sihip::launch_matvec_tuned(type, w, x, y, rows, cols, batch, ctx->ws, ctx->stream, &e);
+    done = sihip::launch_matvec_tuned(type, w, x, y, rows, cols, batch, ctx->ws, stream, &e);
   }
-  if (!done) e = sihip::launch_matvec_generic(type, w, x, y, rows, cols, batch, ctx->stream);
+  if (!done) e = sihip::launch_matvec_generic(type, w, x, y, rows, cols, batch, stream);
   if (e != hipSuccess) return hip_fail(e, "matvec launch");
   return SI_HIP_OK;
 }
 
 int dispatch_gate_up(si_hip_context *ctx, const uint8_t *g, const uint8_t *u, const float *x,
-                     float *h, uint32_t rows, uint32_t cols) {
+                     float *h, uint32_t rows, uint32_t cols, hipStream_t stream) {
   hipError_t e = hipErrorInvalidValue;
   bool done = false;
   if (ctx->policy == SI_HIP_KERNEL_AUTO) {
-    done = sihip::launch_fused_gate_up_tuned(g, u, x, h, rows, cols, ctx->ws, ctx->stream, &e);
+    done = sihip::launch_fused_gate_up_tuned(g, u, x, h, rows, cols, ctx->ws, stream, &e);
   }
-  if (!done) e = sihip::launch_fused_gate_up_generic(g, u, x, h, rows, cols, ctx->stream);
+  if (!done) e = sihip::launch_fused_gate_up_generic(g, u, x, h, rows, cols, stream);
   if (e != hipSuccess) return hip_fail(e, "fused gate/up launch");
   return SI_HIP_OK;
+}
+
+// Stream of the device-resident calls: the capture stream while a graph is
+// being recorded, else the compute stream.
+hipStream_t device_stream(const si_hip_context *ctx) {
+  return ctx->capturing ? ctx->capture_stream : ctx->stream;
 }
 
 // Validation shared by the byte-slice matvec entry points
@@ -247,7 +266,7 @@ int run_matvec_host(si_hip_context *ctx, uint32_t type, const uint8_t *dev_w, si
               "input copy");
   rc = dispatch_matvec(ctx, type, dev_w, static_cast<const float *>(ctx->stage_in),
                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)columns,
-                       (uint32_t)batch);
+                       (uint32_t)batch, ctx->stream);
   if (rc) return rc;
   SIHIP_CHECK(hipMemcpyAsync(output, ctx->stage_out, out_bytes, hipMemcpyDeviceToHost, ctx->stream),
               "output copy");
@@ -344,6 +363,7 @@ const char *si_hip_status_name(int s) {
     case SI_HIP_ERR_DEVICE: return "SI_HIP_ERR_DEVICE";
     case SI_HIP_ERR_OUT_OF_MEMORY: return "SI_HIP_ERR_OUT_OF_MEMORY";
     case SI_HIP_ERR_EMPTY: return "SI_HIP_ERR_EMPTY";
+    case SI_HIP_ERR_STATE: return "SI_HIP_ERR_STATE";
     default: return "SI_HIP_ERR_UNKNOWN";
   }
 }
@@ -399,6 +419,13 @@ void si_hip_context_free(si_hip_context *ctx) {
     if (ev) (void)hipEventDestroy(ev);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
   if (ctx->upload_stream) (void)hipStreamDestroy(ctx->upload_stream);
+  if (ctx->capture_stream) {
+    if (ctx->capturing) {
+      hipGraph_t g = nullptr;
+      if (hipStreamEndCapture(ctx->capture_stream, &g) == hipSuccess && g) (void)hipGraphDestroy(g);
+    }
+    (void)hipStreamDestroy(ctx->capture_stream);
+  }
   delete ctx;
 }
 
@@ -566,7 +593,7 @@ int si_hip_gguf_quant_matvec_many_weights(si_hip_context *ctx,
   for (size_t i = 0; i < count; ++i) {
     rc = dispatch_matvec(ctx, weights[i]->ggml_type, weights[i]->data(),
                          static_cast<const float *>(ctx->stage_in), dst + off, (uint32_t)rows[i],
-                         (uint32_t)cols, 1);
+                         (uint32_t)cols, 1, ctx->stream);
     if (rc) return rc;
     off += rows[i];
   }
@@ -612,7 +639,7 @@ int si_hip_q4_k_fused_gate_up(si_hip_context *ctx, const uint8_t *gate, size_t g
   SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
               "input copy");
   rc = dispatch_gate_up(ctx, dw, dw + expected, static_cast<const float *>(ctx->stage_in),
-                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols);
+                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
   SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
               "output copy");
@@ -655,7 +682,7 @@ int si_hip_q4_k_fused_gate_up_weights(si_hip_context *ctx, const si_hip_quant_we
   SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
               "input copy");
   rc = dispatch_gate_up(ctx, g->data(), u->data(), static_cast<const float *>(ctx->stage_in),
-                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols);
+                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
   SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
               "output copy");
@@ -712,10 +739,10 @@ int si_hip_gguf_quant_fused_mlp_weights(si_hip_context *ctx, const si_hip_quant_
               "input copy");
   float *hidden = static_cast<float *>(ctx->stage_aux);
   rc = dispatch_gate_up(ctx, g->data(), u->data(), static_cast<const float *>(ctx->stage_in), hidden,
-                        (uint32_t)gate_rows, (uint32_t)cols);
+                        (uint32_t)gate_rows, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
   rc = dispatch_matvec(ctx, d->ggml_type, d->data(), hidden, static_cast<float *>(ctx->stage_out),
-                       (uint32_t)down_rows, (uint32_t)gate_rows, 1);
+                       (uint32_t)down_rows, (uint32_t)gate_rows, 1, ctx->stream);
   if (rc) return rc;
   SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, down_rows * sizeof(float), hipMemcpyDeviceToHost,
                              ctx->stream),
@@ -904,7 +931,7 @@ int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_qua
   float *d_logits = static_cast<float *>(ctx->stage_out);
   uint64_t *aux = static_cast<uint64_t *>(ctx->stage_aux);
   rc = dispatch_matvec(ctx, w->ggml_type, w->data(), static_cast<const float *>(ctx->stage_in),
-                       d_logits, (uint32_t)rows, (uint32_t)cols, 1);
+                       d_logits, (uint32_t)rows, (uint32_t)cols, 1, ctx->stream);
   if (rc) return rc;
   hipError_t e = sihip::launch_argmax(d_logits, (uint32_t)rows, rule, ctx->ws, aux, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "argmax launch");
@@ -996,7 +1023,8 @@ int si_hip_copy_from_device(si_hip_context *ctx, void *dst, const void *src, siz
 
 int si_hip_copy_device(si_hip_context *ctx, void *dst, const void *src, size_t bytes) {
   if (!ctx || !dst || !src) return fail(SI_HIP_ERR_NULL, "copy argument is null");
-  SIHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream), "device copy");
+  SIHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, device_stream(ctx)),
+              "device copy");
   return ok();
 }
 
@@ -1022,7 +1050,7 @@ int si_hip_quant_matvec_device(si_hip_context *ctx, const si_hip_quant_weight *w
   if (rc) return rc;
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matvec argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
-  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, 1);
+  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, 1, device_stream(ctx));
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);
   return ok();
@@ -1042,7 +1070,7 @@ int si_hip_quant_matvec_device_repeat(si_hip_context *ctx, const si_hip_quant_we
   std::lock_guard<std::mutex> lock(ctx->mu);
   for (size_t i = 0; i < iters; ++i) {
     const si_hip_quant_weight *w = ws[i % n];
-    int rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, 1);
+    int rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, 1, device_stream(ctx));
     if (rc) return rc;
   }
   ctx->async_submitted.fetch_add(iters);
@@ -1059,7 +1087,7 @@ int si_hip_q4_k_fused_gate_up_device(si_hip_context *ctx, const si_hip_quant_wei
   if (rc) return rc;
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device gate/up argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
-  rc = dispatch_gate_up(ctx, g->data(), u->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols);
+  rc = dispatch_gate_up(ctx, g->data(), u->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, device_stream(ctx));
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);
   return ok();
@@ -1073,10 +1101,10 @@ int si_hip_fused_mlp_device(si_hip_context *ctx, const si_hip_quant_weight *g,
   if (rc) return rc;
   if (!ctx || !d_in || !d_hidden || !d_out) return fail(SI_HIP_ERR_NULL, "device MLP argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
-  rc = dispatch_gate_up(ctx, g->data(), u->data(), d_in, d_hidden, (uint32_t)gate_rows, (uint32_t)cols);
+  rc = dispatch_gate_up(ctx, g->data(), u->data(), d_in, d_hidden, (uint32_t)gate_rows, (uint32_t)cols, device_stream(ctx));
   if (rc) return rc;
   rc = dispatch_matvec(ctx, d->ggml_type, d->data(), d_hidden, d_out, (uint32_t)down_rows,
-                       (uint32_t)gate_rows, 1);
+                       (uint32_t)gate_rows, 1, device_stream(ctx));
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);
   return ok();
@@ -1089,7 +1117,7 @@ int si_hip_matmul_many_device(si_hip_context *ctx, const si_hip_quant_weight *w,
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matmul argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
   rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols,
-                       (uint32_t)batch);
+                       (uint32_t)batch, device_stream(ctx));
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);
   return ok();
@@ -1102,9 +1130,10 @@ int si_hip_matvec_argmax_device(si_hip_context *ctx, const si_hip_quant_weight *
   if (rc) return rc;
   if (!ctx || !d_in || !d_logits || !d_result) return fail(SI_HIP_ERR_NULL, "device head argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
-  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_logits, (uint32_t)rows, (uint32_t)cols, 1);
+  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_logits, (uint32_t)rows, (uint32_t)cols, 1, device_stream(ctx));
   if (rc) return rc;
-  hipError_t e = sihip::launch_argmax(d_logits, (uint32_t)rows, rule, ctx->ws, d_result, ctx->stream);
+  hipError_t e =
+      sihip::launch_argmax(d_logits, (uint32_t)rows, rule, ctx->ws, d_result, device_stream(ctx));
   if (e != hipSuccess) return hip_fail(e, "argmax launch");
   ctx->async_submitted.fetch_add(1);
   return ok();
@@ -1122,7 +1151,7 @@ int si_hip_embedding_device(si_hip_context *ctx, const si_hip_quant_weight *t, s
   if (!ctx || !d_ids || !d_out) return fail(SI_HIP_ERR_NULL, "device embedding argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
   hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, t->data(), d_ids, d_out, (uint32_t)n,
-                                       (uint32_t)cols, ctx->stream);
+                                       (uint32_t)cols, device_stream(ctx));
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
   ctx->async_submitted.fetch_add(1);
   return ok();
@@ -1141,6 +1170,65 @@ int si_hip_event_elapsed_ms(si_hip_context *ctx, uint32_t a, uint32_t b, float *
   SIHIP_CHECK(hipEventSynchronize(ctx->events[b]), "event synchronize");
   SIHIP_CHECK(hipEventElapsedTime(ms, ctx->events[a], ctx->events[b]), "event elapsed");
   return ok();
+}
+
+// ---- captured submission -------------------------------------------------------
+int si_hip_capture_begin(si_hip_context *ctx) {
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  if (ctx->capturing) return fail(SI_HIP_ERR_STATE, "a graph capture is already open");
+  if (!ctx->capture_stream)
+    SIHIP_CHECK(hipStreamCreateWithFlags(&ctx->capture_stream, hipStreamNonBlocking),
+                "capture stream create");
+  SIHIP_CHECK(hipStreamBeginCapture(ctx->capture_stream, hipStreamCaptureModeRelaxed),
+              "begin capture");
+  ctx->capturing = true;
+  ctx->captured_calls = ctx->async_submitted.load();
+  return ok();
+}
+
+int si_hip_capture_end(si_hip_context *ctx, si_hip_graph **out) {
+  if (!ctx || !out) return fail(SI_HIP_ERR_NULL, "capture_end argument is null");
+  *out = nullptr;
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  if (!ctx->capturing) return fail(SI_HIP_ERR_STATE, "no graph capture is open");
+  ctx->capturing = false;
+  hipGraph_t g = nullptr;
+  SIHIP_CHECK(hipStreamEndCapture(ctx->capture_stream, &g), "end capture");
+  if (!g) return fail(SI_HIP_ERR_DEVICE, "HIP returned no captured graph");
+  auto graph = std::make_unique<si_hip_graph>();
+  graph->graph = g;
+  graph->device = ctx->device;
+  graph->calls = ctx->async_submitted.load() - ctx->captured_calls;
+  // the recorded calls did not run
+  ctx->async_submitted.fetch_sub(graph->calls);
+  hipError_t e = hipGraphInstantiate(&graph->exec, g, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    (void)hipGraphDestroy(g);
+    return hip_fail(e, "graph instantiate");
+  }
+  *out = graph.release();
+  return ok();
+}
+
+int si_hip_graph_launch(si_hip_context *ctx, const si_hip_graph *graph) {
+  if (!ctx || !graph) return fail(SI_HIP_ERR_NULL, "graph launch argument is null");
+  if (graph->device != ctx->device)
+    return fail(SI_HIP_ERR_RANGE, "graph was captured on device %d, context is on %d",
+                graph->device, ctx->device);
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  SIHIP_CHECK(hipGraphLaunch(graph->exec, ctx->stream), "graph launch");
+  ctx->async_submitted.fetch_add(graph->calls);
+  return ok();
+}
+
+uint64_t si_hip_graph_calls(const si_hip_graph *graph) { return graph ? graph->calls : 0; }
+
+void si_hip_graph_free(si_hip_graph *graph) {
+  if (!graph) return;
+  if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
+  if (graph->graph) (void)hipGraphDestroy(graph->graph);
+  delete graph;
 }
 
 int si_hip_set_kernel_policy(si_hip_context *ctx, uint32_t policy) {

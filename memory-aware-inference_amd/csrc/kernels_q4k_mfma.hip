@@ -37,8 +37,8 @@
 // Weights arrive by 16-byte buffer->LDS copies in piece-major order (LDS
 // byte 16 (16 q + r) is piece q of row r), so every read is a conflict-free
 // 16-lane sweep; a wave's next stage is in flight while it computes.  Only
-// the 16 lanes whose A rows carry digits read images (exec-masked; the other
-// lanes hold zeros for the whole kernel).  A wave leaves its stage's 16 row
+// the 16 lanes whose A rows carry digits read images, two blocks at a time
+// (exec-masked; the other lanes hold zeros for the whole kernel).  A wave leaves its stage's 16 row
 // partials in an LDS slot of the tile and counts them with an LDS atomic; the
 // wave that completes the tile sums the partials in stage order and stores
 // the rows, so results do not depend on timing.  With MATS = 2 (fused SwiGLU
@@ -106,9 +106,9 @@ __device__ __forceinline__ void lds_read_sums(uint32_t xb, uint32_t eb, u32x2 (&
       : "memory");
 }
 
-// The 16 A images of a stage (block b, MFMA t at addr + 1024 b + 256 t),
+// The 8 A images of two blocks (block b, MFMA t at addr + 1024 b + 256 t),
 // read only by the lanes in `mask`; the other lanes keep their registers.
-__device__ __forceinline__ void lds_read_images(uint32_t addr, uint64_t mask, i32x4 (&a)[16]) {
+__device__ __forceinline__ void lds_read_images8(uint32_t addr, uint64_t mask, i32x4 (&a)[8]) {
   uint64_t saved;
   asm volatile(
       "s_mov_b64 %[sv], exec\n"
@@ -121,19 +121,10 @@ __device__ __forceinline__ void lds_read_images(uint32_t addr, uint64_t mask, i3
       "ds_read_b128 %5, %[ad] offset:1280\n"
       "ds_read_b128 %6, %[ad] offset:1536\n"
       "ds_read_b128 %7, %[ad] offset:1792\n"
-      "ds_read_b128 %8, %[ad] offset:2048\n"
-      "ds_read_b128 %9, %[ad] offset:2304\n"
-      "ds_read_b128 %10, %[ad] offset:2560\n"
-      "ds_read_b128 %11, %[ad] offset:2816\n"
-      "ds_read_b128 %12, %[ad] offset:3072\n"
-      "ds_read_b128 %13, %[ad] offset:3328\n"
-      "ds_read_b128 %14, %[ad] offset:3584\n"
-      "ds_read_b128 %15, %[ad] offset:3840\n"
       "s_waitcnt lgkmcnt(0)\n"
       "s_mov_b64 exec, %[sv]"
       : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(a[4]), "+v"(a[5]), "+v"(a[6]),
-        "+v"(a[7]), "+v"(a[8]), "+v"(a[9]), "+v"(a[10]), "+v"(a[11]), "+v"(a[12]), "+v"(a[13]),
-        "+v"(a[14]), "+v"(a[15]), [sv] "=&s"(saved)
+        "+v"(a[7]), [sv] "=&s"(saved)
       : [ad] "v"(addr), [m] "s"(mask)
       : "memory");
 }
@@ -390,8 +381,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   const uint32_t npairs = sc.npairs;
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
-  auto issue = [&](uint32_t j) {
-    const Pair pr = pair_at(sc, wave + j * WAVES, tstages);
+  auto issue = [&](uint32_t j, const Pair& pr) {
     const uint32_t mat = MATS > 1 && pr.r >= nstages ? 1u : 0u, st = pr.r - mat * nstages;
     const uint32_t row0 = pr.tile * 16u;
     const uint32_t nrows = min(16u, rows - row0);
@@ -406,9 +396,12 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * i), 16,
                                                 voff + 64u * i, 0, 0, 0);
   };
+  // (with one stage in flight, the pair of the next stage, worked out when
+  // its copy is issued, is kept for its turn)
+  Pair pr_next = pair_at(sc, wave, tstages);
 #pragma unroll
   for (int j = 0; j < DEPTH; ++j)
-    if ((uint32_t)j < my_pairs) issue(j);
+    if ((uint32_t)j < my_pairs) issue(j, j == 0 ? pr_next : pair_at(sc, wave + j * WAVES, tstages));
 
   // 3. ring slots, then (once the x copies have landed) digit images, unit
   //    sums and exponents
@@ -439,11 +432,13 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   const uint32_t qb0 = hb0 + (QB == 5 ? 768u : 256u) + 512u * grp;
   // Q5_K: rotations that bring qh bits 2 grp / 2 grp + 1 of each byte to bit 4
   const uint32_t rot_lo = (28u + 2u * grp) & 31u, rot_hi = (29u + 2u * grp) & 31u;
-  i32x4 A[16];
+  // the images of two blocks at a time: the lanes that do not read them keep
+  // zeros, so the registers stay live through the loop (32 rather than 64)
+  i32x4 A[8];
 #pragma unroll
-  for (int t = 0; t < 16; ++t) A[t] = i32x4{0, 0, 0, 0};
+  for (int t = 0; t < 8; ++t) A[t] = i32x4{0, 0, 0, 0};
   for (uint32_t j = 0; j < my_pairs; ++j) {
-    const Pair pr = pair_at(sc, wave + j * WAVES, tstages);
+    const Pair pr = DEPTH == 1 ? pr_next : pair_at(sc, wave + j * WAVES, tstages);
     const uint32_t s = MATS > 1 && pr.r >= nstages ? pr.r - nstages : pr.r;  // stage
     const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
     if (DEPTH >= 3 && later >= 2u)
@@ -455,7 +450,11 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     const uint32_t buf = (j % DEPTH) * kStage;
     StageRegs<QB> v;
     v.read(hb0 + buf, qb0 + buf);
-    if (j + DEPTH < my_pairs) issue(j + DEPTH);  // the buffer just read is free again
+    if (j + DEPTH < my_pairs) {  // the buffer just read is free again
+      const Pair pn = pair_at(sc, wave + (j + DEPTH) * WAVES, tstages);
+      issue(j + DEPTH, pn);
+      if (DEPTH == 1) pr_next = pn;
+    }
     const uint32_t nlive = min(4u, nb - 4u * s);
     if constexpr (NTOK > 1) {
       // the stage's weights are decoded once and meet every vector in turn
@@ -466,7 +465,6 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       float rs[NTOK];
 #pragma unroll
       for (int t = 0; t < NTOK; ++t) {
-        lds_read_images(sbase + L.img + t * L.img_stride + 4096u * s + 16u * n, kActiveLanes, A);
         u32x2 xs[4];
         i32x4 ex;
         lds_read_sums(sbase + L.xsum + t * L.xsum_stride + 128u * s + 8u * grp,
@@ -474,13 +472,19 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
         float part[4];
         bool bad_any = false;
 #pragma unroll
-        for (int b = 0; b < 4; ++b) {
-          const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
-          const bool use = (uint32_t)b < nlive;
-          bad_any |= use && eb == kBadBlock;
-          const float c = block_dot(bw[b], A[4 * b], A[4 * b + 1], A[4 * b + 2], A[4 * b + 3],
-                                    xs[b], eb);
-          part[b] = (use && eb != kBadBlock) ? c : 0.0f;
+        for (int h = 0; h < 2; ++h) {
+          lds_read_images8(sbase + L.img + t * L.img_stride + 4096u * s + 2048u * h + 16u * n,
+                           kActiveLanes, A);
+#pragma unroll
+          for (int b2 = 0; b2 < 2; ++b2) {
+            const int b = 2 * h + b2;
+            const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
+            const bool use = (uint32_t)b < nlive;
+            bad_any |= use && eb == kBadBlock;
+            const float c = block_dot(bw[b], A[4 * b2], A[4 * b2 + 1], A[4 * b2 + 2],
+                                      A[4 * b2 + 3], xs[b], eb);
+            part[b] = (use && eb != kBadBlock) ? c : 0.0f;
+          }
         }
         if (bad_any) {
 #pragma unroll
@@ -494,20 +498,24 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       hand_off_tokens<NTOK>(sbase, L, sc.by_slots, pr, tstages, rs, lane, rows, y);
       continue;
     }
-    lds_read_images(sbase + L.img + 4096u * s + 16u * n, kActiveLanes, A);
     u32x2 xs[4];
     i32x4 ex;
     lds_read_sums(sbase + L.xsum + 128u * s + 8u * grp, sbase + L.expo + 16u * s, xs, ex);
     float part[4];
     bool bad_any = false;
 #pragma unroll
-    for (int b = 0; b < 4; ++b) {
-      const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
-      const bool use = (uint32_t)b < nlive;
-      bad_any |= use && eb == kBadBlock;
-      const float c = block_dot(v.decode(b, hi_units, bsh, rot_lo, rot_hi), A[4 * b],
-                                A[4 * b + 1], A[4 * b + 2], A[4 * b + 3], xs[b], eb);
-      part[b] = (use && eb != kBadBlock) ? c : 0.0f;
+    for (int h = 0; h < 2; ++h) {
+      lds_read_images8(sbase + L.img + 4096u * s + 2048u * h + 16u * n, kActiveLanes, A);
+#pragma unroll
+      for (int b2 = 0; b2 < 2; ++b2) {
+        const int b = 2 * h + b2;
+        const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
+        const bool use = (uint32_t)b < nlive;
+        bad_any |= use && eb == kBadBlock;
+        const float c = block_dot(v.decode(b, hi_units, bsh, rot_lo, rot_hi), A[4 * b2],
+                                  A[4 * b2 + 1], A[4 * b2 + 2], A[4 * b2 + 3], xs[b], eb);
+        part[b] = (use && eb != kBadBlock) ? c : 0.0f;
+      }
     }
     if (bad_any) {
 #pragma unroll

@@ -421,17 +421,6 @@ __device__ __forceinline__ void store_coherent(float* p, float v) {
 __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Takes a published sum, waiting (bounded) until its store has landed, and
-// marks the entry empty again.
-__device__ __forceinline__ float take_part(float* p) {
-  float v = load_coherent(p);
-  for (uint32_t spin = 0; __float_as_uint(v) == kPartEmpty && spin < (1u << 22); ++spin) {
-    __builtin_amdgcn_s_sleep(1);
-    v = load_coherent(p);
-  }
-  return v;
-}
-
 // Hands partial pr.r (of tparts = MATS * nparts per tile) of tile pr.tile to
 // the tile's LDS slot, waiting while an earlier tile still holds it.  The wave
 // that completes the workgroup's share of the tile sums that share in partial
@@ -472,34 +461,82 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
     // Publish the share's sums, then count the share; no fence orders the
     // two: the workgroup that completes the count waits for each entry to
     // leave the empty state.  Only read-modify-write atomics touch the counter.
+    // The tile's shares belong to workgroups g0..g1 (those with pairs of it);
+    // lane group k reads the entry of share g0 + k of each batch of four, the
+    // first batch before the count goes out, so the workgroup that completes
+    // it waits about one memory round trip for the other shares.
     const uint32_t t = pr.tile - sc.split_base;  // leftover tile index
     const uint32_t e = 2u * blockIdx.x + (t == sc.t_a ? 0u : 1u);
     if (grp == 0u) {
       store_coherent(ws.part + (e * MATS) * 16u + n, sum);
       if (MATS > 1) store_coherent(ws.part + (e * MATS + 1u) * 16u + n, sum2);
     }
+    const uint32_t g0 = range_of(sc, sa, t * tparts);
+    const uint32_t g1 = range_of(sc, sa, t * tparts + tparts - 1u);
+    // float offset of share wg's entry for this tile in ws.part, or kNoEntry
+    // when wg holds none of its pairs
+    constexpr uint32_t kNoEntry = 0xffffffffu;
+    auto entry = [&](uint32_t wg) -> uint32_t {
+      if (wg > g1) return kNoEntry;
+      const uint32_t wa = range_start(sc, sa, wg);
+      if (wa == range_start(sc, sa, wg + 1u)) return kNoEntry;  // no leftover pairs
+      const uint32_t t0 = quo(wa, sc.by_parts);
+      return (2u * wg + (t == t0 ? 0u : 1u)) * MATS * 16u + n;
+    };
+    // this workgroup's own share is taken from registers, not read back
+    auto fetch = [&](uint32_t off, uint32_t wg, float& v, float& v2) {
+      if (wg == blockIdx.x) {
+        v = sum;
+        if (MATS > 1) v2 = sum2;
+      } else if (off != kNoEntry) {
+        v = load_coherent(ws.part + off);
+        if (MATS > 1) v2 = load_coherent(ws.part + off + 16u);
+      }
+    };
+    uint32_t off = entry(g0 + grp);
+    float v = 0.0f, v2 = 0.0f;
+    fetch(off, g0 + grp, v, v2);
+    // (the count goes out after those reads, so waiting for it -- and for
+    // every older memory operation of the wave -- takes one round trip)
     uint32_t before = 0u;
     if (lane == 0u)
       before = __hip_atomic_fetch_add(ws.cnt + t, pr.hi - pr.lo, __ATOMIC_RELAXED,
                                       __HIP_MEMORY_SCOPE_AGENT);
     before = __builtin_amdgcn_readlane(before, 0);
     if (before + (pr.hi - pr.lo) == tparts) {
-      const uint32_t g0 = range_of(sc, sa, t * tparts);
-      const uint32_t g1 = range_of(sc, sa, t * tparts + tparts - 1u);
       float g = 0.0f, u = 0.0f;
-      if (grp == 0u) {
-        for (uint32_t wg = g0; wg <= g1; ++wg) {
-          const uint32_t wa = range_start(sc, sa, wg);
-          if (wa == range_start(sc, sa, wg + 1u)) continue;  // no leftover pairs
-          const uint32_t t0 = quo(wa, sc.by_parts);
-          float* pe = ws.part + (2u * wg + (t == t0 ? 0u : 1u)) * MATS * 16u + n;
-          g += take_part(pe);
-          if (MATS > 1) u += take_part(pe + 16u);
-          store_coherent(pe, __uint_as_float(kPartEmpty));
-          if (MATS > 1) store_coherent(pe + 16u, __uint_as_float(kPartEmpty));
+      for (uint32_t base = g0; base <= g1; base += 4u) {
+        const uint32_t wg = base + grp;
+        if (base != g0) {
+          off = entry(wg);
+          fetch(off, wg, v, v2);
         }
-        if (row < rows) y[row] = MATS > 1 ? silu_times(g, u) : g;
+        // wait (bounded) until every entry of the batch has landed
+        for (uint32_t spin = 0; spin < (1u << 22); ++spin) {
+          const bool missing = off != kNoEntry && wg != blockIdx.x &&
+                               (__float_as_uint(v) == kPartEmpty ||
+                                (MATS > 1 && __float_as_uint(v2) == kPartEmpty));
+          if (!__builtin_amdgcn_ballot_w64(missing)) break;
+          __builtin_amdgcn_s_sleep(1);
+          if (missing) fetch(off, wg, v, v2);
+        }
+        // add the batch in workgroup order (lane group 0 keeps the sums)
+        const uint64_t have = __builtin_amdgcn_ballot_w64(off != kNoEntry);
+#pragma unroll
+        for (uint32_t k = 0; k < 4u; ++k) {
+          const float vk = __shfl(v, (int)(n + 16u * k), 64);
+          const float v2k = MATS > 1 ? __shfl(v2, (int)(n + 16u * k), 64) : 0.0f;
+          if ((have >> (16u * k)) & 1u) {
+            g += vk;
+            if (MATS > 1) u += v2k;
+          }
+        }
+        if (off != kNoEntry) {
+          store_coherent(ws.part + off, __uint_as_float(kPartEmpty));
+          if (MATS > 1) store_coherent(ws.part + off + 16u, __uint_as_float(kPartEmpty));
+        }
       }
+      if (grp == 0u && row < rows) y[row] = MATS > 1 ? silu_times(g, u) : g;
       if (lane == 0u)
         (void)__hip_atomic_exchange(ws.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

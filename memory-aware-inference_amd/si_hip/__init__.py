@@ -111,6 +111,11 @@ _SIGS = {
     "si_hip_event_record": (_I, [_P, _U32]),
     "si_hip_event_elapsed_ms": (_I, [_P, _U32, _U32, C.POINTER(C.c_float)]),
     "si_hip_quant_matvec_device_repeat": (_I, [_P, C.POINTER(_P), _SZ, _SZ, _SZ, _P, _P, _SZ]),
+    "si_hip_capture_begin": (_I, [_P]),
+    "si_hip_capture_end": (_I, [_P, C.POINTER(_P)]),
+    "si_hip_graph_launch": (_I, [_P, _P]),
+    "si_hip_graph_calls": (_U64, [_P]),
+    "si_hip_graph_free": (None, [_P]),
     "si_hip_set_kernel_policy": (_I, [_P, _U32]),
     "si_hip_current_allocated_bytes": (_U64, [_P]),
     "si_hip_peak_allocated_bytes": (_U64, [_P]),
@@ -246,6 +251,32 @@ class QuantWeight:
         if self._h:
             lib().si_hip_quant_weight_free(self._h)
             self._h = C.c_void_p()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class HipGraph:
+    """Device calls recorded by HipContext.capture_begin/capture_end."""
+
+    def __init__(self, ctx: "HipContext", handle: C.c_void_p):
+        self._ctx = ctx
+        self.handle = handle
+
+    @property
+    def calls(self) -> int:
+        return int(lib().si_hip_graph_calls(self.handle))
+
+    def launch(self) -> None:
+        _check(lib().si_hip_graph_launch(self._ctx._h, self.handle))
+
+    def free(self) -> None:
+        if self.handle:
+            lib().si_hip_graph_free(self.handle)
+            self.handle = None
 
     def __del__(self):
         try:
@@ -465,6 +496,16 @@ class HipContext:
         ms = C.c_float()
         _check(lib().si_hip_event_elapsed_ms(self._h, a, b, C.byref(ms)))
         return float(ms.value)
+
+    # ---- captured submission
+    def capture_begin(self) -> None:
+        """Record the following *_device calls into a graph instead of running them."""
+        _check(lib().si_hip_capture_begin(self._h))
+
+    def capture_end(self) -> "HipGraph":
+        g = C.c_void_p()
+        _check(lib().si_hip_capture_end(self._h, C.byref(g)))
+        return HipGraph(self, g)
 
     # ---- telemetry
     def current_allocated_bytes(self) -> int:

@@ -564,3 +564,99 @@ def test_matvec_unit_vectors_pick_each_column(hip_ctx, t):
                         float(dq[np.argmax(err - tol), k])))
     cols_bad = sorted({b[0] for b in bad})
     assert bad == [], f"{len(bad)} columns wrong: {cols_bad}; first: {bad[:4]}"
+
+
+# ---- captured submission (HIP graphs) ----------------------------------------------
+def test_graph_replay_matches_eager(hip_ctx):
+    """A decode-like sequence -- Q4_K matvec on a split launch (17408 x 5120),
+    fused gate/up, Q6_K down, Q6_K head + argmax -- recorded once and replayed
+    several times, with eager calls and synchronisations between the replays:
+    every replay equals the eager run bit for bit, and the combine workspace is
+    left clean (an eager split launch afterwards still matches)."""
+    import ctypes as C
+    lib = si_hip.lib()
+    cols, rows, inter, vocab = 5120, 17408, 1024, 20011
+    log("graph replay: building weights")
+    wq = si_hip.synth_matrix(12, seed=3001, rows=rows, cols=cols, threads=8)
+    wg = si_hip.synth_matrix(12, seed=3002, rows=inter, cols=cols, threads=8)
+    wu = si_hip.synth_matrix(12, seed=3003, rows=inter, cols=cols, threads=8)
+    wd = si_hip.synth_matrix(14, seed=3004, rows=cols, cols=inter, threads=8)
+    wh = si_hip.synth_matrix(14, seed=3005, rows=vocab, cols=cols, threads=8)
+    Wq, Wg, Wu, Wd, Wh = (hip_ctx.upload_quant_weight_private(w, t) for w, t in
+                          ((wq, 12), (wg, 12), (wu, 12), (wd, 14), (wh, 14)))
+    x = si_hip.synth_normal(3006, cols)
+    d_x = hip_ctx.device_alloc(cols * 4)
+    d_y = hip_ctx.device_alloc(rows * 4)
+    d_h = hip_ctx.device_alloc(inter * 4)
+    d_o = hip_ctx.device_alloc(cols * 4)
+    d_l = hip_ctx.device_alloc(vocab * 4)
+    d_r = hip_ctx.device_alloc(8)
+    d_e = hip_ctx.device_alloc(cols * 4)  # eager work between replays
+    hip_ctx.to_device(d_x, x)
+    h = hip_ctx.handle
+    P = C.c_void_p
+
+    def enqueue():
+        for rc in (
+            lib.si_hip_quant_matvec_device(h, Wq.handle, rows, cols, P(d_x), P(d_y)),
+            lib.si_hip_q4_k_fused_gate_up_device(h, Wg.handle, Wu.handle, inter, cols, P(d_x),
+                                                 P(d_h)),
+            lib.si_hip_quant_matvec_device(h, Wd.handle, cols, inter, P(d_h), P(d_o)),
+            lib.si_hip_matvec_argmax_device(h, Wh.handle, vocab, cols, P(d_x),
+                                            si_hip.ARGMAX_LAST_FINITE, P(d_l), P(d_r)),
+        ):
+            assert rc == 0, si_hip.last_error()
+
+    def results():
+        hip_ctx.synchronize()
+        return (hip_ctx.from_device(d_y, rows), hip_ctx.from_device(d_h, inter),
+                hip_ctx.from_device(d_o, cols), hip_ctx.from_device(d_l, vocab),
+                hip_ctx.from_device(d_r, 1, np.uint64))
+
+    def clear():
+        for p, n in ((d_y, rows), (d_h, inter), (d_o, cols), (d_l, vocab)):
+            hip_ctx.to_device(p, np.full(n, np.nan, np.float32))
+        hip_ctx.to_device(d_r, np.zeros(1, np.uint64))
+
+    enqueue()
+    ref = results()
+    _, y64, ab = O.matvec(12, wq, rows, cols, x, threads=8)
+    assert_dot_close(ref[0], y64, ab, what="eager split matvec")
+
+    log("graph replay: capture")
+    hip_ctx.capture_begin()
+    enqueue()
+    graph = hip_ctx.capture_end()
+    assert graph.calls == 4
+    for rep in range(3):
+        clear()
+        # eager work on the same context between replays
+        assert lib.si_hip_quant_matvec_device(h, Wd.handle, cols, inter, P(d_h), P(d_e)) == 0
+        hip_ctx.synchronize()
+        log(f"graph replay {rep}")
+        graph.launch()
+        got = results()
+        for a, b in zip(got[:4], ref[:4]):
+            assert same_bits(a, b), f"replay {rep} differs"
+        assert got[4][0] == ref[4][0]
+    graph.free()
+    clear()
+    enqueue()
+    again = results()
+    for a, b in zip(again[:4], ref[:4]):
+        assert same_bits(a, b)
+    for p in (d_x, d_y, d_h, d_o, d_l, d_r, d_e):
+        hip_ctx.device_free(p)
+
+
+def test_graph_capture_state_errors(hip_ctx):
+    with pytest.raises(si_hip.HipError):
+        hip_ctx.capture_end()
+    hip_ctx.capture_begin()
+    try:
+        with pytest.raises(si_hip.HipError):
+            hip_ctx.capture_begin()
+    finally:
+        g = hip_ctx.capture_end()
+    assert g.calls == 0
+    g.free()
