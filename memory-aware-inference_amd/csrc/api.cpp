@@ -41,6 +41,23 @@ int ok() {
   return SI_HIP_OK;
 }
 
+}  // namespace
+
+namespace sihip {
+int set_error(int status, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return status;
+}
+int clear_error() { return ok(); }
+}  // namespace sihip
+
+namespace {
+
 size_t block_bytes_of(uint32_t t) {
   switch (t) {
     case SI_HIP_GGML_TYPE_Q4_K: return 144;

@@ -37,7 +37,7 @@ STATUS = {
     -3: "SI_HIP_ERR_BYTE_LENGTH", -4: "SI_HIP_ERR_OVERFLOW",
     -5: "SI_HIP_ERR_UNSUPPORTED_TYPE", -6: "SI_HIP_ERR_BATCH", -7: "SI_HIP_ERR_RANGE",
     -8: "SI_HIP_ERR_NO_FINITE", -9: "SI_HIP_ERR_DEVICE", -10: "SI_HIP_ERR_OUT_OF_MEMORY",
-    -11: "SI_HIP_ERR_EMPTY",
+    -11: "SI_HIP_ERR_EMPTY", -12: "SI_HIP_ERR_STATE",
 }
 
 
@@ -51,6 +51,18 @@ class HipError(RuntimeError):
 class CommandStats(C.Structure):
     _fields_ = [("submitted", C.c_uint64), ("async_submitted", C.c_uint64),
                 ("waited", C.c_uint64), ("wait_nanos", C.c_uint64)]
+
+
+class GgufValueC(C.Structure):
+    _fields_ = [("type", C.c_uint32), ("array_type", C.c_uint32), ("count", C.c_uint64),
+                ("u64", C.c_uint64), ("i64", C.c_int64), ("f64", C.c_double),
+                ("str", C.c_char_p), ("node", C.c_void_p)]
+
+
+class GgufTensorC(C.Structure):
+    _fields_ = [("name", C.c_char_p), ("n_dims", C.c_uint32), ("ggml_type", C.c_uint32),
+                ("shape", C.POINTER(C.c_uint64)), ("offset", C.c_uint64),
+                ("data_start", C.c_uint64), ("data_end", C.c_uint64)]
 
 
 _P = C.c_void_p
@@ -122,6 +134,26 @@ _SIGS = {
     "si_hip_peak_active_weight_bytes": (_U64, [_P]),
     "si_hip_reset_peaks": (None, [_P]),
     "si_hip_get_command_stats": (_I, [_P, C.POINTER(CommandStats)]),
+    # si_hip_gguf.h
+    "si_hip_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
+    "si_hip_gguf_parse": (_I, [_BP, _SZ, C.POINTER(_P)]),
+    "si_hip_gguf_close": (None, [_P]),
+    "si_hip_gguf_version": (_U32, [_P]),
+    "si_hip_gguf_alignment": (_U64, [_P]),
+    "si_hip_gguf_data_base": (_U64, [_P]),
+    "si_hip_gguf_file_bytes": (_U64, [_P]),
+    "si_hip_gguf_tensor_count": (_U64, [_P]),
+    "si_hip_gguf_tensor_info": (_I, [_P, _U64, C.POINTER(GgufTensorC)]),
+    "si_hip_gguf_find_tensor": (_I, [_P, C.c_char_p, C.POINTER(_U64)]),
+    "si_hip_gguf_tensor_data": (_I, [_P, _U64, C.POINTER(_BP), C.POINTER(_U64)]),
+    "si_hip_gguf_tensor_elements": (_I, [_P, _U64, C.POINTER(_U64)]),
+    "si_hip_gguf_expected_payload_bytes": (_I, [_P, _U64, C.POINTER(_U64), C.POINTER(_I)]),
+    "si_hip_gguf_metadata_count": (_U64, [_P]),
+    "si_hip_gguf_metadata_key": (_I, [_P, _U64, C.POINTER(C.c_char_p)]),
+    "si_hip_gguf_metadata_get": (_I, [_P, C.c_char_p, C.POINTER(GgufValueC)]),
+    "si_hip_gguf_value_item": (_I, [C.POINTER(GgufValueC), _U64, C.POINTER(GgufValueC)]),
+    "si_hip_gguf_upload_tensor": (_I, [_P, _P, _U64, C.POINTER(_P)]),
+    "si_hip_gguf_bind_tensor_mapped": (_I, [_P, _P, _U64, C.POINTER(_P)]),
     # si_hip_synth.h
     "si_hip_synth_blocks": (_I, [_U32, _U64, _U64, _SZ, _BP, _SZ, _I]),
     "si_hip_synth_normal_f32": (_I, [_U64, _U64, _SZ, C.c_float, _FP]),
@@ -530,3 +562,259 @@ class HipContext:
             self.close()
         except Exception:
             pass
+
+
+# ---- GGUF model store (include/si_hip_gguf.h) ---------------------------------
+GGUF_TYPE_NAMES = ("U8", "I8", "U16", "I16", "U32", "I32", "F32", "Bool", "String", "Array",
+                   "U64", "I64", "F64")
+
+
+class GgufValue:
+    """A metadata value with its GGUF type (GgufValue, src/model.rs:304-318)."""
+
+    __slots__ = ("type", "value")
+
+    def __init__(self, type_: int, value):
+        self.type = type_
+        self.value = value
+
+    def __eq__(self, other):
+        if not isinstance(other, GgufValue):
+            return NotImplemented
+        return self.type == other.type and self.value == other.value
+
+    def __repr__(self):
+        """Rust's derived Debug form: U32(32), F32(1e-6), String("qwen35")."""
+        if self.type in (6, 12):
+            body = _debug_float(self.value, self.type == 6)
+        elif self.type == 7:
+            body = "true" if self.value else "false"
+        elif self.type == 8:
+            body = _debug_str(self.value)
+        elif self.type == 9:
+            body = "[" + ", ".join(repr(v) for v in self.value) + "]"
+        else:
+            body = str(self.value)
+        return f"{GGUF_TYPE_NAMES[self.type]}({body})"
+
+
+def _debug_float(v: float, single: bool) -> str:
+    """Debug formatting of an f32/f64: shortest round-trip digits, positional
+    with at least one fractional digit for 1e-4 <= |v| < 1e16 (and zero),
+    scientific ("1e-6", "1.5e16") otherwise."""
+    if v != v:
+        return "NaN"
+    if v in (float("inf"), float("-inf")):
+        return "inf" if v > 0 else "-inf"
+    x = np.float32(v) if single else np.float64(v)
+    a = abs(float(v))
+    if a == 0.0 or 1e-4 <= a < 1e16:
+        return np.format_float_positional(x, unique=True, trim="0")
+    mant, exp = np.format_float_scientific(x, unique=True, trim="-").split("e")
+    return f"{mant}e{int(exp)}"
+
+
+def _debug_str(v: str) -> str:
+    """A string in Rust's Debug form: double quotes, backslash escapes for
+    quote, backslash, tab, CR, LF and NUL, \\u{..} for other unprintables."""
+    out = ['"']
+    for ch in v:
+        if ch in '"\\':
+            out.append("\\" + ch)
+        elif ch == "\n":
+            out.append("\\n")
+        elif ch == "\r":
+            out.append("\\r")
+        elif ch == "\t":
+            out.append("\\t")
+        elif ch == "\0":
+            out.append("\\0")
+        elif not ch.isprintable():
+            out.append("\\u{%x}" % ord(ch))
+        else:
+            out.append(ch)
+    out.append('"')
+    return "".join(out)
+
+
+def _gguf_value(v: GgufValueC) -> GgufValue:
+    t = v.type
+    if t in (0, 2, 4, 10):
+        return GgufValue(t, int(v.u64))
+    if t in (1, 3, 5, 11):
+        return GgufValue(t, int(v.i64))
+    if t in (6, 12):
+        return GgufValue(t, float(v.f64))
+    if t == 7:
+        return GgufValue(t, bool(v.u64))
+    if t == 8:
+        return GgufValue(t, C.string_at(v.str, v.count).decode("utf-8"))
+    items = []
+    for i in range(v.count):
+        it = GgufValueC()
+        _check(lib().si_hip_gguf_value_item(C.byref(v), i, C.byref(it)))
+        items.append(_gguf_value(it))
+    return GgufValue(t, items)
+
+
+class GgufTensorInfo:
+    """One tensor of a GGUF index (GgufTensorInfo, src/model.rs:498-505)."""
+
+    __slots__ = ("index", "name", "shape", "ggml_type", "offset", "data_start", "data_end")
+
+    def __init__(self, index, name, shape, ggml_type, offset, data_start, data_end):
+        self.index, self.name, self.shape, self.ggml_type = index, name, shape, ggml_type
+        self.offset, self.data_start, self.data_end = offset, data_start, data_end
+
+    def byte_len(self) -> int:
+        return self.data_end - self.data_start
+
+    def element_count(self) -> int | None:
+        """The product of the dimensions, None when it overflows 64 bits
+        (the reference's "element count overflows" error)."""
+        n = 1
+        for d in self.shape:
+            n *= d
+            if n >= 1 << 64:
+                return None
+        return n
+
+    def is_q4_k(self) -> bool:
+        return self.ggml_type == GGML_TYPE_Q4_K
+
+
+class GgufFile:
+    """GgufModelStore (src/model.rs:583-681) over the C store: a read-only
+    mapping of the file (or a copy of given bytes), its metadata and tensor
+    index, tensor byte views and uploads of K-quant tensors to HBM."""
+
+    def __init__(self, path: str | os.PathLike | None = None, data: bytes | None = None):
+        h = C.c_void_p()
+        if (path is None) == (data is None):
+            raise ValueError("give exactly one of path and data")
+        if path is not None:
+            _check(lib().si_hip_gguf_open(os.fsencode(path), C.byref(h)))
+        else:
+            b = _u8(data)
+            _check(lib().si_hip_gguf_parse(_bp(b), b.size, C.byref(h)))
+        self._h = h
+        self.path = None if path is None else str(path)
+        n = int(lib().si_hip_gguf_tensor_count(h))
+        self.tensor_list = []
+        for i in range(n):
+            t = GgufTensorC()
+            _check(lib().si_hip_gguf_tensor_info(h, i, C.byref(t)))
+            self.tensor_list.append(GgufTensorInfo(
+                i, t.name.decode("utf-8"), tuple(t.shape[k] for k in range(t.n_dims)),
+                t.ggml_type, t.offset, t.data_start, t.data_end))
+        # name -> info; a repeated name keeps its last tensor, like the reference's map
+        self.tensors = {t.name: t for t in self.tensor_list}
+        self.metadata = {}
+        for i in range(int(lib().si_hip_gguf_metadata_count(h))):
+            key = C.c_char_p()
+            _check(lib().si_hip_gguf_metadata_key(h, i, C.byref(key)))
+            v = GgufValueC()
+            _check(lib().si_hip_gguf_metadata_get(h, key.value, C.byref(v)))
+            self.metadata[key.value.decode("utf-8")] = _gguf_value(v)
+
+    @property
+    def handle(self) -> C.c_void_p:
+        return self._h
+
+    @property
+    def version(self) -> int:
+        return int(lib().si_hip_gguf_version(self._h))
+
+    @property
+    def alignment(self) -> int:
+        return int(lib().si_hip_gguf_alignment(self._h))
+
+    @property
+    def data_base(self) -> int:
+        return int(lib().si_hip_gguf_data_base(self._h))
+
+    def _index(self, name: str) -> int:
+        i = C.c_uint64()
+        _check(lib().si_hip_gguf_find_tensor(self._h, name.encode("utf-8"), C.byref(i)))
+        return int(i.value)
+
+    def tensor(self, name: str) -> tuple[GgufTensorInfo, np.ndarray]:
+        """GgufModelStore::tensor: the info and a copy of the tensor's bytes."""
+        i = self._index(name)
+        p = C.POINTER(C.c_uint8)()
+        n = C.c_uint64()
+        _check(lib().si_hip_gguf_tensor_data(self._h, i, C.byref(p), C.byref(n)))
+        data = np.ctypeslib.as_array(p, shape=(int(n.value),)).copy() if n.value else \
+            np.empty(0, np.uint8)
+        return self.tensor_list[i], data
+
+    def element_count(self, name: str) -> int:
+        out = C.c_uint64()
+        _check(lib().si_hip_gguf_tensor_elements(self._h, self._index(name), C.byref(out)))
+        return int(out.value)
+
+    def expected_payload_bytes(self, name: str) -> int | None:
+        out, known = C.c_uint64(), C.c_int()
+        _check(lib().si_hip_gguf_expected_payload_bytes(self._h, self._index(name), C.byref(out),
+                                                        C.byref(known)))
+        return int(out.value) if known.value else None
+
+    def upload(self, ctx: "HipContext", name: str, mapped: bool = False) -> "QuantWeight":
+        """The K-quant tensor's payload as a QuantWeight in HBM."""
+        w = C.c_void_p()
+        fn = lib().si_hip_gguf_bind_tensor_mapped if mapped else lib().si_hip_gguf_upload_tensor
+        _check(fn(ctx.handle, self._h, self._index(name), C.byref(w)))
+        return QuantWeight(ctx, w.value)
+
+    def inspect(self, model: str | None = None) -> str:
+        """The dump si-gguf-inspect prints (src/bin/si-gguf-inspect.rs:11-60)."""
+        lines = [f"model={model or self.path}", f"tensors={len(self.tensors)}"]
+        by_name = sorted(self.tensors.values(), key=lambda t: t.name.encode("utf-8"))
+        for t in [t for t in by_name if t.is_q4_k()][:12]:
+            lines.append(f"q4_k_tensor={t.name} shape={list(t.shape)} bytes={t.byte_len()} "
+                         f"elements={t.element_count() or 0}")
+        counts = {}
+        for t in by_name:
+            counts[t.ggml_type] = counts.get(t.ggml_type, 0) + 1
+        lines.append("tensor_type_counts={" + ", ".join(
+            f"{k}: {v}" for k, v in sorted(counts.items())) + "}")
+        for name in ("token_embd.weight", "output.weight", "output_norm.weight"):
+            t = self.tensors.get(name)
+            if t is not None:
+                lines.append(f"special_tensor={name} type={t.ggml_type} shape={list(t.shape)} "
+                             f"bytes={t.byte_len()}")
+        for t in [t for t in by_name if not t.is_q4_k()][:24]:
+            lines.append(f"non_q4_tensor={t.name} type={t.ggml_type} shape={list(t.shape)} "
+                         f"bytes={t.byte_len()}")
+        for key in sorted(self.metadata, key=lambda k: k.encode("utf-8")):
+            lines.append(f"metadata.{key}={_summarize(self.metadata[key])}")
+        return "\n".join(lines)
+
+    def close(self) -> None:
+        if self._h:
+            lib().si_hip_gguf_close(self._h)
+            self._h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def _summarize(v: GgufValue) -> str:
+    """summarize() of si-gguf-inspect (src/bin/si-gguf-inspect.rs:86-101)."""
+    if v.type == 9:
+        preview = ", ".join(_summarize(x) for x in v.value[:3])
+        return f"array(len={len(v.value)}, first=[{preview}])"
+    if v.type == 8:
+        if len(v.value.encode("utf-8")) > 160:
+            return f"string(len={len(v.value.encode('utf-8'))}, prefix={_debug_str(v.value[:160])})"
+        return f"string({_debug_str(v.value)})"
+    return repr(v)
