@@ -403,12 +403,15 @@ int si_hip_context_new(int device_ordinal, si_hip_context **out) {
   for (auto &ev : ctx->events) SIHIP_CHECK(hipEventCreate(&ev), "event create");
   {
     void *p = nullptr;
-    if (hipMalloc(&p, sihip::kWorkspaceBytes) != hipSuccess)
+    constexpr size_t total = sihip::kWorkspaceBytes + sihip::kWorkspaceScratchBytes;
+    if (hipMalloc(&p, total) != hipSuccess)
       return fail(SI_HIP_ERR_OUT_OF_MEMORY, "HIP could not allocate the %zu-byte workspace",
-                  sihip::kWorkspaceBytes);
+                  total);
     ctx->ws.ptr = p;
     ctx->ws.bytes = sihip::kWorkspaceBytes;
-    ctx->tel->note_alloc(sihip::kWorkspaceBytes);
+    ctx->ws.scratch = reinterpret_cast<float *>(static_cast<uint8_t *>(p) + sihip::kWorkspaceBytes);
+    ctx->ws.scratch_bytes = sihip::kWorkspaceScratchBytes;
+    ctx->tel->note_alloc(total);
     // counters zero, entries empty; set on the context's own (non-blocking)
     // stream before any kernel
     SIHIP_CHECK(hipMemsetAsync(p, 0, sihip::kWorkspaceCounterBytes, ctx->stream),
@@ -431,7 +434,7 @@ void si_hip_context_free(si_hip_context *ctx) {
   for (void *p : {ctx->stage_in, ctx->stage_out, ctx->stage_weights, ctx->stage_aux, ctx->ws.ptr})
     if (p) (void)hipFree(p);
   ctx->tel->note_free(ctx->stage_in_bytes + ctx->stage_out_bytes + ctx->stage_weights_bytes +
-                      ctx->stage_aux_bytes + ctx->ws.bytes);
+                      ctx->stage_aux_bytes + ctx->ws.bytes + ctx->ws.scratch_bytes);
   for (auto &ev : ctx->events)
     if (ev) (void)hipEventDestroy(ev);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);

@@ -530,6 +530,551 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   }
 }
 
+// ---- Several activation vectors in the MFMA rows --------------------------
+//
+// For a pass over the weights with 2..4 activation vectors (matmul-many,
+// replacing si_q4_k_matmul_many, metal.rs:1052-1262) the vectors share the A
+// operand of v_mfma_i32_16x16x32_i8, whose K = 32 is exactly one unit:
+//
+//  * A row 4 t + d holds digit d of vector t over the unit's 32 activations
+//    (lane 16 g + m supplies activations 8 g .. 8 g + 7 of row m); vectors
+//    past the pass's count are zero.
+//  * B lane (g, n) holds weights 8 g .. 8 g + 7 of the unit for tile row n:
+//    the low (unit 2 j) or high (unit 2 j + 1) nibbles of qs bytes
+//    32 j + 8 g .. 32 j + 8 g + 7.
+//  * Result lane (g, n) holds the four digit sums of vector g and row n, so
+//    T_d = sum_u sc_u C_u[d] over the block's eight units and the row's dot
+//    stay in that lane: y_g[n] += d * (sum_d T_d 256^d) * 2^(e_gb - 30) -
+//    dmin * sum_u m_u X_gu, with X_gu the f32 sum of vector g's unit u.
+//
+// Group images (4 KB per block, in the place of the four vectors' copies):
+// block b at img + 4096 b, unit pair p at + 1024 p, lane l at + 16 l, units
+// 2 p and 2 p + 1 in its two 8-byte halves.
+//
+// K slices.  Four vectors' images of a whole row (4 KB per block) would
+// crowd the stage buffers out of LDS, and with them the bytes in flight.  So
+// a launch with S > 1 cuts K into its S stages: GS workgroups per stage,
+// workgroup g works on stage k = g / GS for tiles g % GS, g % GS + GS, ...,
+// and keeps the images of that stage only.  Each pair is then its
+// workgroup's whole share of a tile: the wave publishes the 4 x 16 sums in
+// the workspace (entry tile * S + k), counts them on the tile's counter, and
+// the wave that completes the count adds the S entries in stage order and
+// stores the rows (deterministic).  With S == 1 a workgroup keeps the whole
+// row's images and sums a tile's stages in its LDS slot ring.
+
+// The image blocks a wave owns: group-blocks q = wave, wave + WAVES, ... of
+// the ng x nbl of a launch (group q / nbl, local block q % nbl), walked
+// without a division.
+template <int WAVES, typename F>
+__device__ __forceinline__ void for_group_blocks(uint32_t ng, uint32_t nbl, uint32_t wave, F f) {
+  uint32_t g = 0u, i = wave;
+  while (i >= nbl && g < ng) {
+    i -= nbl;
+    ++g;
+  }
+  for (; g < ng;) {
+    f(g, i);
+    i += WAVES;
+    while (i >= nbl && g < ng) {
+      i -= nbl;
+      ++g;
+    }
+  }
+}
+
+// Copies of the vectors' blocks blk0 .. blk0 + nbl - 1: vector 4 g + t's
+// block blk0 + i at img + 4096 (g nbl + i) + 1024 t; the slots of vectors past
+// ntok are cleared.
+template <int WAVES>
+__device__ __forceinline__ void copy_x_group(uint8_t* smem, uint32_t img, const float* x,
+                                             uint32_t nb, uint32_t blk0, uint32_t nbl,
+                                             uint32_t ng, uint32_t ntok, uint32_t wave,
+                                             uint32_t lane) {
+  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<float*>(x), 0, (int)(ntok * nb * 1024u), kBufferWord3);
+  for_group_blocks<WAVES>(ng, nbl, wave, [&](uint32_t g, uint32_t i) {
+    const uint32_t dst = img + 4096u * (g * nbl + i);
+#pragma unroll
+    for (uint32_t t = 0; t < 4u; ++t) {
+      const uint32_t v = 4u * g + t;
+      if (v < ntok)
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(smem + dst + 1024u * t), 16,
+                                                  (v * nb + blk0 + i) * 1024u + 16u * lane, 0, 0,
+                                                  0);
+      else
+        lds_write_b128((uint32_t)(uintptr_t)smem + dst + 1024u * t + 16u * lane,
+                       u32x4{0u, 0u, 0u, 0u});
+    }
+  });
+}
+
+// Group images, exponents and unit sums of the copied blocks, in place: a
+// wave converts exactly the group-blocks it copied; lane (t, c) takes
+// elements 16 c .. 16 c + 15 of vector 4 g + t.  Blocks follow build_images'
+// rules (exponent kBadBlock for blocks that must take the exact path).
+template <int WAVES>
+__device__ __forceinline__ void build_group_images(uint32_t sbase, const Layout& L, uint32_t nbl,
+                                                   uint32_t ng, uint32_t wave, uint32_t lane) {
+  const uint32_t t = lane >> 4, c = lane & 15u;
+  const uint32_t u = c >> 1;                                  // unit of the lane's chunk
+  const uint32_t g0 = 2u * (c & 1u);                          // K slice of its first 8
+  const uint32_t woff = 1024u * (u >> 1) + 16u * (16u * g0 + 4u * t) + 8u * (u & 1u);
+  for_group_blocks<WAVES>(ng, nbl, wave, [&](uint32_t g, uint32_t b) {
+    const uint32_t blk = sbase + L.img + 4096u * (g * nbl + b);
+    const uint32_t v = 4u * g + t;  // the lane's vector
+    u32x4 xq[4];
+    lds_read4<16>(blk + 1024u * t + 64u * c, xq);
+    float xv[16];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xv[4 * k + i] = __uint_as_float(xq[k][i]);
+    float amax = 0.0f, xsum = 0.0f;
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const float av = fabsf(xv[k]);
+      amax = fmaxf(amax, av);
+      bad |= !(av < 0x1p100f);
+      xsum += xv[k];
+    }
+    const float cmax = amax;
+    amax = fmaxf(amax, dpp<kRowShr1>(amax));
+    amax = fmaxf(amax, dpp<kRowShr2>(amax));
+    amax = fmaxf(amax, dpp<kRowShr4>(amax));
+    amax = fmaxf(amax, dpp<kRowShr8>(amax));
+    amax = dpp<kRowBcast15>(amax);
+    bad |= cmax > 0.0f && cmax < amax * 0x1p-13f;
+    const int e = __builtin_amdgcn_frexp_expf(amax);
+    uint32_t uq[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      uq[k] = (uint32_t)__float2int_rn(__builtin_amdgcn_ldexpf(xv[k], kFixBits - e)) + 0x80808080u;
+    uint32_t dg[4][4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      transpose_digits(uq[4 * k], uq[4 * k + 1], uq[4 * k + 2], uq[4 * k + 3], dg[k]);
+    // the wave has read the whole block (lds_read4 waits) before any write
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      lds_write_b64(blk + woff + 16u * d, u32x2{dg[0][d], dg[1][d]});
+      lds_write_b64(blk + woff + 16u * d + 256u, u32x2{dg[2][d], dg[3][d]});
+    }
+    xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit c / 2
+    if (c & 1u)
+      lds_write_b32(sbase + L.xsum + v * L.xsum_stride + 32u * b + 4u * u, __float_as_uint(xsum));
+    const bool bad_blk = (__builtin_amdgcn_ballot_w64(bad) >> (16u * t)) & 0xffffull;
+    if (c == 0u)
+      lds_write_b32(sbase + L.expo + v * L.expo_stride + 4u * b,
+                    (uint32_t)(bad_blk ? kBadBlock : e - kFixBits));
+  });
+}
+
+// Headers and the lane's four 8-byte qs slices of the four blocks of a stage
+// buffer: header of block b at hb + 2304 b, slice j at qb + 2304 b + 512 j.
+__device__ __forceinline__ void lds_read_weights_tok(uint32_t hb, uint32_t qb, u32x4 (&h)[4],
+                                                     u32x2 (&q)[16]) {
+  asm volatile(
+      "ds_read_b128 %0, %20\n"
+      "ds_read_b64 %4, %21\n"
+      "ds_read_b64 %5, %21 offset:512\n"
+      "ds_read_b64 %6, %21 offset:1024\n"
+      "ds_read_b64 %7, %21 offset:1536\n"
+      "ds_read_b128 %1, %20 offset:2304\n"
+      "ds_read_b64 %8, %21 offset:2304\n"
+      "ds_read_b64 %9, %21 offset:2816\n"
+      "ds_read_b64 %10, %21 offset:3328\n"
+      "ds_read_b64 %11, %21 offset:3840\n"
+      "ds_read_b128 %2, %20 offset:4608\n"
+      "ds_read_b64 %12, %21 offset:4608\n"
+      "ds_read_b64 %13, %21 offset:5120\n"
+      "ds_read_b64 %14, %21 offset:5632\n"
+      "ds_read_b64 %15, %21 offset:6144\n"
+      "ds_read_b128 %3, %20 offset:6912\n"
+      "ds_read_b64 %16, %21 offset:6912\n"
+      "ds_read_b64 %17, %21 offset:7424\n"
+      "ds_read_b64 %18, %21 offset:7936\n"
+      "ds_read_b64 %19, %21 offset:8448\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(h[0]), "=&v"(h[1]), "=&v"(h[2]), "=&v"(h[3]), "=&v"(q[0]), "=&v"(q[1]),
+        "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]), "=&v"(q[7]),
+        "=&v"(q[8]), "=&v"(q[9]), "=&v"(q[10]), "=&v"(q[11]), "=&v"(q[12]), "=&v"(q[13]),
+        "=&v"(q[14]), "=&v"(q[15])
+      : "v"(hb), "v"(qb)
+      : "memory");
+}
+
+// The lane's group-image quarters of one block (unit pairs 0..3) and its
+// vector's eight unit sums.
+__device__ __forceinline__ void lds_read_group_block(uint32_t ia, uint32_t xa, u32x4 (&a)[4],
+                                                     u32x4 (&xs)[2]) {
+  asm volatile(
+      "ds_read_b128 %0, %6\n"
+      "ds_read_b128 %1, %6 offset:1024\n"
+      "ds_read_b128 %2, %6 offset:2048\n"
+      "ds_read_b128 %3, %6 offset:3072\n"
+      "ds_read_b128 %4, %7\n"
+      "ds_read_b128 %5, %7 offset:16\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3]), "=&v"(xs[0]), "=&v"(xs[1])
+      : "v"(ia), "v"(xa)
+      : "memory");
+}
+
+__device__ __forceinline__ int64_t as_i64(uint32_t lo, uint32_t hi) {
+  return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+
+// One block of row n against vector g (the lane's), fast path: eight MFMAs,
+// the integer scale combine and the f32 digit and min terms.
+__device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[16], int b,
+                                               const u32x4 (&a)[4], const u32x4 (&xs)[2], int eb) {
+  const i32x4 zero = {0, 0, 0, 0};
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  i32x4 c[8];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const u32x2 w = q[4 * b + j];
+    c[2 * j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+        as_i64(a[j][0], a[j][1]), as_i64(w[0] & 0x0f0f0f0fu, w[1] & 0x0f0f0f0fu), zero, 0, 0, 0);
+    c[2 * j + 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+        as_i64(a[j][2], a[j][3]),
+        as_i64((w[0] >> 4) & 0x0f0f0f0fu, (w[1] >> 4) & 0x0f0f0f0fu), zero, 0, 0, 0);
+  }
+  int t[4] = {0, 0, 0, 0};
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int s = (int)(((u < 4 ? sc03 : sc47) >> (8 * (u & 3))) & 0xffu);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) t[d] = __mul24(s, c[u][d]) + t[d];
+  }
+  const float tc =
+      fmaf(fmaf(fmaf((float)t[3], 256.0f, (float)t[2]), 256.0f, (float)t[1]), 256.0f, (float)t[0]);
+  float um = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const float m = (float)(((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu);
+    um = fmaf(m, __uint_as_float(xs[u >> 2][u & 3]), um);
+  }
+  const float d = half_bits_to_float(h[0] & 0xffffu);
+  const float dmin = half_bits_to_float(h[0] >> 16);
+  return __builtin_amdgcn_ldexpf(d * tc, eb) - dmin * um;
+}
+
+// Exact per-weight path of one block of row n against 256 activations: the
+// header and qs pieces 1..8 at hp + 256 k, k = 0..8, of the stage buffer.
+__device__ __forceinline__ float block_exact_row(uint32_t hp, const float* __restrict__ xs) {
+  u32x4 h, qa[4], qb[4];
+  asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(h) : "v"(hp) : "memory");
+  lds_read4<256>(hp + 256u, qa);
+  lds_read4<256>(hp + 1280u, qb);
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  const float d = half_bits_to_float(h[0] & 0xffffu);
+  const float dmin = half_bits_to_float(h[0] >> 16);
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    // unit u: the low (even u) or high nibbles of qs pieces u & ~1, (u & ~1) + 1
+    const uint32_t sc = ((u < 4 ? sc03 : sc47) >> (8 * (u & 3))) & 0xffu;
+    const uint32_t mn = ((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu;
+    const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
+    const int shift = 4 * (u & 1);
+    const int k = u & ~1;
+    acc = exact_dot16(k < 4 ? qa[k] : qb[k - 4], shift, d1, m1, xs + 32 * u, acc);
+    acc = exact_dot16(k < 4 ? qa[k + 1] : qb[k - 3], shift, d1, m1, xs + 32 * u + 16, acc);
+  }
+  return acc;
+}
+
+// Launch constants: the slice count S (1: whole rows), GS workgroups per
+// slice (all of them when S == 1), the ring's slot count, and the division
+// constants of GS, of the stages per tile and of the slot count.
+struct TokArgs {
+  uint32_t slices, groups_per_slice, m_gps, m_parts;
+  uint32_t slots, m_slots;
+};
+
+// LDS map: per-wave stage buffers; the images of ng groups of nbl blocks
+// (4 ng vectors), their unit sums and exponents; the slot ring (unused with
+// K slices).
+__host__ __device__ constexpr Layout tok_layout(uint32_t waves, uint32_t nbl, uint32_t ng,
+                                                uint32_t slots) {
+  return make_layout(stage_bytes(4), 4u, 32u, waves, 1u, nbl, slots, 1u, 4u * ng);
+}
+
+// One vector group's sum over the live blocks of a stage (the weights in h,
+// q) on the fast path; blocks of the lane's vector that must take the exact
+// path count zero here.  iabase/xabase/eabase: the group's images, the
+// vector's unit sums and exponents at the stage's first block.
+__device__ __forceinline__ float tok_group_stage(const u32x4 (&h)[4], const u32x2 (&q)[16],
+                                                 uint32_t nlive, uint32_t iabase,
+                                                 uint32_t xabase, uint32_t eabase) {
+  i32x4 ex;
+  asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(ex) : "v"(eabase) : "memory");
+  float part = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    if ((uint32_t)b < nlive) {
+      u32x4 a[4], xs[2];
+      lds_read_group_block(iabase + 4096u * b, xabase + 32u * b, a, xs);
+      const float v = block_dot_tok(h[b], q, b, a, xs, ex[b]);
+      part += ex[b] == kBadBlock ? 0.0f : v;
+    }
+  }
+  return part;
+}
+
+template <int WAVES, int NG>
+__global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x,
+                                                              float* __restrict__ y, uint32_t rows,
+                                                              uint32_t nb, uint32_t ntok,
+                                                              float* __restrict__ part_out,
+                                                              TokArgs ta) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  constexpr uint32_t kPieces = block_pieces(4);
+  constexpr uint32_t kStage = stage_bytes(4);
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t grp = lane >> 4, n = lane & 15u;
+  const uint32_t row_bytes = nb * kQ4Bytes;
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t nstages = (nb + 3u) / 4u;
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  uint8_t* const wstage = smem + wave * kStage;
+  const bool sliced = ta.slices > 1u;
+  const uint32_t ng = (ntok + 3u) / 4u;  // groups that hold vectors (<= NG)
+
+  // this workgroup's slice k (stages [s0, s0 + spt)) and its tiles tg,
+  // tg + GS, ...
+  const FastDiv by_gps{ta.groups_per_slice, ta.m_gps};
+  const uint32_t k = quo(blockIdx.x, by_gps);
+  const uint32_t tg = blockIdx.x - k * ta.groups_per_slice;
+  const uint32_t tstep = ta.groups_per_slice;
+  const uint32_t s0 = sliced ? k : 0u, spt = sliced ? 1u : nstages;
+  const uint32_t blk0 = 4u * s0, nbl = min(4u * spt, nb - blk0);
+  const Layout L = tok_layout(WAVES, nbl, NG, ta.slots);
+  const uint32_t ntw = tg < ntiles ? quo(ntiles - 1u - tg, by_gps) + 1u : 0u;
+  const uint32_t npairs = ntw * spt;
+  const FastDiv by_parts{spt, sliced ? 0u : ta.m_parts};
+
+  // 1. the vectors' blocks of the range into the image area
+  copy_x_group<WAVES>(smem, L.img, x, nb, blk0, nbl, ng, ntok, wave, lane);
+
+  // 2. this wave's pairs p = wave, wave + WAVES, ...: local tile p / spt,
+  //    stage s0 + p % spt; the first stage's copy goes out now
+  const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
+  const uint32_t voff = n * row_bytes + 16u * grp;
+  auto pair_of = [&](uint32_t p) {
+    Pair pr;
+    const uint32_t i = quo(p, by_parts);
+    pr.tile = tg + i * tstep;
+    pr.r = s0 + (p - i * spt);
+    pr.lt = i;
+    pr.lo = 0u;
+    pr.hi = spt;
+    return pr;
+  };
+  auto issue = [&](const Pair& pr) {
+    const uint32_t row0 = pr.tile * 16u;
+    const uint32_t nrows = min(16u, rows - row0);
+    const uint8_t* sb = w + (size_t)row0 * row_bytes + 4u * kQ4Bytes * pr.r;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - 4u * kQ4Bytes * pr.r), kBufferWord3);
+#pragma unroll
+    for (int i = 0; i < (int)kPieces; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(wstage + 1024 * i), 16,
+                                                voff + 64u * i, 0, 0, 0);
+  };
+  Pair pr_next = pair_of(wave);
+  if (my_pairs > 0u) issue(pr_next);
+
+  // 3. ring slots; once the x copies have landed, the group images (a wave
+  //    converts exactly the blocks it copied)
+  init_slots<WAVES>(sbase, L, ta.slots);
+  if (my_pairs > 0u)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kPieces));
+  else
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+  build_group_images<WAVES>(sbase, L, nbl, ng, wave, lane);
+  lds_wait();
+  __builtin_amdgcn_s_barrier();
+
+  // 4. the wave's pairs: lane (grp, n) accumulates, for each group g, vector
+  //    4 g + grp, row n
+  const uint32_t hb0 = sbase + wave * kStage + 16u * n;
+  const uint32_t qb0 = hb0 + 256u * (1u + (grp >> 1)) + 8u * (grp & 1u);
+  for (uint32_t j = 0; j < my_pairs; ++j) {
+    const Pair pr = pr_next;
+    const uint32_t s = pr.r, sl = s - s0;  // stage, and its place in the image range
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    u32x4 h[4];
+    u32x2 q[16];
+    lds_read_weights_tok(hb0, qb0, h, q);
+    const uint32_t nlive = min(4u, nb - 4u * s);
+    // a block that takes the exact path reads the stage buffer afterwards
+    bool any_bad = false;
+    for (uint32_t g = 0; g < ng; ++g) {
+      i32x4 ex;
+      asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)"
+                   : "=&v"(ex)
+                   : "v"(sbase + L.expo + (4u * g + grp) * L.expo_stride + 16u * sl)
+                   : "memory");
+      bool bad = false;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) bad |= (uint32_t)b < nlive && ex[b] == kBadBlock;
+      any_bad |= __builtin_amdgcn_ballot_w64(bad) != 0u;
+    }
+    if (!any_bad && j + 1u < my_pairs) {
+      pr_next = pair_of(wave + (j + 1u) * WAVES);
+      issue(pr_next);
+    }
+    float part[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) part[g] = 0.0f;
+    // (groups one after another: unrolled, their registers would add up)
+#pragma unroll 1
+    for (uint32_t g = 0; g < (NG == 1 ? 1u : ng); ++g) {
+      const uint32_t v = 4u * g + grp;
+      const float pg = tok_group_stage(h, q, nlive,
+                                       sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane,
+                                       sbase + L.xsum + v * L.xsum_stride + 128u * sl,
+                                       sbase + L.expo + v * L.expo_stride + 16u * sl);
+#pragma unroll
+      for (int gg = 0; gg < NG; ++gg)
+        if ((uint32_t)gg == g) part[gg] = pg;
+    }
+    if (any_bad) {
+      // the rare exact path: one loop over (group, block), everything
+      // addressed in LDS (no register array indexed at run time)
+#pragma unroll 1
+      for (uint32_t g = 0; g < ng; ++g) {
+        const uint32_t v = 4u * g + grp;
+        const float* const xv = x + (size_t)min(v, ntok - 1u) * nb * kBlockElems;
+        float e = 0.0f;
+#pragma unroll 1
+        for (uint32_t b = 0; b < nlive; ++b) {
+          const uint32_t eb = lds_read_b32(sbase + L.expo + v * L.expo_stride + 4u * (4u * sl + b));
+          if ((int)eb == kBadBlock)
+            e += block_exact_row(hb0 + 2304u * b, xv + kBlockElems * (4u * s + b));
+        }
+#pragma unroll
+        for (int gg = 0; gg < NG; ++gg)
+          if ((uint32_t)gg == g) part[gg] += e;
+      }
+    }
+    if (any_bad && j + 1u < my_pairs) {
+      pr_next = pair_of(wave + (j + 1u) * WAVES);
+      issue(pr_next);
+    }
+    if (!sliced) {
+      hand_off_lane_tokens(sbase, L, FastDiv{ta.slots, ta.m_slots}, pr, nstages, part[0], lane,
+                           rows, ntok, y);
+      continue;
+    }
+    // the stage's partial sums of the tile's rows, for tok_reduce
+    const uint32_t row = pr.tile * 16u + n;
+    if (row < rows) {
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        const uint32_t v = 4u * g + grp;
+        if (v < ntok) part_out[((size_t)s * 4u * NG + v) * rows + row] = part[g];
+      }
+    }
+  }
+}
+
+// y[t * rows + row] = sum over the stages s of part[(s * nv + t) * rows + row],
+// in stage order (the sliced launch's second kernel).
+__global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part,
+                                                  float* __restrict__ y, uint32_t rows,
+                                                  uint32_t nstages, uint32_t nv) {
+  const uint32_t row = blockIdx.x * 256u + threadIdx.x, t = blockIdx.y;
+  if (row >= rows) return;
+  float sum = 0.0f;
+  for (uint32_t s = 0; s < nstages; ++s) sum += part[((size_t)s * nv + t) * rows + row];
+  y[(size_t)t * rows + row] = sum;
+}
+
+// Slice count of a launch: one per stage when the stages' partial sums of
+// nv vectors fit the workspace's scratch and every slice still has a
+// workgroup, else 1 (whole rows).
+inline uint32_t tok_slices(uint32_t rows, uint32_t nstages, uint32_t nv, size_t scratch_bytes) {
+  const uint32_t cus = (uint32_t)cu_count();
+  if (nstages < 2u || nstages > cus) return 1u;
+  if ((size_t)nstages * nv * rows * sizeof(float) > scratch_bytes) return 1u;
+  return nstages;
+}
+
+// ntok <= 4 NG vectors in one pass; false when the shape does not fit this
+// kernel (K slices need room in the scratch when NG > 1).
+template <int W, int NG>
+bool launch_tokens_td(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+                      uint32_t ntok, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t nstages = (nb + 3u) / 4u;
+  TokArgs ta{};
+  uint32_t grid, lds;
+  ta.slices = tok_slices(rows, nstages, 4u * NG, ws.scratch_bytes);
+  if (ta.slices > 1u) {
+    ta.groups_per_slice = min((uint32_t)cu_count() / ta.slices, ntiles);
+    ta.slots = 1u;
+    grid = ta.groups_per_slice * ta.slices;
+    lds = tok_layout(W, min(4u, nb), NG, 1u).total;
+  } else {
+    if (NG > 1) return false;  // whole rows: one group's images already fill the LDS
+    ta.groups_per_slice = grid = min(ntiles, (uint32_t)cu_count());
+    const uint32_t tiles_per_group = (ntiles + grid - 1u) / grid;
+    ta.slots = ring_slots(W, 1, tiles_per_group, nstages);
+    ta.m_parts = div_magic(nstages);
+    lds = tok_layout(W, nb, NG, ta.slots).total;
+    // pair indices below tiles_per_group * nstages, divided by nstages
+    if ((uint64_t)tiles_per_group * nstages * nstages >= (1ull << 32)) return false;
+  }
+  ta.m_gps = div_magic(ta.groups_per_slice);
+  ta.m_slots = div_magic(ta.slots);
+  // block and tile indices divided by GS
+  if ((uint64_t)(grid + ntiles) * ta.groups_per_slice >= (1ull << 32)) return false;
+  if (lds > kLdsBytes) return false;
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&q4k_tokens_mfma<W, NG>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
+  if (attr != hipSuccess) {
+    *err = attr;
+    return true;
+  }
+  hipLaunchKernelGGL((q4k_tokens_mfma<W, NG>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
+                     nb, ntok, ws.scratch, ta);
+  *err = hipGetLastError();
+  if (*err == hipSuccess && ta.slices > 1u) {
+    hipLaunchKernelGGL(tok_reduce, dim3((rows + 255u) / 256u, ntok), dim3(256), 0, s, ws.scratch,
+                       y, rows, nstages, 4u * NG);
+    *err = hipGetLastError();
+  }
+  return true;
+}
+
+// 3..16 vectors in one launch (with its reduce): the group count and wave
+// count that fit.
+bool launch_tokens_groups(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+                          uint32_t ntok, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  if (ntok <= 4u)
+    return launch_tokens_td<12, 1>(w, x, y, rows, nb, ntok, ws, s, err) ||
+           launch_tokens_td<8, 1>(w, x, y, rows, nb, ntok, ws, s, err) ||
+           launch_tokens_td<4, 1>(w, x, y, rows, nb, ntok, ws, s, err);
+  // (the weights' decoded operands stay in registers across the groups: two
+  // waves per SIMD)
+  if (ntok <= 8u) return launch_tokens_td<8, 2>(w, x, y, rows, nb, ntok, ws, s, err);
+  return launch_tokens_td<8, 4>(w, x, y, rows, nb, ntok, ws, s, err) ||
+         launch_tokens_td<6, 4>(w, x, y, rows, nb, ntok, ws, s, err);
+}
+
 template <int W, int D, int M, int NT = 1, int QB = 4>
 bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, uint32_t rows,
                uint32_t nb, const Workspace& ws, hipStream_t s, hipError_t* err) {
@@ -580,6 +1125,12 @@ bool launch_q5k_one(const uint8_t* w, const float* x, float* y, uint32_t rows, u
          launch_wd<4, 1, 1, 1, 5>(w, nullptr, x, y, rows, nb, ws, s, err);
 }
 
+// SI_HIP_TOKENS_TD=0 keeps the one-vector-per-MFMA kernel for batches
+inline bool td_policy() {
+  static const int v = env_int("SI_HIP_TOKENS_TD", 1);
+  return v != 0;
+}
+
 // batch >= 2 vectors, up to four per pass over the weights (their activation
 // images share the LDS with the stage buffers)
 template <int QB>
@@ -591,6 +1142,16 @@ bool matmul_passes(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
     const float* xb = x + (size_t)b * cols;
     float* yb = y + (size_t)b * rows;
     bool ok;
+    if (QB == 4 && nt >= 2 && td_policy()) {
+      // up to sixteen vectors share the matrix-core rows in one pass (two
+      // go faster one vector per MFMA)
+      const uint32_t ng = batch - b >= 3u ? min(16u, batch - b) : nt;
+      if (ng >= 3u && launch_tokens_groups(w, xb, yb, rows, nb, ng, ws, s, err)) {
+        if (*err != hipSuccess) return true;
+        b += ng;
+        continue;
+      }
+    }
     switch (nt) {
       case 4: ok = launch_tokens<4, QB>(w, xb, yb, rows, nb, ws, s, err); break;
       case 3: ok = launch_tokens<3, QB>(w, xb, yb, rows, nb, ws, s, err); break;

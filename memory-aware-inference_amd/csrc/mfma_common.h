@@ -89,6 +89,9 @@ __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)"
 __device__ __forceinline__ void lds_write_b128(uint32_t addr, u32x4 v) {
   asm volatile("ds_write_b128 %0, %1" : : "v"(addr), "v"(v) : "memory");
 }
+__device__ __forceinline__ void lds_write_b64(uint32_t addr, u32x2 v) {
+  asm volatile("ds_write_b64 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
 __device__ __forceinline__ void lds_write_b32(uint32_t addr, uint32_t v) {
   asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
 }
@@ -634,6 +637,38 @@ __device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L,
           lds_read_b32(sbase + L.part + 64u * NTOK * (slot * tparts + st) + 64u * t + 4u * n));
     if (row < rows) y[(size_t)t * rows + row] = sum;
   }
+  if (lane == 0u) {
+    lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
+    lds_write_b32(sbase + L.owner + 4u * slot, pr.lt + slots);
+  }
+}
+
+// hand_off_tokens for kernels that keep vector g's row sums in lane group g
+// (lane 16 g + n holds vector g, row n): every lane writes its own sum; the
+// finishing wave's lane group g stores vector g's rows (g < ntok).
+__device__ __forceinline__ void hand_off_lane_tokens(uint32_t sbase, const Layout& L,
+                                                     const FastDiv& by_slots, const Pair& pr,
+                                                     uint32_t tparts, float rowsum, uint32_t lane,
+                                                     uint32_t rows, uint32_t ntok,
+                                                     float* __restrict__ y) {
+  const uint32_t grp = lane >> 4, n = lane & 15u;
+  const uint32_t slots = by_slots.d;
+  const uint32_t slot = pr.lt - quo(pr.lt, by_slots) * slots;
+  for (uint32_t spin = 0;
+       lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
+    __builtin_amdgcn_s_sleep(1);
+  // the slot's partial r holds [vector][16 rows], 256 bytes
+  lds_write_b32(sbase + L.part + 256u * (slot * tparts + pr.r) + 4u * lane,
+                __float_as_uint(rowsum));
+  uint32_t old = 0u;
+  if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);
+  const uint32_t done = __builtin_amdgcn_readlane(old, 0);
+  if (done != tparts - 1u) return;
+  const uint32_t row = pr.tile * 16u + n;
+  float sum = 0.0f;
+  for (uint32_t st = 0; st < tparts; ++st)
+    sum += __uint_as_float(lds_read_b32(sbase + L.part + 256u * (slot * tparts + st) + 4u * lane));
+  if (grp < ntok && row < rows) y[(size_t)grp * rows + row] = sum;
   if (lane == 0u) {
     lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
     lds_write_b32(sbase + L.owner + 4u * slot, pr.lt + slots);

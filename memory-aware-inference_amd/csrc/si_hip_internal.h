@@ -9,12 +9,18 @@ namespace sihip {
 
 // Device memory a context lends to the kernels that combine partial sums
 // across workgroups: kWorkspaceCounterBytes of zeroed counters, then entries
-// that hold kWorkspaceEmpty when unused.  The kernels leave it in that state.
+// that hold kWorkspaceEmpty when unused (kWorkspaceBytes in all; the kernels
+// leave it in that state), then kWorkspaceScratchBytes of scratch that a
+// launch overwrites before it reads (partial sums handed from one kernel to
+// the next in the same stream).
 struct Workspace {
   void* ptr = nullptr;
   size_t bytes = 0;
+  float* scratch = nullptr;
+  size_t scratch_bytes = 0;
 };
 constexpr size_t kWorkspaceBytes = size_t(2) << 20;
+constexpr size_t kWorkspaceScratchBytes = size_t(8) << 20;
 constexpr size_t kWorkspaceCounterBytes = size_t(1) << 20;
 // a signalling-NaN pattern: no arithmetic result has it (results of
 // operations are quiet NaNs)

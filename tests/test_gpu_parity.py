@@ -388,6 +388,42 @@ def test_matmul_many(ctx, t, batch):
         assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
 
 
+@pytest.mark.parametrize("rows,cols,batch", [(100, 2304, 3), (16, 256, 2), (1040, 5120, 4),
+                                             (33, 1280, 7), (48, 9216, 2)])
+def test_matmul_many_ragged_shapes(hip_ctx, rows, cols, batch):
+    """Partial tiles, block counts that leave a short last stage, passes with
+    fewer than four vectors, and a K whose images do not fit the LDS."""
+    log(f"matmul_many ragged {rows}x{cols} batch={batch}")
+    w = si_hip.synth_matrix(12, seed=rows * 7 + cols, rows=rows, cols=cols)
+    X = si_hip.synth_normal(rows + batch, batch * cols).reshape(batch, cols)
+    W = hip_ctx.upload_quant_weight_private(w, 12)
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(batch):
+        _, y64, ab = O.matvec(12, w, rows, cols, X[b])
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+
+
+def test_matmul_many_nonfinite_and_outlier_vectors(hip_ctx):
+    """Blocks that must take the exact path in some vectors of a pass and
+    not in others: huge, subnormal, outlier and non-finite activations."""
+    rows, cols, batch = 48, 2304, 4
+    w = si_hip.synth_matrix(12, seed=4242, rows=rows, cols=cols)
+    W = hip_ctx.upload_quant_weight_private(w, 12)
+    X = si_hip.synth_normal(4243, batch * cols).reshape(batch, cols).copy()
+    X[1, 600:620] = np.float32(3e30)
+    X[1, 1024:1280] = np.float32(1e-41)
+    X[2, 300] = np.float32(1e6)
+    X[2, 2000] = np.float32(-1e6)
+    X[3, 700] = np.inf
+    X[3, 1500] = np.nan
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(3):
+        _, y64, ab = O.matvec(12, w, rows, cols, X[b])
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+    y32, _, _ = O.matvec(12, w, rows, cols, X[3])
+    assert np.array_equal(_category(outs[3]), _category(y32))
+
+
 def test_matmul_many_baseline_shape(hip_ctx):
     """M = 6 candidates on the 17408 x 5120 Q4_K matrix: one pass over the
     weights for four vectors and one for two; each candidate matches its own
@@ -647,6 +683,59 @@ def test_graph_replay_matches_eager(hip_ctx):
         assert same_bits(a, b)
     for p in (d_x, d_y, d_h, d_o, d_l, d_r, d_e):
         hip_ctx.device_free(p)
+
+
+def test_graph_replay_matmul_many_groups(hip_ctx):
+    """Multi-token verify on the grouped path (a K-sliced launch whose stage
+    sums a second kernel adds up): 3, 8 and 16 vectors recorded in one graph,
+    replayed with other launches of the same workspace in between, bit for
+    bit equal to the eager calls and to the oracle's bound."""
+    import ctypes as C
+    lib = si_hip.lib()
+    rows, cols = 1040, 5120
+    w = si_hip.synth_matrix(12, seed=3101, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, 12)
+    X = si_hip.synth_normal(3102, 16 * cols).reshape(16, cols)
+    d_x = hip_ctx.device_alloc(16 * cols * 4)
+    hip_ctx.to_device(d_x, X)
+    outs = {m: hip_ctx.device_alloc(m * rows * 4) for m in (3, 8, 16)}
+    d_e = hip_ctx.device_alloc(4 * rows * 4)
+    h, P = hip_ctx.handle, C.c_void_p
+
+    def enqueue():
+        for m, d in outs.items():
+            assert lib.si_hip_matmul_many_device(h, W.handle, rows, cols, m, P(d_x), P(d)) == 0, \
+                si_hip.last_error()
+
+    def results():
+        hip_ctx.synchronize()
+        return {m: hip_ctx.from_device(d, m * rows).reshape(m, rows) for m, d in outs.items()}
+
+    enqueue()
+    ref = results()
+    for b in range(16):
+        _, y64, ab = O.matvec(12, w, rows, cols, X[b], threads=8)
+        assert_dot_close(ref[16][b], y64, ab, what=f"eager vector {b}")
+        if b < 3:
+            assert_dot_close(ref[3][b], y64, ab, what=f"eager vector {b} of 3")
+        if b < 8:
+            assert_dot_close(ref[8][b], y64, ab, what=f"eager vector {b} of 8")
+    hip_ctx.capture_begin()
+    enqueue()
+    graph = hip_ctx.capture_end()
+    for rep in range(3):
+        for m, d in outs.items():
+            hip_ctx.to_device(d, np.full(m * rows, np.nan, np.float32))
+        # another grouped launch on the same scratch between replays
+        assert lib.si_hip_matmul_many_device(h, W.handle, rows, cols, 4, P(d_x), P(d_e)) == 0
+        hip_ctx.synchronize()
+        graph.launch()
+        got = results()
+        for m in outs:
+            assert same_bits(got[m], ref[m]), f"replay {rep}, {m} vectors"
+    graph.free()
+    for d in list(outs.values()) + [d_x, d_e]:
+        hip_ctx.device_free(d)
 
 
 def test_graph_capture_state_errors(hip_ctx):
