@@ -997,8 +997,18 @@ __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part
                                                   uint32_t nstages, uint32_t nv) {
   const uint32_t row = blockIdx.x * 256u + threadIdx.x, t = blockIdx.y;
   if (row >= rows) return;
+  const float* const p = part + (size_t)t * rows + row;
+  const size_t step = (size_t)nv * rows;
   float sum = 0.0f;
-  for (uint32_t s = 0; s < nstages; ++s) sum += part[((size_t)s * nv + t) * rows + row];
+  // eight loads in flight, added in stage order
+  for (uint32_t base = 0; base < nstages; base += 8u) {
+    float v[8];
+#pragma unroll
+    for (uint32_t i = 0; i < 8u; ++i) v[i] = base + i < nstages ? p[(base + i) * step] : 0.0f;
+#pragma unroll
+    for (uint32_t i = 0; i < 8u; ++i)
+      if (base + i < nstages) sum += v[i];
+  }
   y[(size_t)t * rows + row] = sum;
 }
 
