@@ -114,6 +114,21 @@ int si_hip_gguf_upload_tensor(si_hip_context *ctx, const si_hip_gguf *store, uin
 int si_hip_gguf_bind_tensor_mapped(si_hip_context *ctx, const si_hip_gguf *store, uint64_t index,
                                    si_hip_quant_weight **out_weight);
 
+/* F32 matvec over rows [row_start, row_start + row_count) of a rank-2 F32
+ * tensor (f32_matvec_tensor_rows, metal.rs:3074-3110): "F32 matvec requires a
+ * rank-2 F32 tensor", "F32 row range is invalid", "F32 tensor columns or
+ * input length is invalid", "F32 tensor payload is shorter than its shape". */
+int si_hip_gguf_f32_matvec_tensor_rows(si_hip_context *ctx, const si_hip_gguf *store,
+                                       uint64_t index, size_t row_start, size_t row_count,
+                                       const float *x, size_t x_len, float *y);
+/* F32 matvecs of several rank-2 F32 tensors with the same columns and one
+ * input, one submission (f32_matvec_many_gguf_tensors, metal.rs:4780-4870);
+ * outputs[i] receives tensor indices[i]'s rows.  A tensor's byte range must
+ * hold exactly its payload ("GGUF F32 matvec group tensor is truncated"). */
+int si_hip_gguf_f32_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *store,
+                                        const uint64_t *indices, size_t count, const float *x,
+                                        size_t x_len, float *const *outputs);
+
 #ifdef __cplusplus
 }
 #endif

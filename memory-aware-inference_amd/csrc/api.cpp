@@ -5,6 +5,7 @@
 // event management, telemetry, and kernel selection.  Kernels live in the
 // *.hip files; this file only launches them through si_hip_internal.h.
 #include "si_hip.h"
+#include "si_hip_f32.h"
 
 #include <hip/hip_runtime.h>
 
@@ -12,6 +13,7 @@
 #include <atomic>
 #include <chrono>
 #include <cstdarg>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <memory>
@@ -968,6 +970,219 @@ int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_qua
   } else {
     *token = sihip::argmax_candidate_index(packed, rule);
   }
+  return ok();
+}
+
+// ---- F32 matvec and RMSNorm (metal.rs:2641-3110) ---------------------------------
+namespace {
+// f32_matvec's checks (metal.rs:2983-2998), then the launch limits.
+int validate_f32_matvec(size_t values, size_t rows, size_t cols, size_t input_len) {
+  size_t expected;
+  if (!checked_mul(rows, cols, &expected)) return fail(SI_HIP_ERR_OVERFLOW, "F32 matvec dimensions overflow");
+  if (rows == 0 || cols == 0 || input_len != cols || values != expected)
+    return fail(SI_HIP_ERR_DIMENSIONS, "F32 matvec dimensions or byte length are invalid");
+  if (cols > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "F32 matvec columns exceed HIP limits");
+  if (rows > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "F32 matvec rows exceed HIP limits");
+  return SI_HIP_OK;
+}
+
+// Copies of the weights and x in, y out, one wait (the reference's command
+// buffer with commit_and_wait).
+int run_f32_matvec_host(si_hip_context *ctx, const float *w, size_t rows, size_t cols,
+                        const float *x, float *y) {
+  const size_t wb = rows * cols * sizeof(float);
+  const size_t xb = cols * sizeof(float), yb = rows * sizeof(float);
+  int rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, wb);
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, xb);
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, yb);
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_weights, w, wb, hipMemcpyHostToDevice, ctx->stream), "weight copy");
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, x, xb, hipMemcpyHostToDevice, ctx->stream), "input copy");
+  hipError_t e = sihip::launch_f32_matvec(static_cast<const float *>(ctx->stage_weights),
+                                          static_cast<const float *>(ctx->stage_in),
+                                          static_cast<float *>(ctx->stage_out), (uint32_t)rows,
+                                          (uint32_t)cols, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "F32 matvec launch");
+  SIHIP_CHECK(hipMemcpyAsync(y, ctx->stage_out, yb, hipMemcpyDeviceToHost, ctx->stream), "output copy");
+  rc = wait_stream(ctx, "F32 matvec command");
+  if (rc) return rc;
+  return ok();
+}
+
+// rms_norm / rms_norm_heads / rms_norm_gated's checks (metal.rs:2648-2650,
+// 2864-2875, 2782-2794).
+int validate_rms(uint32_t mode, size_t x_len, size_t gate_len, size_t w_len, size_t heads,
+                 size_t head_dim, float eps) {
+  if (mode == 0) {
+    if (x_len == 0 || x_len != w_len)
+      return fail(SI_HIP_ERR_DIMENSIONS, "RMSNorm input and weight must have equal non-zero length");
+  } else {
+    const char *label = mode == 1 ? "head RMSNorm" : "Gated RMSNorm";
+    size_t n;
+    if (!checked_mul(heads, head_dim, &n)) return fail(SI_HIP_ERR_OVERFLOW, "%s dimensions overflow", label);
+    if (heads == 0 || head_dim == 0 || !std::isfinite(eps) || eps <= 0.0f || x_len != n ||
+        (mode == 2 && gate_len != n) || w_len != head_dim)
+      return fail(SI_HIP_ERR_DIMENSIONS, "%s dimensions are invalid", label);
+  }
+  if (heads > UINT32_MAX || head_dim > UINT32_MAX)
+    return fail(SI_HIP_ERR_OVERFLOW, "RMSNorm dimensions exceed HIP limits");
+  return SI_HIP_OK;
+}
+
+int run_rms_host(si_hip_context *ctx, uint32_t mode, const float *x, const float *gate,
+                 const float *w, size_t heads, size_t head_dim, float eps, float *y) {
+  const size_t n = heads * head_dim, xb = n * sizeof(float), wb = head_dim * sizeof(float);
+  // staging: x (and the gate after it) in, the weight in aux, y out
+  int rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, mode == 2 ? 2 * xb : xb);
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_aux, &ctx->stage_aux_bytes, wb);
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, xb);
+  if (rc) return rc;
+  float *dx = static_cast<float *>(ctx->stage_in);
+  float *dg = mode == 2 ? dx + n : nullptr;
+  SIHIP_CHECK(hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream), "input copy");
+  if (dg) SIHIP_CHECK(hipMemcpyAsync(dg, gate, xb, hipMemcpyHostToDevice, ctx->stream), "gate copy");
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_aux, w, wb, hipMemcpyHostToDevice, ctx->stream), "weight copy");
+  hipError_t e = sihip::launch_rms_norm(mode, dx, dg, static_cast<const float *>(ctx->stage_aux),
+                                        static_cast<float *>(ctx->stage_out), (uint32_t)heads,
+                                        (uint32_t)head_dim, eps, ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "RMSNorm launch");
+  SIHIP_CHECK(hipMemcpyAsync(y, ctx->stage_out, xb, hipMemcpyDeviceToHost, ctx->stream), "output copy");
+  rc = wait_stream(ctx, "RMSNorm command");
+  if (rc) return rc;
+  return ok();
+}
+}  // namespace
+
+int si_hip_f32_matvec(si_hip_context *ctx, const float *w, size_t values, size_t rows, size_t cols,
+                      const float *x, size_t x_len, float *y) {
+  int rc = validate_f32_matvec(values, rows, cols, x_len);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!w || !x || !y) return fail(SI_HIP_ERR_NULL, "F32 matvec buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  return run_f32_matvec_host(ctx, w, rows, cols, x, y);
+}
+
+int si_hip_f32_matvec_bytes(si_hip_context *ctx, const uint8_t *bytes, size_t len, size_t rows,
+                            size_t cols, const float *x, size_t x_len, float *y) {
+  // f32_matvec_bytes (metal.rs:3051-3072)
+  size_t expected;
+  if (!checked_mul(rows, cols, &expected) || !checked_mul(expected, sizeof(float), &expected))
+    return fail(SI_HIP_ERR_OVERFLOW, "F32 matvec byte length overflows");
+  if (len != expected) return fail(SI_HIP_ERR_BYTE_LENGTH, "F32 matvec byte length is invalid");
+  if (reinterpret_cast<uintptr_t>(bytes) % alignof(float) != 0)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "F32 matvec bytes are not 4-byte aligned");
+  return si_hip_f32_matvec(ctx, reinterpret_cast<const float *>(bytes), len / sizeof(float), rows,
+                           cols, x, x_len, y);
+}
+
+int si_hip_f32_matvec_device(si_hip_context *ctx, const float *d_w, size_t rows, size_t cols,
+                             const float *d_x, float *d_y) {
+  int rc = validate_f32_matvec(rows * cols, rows, cols, cols);
+  if (rc) return rc;
+  if (!ctx || !d_w || !d_x || !d_y) return fail(SI_HIP_ERR_NULL, "device F32 matvec argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  hipError_t e = sihip::launch_f32_matvec(d_w, d_x, d_y, (uint32_t)rows, (uint32_t)cols,
+                                          device_stream(ctx));
+  if (e != hipSuccess) return hip_fail(e, "F32 matvec launch");
+  ctx->async_submitted.fetch_add(1);
+  return ok();
+}
+
+int si_hip_f32_matvec_many(si_hip_context *ctx, const float *const *ws, const size_t *rows,
+                           size_t count, size_t cols, const float *x, size_t x_len,
+                           float *const *ys) {
+  // one submission for a group of F32 matvecs sharing x (the command buffer of
+  // f32_matvec_many_gguf_tensors, metal.rs:4780-4870)
+  if (count == 0) return fail(SI_HIP_ERR_EMPTY, "F32 matvec group requires at least one matrix");
+  if (!ws || !rows || !ys) return fail(SI_HIP_ERR_NULL, "F32 matvec group argument is null");
+  size_t wtotal = 0, ytotal = 0;
+  for (size_t i = 0; i < count; ++i) {
+    int rc = validate_f32_matvec(rows[i] * cols, rows[i], cols, x_len);
+    if (rc) return rc;
+    if (!ws[i] || !ys[i]) return fail(SI_HIP_ERR_NULL, "F32 matvec buffer is null");
+    wtotal += rows[i] * cols;
+    ytotal += rows[i];
+  }
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!x) return fail(SI_HIP_ERR_NULL, "F32 matvec buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  int rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, wtotal * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, ytotal * sizeof(float));
+  if (rc) return rc;
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, x, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+              "input copy");
+  float *dw = static_cast<float *>(ctx->stage_weights), *dy = static_cast<float *>(ctx->stage_out);
+  for (size_t i = 0; i < count; ++i) {
+    SIHIP_CHECK(hipMemcpyAsync(dw, ws[i], rows[i] * cols * sizeof(float), hipMemcpyHostToDevice,
+                               ctx->stream),
+                "weight copy");
+    hipError_t e = sihip::launch_f32_matvec(dw, static_cast<const float *>(ctx->stage_in), dy,
+                                            (uint32_t)rows[i], (uint32_t)cols, ctx->stream);
+    if (e != hipSuccess) return hip_fail(e, "F32 matvec launch");
+    SIHIP_CHECK(hipMemcpyAsync(ys[i], dy, rows[i] * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+                "output copy");
+    dw += rows[i] * cols;
+    dy += rows[i];
+  }
+  rc = wait_stream(ctx, "F32 matvec group command");
+  if (rc) return rc;
+  return ok();
+}
+
+int si_hip_rms_norm(si_hip_context *ctx, const float *x, size_t x_len, const float *w, size_t w_len,
+                    float eps, float *y) {
+  int rc = validate_rms(0, x_len, 0, w_len, 1, x_len, eps);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!x || !w || !y) return fail(SI_HIP_ERR_NULL, "RMSNorm buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  return run_rms_host(ctx, 0, x, nullptr, w, 1, x_len, eps, y);
+}
+
+int si_hip_rms_norm_heads(si_hip_context *ctx, const float *x, size_t x_len, const float *w,
+                          size_t w_len, size_t heads, size_t head_dim, float eps, float *y) {
+  int rc = validate_rms(1, x_len, 0, w_len, heads, head_dim, eps);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!x || !w || !y) return fail(SI_HIP_ERR_NULL, "head RMSNorm buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  return run_rms_host(ctx, 1, x, nullptr, w, heads, head_dim, eps, y);
+}
+
+int si_hip_rms_norm_gated(si_hip_context *ctx, const float *x, size_t x_len, const float *gate,
+                          size_t gate_len, const float *w, size_t w_len, size_t heads,
+                          size_t head_dim, float eps, float *y) {
+  int rc = validate_rms(2, x_len, gate_len, w_len, heads, head_dim, eps);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!x || !gate || !w || !y) return fail(SI_HIP_ERR_NULL, "Gated RMSNorm buffer is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  return run_rms_host(ctx, 2, x, gate, w, heads, head_dim, eps, y);
+}
+
+int si_hip_rms_norm_device(si_hip_context *ctx, uint32_t mode, const float *d_x, const float *d_gate,
+                           const float *d_w, size_t heads, size_t head_dim, float eps, float *d_y) {
+  if (mode > 2u) return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported RMSNorm mode %u", mode);
+  const size_t n = heads * head_dim;
+  int rc = validate_rms(mode, mode == 0 ? head_dim : n, n, head_dim, mode == 0 ? 1 : heads,
+                        head_dim, eps);
+  if (rc) return rc;
+  if (mode == 0 && heads != 1) return fail(SI_HIP_ERR_DIMENSIONS, "RMSNorm input and weight must have equal non-zero length");
+  if (!ctx || !d_x || !d_w || !d_y || (mode == 2 && !d_gate))
+    return fail(SI_HIP_ERR_NULL, "device RMSNorm argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  hipError_t e = sihip::launch_rms_norm(mode, d_x, d_gate, d_w, d_y, (uint32_t)heads,
+                                        (uint32_t)head_dim, eps, device_stream(ctx));
+  if (e != hipSuccess) return hip_fail(e, "RMSNorm launch");
+  ctx->async_submitted.fetch_add(1);
   return ok();
 }
 

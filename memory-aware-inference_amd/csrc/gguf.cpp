@@ -8,6 +8,7 @@
 // order, the last one to the end of the file.  Error messages are the
 // reference's.  Files are mapped read-only (GgufModelStore::open,
 // model.rs:625-666); nothing is copied until a tensor is uploaded.
+#include "si_hip_f32.h"
 #include "si_hip_gguf.h"
 
 #include <fcntl.h>
@@ -520,6 +521,65 @@ int si_hip_gguf_upload_tensor(si_hip_context *ctx, const si_hip_gguf *g, uint64_
 int si_hip_gguf_bind_tensor_mapped(si_hip_context *ctx, const si_hip_gguf *g, uint64_t index,
                                    si_hip_quant_weight **out) {
   return weight_of(ctx, g, index, true, out);
+}
+
+// F32 matvec over rows [row_start, row_start + row_count) of a rank-2 F32
+// tensor (f32_matvec_tensor_rows, metal.rs:3074-3110).
+int si_hip_gguf_f32_matvec_tensor_rows(si_hip_context *ctx, const si_hip_gguf *g, uint64_t index,
+                                       size_t row_start, size_t row_count, const float *x,
+                                       size_t x_len, float *y) {
+  const Tensor *t = tensor_at(g, index);
+  if (!t) return g ? SI_HIP_ERR_RANGE : SI_HIP_ERR_NULL;
+  if (t->ggml_type != 0 || t->shape.size() != 2)
+    return set_error(SI_HIP_ERR_UNSUPPORTED_TYPE, "F32 matvec requires a rank-2 F32 tensor");
+  const uint64_t cols = t->shape[0], rows = t->shape[1];
+  if (row_count == 0 || row_start >= rows || row_count > rows - row_start)
+    return set_error(SI_HIP_ERR_RANGE, "F32 row range is invalid");
+  if (x_len != cols) return set_error(SI_HIP_ERR_DIMENSIONS, "F32 tensor columns or input length is invalid");
+  uint64_t row_bytes, start, len, end;
+  if (!checked_mul(cols, (uint64_t)sizeof(float), &row_bytes) || !checked_mul(row_count, row_bytes, &len))
+    return set_error(SI_HIP_ERR_OVERFLOW, "F32 row byte length overflows");
+  if (!checked_mul(row_start, row_bytes, &start) || start > UINT64_MAX - len)
+    return set_error(SI_HIP_ERR_OVERFLOW, "F32 row byte range overflows");
+  end = start + len;
+  if (end > t->data_end - t->data_start)
+    return set_error(SI_HIP_ERR_BYTE_LENGTH, "F32 tensor payload is shorter than its shape");
+  return si_hip_f32_matvec_bytes(ctx, g->bytes + t->data_start + start, (size_t)len, row_count,
+                                 (size_t)cols, x, x_len, y);
+}
+
+// One submission of F32 matvecs over several rank-2 F32 tensors with the same
+// columns and one input (f32_matvec_many_gguf_tensors, metal.rs:4780-4870).
+int si_hip_gguf_f32_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *g,
+                                        const uint64_t *indices, size_t count, const float *x,
+                                        size_t x_len, float *const *outputs) {
+  if (!g) return set_error(SI_HIP_ERR_NULL, "GGUF store is null");
+  if (count == 0) return set_error(SI_HIP_ERR_EMPTY, "GGUF F32 matvec group requires at least one tensor");
+  if (!indices || !outputs) return set_error(SI_HIP_ERR_NULL, "GGUF F32 matvec group argument is null");
+  const Tensor *first = tensor_at(g, indices[0]);
+  if (!first) return SI_HIP_ERR_RANGE;
+  if (first->shape.empty()) return set_error(SI_HIP_ERR_DIMENSIONS, "GGUF F32 matvec tensor is not a matrix");
+  const uint64_t cols = first->shape[0];
+  if (x_len != cols) return set_error(SI_HIP_ERR_DIMENSIONS, "GGUF F32 matvec group input length is invalid");
+  std::vector<const float *> ws(count);
+  std::vector<size_t> rows(count);
+  for (size_t i = 0; i < count; ++i) {
+    const Tensor *t = tensor_at(g, indices[i]);
+    if (!t) return SI_HIP_ERR_RANGE;
+    if (t->ggml_type != 0 || t->shape.size() != 2 || t->shape[0] != cols)
+      return set_error(SI_HIP_ERR_DIMENSIONS, "GGUF F32 matvec group shapes or types differ");
+    uint64_t expected;
+    if (!checked_mul(t->shape[1], cols, &expected) || !checked_mul(expected, (uint64_t)sizeof(float), &expected))
+      return set_error(SI_HIP_ERR_OVERFLOW, "GGUF F32 matvec group byte length overflows");
+    if (t->data_end - t->data_start != expected)
+      return set_error(SI_HIP_ERR_BYTE_LENGTH, "GGUF F32 matvec group tensor is truncated");
+    const uint8_t *p = g->bytes + t->data_start;
+    if (reinterpret_cast<uintptr_t>(p) % alignof(float) != 0)
+      return set_error(SI_HIP_ERR_BYTE_LENGTH, "F32 matvec bytes are not 4-byte aligned");
+    ws[i] = reinterpret_cast<const float *>(p);
+    rows[i] = (size_t)t->shape[1];
+  }
+  return si_hip_f32_matvec_many(ctx, ws.data(), rows.data(), count, (size_t)cols, x, x_len, outputs);
 }
 
 }  // extern "C"

@@ -71,6 +71,14 @@ hipError_t launch_fused_gate_up_generic(const uint8_t* gate, const uint8_t* up, 
 hipError_t launch_dequant(uint32_t type, const uint8_t* w, const uint32_t* row_index, float* out,
                           uint32_t out_rows, uint32_t cols, hipStream_t s);
 
+// kernels_f32.hip: y = W x for a row-major F32 matrix; RMSNorm of `heads`
+// vectors of head_dim values, mode 0 (x * inv * w), 1 (x * inv * (1 + w)) or
+// 2 (x * inv * w * silu(gate)).
+hipError_t launch_f32_matvec(const float* w, const float* x, float* y, uint32_t rows,
+                             uint32_t cols, hipStream_t s);
+hipError_t launch_rms_norm(uint32_t mode, const float* x, const float* gate, const float* w,
+                           float* y, uint32_t heads, uint32_t head_dim, float eps, hipStream_t s);
+
 // kernels_argmax.hip: max-loc over n < 2^31 logits in one launch, using the
 // context workspace's argmax area; the winner lands in *result (packed
 // candidate, 0 when there is none).

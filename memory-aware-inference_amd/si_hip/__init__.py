@@ -134,6 +134,19 @@ _SIGS = {
     "si_hip_peak_active_weight_bytes": (_U64, [_P]),
     "si_hip_reset_peaks": (None, [_P]),
     "si_hip_get_command_stats": (_I, [_P, C.POINTER(CommandStats)]),
+    # si_hip_f32.h
+    "si_hip_f32_matvec": (_I, [_P, _FP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_f32_matvec_bytes": (_I, [_P, _BP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_f32_matvec_many": (_I, [_P, C.POINTER(_FP), C.POINTER(_SZ), _SZ, _SZ, _FP, _SZ,
+                                    C.POINTER(_FP)]),
+    "si_hip_f32_matvec_device": (_I, [_P, _P, _SZ, _SZ, _P, _P]),
+    "si_hip_rms_norm": (_I, [_P, _FP, _SZ, _FP, _SZ, C.c_float, _FP]),
+    "si_hip_rms_norm_heads": (_I, [_P, _FP, _SZ, _FP, _SZ, _SZ, _SZ, C.c_float, _FP]),
+    "si_hip_rms_norm_gated": (_I, [_P, _FP, _SZ, _FP, _SZ, _FP, _SZ, _SZ, _SZ, C.c_float, _FP]),
+    "si_hip_rms_norm_device": (_I, [_P, _U32, _P, _P, _P, _SZ, _SZ, C.c_float, _P]),
+    "si_hip_gguf_f32_matvec_tensor_rows": (_I, [_P, _P, _U64, _SZ, _SZ, _FP, _SZ, _FP]),
+    "si_hip_gguf_f32_matvec_many_tensors": (_I, [_P, _P, C.POINTER(_U64), _SZ, _FP, _SZ,
+                                                 C.POINTER(_FP)]),
     # si_hip_gguf.h
     "si_hip_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
     "si_hip_gguf_parse": (_I, [_BP, _SZ, C.POINTER(_P)]),
@@ -489,6 +502,57 @@ class HipContext:
             _fp(logits) if logits is not None else None))
         return int(tok.value), logits
 
+    # ---- F32 matvec and RMSNorm (include/si_hip_f32.h) ----
+    def f32_matvec(self, weight_values, rows: int, columns: int, input) -> np.ndarray:
+        w = _f32(weight_values).reshape(-1)
+        x = _f32(input)
+        y = np.empty(max(rows, 1), dtype=np.float32)
+        _check(lib().si_hip_f32_matvec(self._h, _fp(w), w.size, rows, columns, _fp(x), x.size,
+                                       _fp(y)))
+        return y[:rows]
+
+    def f32_matvec_bytes(self, weight_bytes, rows: int, columns: int, input) -> np.ndarray:
+        b = _u8(weight_bytes)
+        x = _f32(input)
+        y = np.empty(max(rows, 1), dtype=np.float32)
+        _check(lib().si_hip_f32_matvec_bytes(self._h, _bp(b), b.size, rows, columns, _fp(x),
+                                             x.size, _fp(y)))
+        return y[:rows]
+
+    def f32_matvec_many(self, weights: Sequence, rows: Sequence[int], columns: int,
+                        input) -> list:
+        ws = [_f32(w).reshape(-1) for w in weights]
+        x = _f32(input)
+        ys = [np.empty(max(r, 1), dtype=np.float32) for r in rows]
+        wp = (_FP * len(ws))(*[_fp(w) for w in ws])
+        yp = (_FP * len(ys))(*[_fp(y) for y in ys])
+        rp = (C.c_size_t * len(rows))(*rows)
+        _check(lib().si_hip_f32_matvec_many(self._h, wp, rp, len(ws), columns, _fp(x), x.size,
+                                            yp))
+        return [y[:r] for y, r in zip(ys, rows)]
+
+    def rms_norm(self, input, weight, epsilon: float) -> np.ndarray:
+        x, w = _f32(input), _f32(weight)
+        y = np.empty(max(x.size, 1), dtype=np.float32)
+        _check(lib().si_hip_rms_norm(self._h, _fp(x), x.size, _fp(w), w.size, epsilon, _fp(y)))
+        return y[:x.size]
+
+    def rms_norm_heads(self, input, weight, heads: int, head_dim: int,
+                       epsilon: float) -> np.ndarray:
+        x, w = _f32(input), _f32(weight)
+        y = np.empty(max(x.size, 1), dtype=np.float32)
+        _check(lib().si_hip_rms_norm_heads(self._h, _fp(x), x.size, _fp(w), w.size, heads,
+                                           head_dim, epsilon, _fp(y)))
+        return y[:x.size]
+
+    def rms_norm_gated(self, input, gate, weight, heads: int, head_dim: int,
+                       epsilon: float) -> np.ndarray:
+        x, g, w = _f32(input), _f32(gate), _f32(weight)
+        y = np.empty(max(x.size, 1), dtype=np.float32)
+        _check(lib().si_hip_rms_norm_gated(self._h, _fp(x), x.size, _fp(g), g.size, _fp(w),
+                                           w.size, heads, head_dim, epsilon, _fp(y)))
+        return y[:x.size]
+
     def dequantize(self, ggml_type: int, data, elements: int) -> np.ndarray:
         b = _u8(data)
         y = np.empty(max(elements, 1), dtype=np.float32)
@@ -765,6 +829,28 @@ class GgufFile:
         fn = lib().si_hip_gguf_bind_tensor_mapped if mapped else lib().si_hip_gguf_upload_tensor
         _check(fn(ctx.handle, self._h, self._index(name), C.byref(w)))
         return QuantWeight(ctx, w.value)
+
+    def f32_matvec_tensor_rows(self, ctx: "HipContext", name: str, row_start: int,
+                               row_count: int, input) -> np.ndarray:
+        """f32_matvec_tensor_rows (src/metal.rs:3074-3110) on this store's tensor."""
+        x = _f32(input)
+        y = np.empty(max(row_count, 1), dtype=np.float32)
+        _check(lib().si_hip_gguf_f32_matvec_tensor_rows(ctx.handle, self._h, self._index(name),
+                                                        row_start, row_count, _fp(x), x.size,
+                                                        _fp(y)))
+        return y[:row_count]
+
+    def f32_matvec_many(self, ctx: "HipContext", names: Sequence[str], input) -> list:
+        """f32_matvec_many_gguf_tensors (src/metal.rs:4780-4870): one result per tensor."""
+        x = _f32(input)
+        idx = [self._index(n) for n in names]
+        ys = [np.empty(max(int(self.tensor_list[i].shape[1]), 1) if len(self.tensor_list[i].shape) == 2
+                       else 1, dtype=np.float32) for i in idx]
+        yp = (_FP * len(ys))(*[_fp(y) for y in ys])
+        ip = (C.c_uint64 * len(idx))(*idx)
+        _check(lib().si_hip_gguf_f32_matvec_many_tensors(ctx.handle, self._h, ip, len(idx), _fp(x),
+                                                         x.size, yp))
+        return ys
 
     def inspect(self, model: str | None = None) -> str:
         """The dump si-gguf-inspect prints (src/bin/si-gguf-inspect.rs:11-60)."""

@@ -61,6 +61,11 @@ def lib() -> C.CDLL:
         h.kq_argmax_last_finite.argtypes = [_FP, C.c_size_t, C.POINTER(C.c_uint32)]
         h.kq_argmax_first_greater.restype = C.c_uint32
         h.kq_argmax_first_greater.argtypes = [_FP, C.c_size_t]
+        h.kq_f32_matvec_ref.restype = C.c_int
+        h.kq_f32_matvec_ref.argtypes = [_FP, _FP, C.c_size_t, C.c_size_t, _FP]
+        h.kq_rms_norm_ref.restype = C.c_int
+        h.kq_rms_norm_ref.argtypes = [C.c_uint32, _FP, _FP, _FP, C.c_size_t, C.c_size_t,
+                                      C.c_float, _FP]
         _lib = h
     return _lib
 
@@ -132,3 +137,27 @@ def argmax_last_finite(v) -> int | None:
 def argmax_first_greater(v) -> int:
     a = np.ascontiguousarray(v, dtype=np.float32)
     return int(lib().kq_argmax_first_greater(a.ctypes.data_as(_FP), a.size))
+
+
+def _fp(a: np.ndarray):
+    return a.ctypes.data_as(_FP)
+
+
+def f32_matvec(w, x, rows: int, cols: int) -> np.ndarray:
+    """Sequential-f32 F32 matvec of the reference's test (oracle/f32_ref.c)."""
+    w = np.ascontiguousarray(w, dtype=np.float32).reshape(-1)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(rows, dtype=np.float32)
+    assert lib().kq_f32_matvec_ref(_fp(w), _fp(x), rows, cols, _fp(out)) == 0
+    return out
+
+
+def rms_norm(mode: int, x, w, heads: int, head_dim: int, eps: float, gate=None) -> np.ndarray:
+    """RMSNorm of oracle/f32_ref.c: mode 0 (x*inv*w), 1 (x*inv*(1+w)), 2 (gated)."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    g = np.ascontiguousarray(gate if gate is not None else np.zeros(1), dtype=np.float32)
+    out = np.empty(heads * head_dim, dtype=np.float32)
+    assert lib().kq_rms_norm_ref(mode, _fp(x), _fp(g) if gate is not None else None, _fp(w),
+                                 heads, head_dim, eps, _fp(out)) == 0
+    return out
