@@ -181,7 +181,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
                                                               uint32_t nb, void* __restrict__ wsp,
-                                                              SchedArgs sa) {
+                                                              SchedArgs sa, uint32_t prefetch) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t slots = sa.packed & 0xffu;
   const Layout L = layout(WAVES, DEPTH, nb, slots);
@@ -231,16 +231,40 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
 #pragma unroll
   for (int j = 0; j < DEPTH; ++j)
     if ((uint32_t)j < my_pairs) issue(j);
+  // With one stage in flight, up to `prefetch` (<= 2) later pairs of the wave
+  // are touched into L2 while the images are built: every 128-byte line of
+  // their rows' 420 bytes is read 4 bytes wide (offsets 0, 128, 256, 384 and
+  // 416 of each row) into a 256-byte LDS sink past the layout that nothing
+  // reads.  Their copies then find the lines in L2.
+  const uint32_t npf = DEPTH == 1 && my_pairs > 1u ? min(min(prefetch, 2u), my_pairs - 1u) : 0u;
+  for (uint32_t j = 1; j <= npf; ++j) {
+    const Pair pr = pair_at(sc, wave + j * WAVES, nstages);
+    const uint32_t row0 = pr.tile * 16u;
+    const uint32_t nrows = min(16u, rows - row0);
+    const uint8_t* sb = w + (size_t)row0 * row_bytes + kStageRowBytes * pr.r;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - kStageRowBytes * pr.r),
+        kBufferWord3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(smem + L.total), 4,
+                                              n * row_bytes + 128u * grp, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(smem + L.total), 4,
+                                              n * row_bytes + kStageRowBytes - 4u, 0, 0, 0);
+  }
 
   // 3. ring slots, then (once the x copies have landed) digit images and
   //    exponents
   init_slots<WAVES>(sbase, L, slots);
-  // the stage copies were issued after x's and complete in order
+  // the stage copies (then the touches) were issued after x's and complete in
+  // order
   const uint32_t early = min((uint32_t)DEPTH, my_pairs);
   if (early >= 3u)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * kCopies));
   else if (early == 2u)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kCopies));
+  else if (early == 1u && npf == 2u)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies + 4));
+  else if (early == 1u && npf == 1u)
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies + 2));
   else if (early == 1u)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies));
   else
@@ -322,7 +346,11 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
   const LaunchShape ls = launch_shape(ntiles, nstages, W, ws.bytes, 1u);
   const uint32_t grid = ls.groups;
   const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, nstages);
-  const uint32_t lds = layout(W, D, nb, slots).total;
+  // One pair touched ahead pays where the image build is long (the 68-block
+  // down projection: 1 us of 22); with 20 blocks (the output head) it costs.
+  static const int pf_env = env_int("SI_HIP_Q6K_PREFETCH", -1);
+  const uint32_t prefetch = pf_env >= 0 ? (uint32_t)pf_env : (nb >= 48u ? 1u : 0u);
+  const uint32_t lds = layout(W, D, nb, slots).total + (D == 1 && prefetch ? 256u : 0u);
   SchedArgs sa;
   if (lds > kLdsBytes || !make_sched_args(ntiles, nstages, slots, ls, &sa)) return false;
   static const hipError_t attr = hipFuncSetAttribute(
@@ -333,7 +361,7 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
     return true;
   }
   hipLaunchKernelGGL((q6k_matvec_mfma<W, D>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
-                     nb, ws.ptr, sa);
+                     nb, ws.ptr, sa, D == 1 ? prefetch : 0u);
   *err = hipGetLastError();
   return true;
 }
