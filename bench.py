@@ -300,6 +300,23 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     for w in ws:
         w.free()
     ctx.device_free(X); ctx.device_free(Y)
+    # the same verify through the Q6_K output head (638 MB, one copy: it
+    # exceeds the 256 MB MALL on its own)
+    Q6, HN = si_hip.GGML_TYPE_Q6_K, 151936
+    head = upload(Q6, 502, HN, K)
+    X = dev_f32(si_hip.synth_normal(503, 16 * K))
+    Y = ctx.device_alloc(16 * HN * 4)
+    many = {}
+    for m in (1, 4, 16):
+        ms = _timed(ctx, lambda i, m=m: si_hip._check(lib.si_hip_matmul_many_device(
+            ctx.handle, head.handle, HN, K, m, C.c_void_p(X), C.c_void_p(Y))),
+            max(4, steps // 4), min(warmup, 2))
+        r = _rate(bpc(Q6, HN, K), ms)
+        r["tflop_per_s"] = round(2.0 * m * HN * K / (ms * 1e-3) / 1e12, 3)
+        many[f"M{m}"] = r
+    res["matmul_many_q6k_head_151936x5120"] = many
+    head.free()
+    ctx.device_free(X); ctx.device_free(Y)
     return res
 
 

@@ -48,8 +48,8 @@ static_assert(16u * (kRowPieces - 1u) <= kStageRowBytes && kLastPiece % 4u == 0u
 static_assert(16u * kRowPieces <= kCopies * 64u, "copies cover every piece");
 
 __host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
-                                            uint32_t slots) {
-  return make_layout(kStageBytes, 2u, 0u, waves, depth, nb, slots, 1u);
+                                            uint32_t slots, uint32_t ntok = 1u) {
+  return make_layout(kStageBytes, 2u, 0u, waves, depth, nb, slots, 1u, ntok);
 }
 
 // The lane's 13 pieces of a stage buffer (piece q of row n at 256 q + 16 n;
@@ -176,7 +176,32 @@ __device__ __forceinline__ float block_exact(const i32x4 (&q)[4], const int (&sc
   return acc;
 }
 
-template <int WAVES, int DEPTH>
+// The same sum in the same order, one weight per iteration: for kernels that
+// keep several vectors' state live, where the unrolled form's 64 loads in
+// flight would crowd the registers.
+__device__ __forceinline__ float block_exact_lean(const i32x4 (&q)[4], const int (&sc)[4],
+                                                  float d, const float* __restrict__ xs) {
+  float acc = 0.0f;
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+#pragma unroll 1
+    for (uint32_t i = 0; i < 16u; ++i) {
+      const uint32_t k = i >> 2;
+      const uint32_t word = (uint32_t)(k == 0u   ? q[t][0]
+                                       : k == 1u ? q[t][1]
+                                       : k == 2u ? q[t][2]
+                                                 : q[t][3]);
+      const int qv = (int)((word >> (8u * (i & 3u))) & 0xffu) - 32;
+      acc = fmaf(k6_value_exact(d, sc[t], qv), xs[32 * t + (int)i], acc);
+    }
+  }
+  return acc;
+}
+
+// NTOK activation vectors (batch-major x and y) share each decoded stage:
+// vector t's images sit at img + t img_stride, and a launch with NTOK > 1
+// gives every workgroup whole tiles (no split).
+template <int WAVES, int DEPTH, int NTOK>
 __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
@@ -184,7 +209,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
                                                               SchedArgs sa, uint32_t prefetch) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t slots = sa.packed & 0xffu;
-  const Layout L = layout(WAVES, DEPTH, nb, slots);
+  const Layout L = layout(WAVES, DEPTH, nb, slots, NTOK);
   const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
@@ -196,8 +221,12 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
   uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
 
-  // 1. x into the image area, natural order (block b at img + 1024 b)
-  copy_x<WAVES>(smem, L.img, x, nb, wave, lane);
+  // 1. x into the image area, natural order (block b of vector t at
+  //    img + t img_stride + 1024 b)
+#pragma unroll
+  for (int t = 0; t < NTOK; ++t)
+    copy_x<WAVES>(smem, L.img + t * L.img_stride, x + (size_t)t * nb * kBlockElems, nb, wave,
+                  lane);
 
   // 2. this wave's pairs k = wave, wave + WAVES, ... of the workgroup's pairs
   //    (pair_at: a tile and its stage) and the copies of its first DEPTH, pair
@@ -270,9 +299,11 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   else
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
   // chunk c = 8 h + 2 t + s: MFMA t of lane group 2 h + s
-  build_images<WAVES>(sbase, L, nb, wave, grp, n, [](uint32_t c) {
-    return 256u * ((c >> 1) & 3u) + 64u * (2u * (c >> 3) + (c & 1u));
-  });
+#pragma unroll
+  for (int t = 0; t < NTOK; ++t)
+    build_images<WAVES>(sbase, L, nb, wave, grp, n, [](uint32_t c) {
+      return 256u * ((c >> 1) & 3u) + 64u * (2u * (c >> 3) + (c & 1u));
+    }, t);
   lds_wait();
   __builtin_amdgcn_s_barrier();
 
@@ -322,6 +353,38 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
                          scale_at(u2, sb_lo)};
     const float d1 = half_bits_to_float(v[12][3] >> 16);
 
+    if constexpr (NTOK > 1) {
+      // the decoded stage meets every vector in turn (vector 0's images and
+      // exponents are already in A, e0, e1); each vector's row sums go
+      // straight to the tile's slot
+      const uint32_t part_at = token_slot(sbase, L, sc.by_slots, pr, nstages, NTOK, lane);
+#pragma unroll 1
+      for (uint32_t t = 0; t < (uint32_t)NTOK; ++t) {
+        int f0 = e0, f1 = e1;
+        if (t > 0u) {
+          lds_read_images(sbase + L.img + t * L.img_stride + 2048u * st + 16u * n, kActiveLanes,
+                          A);
+          const u32x2 et = lds_read_b64(sbase + L.expo + t * L.expo_stride + 8u * st);
+          f0 = __builtin_amdgcn_readfirstlane(et[0]);
+          f1 = __builtin_amdgcn_readfirstlane(et[1]);
+        }
+        const float a0 = block_terms(q0, sc_0, d0, A[0], A[1], A[2], A[3], f0);
+        const float a1 = block_terms(q1, sc_1, d1, A[4], A[5], A[6], A[7], f1);
+        float p0 = f0 != kBadBlock ? a0 : 0.0f;
+        float p1 = f1 != kBadBlock ? a1 : 0.0f;
+        if (f0 == kBadBlock || f1 == kBadBlock) {
+          const float* xb =
+              x + (size_t)t * nb * kBlockElems + 512u * st + 128u * half + 16u * sub;
+          if (f0 == kBadBlock) p0 = block_exact_lean(q0, sc_0, d0, xb);
+          if (f1 == kBadBlock) p1 = block_exact_lean(q1, sc_1, d1, xb + 256);
+        }
+        const float rowsum = sum_lane_groups(p0 + p1);
+        if (grp == 0u) lds_write_b32(part_at + 64u * t, __float_as_uint(rowsum));
+      }
+      token_slot_done<NTOK>(sbase, L, sc.by_slots, pr, nstages, lane, rows, y);
+      continue;
+    }
+
     const float c0 = block_terms(q0, sc_0, d0, A[0], A[1], A[2], A[3], e0);
     const float c1 = block_terms(q1, sc_1, d1, A[4], A[5], A[6], A[7], e1);
     float part0 = e0 != kBadBlock ? c0 : 0.0f;
@@ -338,32 +401,42 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   }
 }
 
-template <int W, int D>
+template <int W, int D, int NT = 1>
 bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = (nb + 1u) / 2u;
-  const LaunchShape ls = launch_shape(ntiles, nstages, W, ws.bytes, 1u);
+  // several vectors: whole tiles only
+  const LaunchShape ls = launch_shape(ntiles, nstages, W, NT == 1 ? ws.bytes : 0u, 1u);
   const uint32_t grid = ls.groups;
   const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, nstages);
   // One pair touched ahead pays where the image build is long (the 68-block
   // down projection: 1 us of 22); with 20 blocks (the output head) it costs.
   static const int pf_env = env_int("SI_HIP_Q6K_PREFETCH", -1);
   const uint32_t prefetch = pf_env >= 0 ? (uint32_t)pf_env : (nb >= 48u ? 1u : 0u);
-  const uint32_t lds = layout(W, D, nb, slots).total + (D == 1 && prefetch ? 256u : 0u);
+  const uint32_t lds = layout(W, D, nb, slots, NT).total + (D == 1 && prefetch ? 256u : 0u);
   SchedArgs sa;
   if (lds > kLdsBytes || !make_sched_args(ntiles, nstages, slots, ls, &sa)) return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D>),
+      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, NT>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q6k_matvec_mfma<W, D>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
+  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, NT>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
                      nb, ws.ptr, sa, D == 1 ? prefetch : 0u);
   *err = hipGetLastError();
   return true;
+}
+
+// even nb (4-byte aligned rows and stages); in-tile offsets (16 rows) and the
+// descriptor sizes are 32-bit
+bool q6_shape_ok(uint32_t rows, uint32_t nb) {
+  return nb != 0 && (nb & 1u) == 0 && rows != 0 && (uint64_t)nb * kQ6Bytes * 16u <= 0x7fffffffu &&
+         (uint64_t)nb * 1024u <= 0x7fffffffu &&
+         (uint64_t)((rows + 15u) / 16u) * (nb / 2u) <= 0xffffffffu &&
+         quotients_fit((rows + 15u) / 16u, nb / 2u);
 }
 
 }  // namespace
@@ -371,13 +444,7 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t nb = cols / kBlockElems;
-  // even nb (4-byte aligned rows and stages); in-tile offsets (16 rows) and
-  // the descriptor sizes are 32-bit
-  if (nb == 0 || (nb & 1u) || rows == 0 || (uint64_t)nb * kQ6Bytes * 16u > 0x7fffffffu ||
-      (uint64_t)nb * 1024u > 0x7fffffffu ||
-      (uint64_t)((rows + 15u) / 16u) * (nb / 2u) > 0xffffffffu ||
-      !quotients_fit((rows + 15u) / 16u, nb / 2u))
-    return false;
+  if (!q6_shape_ok(rows, nb)) return false;
   static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
   switch (cfg) {
     case 1: return launch_wd<12, 1>(w, x, y, rows, nb, ws, s, err);
@@ -388,6 +455,41 @@ bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
   }
   return launch_wd<12, 1>(w, x, y, rows, nb, ws, s, err) || launch_wd<10, 1>(w, x, y, rows, nb, ws, s, err) ||
          launch_wd<8, 1>(w, x, y, rows, nb, ws, s, err) || launch_wd<4, 1>(w, x, y, rows, nb, ws, s, err);
+}
+
+// batch >= 2 vectors: four, three or two per pass over the weights while
+// their images fit the LDS beside the stage buffers (K up to about 5120 for
+// four), one per pass otherwise.
+bool launch_q6k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
+                            hipError_t* err) {
+  const uint32_t nb = cols / kBlockElems;
+  if (!q6_shape_ok(rows, nb)) return false;
+  for (uint32_t b = 0; b < batch;) {
+    const uint32_t left = batch - b;
+    const float* xb = x + (size_t)b * cols;
+    float* yb = y + (size_t)b * rows;
+    uint32_t nt = 0;
+    if (left >= 4u && (launch_wd<8, 1, 4>(w, xb, yb, rows, nb, ws, s, err) ||
+                       launch_wd<6, 1, 4>(w, xb, yb, rows, nb, ws, s, err)))
+      nt = 4;
+    else if (left == 3u && (launch_wd<8, 1, 3>(w, xb, yb, rows, nb, ws, s, err) ||
+                            launch_wd<6, 1, 3>(w, xb, yb, rows, nb, ws, s, err)))
+      nt = 3;
+    else if (left >= 2u && (launch_wd<8, 1, 2>(w, xb, yb, rows, nb, ws, s, err) ||
+                            launch_wd<6, 1, 2>(w, xb, yb, rows, nb, ws, s, err)))
+      nt = 2;
+    else if (launch_q6k_matvec_mfma(w, xb, yb, rows, cols, ws, s, err))
+      nt = 1;
+    if (nt == 0) {
+      if (b == 0) return false;
+      *err = hipErrorInvalidValue;
+      return true;
+    }
+    if (*err != hipSuccess) return true;
+    b += nt;
+  }
+  return true;
 }
 
 }  // namespace sihip

@@ -309,6 +309,9 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
   if (type == kTypeQ5K && mode == 0)
     return batch == 1 ? launch_q5k_matvec_mfma(w, x, y, rows, cols, ws, s, err)
                       : launch_q5k_matmul_mfma(w, x, y, rows, cols, batch, ws, s, err);
+  if (type == kTypeQ6K && batch > 1 &&
+      launch_q6k_matmul_mfma(w, x, y, rows, cols, batch, ws, s, err))
+    return true;
   if (type == kTypeQ6K || (q4_mfma && batch > 1)) {
     // several candidates (batch-major x and y, metal.rs:1104-1126): one
     // matrix-core matvec per candidate, each bit-identical to its M = 1 call

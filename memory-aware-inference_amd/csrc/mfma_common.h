@@ -606,24 +606,29 @@ inline LaunchShape launch_shape(uint32_t ntiles, uint32_t tparts, uint32_t waves
 
 // hand_off for NTOK activation vectors at once, whole tiles only: partial r
 // of the tile holds 16 rows x NTOK sums; the finishing wave stores
-// y[tok * rows + row] for every token.
-template <int NTOK>
-__device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L,
-                                                const FastDiv& by_slots, const Pair& pr,
-                                                uint32_t tparts, const float (&rowsum)[NTOK],
-                                                uint32_t lane, uint32_t rows,
-                                                float* __restrict__ y) {
-  const uint32_t grp = lane >> 4, n = lane & 15u;
+// y[tok * rows + row] for every token.  In two halves for kernels that write
+// one vector's sums at a time: token_slot waits until the tile owns its ring
+// slot and returns the LDS address of this lane's row in partial pr.r (vector
+// t at + 64 t); token_slot_done counts the partial and, in the wave that
+// completes the tile, adds the partials in order and stores the rows.
+__device__ __forceinline__ uint32_t token_slot(uint32_t sbase, const Layout& L,
+                                               const FastDiv& by_slots, const Pair& pr,
+                                               uint32_t tparts, uint32_t ntok, uint32_t lane) {
   const uint32_t slots = by_slots.d;
   const uint32_t slot = pr.lt - quo(pr.lt, by_slots) * slots;
   for (uint32_t spin = 0;
        lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
     __builtin_amdgcn_s_sleep(1);
-  const uint32_t base = sbase + L.part + 64u * NTOK * (slot * tparts + pr.r) + 4u * n;
-  if (grp == 0u) {
-#pragma unroll
-    for (int t = 0; t < NTOK; ++t) lds_write_b32(base + 64u * t, __float_as_uint(rowsum[t]));
-  }
+  return sbase + L.part + 64u * ntok * (slot * tparts + pr.r) + 4u * (lane & 15u);
+}
+template <int NTOK>
+__device__ __forceinline__ void token_slot_done(uint32_t sbase, const Layout& L,
+                                                const FastDiv& by_slots, const Pair& pr,
+                                                uint32_t tparts, uint32_t lane, uint32_t rows,
+                                                float* __restrict__ y) {
+  const uint32_t grp = lane >> 4, n = lane & 15u;
+  const uint32_t slots = by_slots.d;
+  const uint32_t slot = pr.lt - quo(pr.lt, by_slots) * slots;
   uint32_t old = 0u;
   if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);
   const uint32_t done = __builtin_amdgcn_readlane(old, 0);
@@ -641,6 +646,19 @@ __device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L,
     lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
     lds_write_b32(sbase + L.owner + 4u * slot, pr.lt + slots);
   }
+}
+template <int NTOK>
+__device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L,
+                                                const FastDiv& by_slots, const Pair& pr,
+                                                uint32_t tparts, const float (&rowsum)[NTOK],
+                                                uint32_t lane, uint32_t rows,
+                                                float* __restrict__ y) {
+  const uint32_t base = token_slot(sbase, L, by_slots, pr, tparts, NTOK, lane);
+  if ((lane >> 4) == 0u) {
+#pragma unroll
+    for (int t = 0; t < NTOK; ++t) lds_write_b32(base + 64u * t, __float_as_uint(rowsum[t]));
+  }
+  token_slot_done<NTOK>(sbase, L, by_slots, pr, tparts, lane, rows, y);
 }
 
 // hand_off_tokens for kernels that keep vector g's row sums in lane group g

@@ -28,9 +28,13 @@ bool launch_q5k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
 bool launch_q5k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
                             hipError_t* err);
-// Q6_K, one vector, on the matrix cores.
+// Q6_K, one vector / batch >= 2 vectors (up to four per pass over the
+// weights), on the matrix cores.
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
+bool launch_q6k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
+                            hipError_t* err);
 // Fused SwiGLU gate/up (both Q4_K) on the matrix cores: h = silu(gate.x) * (up.x).
 bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float* x, float* h,
                              uint32_t rows, uint32_t cols, const Workspace& ws, hipStream_t s,

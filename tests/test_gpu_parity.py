@@ -440,6 +440,59 @@ def test_matmul_many_baseline_shape(hip_ctx):
         assert np.array_equal(outs[b], again[b])
 
 
+@pytest.mark.parametrize("rows,cols,batch", [(100, 2560, 3), (33, 512, 2), (1040, 5120, 7),
+                                             (512, 5120, 16), (300, 17408, 2), (48, 2304, 3)])
+def test_q6_k_matmul_many_shapes(hip_ctx, rows, cols, batch):
+    """Q6_K candidates four, three or two per pass over the weights: partial
+    tiles, a short K, the down projection's K (whose images do not fit two
+    vectors: one per pass) and an odd block count (the generic kernel)."""
+    log(f"q6_k matmul_many {rows}x{cols} batch={batch}")
+    w = si_hip.synth_matrix(14, seed=rows * 3 + cols, rows=rows, cols=cols)
+    X = si_hip.synth_normal(rows + 2 * batch, batch * cols).reshape(batch, cols)
+    W = hip_ctx.upload_quant_weight_private(w, 14)
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    again = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(batch):
+        _, y64, ab = O.matvec(14, w, rows, cols, X[b])
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+        assert np.array_equal(outs[b], again[b])
+
+
+def test_q6_k_matmul_many_nonfinite_and_outlier_vectors(hip_ctx):
+    """Q6_K blocks on the exact path in some vectors of a pass and not in
+    others."""
+    rows, cols, batch = 48, 2560, 4
+    w = si_hip.synth_matrix(14, seed=4244, rows=rows, cols=cols)
+    W = hip_ctx.upload_quant_weight_private(w, 14)
+    X = si_hip.synth_normal(4245, batch * cols).reshape(batch, cols).copy()
+    X[0, 600:620] = np.float32(3e30)
+    X[1, 1024:1280] = np.float32(1e-41)
+    X[1, 300] = np.float32(1e6)
+    X[2, 2000] = np.float32(-1e6)
+    X[3, 700] = np.inf
+    X[3, 1500] = np.nan
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(3):
+        _, y64, ab = O.matvec(14, w, rows, cols, X[b])
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+    y32, _, _ = O.matvec(14, w, rows, cols, X[3])
+    assert np.array_equal(_category(outs[3]), _category(y32))
+
+
+def test_q6_k_matmul_many_head_shape(hip_ctx):
+    """Four candidates through the 151936 x 5120 Q6_K output head in one pass:
+    each within the bound of the oracle."""
+    rows, cols, batch = 151936, 5120, 4
+    w = si_hip.synth_matrix(14, seed=2025, rows=rows, cols=cols, threads=8)
+    X = si_hip.synth_normal(2030, batch * cols).reshape(batch, cols)
+    W = hip_ctx.upload_quant_weight_private(w, 14)
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(batch):
+        _, y64, ab = O.matvec(14, w, rows, cols, X[b], threads=8)
+        worst = assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+        log(f"  candidate {b}: worst error / bound = {worst:.4f}")
+
+
 def test_matmul_many_bytes_matches_weight(hip_ctx):
     rows, cols, batch = 96, 1024, 3
     w = si_hip.synth_matrix(13, seed=9, rows=rows, cols=cols)
