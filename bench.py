@@ -300,6 +300,31 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     for w in ws:
         w.free()
     ctx.device_free(X); ctx.device_free(Y)
+    # grouped matvec over one x (q/k/v-like projections): one launch against
+    # one launch per matrix
+    g_rows = (6144, 1024, 1024)
+    gws = [[upload(Q4, 510 + 3 * c + i, r, K) for i, r in enumerate(g_rows)] for c in range(4)]
+    Xg = dev_f32(si_hip.synth_normal(511, K))
+    Yg = ctx.device_alloc(sum(g_rows) * 4)
+    g_bytes = sum(bpc(Q4, r, K) for r in g_rows)
+    ms_one = _timed(ctx, lambda i: ctx.quant_matvec_many_device(gws[i % 4], g_rows, K, Xg, Yg),
+                    steps, warmup)
+
+    def per_matrix(i):
+        off = 0
+        for wq, r in zip(gws[i % 4], g_rows):
+            si_hip._check(lib.si_hip_quant_matvec_device(ctx.handle, wq.handle, r, K,
+                                                         C.c_void_p(Xg), C.c_void_p(Yg + 4 * off)))
+            off += r
+
+    ms_each = _timed(ctx, per_matrix, steps, warmup)
+    res["grouped_q4k_6144+1024+1024x5120"] = {
+        "bytes_per_call": g_bytes, "one_launch": _rate(g_bytes, ms_one),
+        "launch_per_matrix": _rate(g_bytes, ms_each)}
+    for grp in gws:
+        for wq in grp:
+            wq.free()
+    ctx.device_free(Xg); ctx.device_free(Yg)
     # the same verify through the Q6_K output head (638 MB, one copy: it
     # exceeds the 256 MB MALL on its own)
     Q6, HN = si_hip.GGML_TYPE_Q6_K, 151936

@@ -241,6 +241,39 @@ int dispatch_matvec(si_hip_context *ctx, uint32_t type, const uint8_t *w, const 
   return SI_HIP_OK;
 }
 
+// Several matvecs over one x into consecutive outputs (y of weight i at the
+// sum of the earlier rows): one launch when the matrix-core kernel takes the
+// group (Q4_K, 2..8 matrices, rows of all but the last a multiple of 16),
+// else one launch per matrix.
+int dispatch_matvec_group(si_hip_context *ctx, const si_hip_quant_weight *const *ws,
+                          const size_t *rows, size_t count, const float *x, float *y,
+                          uint32_t cols, hipStream_t stream) {
+  if (ctx->policy == SI_HIP_KERNEL_AUTO && count >= 2 && count <= sihip::kMaxGroupWeights) {
+    bool same = true;
+    const uint8_t *w[sihip::kMaxGroupWeights];
+    uint32_t r[sihip::kMaxGroupWeights];
+    for (size_t i = 0; i < count; ++i) {
+      same = same && ws[i]->ggml_type == SI_HIP_GGML_TYPE_Q4_K;
+      w[i] = ws[i]->data();
+      r[i] = (uint32_t)rows[i];
+    }
+    hipError_t e = hipErrorInvalidValue;
+    if (same && sihip::launch_q4k_matvec_group(w, r, (uint32_t)count, cols, x, y, ctx->ws, stream,
+                                               &e)) {
+      if (e != hipSuccess) return hip_fail(e, "grouped matvec launch");
+      return SI_HIP_OK;
+    }
+  }
+  size_t off = 0;
+  for (size_t i = 0; i < count; ++i) {
+    int rc = dispatch_matvec(ctx, ws[i]->ggml_type, ws[i]->data(), x, y + off, (uint32_t)rows[i],
+                             cols, 1, stream);
+    if (rc) return rc;
+    off += rows[i];
+  }
+  return SI_HIP_OK;
+}
+
 int dispatch_gate_up(si_hip_context *ctx, const uint8_t *g, const uint8_t *u, const float *x,
                      float *h, uint32_t rows, uint32_t cols, hipStream_t stream) {
   hipError_t e = hipErrorInvalidValue;
@@ -611,15 +644,10 @@ int si_hip_gguf_quant_matvec_many_weights(si_hip_context *ctx,
   SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
               "input copy");
   float *dst = static_cast<float *>(ctx->stage_out);
+  rc = dispatch_matvec_group(ctx, weights, rows, count, static_cast<const float *>(ctx->stage_in),
+                             dst, (uint32_t)cols, ctx->stream);
+  if (rc) return rc;
   size_t off = 0;
-  for (size_t i = 0; i < count; ++i) {
-    rc = dispatch_matvec(ctx, weights[i]->ggml_type, weights[i]->data(),
-                         static_cast<const float *>(ctx->stage_in), dst + off, (uint32_t)rows[i],
-                         (uint32_t)cols, 1, ctx->stream);
-    if (rc) return rc;
-    off += rows[i];
-  }
-  off = 0;
   for (size_t i = 0; i < count; ++i) {
     SIHIP_CHECK(hipMemcpyAsync(outputs[i], dst + off, rows[i] * sizeof(float), hipMemcpyDeviceToHost,
                                ctx->stream),
@@ -1286,6 +1314,27 @@ int si_hip_quant_matvec_device(si_hip_context *ctx, const si_hip_quant_weight *w
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matvec argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
   rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, 1, device_stream(ctx));
+  if (rc) return rc;
+  ctx->async_submitted.fetch_add(1);
+  return ok();
+}
+
+int si_hip_quant_matvec_many_device(si_hip_context *ctx, const si_hip_quant_weight *const *ws,
+                                    const size_t *rows, size_t count, size_t cols,
+                                    const float *d_in, float *d_out) {
+  if (!ws || !rows) return fail(SI_HIP_ERR_NULL, "grouped matvec arrays are null");
+  if (count == 0) return fail(SI_HIP_ERR_DIMENSIONS, "grouped quantized matvec needs at least one weight");
+  uint64_t total = 0;
+  for (size_t i = 0; i < count; ++i) {
+    int rc = validate_device_matvec(ws[i], rows[i], cols, 1);
+    if (rc) return rc;
+    total += rows[i];
+  }
+  if (total > 0xffffffffu) return fail(SI_HIP_ERR_DIMENSIONS, "grouped quantized matvec rows overflow");
+  if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matvec argument is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  int rc = dispatch_matvec_group(ctx, ws, rows, count, d_in, d_out, (uint32_t)cols,
+                                 device_stream(ctx));
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);
   return ok();

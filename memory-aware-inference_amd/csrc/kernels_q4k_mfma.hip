@@ -340,13 +340,16 @@ struct StageRegs {
   }
 };
 
-template <int WAVES, int DEPTH, int MATS, int NTOK, int QB>
+// GROUPED: the rows are those of ga.count matrices with one K, one after the
+// other (every matrix but the last a whole number of 16-row tiles), and tile
+// t's weights are those of the matrix whose tiles reach past t.
+template <int WAVES, int DEPTH, int MATS, int NTOK, int QB, bool GROUPED>
 __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const uint8_t* __restrict__ w2,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
                                                               uint32_t nb, void* __restrict__ wsp,
-                                                              SchedArgs sa) {
+                                                              SchedArgs sa, GroupArgs ga) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   static_assert(NTOK == 1 || MATS == 1, "several activation vectors: one matrix");
   static_assert(QB == 4 || QB == 5, "Q4_K or Q5_K");
@@ -383,9 +386,21 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
   auto issue = [&](uint32_t j, const Pair& pr) {
     const uint32_t mat = MATS > 1 && pr.r >= nstages ? 1u : 0u, st = pr.r - mat * nstages;
-    const uint32_t row0 = pr.tile * 16u;
-    const uint32_t nrows = min(16u, rows - row0);
-    const uint8_t* sb = (mat ? w2 : w) + (size_t)row0 * row_bytes + 4u * block_bytes(QB) * st;
+    uint32_t row0 = pr.tile * 16u, mrows = rows;
+    const uint8_t* wm = mat ? w2 : w;
+    if constexpr (GROUPED) {
+      wm = ga.w[0];
+      mrows = ga.rows[0];
+#pragma unroll
+      for (uint32_t k = 1; k < kMaxGroup; ++k)
+        if (k < ga.count && pr.tile >= ga.tile_end[k - 1]) {
+          wm = ga.w[k];
+          mrows = ga.rows[k];
+          row0 = (pr.tile - ga.tile_end[k - 1]) * 16u;
+        }
+    }
+    const uint32_t nrows = min(16u, mrows - row0);
+    const uint8_t* sb = wm + (size_t)row0 * row_bytes + 4u * block_bytes(QB) * st;
     // the descriptor ends at the tile's last row: pieces past it read zero
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - 4u * block_bytes(QB) * st),
@@ -1085,9 +1100,10 @@ bool launch_tokens_groups(const uint8_t* w, const float* x, float* y, uint32_t r
          launch_tokens_td<6, 4>(w, x, y, rows, nb, ntok, ws, s, err);
 }
 
-template <int W, int D, int M, int NT = 1, int QB = 4>
+template <int W, int D, int M, int NT = 1, int QB = 4, bool G = false>
 bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, uint32_t rows,
-               uint32_t nb, const Workspace& ws, hipStream_t s, hipError_t* err) {
+               uint32_t nb, const Workspace& ws, hipStream_t s, hipError_t* err,
+               const GroupArgs& ga = GroupArgs{}) {
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t tstages = (nb + 3u) / 4u * M;
   // several vectors: whole tiles only
@@ -1098,14 +1114,14 @@ bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, ui
   SchedArgs sa;
   if (lds > kLdsBytes || !make_sched_args(ntiles, tstages, slots, ls, &sa)) return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT, QB>),
+      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT, QB, G>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT, QB>), dim3(grid), dim3(W * 64), lds, s, w, w2,
-                     x, y, rows, nb, ws.ptr, sa);
+  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT, QB, G>), dim3(grid), dim3(W * 64), lds, s, w,
+                     w2, x, y, rows, nb, ws.ptr, sa, ga);
   *err = hipGetLastError();
   return true;
 }
@@ -1199,6 +1215,31 @@ bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
   return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err) ||
          launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err) ||
          launch_wd<4, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
+}
+
+static_assert(kMaxGroupWeights == kMaxGroup, "the C ABI's group limit is the kernels'");
+
+bool launch_q4k_matvec_group(const uint8_t* const* w, const uint32_t* rows, uint32_t count,
+                             uint32_t cols, const float* x, float* y, const Workspace& ws,
+                             hipStream_t s, hipError_t* err) {
+  if (count < 2u || count > kMaxGroup) return false;
+  GroupArgs ga{};
+  ga.count = count;
+  uint64_t tiles = 0, total = 0;
+  for (uint32_t k = 0; k < count; ++k) {
+    if (rows[k] == 0u || (k + 1u < count && rows[k] % 16u != 0u)) return false;
+    ga.w[k] = w[k];
+    ga.rows[k] = rows[k];
+    total += rows[k];
+    tiles += (rows[k] + 15u) / 16u;
+    if (total > 0xffffffffu) return false;
+    ga.tile_end[k] = (uint32_t)tiles;
+  }
+  if (!shape_ok((uint32_t)total, cols, 1u, 4)) return false;
+  const uint32_t nb = cols / kBlockElems;
+  return launch_wd<12, 1, 1, 1, 4, true>(w[0], nullptr, x, y, (uint32_t)total, nb, ws, s, err,
+                                         ga) ||
+         launch_wd<8, 1, 1, 1, 4, true>(w[0], nullptr, x, y, (uint32_t)total, nb, ws, s, err, ga);
 }
 
 bool launch_q5k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,

@@ -276,6 +276,18 @@ struct SchedArgs {
   uint32_t m_groups, m_parts, m_slots;
 };
 
+// Several matrices of one K in one launch (grouped matvec): matrix k's packed
+// rows, its row count and the running count of 16-row tiles up to and
+// including it.  After SchedArgs, so kernels that do not read it keep their
+// first 64 bytes of arguments as they were.
+constexpr uint32_t kMaxGroup = 8;
+struct GroupArgs {
+  uint32_t count;
+  uint32_t tile_end[kMaxGroup];
+  uint32_t rows[kMaxGroup];
+  const uint8_t* w[kMaxGroup];
+};
+
 // Work split.  With G workgroups and T tiles of S partials each, workgroup g
 // owns the whole tiles g, g + G, ...  When that leaves some workgroups a
 // round of pairs more than others (rounds = pairs / waves, rounded up), the

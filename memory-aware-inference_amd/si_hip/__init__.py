@@ -114,6 +114,8 @@ _SIGS = {
     "si_hip_copy_device": (_I, [_P, _P, _P, _SZ]),
     "si_hip_synchronize": (_I, [_P]),
     "si_hip_quant_matvec_device": (_I, [_P, _P, _SZ, _SZ, _P, _P]),
+    "si_hip_quant_matvec_many_device": (_I, [_P, C.POINTER(_P), C.POINTER(_SZ), _SZ, _SZ, _P,
+                                             _P]),
     "si_hip_q4_k_fused_gate_up_device": (_I, [_P, _P, _P, _SZ, _SZ, _P, _P]),
     "si_hip_fused_mlp_device": (_I, [_P, _P, _P, _P, _SZ, _SZ, _SZ, _P, _P, _P]),
     "si_hip_matmul_many_device": (_I, [_P, _P, _SZ, _SZ, _SZ, _P, _P]),
@@ -423,6 +425,16 @@ class HipContext:
         _check(lib().si_hip_gguf_quant_matvec_many_weights(self._h, harr, rarr, n, columns,
                                                            _fp(x), x.size, oarr))
         return outs
+
+    def quant_matvec_many_device(self, weights: Sequence[QuantWeight], rows: Sequence[int],
+                                 columns: int, d_input: int, d_output: int) -> None:
+        """Device-resident grouped matvec: weight i's rows land in d_output
+        after those of the weights before it (enqueued; synchronize() waits)."""
+        n = len(weights)
+        harr = (C.c_void_p * n)(*[w.handle.value for w in weights])
+        rarr = (C.c_size_t * n)(*rows)
+        _check(lib().si_hip_quant_matvec_many_device(self._h, harr, rarr, n, columns,
+                                                     C.c_void_p(d_input), C.c_void_p(d_output)))
 
     # ---- fused SwiGLU
     def q4_k_fused_gate_up(self, gate_bytes, up_bytes, rows: int, columns: int,

@@ -493,6 +493,39 @@ def test_q6_k_matmul_many_head_shape(hip_ctx):
         log(f"  candidate {b}: worst error / bound = {worst:.4f}")
 
 
+@pytest.mark.parametrize("types,rows,cols", [
+    ((12, 12, 12), (6144, 1024, 1024), 5120),   # one launch
+    ((12, 12, 12), (16, 48, 33), 2304),         # one launch, ragged last matrix
+    ((12,) * 8, (64,) * 7 + (100,), 1024),      # the largest group of one launch
+    ((12, 12), (100, 64), 1024),                # first rows not whole tiles: one launch each
+    ((12, 14, 13), (64, 32, 48), 2560),         # mixed types: one launch each
+])
+def test_grouped_matvec(hip_ctx, types, rows, cols):
+    """Several matvecs over one input (gguf_quant_matvec_many_weights), as one
+    matrix-core launch where the group allows it: every output within the
+    bound of the oracle, the device-resident form bit-identical to the host
+    form, and repeat calls deterministic."""
+    log(f"grouped matvec types={types} rows={rows} cols={cols}")
+    hosts = [si_hip.synth_matrix(t, seed=70 + i, rows=r, cols=cols)
+             for i, (t, r) in enumerate(zip(types, rows))]
+    ws = [hip_ctx.upload_quant_weight_private(w, t) for w, t in zip(hosts, types)]
+    x = si_hip.synth_normal(71, cols)
+    outs = hip_ctx.gguf_quant_matvec_many_weights(ws, rows, cols, x)
+    for i, (t, r) in enumerate(zip(types, rows)):
+        _, y64, ab = O.matvec(t, hosts[i], r, cols, x)
+        assert_dot_close(outs[i], y64, ab, what=f"matrix {i}")
+    total = sum(rows)
+    d_x, d_y = hip_ctx.device_alloc(cols * 4), hip_ctx.device_alloc(total * 4)
+    hip_ctx.to_device(d_x, x)
+    for _ in range(2):
+        hip_ctx.quant_matvec_many_device(ws, rows, cols, d_x, d_y)
+        hip_ctx.synchronize()
+        y = hip_ctx.from_device(d_y, (total,))
+        assert np.array_equal(y, np.concatenate(outs))
+    hip_ctx.device_free(d_x)
+    hip_ctx.device_free(d_y)
+
+
 def test_matmul_many_bytes_matches_weight(hip_ctx):
     rows, cols, batch = 96, 1024, 3
     w = si_hip.synth_matrix(13, seed=9, rows=rows, cols=cols)
