@@ -222,9 +222,9 @@ int si_hip_quant_matvec_device(si_hip_context *ctx, const si_hip_quant_weight *w
                                size_t rows, size_t columns, const float *d_input,
                                float *d_output);
 /* gguf_quant_matvec_many_weights (metal.rs:4652-4775) on device buffers:
- * weight i's rows land in d_output after those of weights 0..i-1.  Q4_K
- * groups of 2..8 whose row counts (all but the last) are multiples of 16 run
- * as one launch. */
+ * weight i's rows land in d_output after those of weights 0..i-1.  Groups
+ * of 2..8 weights of one type (Q4_K, Q5_K or Q6_K) whose row counts (all but
+ * the last) are multiples of 16 run as one launch. */
 int si_hip_quant_matvec_many_device(si_hip_context *ctx, const si_hip_quant_weight *const *weights,
                                     const size_t *rows, size_t count, size_t columns,
                                     const float *d_input, float *d_output);

@@ -242,9 +242,9 @@ int dispatch_matvec(si_hip_context *ctx, uint32_t type, const uint8_t *w, const 
 }
 
 // Several matvecs over one x into consecutive outputs (y of weight i at the
-// sum of the earlier rows): one launch when the matrix-core kernel takes the
-// group (Q4_K, 2..8 matrices, rows of all but the last a multiple of 16),
-// else one launch per matrix.
+// sum of the earlier rows): one launch when a matrix-core kernel takes the
+// group (2..8 matrices of one of Q4_K, Q5_K, Q6_K, rows of all but the last a
+// multiple of 16), else one launch per matrix.
 int dispatch_matvec_group(si_hip_context *ctx, const si_hip_quant_weight *const *ws,
                           const size_t *rows, size_t count, const float *x, float *y,
                           uint32_t cols, hipStream_t stream) {
@@ -253,13 +253,13 @@ int dispatch_matvec_group(si_hip_context *ctx, const si_hip_quant_weight *const 
     const uint8_t *w[sihip::kMaxGroupWeights];
     uint32_t r[sihip::kMaxGroupWeights];
     for (size_t i = 0; i < count; ++i) {
-      same = same && ws[i]->ggml_type == SI_HIP_GGML_TYPE_Q4_K;
+      same = same && ws[i]->ggml_type == ws[0]->ggml_type;
       w[i] = ws[i]->data();
       r[i] = (uint32_t)rows[i];
     }
     hipError_t e = hipErrorInvalidValue;
-    if (same && sihip::launch_q4k_matvec_group(w, r, (uint32_t)count, cols, x, y, ctx->ws, stream,
-                                               &e)) {
+    if (same && sihip::launch_matvec_group(ws[0]->ggml_type, w, r, (uint32_t)count, cols, x, y,
+                                           ctx->ws, stream, &e)) {
       if (e != hipSuccess) return hip_fail(e, "grouped matvec launch");
       return SI_HIP_OK;
     }

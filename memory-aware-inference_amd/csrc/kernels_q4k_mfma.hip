@@ -1219,9 +1219,9 @@ bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
 
 static_assert(kMaxGroupWeights == kMaxGroup, "the C ABI's group limit is the kernels'");
 
-bool launch_q4k_matvec_group(const uint8_t* const* w, const uint32_t* rows, uint32_t count,
-                             uint32_t cols, const float* x, float* y, const Workspace& ws,
-                             hipStream_t s, hipError_t* err) {
+bool launch_matvec_group(uint32_t type, const uint8_t* const* w, const uint32_t* rows,
+                         uint32_t count, uint32_t cols, const float* x, float* y,
+                         const Workspace& ws, hipStream_t s, hipError_t* err) {
   if (count < 2u || count > kMaxGroup) return false;
   GroupArgs ga{};
   ga.count = count;
@@ -1235,11 +1235,21 @@ bool launch_q4k_matvec_group(const uint8_t* const* w, const uint32_t* rows, uint
     if (total > 0xffffffffu) return false;
     ga.tile_end[k] = (uint32_t)tiles;
   }
-  if (!shape_ok((uint32_t)total, cols, 1u, 4)) return false;
-  const uint32_t nb = cols / kBlockElems;
-  return launch_wd<12, 1, 1, 1, 4, true>(w[0], nullptr, x, y, (uint32_t)total, nb, ws, s, err,
-                                         ga) ||
-         launch_wd<8, 1, 1, 1, 4, true>(w[0], nullptr, x, y, (uint32_t)total, nb, ws, s, err, ga);
+  const uint32_t nb = cols / kBlockElems, trows = (uint32_t)total;
+  switch (type) {
+    case kTypeQ4K:
+      return shape_ok(trows, cols, 1u, 4) &&
+             (launch_wd<12, 1, 1, 1, 4, true>(w[0], nullptr, x, y, trows, nb, ws, s, err, ga) ||
+              launch_wd<8, 1, 1, 1, 4, true>(w[0], nullptr, x, y, trows, nb, ws, s, err, ga));
+    case kTypeQ5K:
+      return shape_ok(trows, cols, 1u, 5) &&
+             (launch_wd<8, 1, 1, 1, 5, true>(w[0], nullptr, x, y, trows, nb, ws, s, err, ga) ||
+              launch_wd<4, 1, 1, 1, 5, true>(w[0], nullptr, x, y, trows, nb, ws, s, err, ga));
+    case kTypeQ6K:
+      return launch_q6k_matvec_group(ga, trows, cols, x, y, ws, s, err);
+    default:
+      return false;
+  }
 }
 
 bool launch_q5k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,

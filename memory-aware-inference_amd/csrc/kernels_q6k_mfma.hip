@@ -200,13 +200,17 @@ __device__ __forceinline__ float block_exact_lean(const i32x4 (&q)[4], const int
 
 // NTOK activation vectors (batch-major x and y) share each decoded stage:
 // vector t's images sit at img + t img_stride, and a launch with NTOK > 1
-// gives every workgroup whole tiles (no split).
-template <int WAVES, int DEPTH, int NTOK>
+// gives every workgroup whole tiles (no split).  GROUPED: the rows are those
+// of ga.count matrices of one K, one after the other (every matrix but the
+// last a whole number of tiles); tile t reads the matrix whose tiles reach
+// past t.
+template <int WAVES, int DEPTH, int NTOK, bool GROUPED>
 __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
                                                               uint32_t nb, void* __restrict__ wsp,
-                                                              SchedArgs sa, uint32_t prefetch) {
+                                                              SchedArgs sa, uint32_t prefetch,
+                                                              GroupArgs ga) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t slots = sa.packed & 0xffu;
   const Layout L = layout(WAVES, DEPTH, nb, slots, NTOK);
@@ -239,12 +243,29 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t voff_last = n * row_bytes + (grp < 2u ? 16u * (24u + grp) : kLastPiece);
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
+  // the stage bytes of a pair's tile and the tile's row count
+  auto tile_at = [&](const Pair& pr, uint32_t& nrows) -> const uint8_t* {
+    uint32_t row0 = pr.tile * 16u, mrows = rows;
+    const uint8_t* wm = w;
+    if constexpr (GROUPED) {
+      wm = ga.w[0];
+      mrows = ga.rows[0];
+#pragma unroll
+      for (uint32_t k = 1; k < kMaxGroup; ++k)
+        if (k < ga.count && pr.tile >= ga.tile_end[k - 1]) {
+          wm = ga.w[k];
+          mrows = ga.rows[k];
+          row0 = (pr.tile - ga.tile_end[k - 1]) * 16u;
+        }
+    }
+    nrows = min(16u, mrows - row0);
+    return wm + (size_t)row0 * row_bytes + kStageRowBytes * pr.r;
+  };
   auto issue = [&](uint32_t j) {
     const Pair pr = pair_at(sc, wave + j * WAVES, nstages);
     const uint32_t st = pr.r;
-    const uint32_t row0 = pr.tile * 16u;
-    const uint32_t nrows = min(16u, rows - row0);
-    const uint8_t* sb = w + (size_t)row0 * row_bytes + kStageRowBytes * st;
+    uint32_t nrows;
+    const uint8_t* sb = tile_at(pr, nrows);
     // the descriptor ends at the tile's last row: pieces past it read zero
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - kStageRowBytes * st),
@@ -268,9 +289,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   const uint32_t npf = DEPTH == 1 && my_pairs > 1u ? min(min(prefetch, 2u), my_pairs - 1u) : 0u;
   for (uint32_t j = 1; j <= npf; ++j) {
     const Pair pr = pair_at(sc, wave + j * WAVES, nstages);
-    const uint32_t row0 = pr.tile * 16u;
-    const uint32_t nrows = min(16u, rows - row0);
-    const uint8_t* sb = w + (size_t)row0 * row_bytes + kStageRowBytes * pr.r;
+    uint32_t nrows;
+    const uint8_t* sb = tile_at(pr, nrows);
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - kStageRowBytes * pr.r),
         kBufferWord3);
@@ -401,9 +421,10 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   }
 }
 
-template <int W, int D, int NT = 1>
+template <int W, int D, int NT = 1, bool G = false>
 bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
-               const Workspace& ws, hipStream_t s, hipError_t* err) {
+               const Workspace& ws, hipStream_t s, hipError_t* err,
+               const GroupArgs& ga = GroupArgs{}) {
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = (nb + 1u) / 2u;
   // several vectors: whole tiles only
@@ -418,14 +439,14 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
   SchedArgs sa;
   if (lds > kLdsBytes || !make_sched_args(ntiles, nstages, slots, ls, &sa)) return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, NT>),
+      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, NT, G>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, NT>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
-                     nb, ws.ptr, sa, D == 1 ? prefetch : 0u);
+  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, NT, G>), dim3(grid), dim3(W * 64), lds, s, w, x, y,
+                     rows, nb, ws.ptr, sa, D == 1 ? prefetch : 0u, ga);
   *err = hipGetLastError();
   return true;
 }
@@ -490,6 +511,15 @@ bool launch_q6k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t
     b += nt;
   }
   return true;
+}
+
+bool mfma::launch_q6k_matvec_group(const GroupArgs& ga, uint32_t total_rows, uint32_t cols,
+                             const float* x, float* y, const Workspace& ws, hipStream_t s,
+                             hipError_t* err) {
+  const uint32_t nb = cols / kBlockElems;
+  if (!q6_shape_ok(total_rows, nb)) return false;
+  return launch_wd<12, 1, 1, true>(ga.w[0], x, y, total_rows, nb, ws, s, err, ga) ||
+         launch_wd<8, 1, 1, true>(ga.w[0], x, y, total_rows, nb, ws, s, err, ga);
 }
 
 }  // namespace sihip

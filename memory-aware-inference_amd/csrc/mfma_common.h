@@ -733,5 +733,10 @@ inline uint32_t ring_slots(uint32_t waves, uint32_t depth, uint32_t tiles_per_wg
   return slots;
 }
 
+// kernels_q6k_mfma.hip: a group of Q6_K matrices (GroupArgs) in one launch.
+bool launch_q6k_matvec_group(const GroupArgs& ga, uint32_t total_rows, uint32_t cols,
+                             const float* x, float* y, const Workspace& ws, hipStream_t s,
+                             hipError_t* err);
+
 }  // namespace mfma
 }  // namespace sihip

@@ -29,11 +29,12 @@ bool launch_q5k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t
                             uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
                             hipError_t* err);
 constexpr size_t kMaxGroupWeights = 8;  // = kMaxGroup of the kernels
-// Q4_K, one vector, 2..8 matrices of one K (rows of each but the last a
-// multiple of 16) in one launch: y holds their outputs one after the other.
-bool launch_q4k_matvec_group(const uint8_t* const* w, const uint32_t* rows, uint32_t count,
-                             uint32_t cols, const float* x, float* y, const Workspace& ws,
-                             hipStream_t s, hipError_t* err);
+// One vector, 2..8 matrices of one type (Q4_K, Q5_K or Q6_K) and one K (rows
+// of each but the last a multiple of 16) in one launch: y holds their outputs
+// one after the other.
+bool launch_matvec_group(uint32_t type, const uint8_t* const* w, const uint32_t* rows,
+                         uint32_t count, uint32_t cols, const float* x, float* y,
+                         const Workspace& ws, hipStream_t s, hipError_t* err);
 // Q6_K, one vector / batch >= 2 vectors (up to four per pass over the
 // weights), on the matrix cores.
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,

@@ -499,6 +499,10 @@ def test_q6_k_matmul_many_head_shape(hip_ctx):
     ((12,) * 8, (64,) * 7 + (100,), 1024),      # the largest group of one launch
     ((12, 12), (100, 64), 1024),                # first rows not whole tiles: one launch each
     ((12, 14, 13), (64, 32, 48), 2560),         # mixed types: one launch each
+    ((13, 13, 13), (1024, 512, 300), 5120),     # Q5_K, one launch
+    ((14, 14), (1024, 160), 17408),             # Q6_K, one launch (long K: L2 touch)
+    ((14,) * 4, (64, 64, 64, 40), 2560),        # Q6_K, one launch
+    ((14, 14), (48, 40), 2304),                 # Q6_K with an odd block count: one launch each
 ])
 def test_grouped_matvec(hip_ctx, types, rows, cols):
     """Several matvecs over one input (gguf_quant_matvec_many_weights), as one
