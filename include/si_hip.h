@@ -147,6 +147,14 @@ int si_hip_gguf_quant_matvec_many_weights(si_hip_context *ctx,
                                           const size_t *rows, size_t count, size_t columns,
                                           const float *input, size_t input_len,
                                           float *const *outputs);
+/* gguf_quant_matvec_many_bytes (metal.rs:4878-5001): several matvecs over
+ * host bytes (tensor i: types[i], bytes[i] of lens[i], rows[i] x columns[i]),
+ * one input, one submission and one wait. */
+int si_hip_gguf_quant_matvec_many_bytes(si_hip_context *ctx, const uint32_t *types,
+                                        const uint8_t *const *bytes, const size_t *lens,
+                                        const size_t *rows, const size_t *columns, size_t count,
+                                        const float *input, size_t input_len,
+                                        float *const *outputs);
 
 /* ---- fused SwiGLU ------------------------------------------------------ */
 /* q4_k_fused_gate_up (metal.rs:3402-3486): out = silu(gate.x) * (up.x). */

@@ -128,6 +128,12 @@ int si_hip_gguf_f32_matvec_tensor_rows(si_hip_context *ctx, const si_hip_gguf *s
 int si_hip_gguf_f32_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *store,
                                         const uint64_t *indices, size_t count, const float *x,
                                         size_t x_len, float *const *outputs);
+/* gguf_quant_matvec_many_tensors (metal.rs:4532-4646): several Q4_K / Q5_K /
+ * Q6_K tensors of the store (indices) over one input, one submission. */
+int si_hip_gguf_quant_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *store,
+                                          const uint64_t *indices, size_t count,
+                                          const float *input, size_t input_len,
+                                          float *const *outputs);
 
 #ifdef __cplusplus
 }

@@ -245,33 +245,42 @@ int dispatch_matvec(si_hip_context *ctx, uint32_t type, const uint8_t *w, const 
 // sum of the earlier rows): one launch when a matrix-core kernel takes the
 // group (2..8 matrices of one of Q4_K, Q5_K, Q6_K, rows of all but the last a
 // multiple of 16), else one launch per matrix.
-int dispatch_matvec_group(si_hip_context *ctx, const si_hip_quant_weight *const *ws,
+int dispatch_matvec_group(si_hip_context *ctx, const uint32_t *types, const uint8_t *const *w,
                           const size_t *rows, size_t count, const float *x, float *y,
                           uint32_t cols, hipStream_t stream) {
   if (ctx->policy == SI_HIP_KERNEL_AUTO && count >= 2 && count <= sihip::kMaxGroupWeights) {
     bool same = true;
-    const uint8_t *w[sihip::kMaxGroupWeights];
     uint32_t r[sihip::kMaxGroupWeights];
     for (size_t i = 0; i < count; ++i) {
-      same = same && ws[i]->ggml_type == ws[0]->ggml_type;
-      w[i] = ws[i]->data();
+      same = same && types[i] == types[0];
       r[i] = (uint32_t)rows[i];
     }
     hipError_t e = hipErrorInvalidValue;
-    if (same && sihip::launch_matvec_group(ws[0]->ggml_type, w, r, (uint32_t)count, cols, x, y,
-                                           ctx->ws, stream, &e)) {
+    if (same && sihip::launch_matvec_group(types[0], w, r, (uint32_t)count, cols, x, y, ctx->ws,
+                                           stream, &e)) {
       if (e != hipSuccess) return hip_fail(e, "grouped matvec launch");
       return SI_HIP_OK;
     }
   }
   size_t off = 0;
   for (size_t i = 0; i < count; ++i) {
-    int rc = dispatch_matvec(ctx, ws[i]->ggml_type, ws[i]->data(), x, y + off, (uint32_t)rows[i],
-                             cols, 1, stream);
+    int rc = dispatch_matvec(ctx, types[i], w[i], x, y + off, (uint32_t)rows[i], cols, 1, stream);
     if (rc) return rc;
     off += rows[i];
   }
   return SI_HIP_OK;
+}
+
+int dispatch_weight_group(si_hip_context *ctx, const si_hip_quant_weight *const *ws,
+                          const size_t *rows, size_t count, const float *x, float *y,
+                          uint32_t cols, hipStream_t stream) {
+  std::vector<uint32_t> types(count);
+  std::vector<const uint8_t *> w(count);
+  for (size_t i = 0; i < count; ++i) {
+    types[i] = ws[i]->ggml_type;
+    w[i] = ws[i]->data();
+  }
+  return dispatch_matvec_group(ctx, types.data(), w.data(), rows, count, x, y, cols, stream);
 }
 
 int dispatch_gate_up(si_hip_context *ctx, const uint8_t *g, const uint8_t *u, const float *x,
@@ -550,6 +559,79 @@ int si_hip_gguf_quant_matvec_bytes(si_hip_context *ctx, uint32_t type, const uin
   return typed_matvec(ctx, type, wb, wl, rows, cols, in, in_len, out);
 }
 
+int si_hip_gguf_quant_matvec_many_bytes(si_hip_context *ctx, const uint32_t *types,
+                                        const uint8_t *const *bytes, const size_t *lens,
+                                        const size_t *rows, const size_t *columns, size_t count,
+                                        const float *in, size_t in_len, float *const *outputs) {
+  // gguf_quant_matvec_many_bytes (metal.rs:4878-5001): the checks in its order
+  if (count == 0)
+    return fail(SI_HIP_ERR_EMPTY, "staged quantized matvec group requires at least one tensor");
+  if (!types || !bytes || !lens || !rows || !columns || !outputs)
+    return fail(SI_HIP_ERR_NULL, "staged grouped matvec arrays are null");
+  const size_t cols = columns[0];
+  if (cols == 0 || in_len != cols)
+    return fail(SI_HIP_ERR_DIMENSIONS, "staged quantized matvec group input length is invalid");
+  size_t staged = 0;
+  std::vector<size_t> offs(count);
+  for (size_t i = 0; i < count; ++i) {
+    if (rows[i] == 0 || columns[i] != cols || cols % 256 != 0)
+      return fail(SI_HIP_ERR_DIMENSIONS, "staged quantized matvec group shapes differ");
+    const size_t bb = block_bytes_of(types[i]);
+    if (bb == 0) return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported staged quantized tensor type");
+    size_t expected;
+    if (!checked_mul(rows[i], cols / 256, &expected) || !checked_mul(expected, bb, &expected))
+      return fail(SI_HIP_ERR_OVERFLOW, "staged quantized matvec group byte length overflows");
+    if (expected != lens[i])
+      return fail(SI_HIP_ERR_BYTE_LENGTH, "staged quantized matvec tensor byte length is invalid");
+    offs[i] = staged;
+    staged += (lens[i] + 255) & ~(size_t)255;  // each matrix 256-byte aligned in the staging buffer
+  }
+  if (cols > UINT32_MAX)
+    return fail(SI_HIP_ERR_OVERFLOW, "staged grouped quantized columns exceed HIP limits");
+  uint64_t total_rows = 0;
+  for (size_t i = 0; i < count; ++i) {
+    if (rows[i] > UINT32_MAX)
+      return fail(SI_HIP_ERR_OVERFLOW, "staged grouped quantized rows exceed HIP limits");
+    total_rows += rows[i];
+  }
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!in) return fail(SI_HIP_ERR_NULL, "staged grouped matvec input is null");
+  for (size_t i = 0; i < count; ++i)
+    if (!bytes[i] || !outputs[i])
+      return fail(SI_HIP_ERR_NULL, "staged grouped matvec buffer %zu is null", i);
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  int rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, staged);
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, total_rows * sizeof(float));
+  if (rc) return rc;
+  std::vector<const uint8_t *> dev(count);
+  for (size_t i = 0; i < count; ++i) {
+    uint8_t *d = static_cast<uint8_t *>(ctx->stage_weights) + offs[i];
+    SIHIP_CHECK(hipMemcpyAsync(d, bytes[i], lens[i], hipMemcpyHostToDevice, ctx->stream),
+                "weight copy");
+    dev[i] = d;
+  }
+  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+              "input copy");
+  float *dst = static_cast<float *>(ctx->stage_out);
+  rc = dispatch_matvec_group(ctx, types, dev.data(), rows, count,
+                             static_cast<const float *>(ctx->stage_in), dst, (uint32_t)cols,
+                             ctx->stream);
+  if (rc) return rc;
+  size_t off = 0;
+  for (size_t i = 0; i < count; ++i) {
+    SIHIP_CHECK(hipMemcpyAsync(outputs[i], dst + off, rows[i] * sizeof(float), hipMemcpyDeviceToHost,
+                               ctx->stream),
+                "output copy");
+    off += rows[i];
+  }
+  rc = wait_stream(ctx, "staged grouped quantized matvec command");
+  if (rc) return rc;
+  return ok();
+}
+
 int si_hip_gguf_quant_matvec_weight(si_hip_context *ctx, const si_hip_quant_weight *w, size_t rows,
                                     size_t cols, const float *in, size_t in_len, float *out) {
   int rc = check_weight(w, "retained matvec");
@@ -644,7 +726,7 @@ int si_hip_gguf_quant_matvec_many_weights(si_hip_context *ctx,
   SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
               "input copy");
   float *dst = static_cast<float *>(ctx->stage_out);
-  rc = dispatch_matvec_group(ctx, weights, rows, count, static_cast<const float *>(ctx->stage_in),
+  rc = dispatch_weight_group(ctx, weights, rows, count, static_cast<const float *>(ctx->stage_in),
                              dst, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
   size_t off = 0;
@@ -1333,7 +1415,7 @@ int si_hip_quant_matvec_many_device(si_hip_context *ctx, const si_hip_quant_weig
   if (total > 0xffffffffu) return fail(SI_HIP_ERR_DIMENSIONS, "grouped quantized matvec rows overflow");
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matvec argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
-  int rc = dispatch_matvec_group(ctx, ws, rows, count, d_in, d_out, (uint32_t)cols,
+  int rc = dispatch_weight_group(ctx, ws, rows, count, d_in, d_out, (uint32_t)cols,
                                  device_stream(ctx));
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);

@@ -582,4 +582,43 @@ int si_hip_gguf_f32_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *
   return si_hip_f32_matvec_many(ctx, ws.data(), rows.data(), count, (size_t)cols, x, x_len, outputs);
 }
 
+// Several quantized matvecs over one input (gguf_quant_matvec_many_tensors,
+// metal.rs:4532-4646): the reference's checks and messages, then the staged
+// group path with each tensor's first rows x cols / 256 blocks.
+int si_hip_gguf_quant_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *g,
+                                          const uint64_t *indices, size_t count, const float *x,
+                                          size_t x_len, float *const *outputs) {
+  if (!g) return set_error(SI_HIP_ERR_NULL, "GGUF store is null");
+  if (count == 0) return set_error(SI_HIP_ERR_EMPTY, "quantized matvec group requires at least one tensor");
+  if (!indices || !outputs) return set_error(SI_HIP_ERR_NULL, "quantized matvec group argument is null");
+  const Tensor *first = tensor_at(g, indices[0]);
+  if (!first) return SI_HIP_ERR_RANGE;
+  if (first->shape.empty()) return set_error(SI_HIP_ERR_DIMENSIONS, "quantized matvec tensor is not a matrix");
+  const uint64_t cols = first->shape[0];
+  if (x_len != cols) return set_error(SI_HIP_ERR_DIMENSIONS, "quantized matvec group input length is invalid");
+  std::vector<uint32_t> types(count);
+  std::vector<const uint8_t *> bytes(count);
+  std::vector<size_t> lens(count), rows(count), columns(count);
+  for (size_t i = 0; i < count; ++i) {
+    const Tensor *t = tensor_at(g, indices[i]);
+    if (!t) return SI_HIP_ERR_RANGE;
+    const uint32_t ty = t->ggml_type;
+    if (t->shape.size() != 2 || t->shape[0] != cols || (ty != 12 && ty != 13 && ty != 14))
+      return set_error(SI_HIP_ERR_DIMENSIONS, "quantized matvec group tensor shapes or types differ");
+    const uint64_t bb = ty == 12 ? 144u : ty == 13 ? 176u : 210u;
+    uint64_t expected;
+    if (!checked_mul(t->shape[1], cols / 256, &expected) || !checked_mul(expected, bb, &expected))
+      return set_error(SI_HIP_ERR_OVERFLOW, "quantized matvec group byte length overflows");
+    if (t->data_end - t->data_start < expected)
+      return set_error(SI_HIP_ERR_BYTE_LENGTH, "quantized matvec group tensor is truncated");
+    types[i] = ty;
+    bytes[i] = g->bytes + t->data_start;
+    lens[i] = (size_t)expected;
+    rows[i] = (size_t)t->shape[1];
+    columns[i] = (size_t)cols;
+  }
+  return si_hip_gguf_quant_matvec_many_bytes(ctx, types.data(), bytes.data(), lens.data(),
+                                             rows.data(), columns.data(), count, x, x_len, outputs);
+}
+
 }  // extern "C"

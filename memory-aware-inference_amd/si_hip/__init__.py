@@ -149,6 +149,11 @@ _SIGS = {
     "si_hip_gguf_f32_matvec_tensor_rows": (_I, [_P, _P, _U64, _SZ, _SZ, _FP, _SZ, _FP]),
     "si_hip_gguf_f32_matvec_many_tensors": (_I, [_P, _P, C.POINTER(_U64), _SZ, _FP, _SZ,
                                                  C.POINTER(_FP)]),
+    "si_hip_gguf_quant_matvec_many_tensors": (_I, [_P, _P, C.POINTER(_U64), _SZ, _FP, _SZ,
+                                                   C.POINTER(_FP)]),
+    "si_hip_gguf_quant_matvec_many_bytes": (
+        _I, [_P, C.POINTER(C.c_uint32), C.POINTER(_BP), C.POINTER(_SZ), C.POINTER(_SZ),
+             C.POINTER(_SZ), _SZ, _FP, _SZ, C.POINTER(_FP)]),
     # si_hip_gguf.h
     "si_hip_gguf_open": (_I, [C.c_char_p, C.POINTER(_P)]),
     "si_hip_gguf_parse": (_I, [_BP, _SZ, C.POINTER(_P)]),
@@ -424,6 +429,23 @@ class HipContext:
         oarr = (_FP * n)(*[_fp(o) for o in outs])
         _check(lib().si_hip_gguf_quant_matvec_many_weights(self._h, harr, rarr, n, columns,
                                                            _fp(x), x.size, oarr))
+        return outs
+
+    def gguf_quant_matvec_many_bytes(self, tensors: Sequence, input) -> list:
+        """gguf_quant_matvec_many_bytes (src/metal.rs:4878-5001): tensors are
+        (ggml_type, bytes, rows, columns); one result per tensor."""
+        x = _f32(input)
+        n = len(tensors)
+        arrs = [_u8(b) for (_, b, _, _) in tensors]
+        outs = [np.empty(max(int(r), 1), dtype=np.float32) for (_, _, r, _) in tensors]
+        types = (C.c_uint32 * n)(*[int(t) for (t, _, _, _) in tensors])
+        bp = (_BP * n)(*[_bp(a) for a in arrs])
+        lens = (C.c_size_t * n)(*[a.size for a in arrs])
+        rows = (C.c_size_t * n)(*[int(r) for (_, _, r, _) in tensors])
+        cols = (C.c_size_t * n)(*[int(c) for (_, _, _, c) in tensors])
+        oarr = (_FP * n)(*[_fp(o) for o in outs])
+        _check(lib().si_hip_gguf_quant_matvec_many_bytes(self._h, types, bp, lens, rows, cols, n,
+                                                         _fp(x), x.size, oarr))
         return outs
 
     def quant_matvec_many_device(self, weights: Sequence[QuantWeight], rows: Sequence[int],
@@ -862,6 +884,18 @@ class GgufFile:
         ip = (C.c_uint64 * len(idx))(*idx)
         _check(lib().si_hip_gguf_f32_matvec_many_tensors(ctx.handle, self._h, ip, len(idx), _fp(x),
                                                          x.size, yp))
+        return ys
+
+    def quant_matvec_many(self, ctx: "HipContext", names: Sequence[str], input) -> list:
+        """gguf_quant_matvec_many_tensors (src/metal.rs:4532-4646): one result per tensor."""
+        x = _f32(input)
+        idx = [self._index(n) for n in names]
+        ys = [np.empty(max(int(self.tensor_list[i].shape[1]), 1) if len(self.tensor_list[i].shape) == 2
+                       else 1, dtype=np.float32) for i in idx]
+        yp = (_FP * len(ys))(*[_fp(y) for y in ys])
+        ip = (C.c_uint64 * len(idx))(*idx)
+        _check(lib().si_hip_gguf_quant_matvec_many_tensors(ctx.handle, self._h, ip, len(idx),
+                                                           _fp(x), x.size, yp))
         return ys
 
     def inspect(self, model: str | None = None) -> str:

@@ -109,6 +109,38 @@ def test_matmul_many_batch_bounds():
     assert f(NULL, 12, _bp(w), 144, 1, 256, 16, _fp(x), 16 * 256, _fp(y)) == -1
 
 
+_BP = C.POINTER(C.c_uint8)
+_FP = C.POINTER(C.c_float)
+
+
+def test_grouped_bytes_rejections():
+    """gguf_quant_matvec_many_bytes's checks, in its order (metal.rs:4878-4935)."""
+    L = lib()
+    w = np.zeros(2 * 144, np.uint8)
+    x, y = _x(256), _x(4)
+    f = L.si_hip_gguf_quant_matvec_many_bytes
+
+    def call(types, lens, rows, cols, n=None, xl=256):
+        n = len(types) if n is None else n
+        return f(NULL, (C.c_uint32 * max(n, 1))(*types), (_BP * max(n, 1))(*[_bp(w)] * max(n, 1)),
+                 (C.c_size_t * max(n, 1))(*lens), (C.c_size_t * max(n, 1))(*rows),
+                 (C.c_size_t * max(n, 1))(*cols), n, _fp(x), xl,
+                 (_FP * max(n, 1))(*[_fp(y)] * max(n, 1)))
+
+    assert call([12], [144], [1], [256], n=0) == -11
+    assert si_hip.last_error() == "staged quantized matvec group requires at least one tensor"
+    assert call([12], [144], [1], [256], xl=255) == -2
+    assert si_hip.last_error() == "staged quantized matvec group input length is invalid"
+    assert call([12, 12], [144, 144], [1, 1], [256, 512]) == -2
+    assert si_hip.last_error() == "staged quantized matvec group shapes differ"
+    assert call([12, 12], [144, 144], [1, 0], [256, 256]) == -2
+    assert call([12, 9], [144, 144], [1, 1], [256, 256]) == -5
+    assert si_hip.last_error() == "unsupported staged quantized tensor type"
+    assert call([12, 13], [144, 144], [1, 1], [256, 256]) == -3
+    assert si_hip.last_error() == "staged quantized matvec tensor byte length is invalid"
+    assert call([12, 12], [144, 288], [1, 2], [256, 256]) == -1  # valid: the context is null
+
+
 def test_embedding_row_and_dequantize_rejections():
     L = lib()
     w = np.zeros(288, np.uint8)

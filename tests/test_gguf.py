@@ -522,6 +522,51 @@ def test_store_upload_matches_direct_upload(hip_ctx, tmp_path, mapped):
     g.close()
 
 
+def test_store_quant_group_rejections(tmp_path):
+    """gguf_quant_matvec_many_tensors's checks (metal.rs:4537-4576), before any
+    device work (a null context)."""
+    rows, cols, mats, data = _kquant_file()
+    p = tmp_path / "k.gguf"
+    p.write_bytes(data)
+    g = GgufFile(path=p)
+
+    class NoCtx:
+        handle = None
+
+    with pytest.raises(si_hip.HipError) as e:
+        g.quant_matvec_many(NoCtx(), ["q4", "q5"], np.zeros(cols + 1, np.float32))
+    assert e.value.message == "quantized matvec group input length is invalid"
+    with pytest.raises(si_hip.HipError) as e:
+        g.quant_matvec_many(NoCtx(), [], np.zeros(cols, np.float32))
+    assert e.value.message == "quantized matvec group requires at least one tensor"
+    g.close()
+
+
+@pytest.mark.gpu
+def test_store_quant_group_matches_single_calls(hip_ctx, tmp_path):
+    """gguf_quant_matvec_many_tensors over the store's Q4_K, Q5_K and Q6_K
+    tensors, and gguf_quant_matvec_many_bytes over the same bytes (an
+    all-Q4_K group runs as one launch): each output within the oracle's
+    bound, and both entry points bit-identical."""
+    import oracle_lib as O
+    rows, cols, mats, data = _kquant_file()
+    p = tmp_path / "k.gguf"
+    p.write_bytes(data)
+    g = GgufFile(path=p)
+    x = si_hip.synth_normal(9, cols)
+    types = {"q4": Q4K, "q5": Q5K, "q6": Q6K}
+    for names in (["q4", "q5", "q6"], ["q4", "q4", "q4"], ["q6", "q6"]):
+        outs = g.quant_matvec_many(hip_ctx, names, x)
+        again = hip_ctx.gguf_quant_matvec_many_bytes(
+            [(types[n], mats[n], rows, cols) for n in names], x)
+        for n, y, y2 in zip(names, outs, again):
+            _, y64, ab = O.matvec(types[n], mats[n], rows, cols, x)
+            err = np.max(np.abs(y.astype(np.float64) - y64) / (2e-5 * ab + 1e-30))
+            assert err <= 1.0, (names, n, err)
+            assert np.array_equal(y.view(np.uint32), y2.view(np.uint32))
+    g.close()
+
+
 @pytest.mark.gpu
 def test_store_embedding_rows_are_the_packed_rows(hip_ctx):
     import oracle_lib
