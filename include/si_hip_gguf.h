@@ -128,6 +128,13 @@ int si_hip_gguf_f32_matvec_tensor_rows(si_hip_context *ctx, const si_hip_gguf *s
 int si_hip_gguf_f32_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *store,
                                         const uint64_t *indices, size_t count, const float *x,
                                         size_t x_len, float *const *outputs);
+/* gguf_matvec_tensor_rows (metal.rs:5003-5015): rows [row_start, row_start +
+ * row_count) of a rank-2 F32, Q4_K, Q5_K or Q6_K tensor of the store (the
+ * quantized checks of q4_k_matvec_tensor_rows / quant_k_matvec_tensor_rows,
+ * metal.rs:4346-4467). */
+int si_hip_gguf_matvec_tensor_rows(si_hip_context *ctx, const si_hip_gguf *store, uint64_t index,
+                                   size_t row_start, size_t row_count, const float *input,
+                                   size_t input_len, float *output);
 /* gguf_quant_matvec_many_tensors (metal.rs:4532-4646): several Q4_K / Q5_K /
  * Q6_K tensors of the store (indices) over one input, one submission. */
 int si_hip_gguf_quant_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *store,

@@ -582,6 +582,45 @@ int si_hip_gguf_f32_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *
   return si_hip_f32_matvec_many(ctx, ws.data(), rows.data(), count, (size_t)cols, x, x_len, outputs);
 }
 
+// Rows [row_start, row_start + row_count) of a rank-2 tensor of the store:
+// F32 through the F32 matvec, Q4_K / Q5_K / Q6_K through the quantized one
+// over the mapped row bytes (gguf_matvec_tensor_rows, metal.rs:5003-5015, with
+// q4_k_matvec_tensor_rows / quant_k_matvec_tensor_rows, 4346-4467, and
+// gguf_quant_matvec_tensor_rows, 4505-4527: their checks and messages).
+int si_hip_gguf_matvec_tensor_rows(si_hip_context *ctx, const si_hip_gguf *g, uint64_t index,
+                                   size_t row_start, size_t row_count, const float *x,
+                                   size_t x_len, float *y) {
+  const Tensor *t = tensor_at(g, index);
+  if (!t) return g ? SI_HIP_ERR_RANGE : SI_HIP_ERR_NULL;
+  if (t->ggml_type == 0)
+    return si_hip_gguf_f32_matvec_tensor_rows(ctx, g, index, row_start, row_count, x, x_len, y);
+  const uint32_t ty = t->ggml_type;
+  if (ty != 12 && ty != 13 && ty != 14)
+    return set_error(SI_HIP_ERR_UNSUPPORTED_TYPE, "GGUF tensor %s has unsupported quantized type %u",
+                     t->name.c_str(), ty);
+  const char *label = ty == 12 ? "Q4_K" : ty == 13 ? "Q5_K" : "Q6_K";
+  const uint64_t bb = ty == 12 ? 144u : ty == 13 ? 176u : 210u;
+  if (t->shape.size() != 2)
+    return set_error(SI_HIP_ERR_UNSUPPORTED_TYPE, "%s matvec requires a rank-2 %s tensor", label, label);
+  const uint64_t cols = t->shape[0], rows = t->shape[1];
+  if (row_count == 0 || row_start >= rows || row_count > rows - row_start)
+    return set_error(SI_HIP_ERR_RANGE, "%s row range is invalid", label);
+  if (cols % 256 != 0 || x_len != cols)
+    return set_error(SI_HIP_ERR_DIMENSIONS, "%s tensor columns or input length is invalid", label);
+  const uint64_t row_bytes = cols / 256 * bb;
+  uint64_t start, len, end;
+  if (!checked_mul(row_start, row_bytes, &start))
+    return set_error(SI_HIP_ERR_OVERFLOW, "%s row byte range overflows", label);
+  if (!checked_mul(row_count, row_bytes, &len))
+    return set_error(SI_HIP_ERR_OVERFLOW, "%s row byte length overflows", label);
+  end = start + len;
+  if (end < start) return set_error(SI_HIP_ERR_OVERFLOW, "%s row byte range overflows", label);
+  if (end > t->data_end - t->data_start)
+    return set_error(SI_HIP_ERR_BYTE_LENGTH, "%s tensor payload is shorter than its shape", label);
+  return si_hip_gguf_quant_matvec_bytes(ctx, ty, g->bytes + t->data_start + start, (size_t)len,
+                                        row_count, (size_t)cols, x, x_len, y);
+}
+
 // Several quantized matvecs over one input (gguf_quant_matvec_many_tensors,
 // metal.rs:4532-4646): the reference's checks and messages, then the staged
 // group path with each tensor's first rows x cols / 256 blocks.

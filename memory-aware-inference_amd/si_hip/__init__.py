@@ -149,6 +149,7 @@ _SIGS = {
     "si_hip_gguf_f32_matvec_tensor_rows": (_I, [_P, _P, _U64, _SZ, _SZ, _FP, _SZ, _FP]),
     "si_hip_gguf_f32_matvec_many_tensors": (_I, [_P, _P, C.POINTER(_U64), _SZ, _FP, _SZ,
                                                  C.POINTER(_FP)]),
+    "si_hip_gguf_matvec_tensor_rows": (_I, [_P, _P, _U64, _SZ, _SZ, _FP, _SZ, _FP]),
     "si_hip_gguf_quant_matvec_many_tensors": (_I, [_P, _P, C.POINTER(_U64), _SZ, _FP, _SZ,
                                                    C.POINTER(_FP)]),
     "si_hip_gguf_quant_matvec_many_bytes": (
@@ -885,6 +886,16 @@ class GgufFile:
         _check(lib().si_hip_gguf_f32_matvec_many_tensors(ctx.handle, self._h, ip, len(idx), _fp(x),
                                                          x.size, yp))
         return ys
+
+    def matvec_tensor_rows(self, ctx: "HipContext", name: str, row_start: int, row_count: int,
+                           input) -> np.ndarray:
+        """gguf_matvec_tensor_rows (src/metal.rs:5003-5015): F32 or K-quant rows."""
+        x = _f32(input)
+        y = np.empty(max(row_count, 1), dtype=np.float32)
+        _check(lib().si_hip_gguf_matvec_tensor_rows(ctx.handle, self._h, self._index(name),
+                                                    row_start, row_count, _fp(x), x.size,
+                                                    _fp(y)))
+        return y[:row_count]
 
     def quant_matvec_many(self, ctx: "HipContext", names: Sequence[str], input) -> list:
         """gguf_quant_matvec_many_tensors (src/metal.rs:4532-4646): one result per tensor."""

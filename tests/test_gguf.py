@@ -542,6 +542,47 @@ def test_store_quant_group_rejections(tmp_path):
     g.close()
 
 
+def test_store_tensor_rows_rejections():
+    """q4_k_matvec_tensor_rows / quant_k_matvec_tensor_rows checks
+    (metal.rs:4353-4376, 4407-4430), before any device work."""
+    rows, cols, mats, data = _kquant_file()
+    g = GgufFile(data=data)
+
+    class NoCtx:
+        handle = None
+
+    for name, label in (("q4", "Q4_K"), ("q5", "Q5_K"), ("q6", "Q6_K")):
+        for start, count in ((0, 0), (rows, 1), (rows - 1, 2)):
+            with pytest.raises(si_hip.HipError) as e:
+                g.matvec_tensor_rows(NoCtx(), name, start, count, np.zeros(cols, np.float32))
+            assert e.value.message == f"{label} row range is invalid"
+        with pytest.raises(si_hip.HipError) as e:
+            g.matvec_tensor_rows(NoCtx(), name, 0, 1, np.zeros(cols - 1, np.float32))
+        assert e.value.message == f"{label} tensor columns or input length is invalid"
+    g.close()
+
+
+@pytest.mark.gpu
+def test_store_tensor_rows_match_the_oracle(hip_ctx):
+    """gguf_matvec_tensor_rows over row ranges of the store's Q4_K, Q5_K and
+    Q6_K tensors: within the oracle's bound over the same rows."""
+    import oracle_lib as O
+    rows, cols, mats, data = _kquant_file(11)
+    g = GgufFile(data=data)
+    x = si_hip.synth_normal(12, cols)
+    types = {"q4": Q4K, "q5": Q5K, "q6": Q6K}
+    rb = {Q4K: 144, Q5K: 176, Q6K: 210}
+    for name, (start, count) in (("q4", (5, 37)), ("q5", (0, rows)), ("q6", (rows - 3, 3))):
+        t = types[name]
+        y = g.matvec_tensor_rows(hip_ctx, name, start, count, x)
+        b = cols // 256 * rb[t]
+        part = mats[name][start * b:(start + count) * b]
+        _, y64, ab = O.matvec(t, part, count, cols, x)
+        err = np.max(np.abs(y.astype(np.float64) - y64) / (2e-5 * ab + 1e-30))
+        assert err <= 1.0, (name, err)
+    g.close()
+
+
 @pytest.mark.gpu
 def test_store_quant_group_matches_single_calls(hip_ctx, tmp_path):
     """gguf_quant_matvec_many_tensors over the store's Q4_K, Q5_K and Q6_K
