@@ -297,6 +297,8 @@ uint64_t si_hip_current_allocated_bytes(const si_hip_context *ctx);
 uint64_t si_hip_peak_allocated_bytes(const si_hip_context *ctx);
 uint64_t si_hip_peak_active_weight_bytes(const si_hip_context *ctx);
 void si_hip_reset_peaks(si_hip_context *ctx);
+/* sample_allocated (metal.rs:2374-2378): peak = max(peak, current). */
+void si_hip_sample_allocated(si_hip_context *ctx);
 int si_hip_get_command_stats(const si_hip_context *ctx, si_hip_command_stats *out);
 
 #ifdef __cplusplus

@@ -1620,6 +1620,16 @@ void si_hip_reset_peaks(si_hip_context *ctx) {
   ctx->tel->peak_allocated.store(ctx->tel->allocated.load());
   ctx->tel->peak_active_weights.store(ctx->tel->active_weights.load());
 }
+void si_hip_sample_allocated(si_hip_context *ctx) {
+  // sample_allocated (metal.rs:2374-2378): the peak takes the current device
+  // allocation.  Allocations here already raise the peak as they happen, so a
+  // sample only matters after reset_peaks.
+  if (!ctx) return;
+  const uint64_t now = ctx->tel->allocated.load();
+  uint64_t prev = ctx->tel->peak_allocated.load();
+  while (now > prev && !ctx->tel->peak_allocated.compare_exchange_weak(prev, now)) {
+  }
+}
 int si_hip_get_command_stats(const si_hip_context *ctx, si_hip_command_stats *out) {
   if (!ctx || !out) return fail(SI_HIP_ERR_NULL, "command stats argument is null");
   out->submitted = ctx->submitted.load();

@@ -135,6 +135,7 @@ _SIGS = {
     "si_hip_peak_allocated_bytes": (_U64, [_P]),
     "si_hip_peak_active_weight_bytes": (_U64, [_P]),
     "si_hip_reset_peaks": (None, [_P]),
+    "si_hip_sample_allocated": (None, [_P]),
     "si_hip_get_command_stats": (_I, [_P, C.POINTER(CommandStats)]),
     # si_hip_f32.h
     "si_hip_f32_matvec": (_I, [_P, _FP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
@@ -650,6 +651,10 @@ class HipContext:
 
     def reset_peaks(self) -> None:
         lib().si_hip_reset_peaks(self._h)
+
+    def sample_allocated(self) -> None:
+        """sample_allocated (src/metal.rs:2374-2378): peak = max(peak, current)."""
+        lib().si_hip_sample_allocated(self._h)
 
     def command_stats(self) -> dict:
         s = CommandStats()

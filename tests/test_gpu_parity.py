@@ -652,6 +652,10 @@ def test_telemetry_counts_weights(hip_ctx):
     W.free()
     M.free()
     assert hip_ctx.current_allocated_bytes() == base
+    assert hip_ctx.peak_allocated_bytes() >= base + w.size
+    hip_ctx.reset_peaks()
+    hip_ctx.sample_allocated()
+    assert hip_ctx.peak_allocated_bytes() == hip_ctx.current_allocated_bytes() == base
 
 
 def test_retained_errors_with_context(hip_ctx):
