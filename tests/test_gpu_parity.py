@@ -530,6 +530,37 @@ def test_grouped_matvec(hip_ctx, types, rows, cols):
     hip_ctx.device_free(d_y)
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_random_shapes_batches_and_groups(hip_ctx, seed):
+    """Seeded random types, shapes (partial tiles, short and long K, odd block
+    counts), batches 1-16 and groups of 2-9 matrices: every output within the
+    bound of the oracle.  Covers the choice between the one-vector, several-
+    vector, vectors-in-rows, grouped and generic launches together."""
+    rng = np.random.default_rng(9000 + seed)
+    t = int(rng.choice([12, 13, 14]))
+    cols = 256 * int(rng.choice([1, 2, 3, 9, 20, 36, 68]))
+    rows = int(rng.integers(1, 700))
+    batch = int(rng.integers(1, 17))
+    log(f"random seed={seed}: type {t} {rows}x{cols} batch {batch}")
+    w = si_hip.synth_matrix(t, seed=9100 + seed, rows=rows, cols=cols)
+    X = si_hip.synth_normal(9200 + seed, batch * cols).reshape(batch, cols)
+    W = hip_ctx.upload_quant_weight_private(w, t)
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(batch):
+        _, y64, ab = O.matvec(t, w, rows, cols, X[b])
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+    n = int(rng.integers(2, 10))
+    g_rows = [16 * int(rng.integers(1, 40)) for _ in range(n - 1)] + [int(rng.integers(1, 300))]
+    g_types = [t] * n if rng.random() < 0.7 else [int(rng.choice([12, 13, 14])) for _ in range(n)]
+    hosts = [si_hip.synth_matrix(tt, seed=9300 + 10 * seed + i, rows=r, cols=cols)
+             for i, (tt, r) in enumerate(zip(g_types, g_rows))]
+    ws = [hip_ctx.upload_quant_weight_private(hb, tt) for hb, tt in zip(hosts, g_types)]
+    youts = hip_ctx.gguf_quant_matvec_many_weights(ws, g_rows, cols, X[0])
+    for i, (tt, r) in enumerate(zip(g_types, g_rows)):
+        _, y64, ab = O.matvec(tt, hosts[i], r, cols, X[0])
+        assert_dot_close(youts[i], y64, ab, what=f"group matrix {i}")
+
+
 def test_matmul_many_bytes_matches_weight(hip_ctx):
     rows, cols, batch = 96, 1024, 3
     w = si_hip.synth_matrix(13, seed=9, rows=rows, cols=cols)
