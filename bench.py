@@ -448,8 +448,9 @@ def main() -> int:
                          "that scales HBM traffic counters)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
-              "(see DESIGN.md for how the matvec would shard)", file=sys.stderr)
+        print("bench.py measures one GPU: this build has no multi-GPU path (the matvec "
+              "would shard its rows across GPUs, each streaming its share of the weights)",
+              file=sys.stderr)
         return 2
 
     ctx = si_hip.HipContext(0)
