@@ -326,7 +326,11 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
     return true;
   }
   if (type != kTypeQ4K || batch != 1) return false;
-  if (mode == 0 && launch_q4k_matvec_mfma(w, x, y, rows, cols, ws, s, err)) return true;
+  // The VALU kernel below forms sums of x, so a non-finite activation turns
+  // every row into NaN where the reference's per-weight products give +-inf:
+  // it runs only when asked for (SI_HIP_Q4K_MODE=1).  By default a shape the
+  // matrix-core kernel does not take goes to the exact generic kernel.
+  if (mode == 0) return launch_q4k_matvec_mfma(w, x, y, rows, cols, ws, s, err);
   const uint32_t nb = cols / kBlockElems;
   const uint32_t nstages = (nb + 3) / 4;
   // offsets inside one 16-row tile are 32-bit

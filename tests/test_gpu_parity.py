@@ -132,6 +132,22 @@ def _category(v):
     return np.where(np.isnan(v), 3, np.where(np.isposinf(v), 1, np.where(np.isneginf(v), 2, 0)))
 
 
+@pytest.mark.parametrize("cols", [27648, 31744])
+def test_nonfinite_activations_beyond_the_matrix_core_budget(hip_ctx, cols):
+    """Q4_K with K past the matrix-core kernel's LDS budget (31744) and just
+    inside it (27648): an infinite activation gives +-inf rows by weight sign
+    (NaN where a product is 0 * inf), as the reference's per-weight products
+    do."""
+    rows = 16
+    w = si_hip.synth_matrix(12, seed=cols, rows=rows, cols=cols)
+    W = hip_ctx.upload_quant_weight_private(w, 12)
+    x = si_hip.synth_normal(cols + 1, cols).copy()
+    x[300] = np.inf
+    y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+    y32, _, _ = O.matvec(12, w, rows, cols, x)
+    assert np.array_equal(_category(y), _category(y32))
+
+
 @pytest.mark.parametrize("t", [12, 13, 14])
 def test_matvec_nonfinite_and_huge_activations(ctx, t):
     """Blocks whose activations are not finite, or so large that a fixed-point
