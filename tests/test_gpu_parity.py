@@ -132,6 +132,31 @@ def _category(v):
     return np.where(np.isnan(v), 3, np.where(np.isposinf(v), 1, np.where(np.isneginf(v), 2, 0)))
 
 
+@pytest.mark.parametrize("policy", POLICIES)
+def test_fused_gate_up_nonfinite_activations(hip_ctx, policy):
+    """h = silu(gate.x) * (up.x) with an infinite or NaN activation: +-inf /
+    NaN in the same rows as the per-weight f32 products and the reference's
+    g / (1 + exp(-g)) * u (runtime.rs:4296-4298) give."""
+    rows, cols = 48, 2304
+    g = si_hip.synth_matrix(12, seed=31, rows=rows, cols=cols)
+    u = si_hip.synth_matrix(12, seed=32, rows=rows, cols=cols)
+    G = hip_ctx.upload_quant_weight_private(g, 12)
+    U = hip_ctx.upload_quant_weight_private(u, 12)
+    hip_ctx.set_kernel_policy(policy)
+    try:
+        for k, v in ((300, np.inf), (700, -np.inf), (1500, np.nan)):
+            x = si_hip.synth_normal(33, cols).copy()
+            x[k] = v
+            h = hip_ctx.q4_k_fused_gate_up_weights(G, U, rows, cols, x)
+            g32, _, _ = O.matvec(12, g, rows, cols, x)
+            u32, _, _ = O.matvec(12, u, rows, cols, x)
+            with np.errstate(all="ignore"):
+                ref = (g32 / (np.float32(1) + np.exp(-g32)) * u32).astype(np.float32)
+            assert np.array_equal(_category(h), _category(ref)), f"x[{k}] = {v}"
+    finally:
+        hip_ctx.set_kernel_policy(si_hip.KERNEL_AUTO)
+
+
 @pytest.mark.parametrize("cols", [27648, 31744])
 def test_nonfinite_activations_beyond_the_matrix_core_budget(hip_ctx, cols):
     """Q4_K with K past the matrix-core kernel's LDS budget (31744) and just
