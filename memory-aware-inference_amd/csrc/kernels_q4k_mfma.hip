@@ -91,21 +91,24 @@ __device__ __forceinline__ void lds_read_weights(uint32_t hb, uint32_t qb, u32x4
       : "memory");
 }
 
-// Unit sums of the lane's two units in the four blocks (xb + 32 b) and the
-// four block exponents (eb).
-__device__ __forceinline__ void lds_read_sums(uint32_t xb, uint32_t eb, u32x2 (&xs)[4], i32x4& ex) {
+// Unit sums of the lane's two units in the four blocks (xb + 32 b), the
+// four block exponents (eb) and their four side counts (one byte each, at
+// eb + kCountOff).
+__device__ __forceinline__ void lds_read_sums(uint32_t xb, uint32_t eb, u32x2 (&xs)[4], i32x4& ex,
+                                              uint32_t& cnt) {
+  static_assert(kCountOff == 512, "the offset below");
   asm volatile(
-      "ds_read_b64 %0, %5\n"
-      "ds_read_b64 %1, %5 offset:32\n"
-      "ds_read_b64 %2, %5 offset:64\n"
-      "ds_read_b64 %3, %5 offset:96\n"
-      "ds_read_b128 %4, %6\n"
+      "ds_read_b64 %0, %6\n"
+      "ds_read_b64 %1, %6 offset:32\n"
+      "ds_read_b64 %2, %6 offset:64\n"
+      "ds_read_b64 %3, %6 offset:96\n"
+      "ds_read_b128 %4, %7\n"
+      "ds_read_b32 %5, %7 offset:512\n"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(xs[0]), "=&v"(xs[1]), "=&v"(xs[2]), "=&v"(xs[3]), "=&v"(ex)
+      : "=&v"(xs[0]), "=&v"(xs[1]), "=&v"(xs[2]), "=&v"(xs[3]), "=&v"(ex), "=&v"(cnt)
       : "v"(xb), "v"(eb)
       : "memory");
 }
-
 // The 8 A images of two blocks (block b, MFMA t at addr + 1024 b + 256 t),
 // read only by the lanes in `mask`; the other lanes keep their registers.
 __device__ __forceinline__ void lds_read_images8(uint32_t addr, uint64_t mask, i32x4 (&a)[8]) {
@@ -136,6 +139,21 @@ __device__ __forceinline__ i32x4 low_nibbles(const u32x4& q) {
 __device__ __forceinline__ i32x4 high_nibbles(const u32x4& q) {
   return i32x4{(int)((q[0] >> 4) & 0x0f0f0f0fu), (int)((q[1] >> 4) & 0x0f0f0f0fu),
                (int)((q[2] >> 4) & 0x0f0f0f0fu), (int)((q[3] >> 4) & 0x0f0f0f0fu)};
+}
+
+// Exact value of a Q4_K/Q5_K weight with quant q of unit u (uniform) from
+// the block's 16-byte header (d, dmin, the 12 scale bytes; quant.rs:176-185).
+__device__ __forceinline__ float k4_weight(const u32x4& h, uint32_t u, uint32_t q) {
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  const uint32_t sh = 8u * (u & 3u);
+  const uint32_t sc = ((u < 4u ? sc03 : sc47) >> sh) & 0xffu;
+  const uint32_t mn = ((u < 4u ? mn03 : mn47) >> sh) & 0xffu;
+  const float d = half_bits_to_float(h[0] & 0xffffu);
+  const float dmin = half_bits_to_float(h[0] >> 16);
+  return k4_value_exact(__fmul_rn(d, (float)sc), __fmul_rn(dmin, (float)mn), q);
 }
 
 // Exact per-weight f32 dot of 16 nibbles (low or high half of each byte of q)
@@ -311,6 +329,32 @@ __device__ __forceinline__ float block_exact5(const BlockQ4& w, const u32x4& h, 
   return exact_dot16_bytes(w.hb, d1o, m1o, xs + 48, acc);
 }
 
+// Exact per-weight path of one decoded block (the order of block_exact):
+// units 2 grp (la: elements 0..15, lb: 16..31 of the lane's 64) and
+// 2 grp + 1 (ha, hb), quant.rs rounding.
+__device__ __forceinline__ float block_exact_dec(const BlockQ4& w, const float* __restrict__ xs) {
+  const float d1e = __fmul_rn(w.d, (float)w.sce), m1e = __fmul_rn(w.dmin, w.mne);
+  const float d1o = __fmul_rn(w.d, (float)w.sco), m1o = __fmul_rn(w.dmin, w.mno);
+  float acc = exact_dot16_bytes(w.la, d1e, m1e, xs, 0.0f);
+  acc = exact_dot16_bytes(w.lb, d1e, m1e, xs + 16, acc);
+  acc = exact_dot16_bytes(w.ha, d1o, m1o, xs + 32, acc);
+  return exact_dot16_bytes(w.hb, d1o, m1o, xs + 48, acc);
+}
+
+// Exact weight of element i (uniform) of a decoded block for the lane's row;
+// valid in lane group i / 64, which holds units 2 grp and 2 grp + 1.
+__device__ __forceinline__ float side_weight_dec(BlockQ4 w, uint32_t i) {
+  const uint32_t l = i & 31u;
+  const bool odd = (i >> 5) & 1u;
+  const i32x4 lo = l < 16u ? w.la : w.lb, hi = l < 16u ? w.ha : w.hb;
+  const i32x4 qv = odd ? hi : lo;
+  const uint32_t q =
+      byte_of(u32x4{(uint32_t)qv[0], (uint32_t)qv[1], (uint32_t)qv[2], (uint32_t)qv[3]}, l & 15u);
+  const float d1 = __fmul_rn(w.d, (float)(odd ? w.sco : w.sce));
+  const float m1 = __fmul_rn(w.dmin, odd ? w.mno : w.mne);
+  return k4_value_exact(d1, m1, q);
+}
+
 // The weights of a stage in registers, per format: Q4_K keeps (header, qs
 // piece a, qs piece b) per block, Q5_K adds the two qh pieces.
 template <int QB>
@@ -338,7 +382,35 @@ struct StageRegs {
     else
       return block_exact(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh, xs);
   }
+  // Exact weight (quant.rs:36-63, 90-122 rounding) of element i (uniform,
+  // 0..255) of block B in the lane's row.  Only lane group i / 64 holds the
+  // qs bytes of unit i / 32; other lanes return a value that is not used.
+  template <int B>
+  __device__ __forceinline__ float side_weight(uint32_t i) const {
+    const uint32_t u = i >> 5, l = i & 31u;
+    const u32x4 qa = v[kPer * B + kPer - 2], qb = v[kPer * B + kPer - 1];
+    uint32_t q = (byte_of(l < 16u ? qa : qb, l & 15u) >> (4u * (u & 1u))) & 0x0fu;
+    if constexpr (QB == 5) {
+      const u32x4 h0 = v[5 * B + 1], h1 = v[5 * B + 2];
+      q |= ((byte_of(l < 16u ? h0 : h1, l & 15u) >> u) & 1u) << 4;  // quant.rs:99-122
+    }
+    return k4_weight(v[kPer * B], u, q);
+  }
 };
+
+// Side elements of a stage's four blocks: for each entry (element i, x_i) of
+// block b's list (at list + 32 b, kSideMax entries per block), lane group
+// i / 64 adds w_i * x_i of its row to part[b].  `counts` holds the blocks'
+// side counts, one byte each (0 for blocks that take the exact path or lie
+// past the matrix); nearly always 0.
+// Largest |w| of the lane's two units of a decoded Q4_K (QMAX 15) or Q5_K
+// (QMAX 31) block: |d| sc QMAX + |dmin| m, the larger of the two units.
+template <int QMAX>
+__device__ __forceinline__ float k4_bound(const BlockQ4& w) {
+  const float ad = fabsf(w.d), am = fabsf(w.dmin);
+  return fmaxf(fmaf(ad, (float)(w.sce * QMAX), am * w.mne),
+               fmaf(ad, (float)(w.sco * QMAX), am * w.mno));
+}
 
 // GROUPED: the rows are those of ga.count matrices with one K, one after the
 // other (every matrix but the last a whole number of 16-row tiles), and tile
@@ -482,8 +554,9 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       for (int t = 0; t < NTOK; ++t) {
         u32x2 xs[4];
         i32x4 ex;
+        uint32_t cnt;
         lds_read_sums(sbase + L.xsum + t * L.xsum_stride + 128u * s + 8u * grp,
-                      sbase + L.expo + t * L.expo_stride + 16u * s, xs, ex);
+                      sbase + L.expo + t * L.expo_stride + 16u * s, xs, ex, cnt);
         float part[4];
         bool bad_any = false;
 #pragma unroll
@@ -501,12 +574,24 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
             part[b] = (use && eb != kBadBlock) ? c : 0.0f;
           }
         }
-        if (bad_any) {
+        const uint32_t counts = live_counts(__builtin_amdgcn_readfirstlane(cnt), nlive);
+        uint32_t redo = 0u;
+        if (counts != 0u) {
+          const uint32_t list =
+              sbase + L.expo + t * L.expo_stride + L.side_off + 4u * kSideBytes * s;
+          add_listed<4>(list, counts, grp, part, [](uint32_t i) { return i >> 6; },
+                        [&](auto b, uint32_t i) { return side_weight_dec(bw[decltype(b)::value], i); });
+          redo = rounded_redo<4>(list, counts, grp, part, [&](auto b) {
+            return k4_bound<QB == 5 ? 31 : 15>(bw[decltype(b)::value]);
+          });
+        }
+        if (bad_any || redo != 0u) {
 #pragma unroll
           for (int b = 0; b < 4; ++b)
-            if ((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock)
-              part[b] = v.exact(b, hi_units, bsh, rot_lo, rot_hi,
-                                x + (size_t)t * nb * kBlockElems + 256u * (4u * s + b) + 64u * grp);
+            if (((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock) ||
+                ((redo >> b) & 1u))
+              part[b] = block_exact_dec(
+                  bw[b], x + (size_t)t * nb * kBlockElems + 256u * (4u * s + b) + 64u * grp);
         }
         rs[t] = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
       }
@@ -515,7 +600,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     }
     u32x2 xs[4];
     i32x4 ex;
-    lds_read_sums(sbase + L.xsum + 128u * s + 8u * grp, sbase + L.expo + 16u * s, xs, ex);
+    uint32_t cnt;
+    lds_read_sums(sbase + L.xsum + 128u * s + 8u * grp, sbase + L.expo + 16u * s, xs, ex, cnt);
     float part[4];
     bool bad_any = false;
 #pragma unroll
@@ -532,10 +618,25 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
         part[b] = (use && eb != kBadBlock) ? c : 0.0f;
       }
     }
-    if (bad_any) {
+    // side elements (lane group i / 64 holds element i), then the rounded
+    // blocks' check; blocks on the exact path, and rounded blocks of rows that
+    // fail the check, take the per-weight path
+    const uint32_t counts = live_counts(__builtin_amdgcn_readfirstlane(cnt), nlive);
+    uint32_t redo = 0u;
+    if (counts != 0u) {
+      const uint32_t list = sbase + L.expo + L.side_off + 4u * kSideBytes * s;
+      add_listed<4>(list, counts, grp, part, [](uint32_t i) { return i >> 6; },
+                    [&](auto b, uint32_t i) { return v.template side_weight<decltype(b)::value>(i); });
+      redo = rounded_redo<4>(list, counts, grp, part, [&](auto b) {
+        return k4_bound<QB == 5 ? 31 : 15>(
+            v.decode(decltype(b)::value, hi_units, bsh, rot_lo, rot_hi));
+      });
+    }
+    if (bad_any || redo != 0u) {
 #pragma unroll
       for (int b = 0; b < 4; ++b)
-        if ((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock)
+        if (((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock) ||
+            ((redo >> b) & 1u))
           part[b] = v.exact(b, hi_units, bsh, rot_lo, rot_hi, x + 256u * (4u * s + b) + 64u * grp);
     }
     const float rowsum = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
@@ -623,10 +724,11 @@ __device__ __forceinline__ void copy_x_group(uint8_t* smem, uint32_t img, const 
   });
 }
 
-// Group images, exponents and unit sums of the copied blocks, in place: a
-// wave converts exactly the group-blocks it copied; lane (t, c) takes
-// elements 16 c .. 16 c + 15 of vector 4 g + t.  Blocks follow build_images'
-// rules (exponent kBadBlock for blocks that must take the exact path).
+// Group images, exponents, side lists and unit sums of the copied blocks, in
+// place: a wave converts exactly the group-blocks it copied; lane (t, c)
+// takes elements 16 c .. 16 c + 15 of vector 4 g + t.  Blocks follow
+// build_images' rules (side elements, exponent kBadBlock for blocks that
+// must take the exact path).
 template <int WAVES>
 __device__ __forceinline__ void build_group_images(uint32_t sbase, const Layout& L, uint32_t nbl,
                                                    uint32_t ng, uint32_t wave, uint32_t lane) {
@@ -644,27 +746,15 @@ __device__ __forceinline__ void build_group_images(uint32_t sbase, const Layout&
     for (int k = 0; k < 4; ++k)
 #pragma unroll
       for (int i = 0; i < 4; ++i) xv[4 * k + i] = __uint_as_float(xq[k][i]);
-    float amax = 0.0f, xsum = 0.0f;
-    bool bad = false;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float av = fabsf(xv[k]);
-      amax = fmaxf(amax, av);
-      bad |= !(av < 0x1p100f);
-      xsum += xv[k];
-    }
-    const float cmax = amax;
-    amax = fmaxf(amax, dpp<kRowShr1>(amax));
-    amax = fmaxf(amax, dpp<kRowShr2>(amax));
-    amax = fmaxf(amax, dpp<kRowShr4>(amax));
-    amax = fmaxf(amax, dpp<kRowShr8>(amax));
-    amax = dpp<kRowBcast15>(amax);
-    bad |= cmax > 0.0f && cmax < amax * 0x1p-13f;
-    const int e = __builtin_amdgcn_frexp_expf(amax);
+    const ChunkSplit cs = split_chunk(xv);
+    const bool bad_blk = (__builtin_amdgcn_ballot_w64(cs.bad) >> (16u * t)) & 0xffffull;
+    const uint32_t meta = sbase + L.expo + v * L.expo_stride;
+    const uint32_t list = meta + L.side_off + kSideBytes * b;
+    const uint32_t nside =
+        __builtin_amdgcn_ballot_w64(cs.smask != 0u) ? side_list(xv, cs.smask, c, list, !bad_blk) : 0u;
+    const bool rounded = !bad_blk && nside > kSideMax;
     uint32_t uq[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k)
-      uq[k] = (uint32_t)__float2int_rn(__builtin_amdgcn_ldexpf(xv[k], kFixBits - e)) + 0x80808080u;
+    biased_values(cs, !rounded, uq);
     uint32_t dg[4][4];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
@@ -675,13 +765,16 @@ __device__ __forceinline__ void build_group_images(uint32_t sbase, const Layout&
       lds_write_b64(blk + woff + 16u * d, u32x2{dg[0][d], dg[1][d]});
       lds_write_b64(blk + woff + 16u * d + 256u, u32x2{dg[2][d], dg[3][d]});
     }
+    if (rounded)  // chunk c's error sum at position c (read whole by tok_side)
+      lds_write_b32(list + 4u * c, __float_as_uint(cs.err_side));
+    float xsum = rounded ? cs.xsum : cs.xsum - cs.xsum_side;
     xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit c / 2
     if (c & 1u)
       lds_write_b32(sbase + L.xsum + v * L.xsum_stride + 32u * b + 4u * u, __float_as_uint(xsum));
-    const bool bad_blk = (__builtin_amdgcn_ballot_w64(bad) >> (16u * t)) & 0xffffull;
-    if (c == 0u)
-      lds_write_b32(sbase + L.expo + v * L.expo_stride + 4u * b,
-                    (uint32_t)(bad_blk ? kBadBlock : e - kFixBits));
+    if (c == 0u) {
+      lds_write_b32(meta + 4u * b, (uint32_t)(bad_blk ? kBadBlock : cs.e - kFixBits));
+      lds_write_b8(meta + count_pos(L, b), bad_blk ? 0u : rounded ? kSideRounded : nside);
+    }
   });
 }
 
@@ -829,20 +922,123 @@ __host__ __device__ constexpr Layout tok_layout(uint32_t waves, uint32_t nbl, ui
 // vector's unit sums and exponents at the stage's first block.
 __device__ __forceinline__ float tok_group_stage(const u32x4 (&h)[4], const u32x2 (&q)[16],
                                                  uint32_t nlive, uint32_t iabase,
-                                                 uint32_t xabase, uint32_t eabase) {
+                                                 uint32_t xabase, uint32_t eabase,
+                                                 float& abs_part) {
   i32x4 ex;
   asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(ex) : "v"(eabase) : "memory");
   float part = 0.0f;
+  abs_part = 0.0f;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     if ((uint32_t)b < nlive) {
       u32x4 a[4], xs[2];
       lds_read_group_block(iabase + 4096u * b, xabase + 32u * b, a, xs);
       const float v = block_dot_tok(h[b], q, b, a, xs, ex[b]);
-      part += ex[b] == kBadBlock ? 0.0f : v;
+      const float c = ex[b] == kBadBlock ? 0.0f : v;
+      part += c;
+      abs_part += fabsf(c);
     }
   }
   return part;
+}
+
+// Side elements of a stage for the four vectors of one group (lane group r
+// accumulates vector r of the group, row n).  list0 / cnt0: side lists and
+// counts of the group's first vector at the stage's first block; the other
+// vectors follow at side_stride).  For an entry (i, x_i) of
+// vector r's block b, the lanes of group (i & 31) / 8 hold the qs byte of
+// element i for their rows (slice (i / 32) / 2 of the block); lane group r
+// takes w_i from them and adds w_i x_i.
+template <int B>
+__device__ __forceinline__ float tok_side_block(u32x4 h, u32x2 s0, u32x2 s1, u32x2 s2, u32x2 s3,
+                                                uint32_t list,
+                                                uint32_t counts, uint32_t r, uint32_t lane,
+                                                float part) {
+  const uint32_t grp = lane >> 4, n = lane & 15u;
+  uint32_t c = (counts >> (8 * B)) & 0xffu;
+  if (c == kSideRounded) c = 0u;
+  for (uint32_t k = 0; k < c; ++k) {
+    const u32x2 ent = lds_read_b64(list + kSideBytes * B + kSideEntryBytes * k);
+    const uint32_t i = ent[0];  // the same in every lane
+    const float xi = __uint_as_float(ent[1]);
+    const uint32_t u = i >> 5, l = i & 31u, j = u >> 1;
+    const u32x2 sl = j == 0u ? s0 : j == 1u ? s1 : j == 2u ? s2 : s3;
+    const uint32_t byte = (((l & 4u) ? sl[1] : sl[0]) >> (8u * (l & 3u))) & 0xffu;
+    const float wv = k4_weight(h, u, (byte >> (4u * (u & 1u))) & 0x0fu);
+    const float wr = __int_as_float(
+        __builtin_amdgcn_ds_bpermute((int)(4u * (16u * (l >> 3) + n)), __float_as_int(wv)));
+    if (grp == r) part = fmaf(wr, xi, part);
+  }
+  return part;
+}
+// Largest |w| of a Q4_K block (all eight units) from its header.
+__device__ __forceinline__ float k4_block_bound(const u32x4& h) {
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  const float ad = fabsf(half_bits_to_float(h[0] & 0xffffu));
+  const float am = fabsf(half_bits_to_float(h[0] >> 16));
+  float mx = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const uint32_t sc = ((u < 4 ? sc03 : sc47) >> (8 * (u & 3))) & 0xffu;
+    const uint32_t mn = ((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu;
+    mx = fmaxf(mx, fmaf(ad, (float)(15u * sc), am * (float)mn));
+  }
+  return mx;
+}
+
+// Sum of all 16 error sums of a rounded block.
+__device__ __forceinline__ float rounded_err_all(uint32_t list) {
+  return (rounded_err(list, 0u) + rounded_err(list, 1u)) +
+         (rounded_err(list, 2u) + rounded_err(list, 3u));
+}
+
+// Listed side elements of a stage for the four vectors of one group: lane
+// (r, n) gets vector r's sum of w_i x_i over them for row n.  list0 / cnt0:
+// side areas and counts of the group's first vector at the stage's first
+// block (the other vectors at side_stride); `mine`: the lane's
+// vector's counts.
+__device__ __forceinline__ float tok_listed(const u32x4 (&h)[4], const u32x2 (&q)[16],
+                                            uint32_t list0, uint32_t mine, uint32_t side_stride,
+                                            uint32_t lane) {
+  float part = 0.0f;
+  if (__builtin_amdgcn_ballot_w64((mine & ~(rounded_mask(mine) * 0xffu)) != 0u) == 0u)
+    return part;
+#pragma unroll 1
+  for (uint32_t r = 0; r < 4u; ++r) {
+    const uint32_t counts = __builtin_amdgcn_readlane(mine, 16 * r);
+    if (counts == 0u) continue;
+    const uint32_t list = list0 + r * side_stride;
+    part = tok_side_block<0>(h[0], q[0], q[1], q[2], q[3], list, counts, r, lane, part);
+    part = tok_side_block<1>(h[1], q[4], q[5], q[6], q[7], list, counts, r, lane, part);
+    part = tok_side_block<2>(h[2], q[8], q[9], q[10], q[11], list, counts, r, lane, part);
+    part = tok_side_block<3>(h[3], q[12], q[13], q[14], q[15], list, counts, r, lane, part);
+  }
+  return part;
+}
+
+// Whether the lane (vector r of the group, row n) must recompute its stage
+// exactly: its vector has rounded blocks whose error bound (largest |w| of the
+// block x its error sum) exceeds kRoundedTol of abs_part, the sum of the
+// stage's per-block |dot|.  The headers come from the stage buffer (hb: the
+// row's header at the stage's first block), which is still intact whenever a
+// rounded block is present.
+__device__ __forceinline__ bool tok_rounded_redo(uint32_t mine, uint32_t mylist, uint32_t hb,
+                                                 float abs_part) {
+  const uint32_t rmask = rounded_mask(mine);
+  if (__builtin_amdgcn_ballot_w64(rmask != 0u) == 0u) return false;
+  float err = 0.0f;
+#pragma unroll 1
+  for (uint32_t b = 0; b < 4u; ++b) {
+    if ((rmask >> b) & 1u) {
+      u32x4 h;
+      asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(h) : "v"(hb + 2304u * b) : "memory");
+      err = fmaf(k4_block_bound(h), rounded_err_all(mylist + kSideBytes * b), err);
+    }
+  }
+  return !(err * 1.01f <= kRoundedTol * (abs_part - err));
 }
 
 template <int WAVES, int NG>
@@ -935,15 +1131,30 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
     const uint32_t nlive = min(4u, nb - 4u * s);
     // a block that takes the exact path reads the stage buffer afterwards
     bool any_bad = false;
+    // (so does a rounded block, should a row need it exactly); the lane's
+    // vector's side counts of each group are kept for the groups' passes
+    uint32_t counts[NG];
+#pragma unroll
+    for (int g = 0; g < NG; ++g) counts[g] = 0u;
     for (uint32_t g = 0; g < ng; ++g) {
       i32x4 ex;
-      asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)"
-                   : "=&v"(ex)
-                   : "v"(sbase + L.expo + (4u * g + grp) * L.expo_stride + 16u * sl)
-                   : "memory");
+      uint32_t cw;
+      asm volatile(
+          "ds_read_b128 %0, %2\n"
+          "ds_read_b32 %1, %2 offset:512\n"
+          "s_waitcnt lgkmcnt(0)"
+          : "=&v"(ex), "=&v"(cw)
+          : "v"(sbase + L.expo + (4u * g + grp) * L.expo_stride + 16u * sl)
+          : "memory");
+      cw = live_counts(cw, nlive);
+#pragma unroll
+      for (int gg = 0; gg < NG; ++gg)
+        if ((uint32_t)gg == g) counts[gg] = cw;
       bool bad = false;
 #pragma unroll
-      for (int b = 0; b < 4; ++b) bad |= (uint32_t)b < nlive && ex[b] == kBadBlock;
+      for (int b = 0; b < 4; ++b)
+        bad |= (uint32_t)b < nlive &&
+               (ex[b] == kBadBlock || ((cw >> (8 * b)) & 0xffu) == kSideRounded);
       any_bad |= __builtin_amdgcn_ballot_w64(bad) != 0u;
     }
     if (!any_bad && j + 1u < my_pairs) {
@@ -953,14 +1164,26 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
     float part[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) part[g] = 0.0f;
+    uint32_t redo = 0u;  // bit g: the lane recomputes group g's stage exactly
     // (groups one after another: unrolled, their registers would add up)
 #pragma unroll 1
     for (uint32_t g = 0; g < (NG == 1 ? 1u : ng); ++g) {
       const uint32_t v = 4u * g + grp;
-      const float pg = tok_group_stage(h, q, nlive,
-                                       sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane,
-                                       sbase + L.xsum + v * L.xsum_stride + 128u * sl,
-                                       sbase + L.expo + v * L.expo_stride + 16u * sl);
+      uint32_t mine = counts[0];
+#pragma unroll
+      for (int gg = 1; gg < NG; ++gg)
+        if ((uint32_t)gg == g) mine = counts[gg];
+      const bool any = __builtin_amdgcn_ballot_w64(mine != 0u) != 0u;
+      const uint32_t list0 =
+          sbase + L.expo + 4u * g * L.expo_stride + L.side_off + 4u * kSideBytes * sl;
+      const float side = any ? tok_listed(h, q, list0, mine, L.expo_stride, lane) : 0.0f;
+      float abs_pg;
+      const float pg = side + tok_group_stage(h, q, nlive,
+                                              sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane,
+                                              sbase + L.xsum + v * L.xsum_stride + 128u * sl,
+                                              sbase + L.expo + v * L.expo_stride + 16u * sl, abs_pg);
+      if (any && tok_rounded_redo(mine, list0 + grp * L.expo_stride, hb0, abs_pg + fabsf(side)))
+        redo |= 1u << g;
 #pragma unroll
       for (int gg = 0; gg < NG; ++gg)
         if ((uint32_t)gg == g) part[gg] = pg;
@@ -972,16 +1195,17 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       for (uint32_t g = 0; g < ng; ++g) {
         const uint32_t v = 4u * g + grp;
         const float* const xv = x + (size_t)min(v, ntok - 1u) * nb * kBlockElems;
+        const bool whole = (redo >> g) & 1u;
         float e = 0.0f;
 #pragma unroll 1
         for (uint32_t b = 0; b < nlive; ++b) {
           const uint32_t eb = lds_read_b32(sbase + L.expo + v * L.expo_stride + 4u * (4u * sl + b));
-          if ((int)eb == kBadBlock)
+          if ((int)eb == kBadBlock || whole)
             e += block_exact_row(hb0 + 2304u * b, xv + kBlockElems * (4u * s + b));
         }
 #pragma unroll
         for (int gg = 0; gg < NG; ++gg)
-          if ((uint32_t)gg == g) part[gg] += e;
+          if ((uint32_t)gg == g) part[gg] = (whole ? 0.0f : part[gg]) + e;
       }
     }
     if (any_bad && j + 1u < my_pairs) {
@@ -1138,7 +1362,8 @@ bool launch_tokens(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
 bool shape_ok(uint32_t rows, uint32_t cols, uint32_t mats, int qb) {
   const uint32_t nb = cols / kBlockElems;
   const uint64_t pairs = (uint64_t)((rows + 15u) / 16u) * ((nb + 3u) / 4u) * mats;
-  return rows != 0 && nb != 0 && (uint64_t)nb * block_bytes(qb) * 16u <= 0x7fffffffu &&
+  return rows != 0 && nb != 0 && nb <= kMaxMetaBlocks &&
+         (uint64_t)nb * block_bytes(qb) * 16u <= 0x7fffffffu &&
          (uint64_t)nb * 1024u <= 0x7fffffffu && pairs <= 0xffffffffu &&
          quotients_fit((rows + 15u) / 16u, (nb + 3u) / 4u * mats);
 }

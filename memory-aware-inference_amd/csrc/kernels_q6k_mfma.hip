@@ -15,8 +15,10 @@
 //
 // Per block and lane: T_d = sum_t sc_t * C_t[d] in integers, y += d * (sum_d
 // T_d * 256^d) * 2^(e_b - 30) (the digit images of the activations are built
-// as for Q4_K).  Blocks whose activations are not finite or reach 2^100 take
-// an exact per-weight f32 path (w = (d * sc) * (q - 32), quant.rs rounding).
+// as for Q4_K, mfma_common.h), plus w_i x_i for the block's side elements.
+// Blocks whose activations are not finite or reach 2^100, or that have more
+// side elements than the list holds, take an exact per-weight f32 path
+// (w = (d * sc) * (q - 32), quant.rs rounding).
 //
 // Data path.  Blocks are 210 bytes, so they are not 16-byte aligned; with an
 // even block count nb every row and every stage of two blocks (420 bytes)
@@ -106,10 +108,17 @@ __device__ __forceinline__ void lds_read_images(uint32_t addr, uint64_t mask, i3
       : "memory");
 }
 
-__device__ __forceinline__ u32x2 lds_read_b64(uint32_t addr) {
-  u32x2 v;
-  asm volatile("ds_read_b64 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
-  return v;
+// The stage's two block exponents (ea) and their side counts (one byte
+// each, at ea + kCountOff).
+__device__ __forceinline__ void lds_read_expo(uint32_t ea, u32x2& ex, uint32_t& cnt) {
+  static_assert(kCountOff == 512, "the offset below");
+  asm volatile(
+      "ds_read_b64 %0, %2\n"
+      "ds_read_u16 %1, %2 offset:512\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(ex), "=&v"(cnt)
+      : "v"(ea)
+      : "memory");
 }
 
 // Signed byte of w at bit offset `bit` (an int8 scale).
@@ -196,6 +205,26 @@ __device__ __forceinline__ float block_exact_lean(const i32x4 (&q)[4], const int
     }
   }
   return acc;
+}
+
+// Exact weight (quant.rs:145-171 rounding) of element i = 128 h + 32 t + l
+// (uniform) of a block in the lane's row, from the lane's sets q and scales
+// sc; valid in lane group q6_owner(i) = 2 h + l / 16, which holds set t of
+// element i.
+__device__ __forceinline__ uint32_t q6_owner(uint32_t i) { return 2u * (i >> 7) + ((i & 31u) >> 4); }
+__device__ __forceinline__ float q6_side_weight(i32x4 q0, i32x4 q1, i32x4 q2, i32x4 q3, int s0,
+                                                int s1, int s2, int s3, float d, uint32_t i) {
+  const uint32_t t = (i >> 5) & 3u, l = i & 31u;
+  const i32x4 qt = t == 0u ? q0 : t == 1u ? q1 : t == 2u ? q2 : q3;
+  const int st = t == 0u ? s0 : t == 1u ? s1 : t == 2u ? s2 : s3;
+  const uint32_t qv =
+      byte_of(u32x4{(uint32_t)qt[0], (uint32_t)qt[1], (uint32_t)qt[2], (uint32_t)qt[3]}, l & 15u);
+  return k6_value_exact(d, st, (int)qv - 32);
+}
+// Largest |w| of the lane's share of a block: |d| * 32 * max |scale|.
+__device__ __forceinline__ float q6_bound(const int (&sc)[4], float d) {
+  const int m = max(max(abs(sc[0]), abs(sc[1])), max(abs(sc[2]), abs(sc[3])));
+  return fabsf(d) * (float)(32 * m);
 }
 
 // NTOK activation vectors (batch-major x and y) share each decoded stage:
@@ -352,7 +381,9 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     lds_read_stage(qa0 + buf, qh0 + buf, sc0 + buf, v);
     if (j + DEPTH < my_pairs) issue(j + DEPTH);  // the buffer just read is free again
     lds_read_images(sbase + L.img + 2048u * st + 16u * n, kActiveLanes, A);
-    const u32x2 ex = lds_read_b64(sbase + L.expo + 8u * st);
+    u32x2 ex;
+    uint32_t cnt;
+    lds_read_expo(sbase + L.expo + 8u * st, ex, cnt);
     const int e0 = __builtin_amdgcn_readfirstlane(ex[0]);
     const int e1 = __builtin_amdgcn_readfirstlane(ex[1]);
 
@@ -381,24 +412,39 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
 #pragma unroll 1
       for (uint32_t t = 0; t < (uint32_t)NTOK; ++t) {
         int f0 = e0, f1 = e1;
+        uint32_t ct = cnt;
         if (t > 0u) {
           lds_read_images(sbase + L.img + t * L.img_stride + 2048u * st + 16u * n, kActiveLanes,
                           A);
-          const u32x2 et = lds_read_b64(sbase + L.expo + t * L.expo_stride + 8u * st);
+          u32x2 et;
+          lds_read_expo(sbase + L.expo + t * L.expo_stride + 8u * st, et, ct);
           f0 = __builtin_amdgcn_readfirstlane(et[0]);
           f1 = __builtin_amdgcn_readfirstlane(et[1]);
         }
         const float a0 = block_terms(q0, sc_0, d0, A[0], A[1], A[2], A[3], f0);
         const float a1 = block_terms(q1, sc_1, d1, A[4], A[5], A[6], A[7], f1);
-        float p0 = f0 != kBadBlock ? a0 : 0.0f;
-        float p1 = f1 != kBadBlock ? a1 : 0.0f;
-        if (f0 == kBadBlock || f1 == kBadBlock) {
-          const float* xb =
-              x + (size_t)t * nb * kBlockElems + 512u * st + 128u * half + 16u * sub;
-          if (f0 == kBadBlock) p0 = block_exact_lean(q0, sc_0, d0, xb);
-          if (f1 == kBadBlock) p1 = block_exact_lean(q1, sc_1, d1, xb + 256);
+        float pp[2] = {f0 != kBadBlock ? a0 : 0.0f, f1 != kBadBlock ? a1 : 0.0f};
+        const float* const xs =
+            x + (size_t)t * nb * kBlockElems + 512u * st + 128u * half + 16u * sub;
+        const uint32_t counts = __builtin_amdgcn_readfirstlane(ct);
+        uint32_t redo = 0u;
+        if (counts != 0u) {
+          const uint32_t list =
+              sbase + L.expo + t * L.expo_stride + L.side_off + 2u * kSideBytes * st;
+          add_listed<2>(list, counts, grp, pp, q6_owner, [&](auto b, uint32_t i) {
+            return decltype(b)::value == 0
+                       ? q6_side_weight(q0[0], q0[1], q0[2], q0[3], sc_0[0], sc_0[1], sc_0[2],
+                                        sc_0[3], d0, i)
+                       : q6_side_weight(q1[0], q1[1], q1[2], q1[3], sc_1[0], sc_1[1], sc_1[2],
+                                        sc_1[3], d1, i);
+          });
+          redo = rounded_redo<2>(list, counts, grp, pp, [&](auto b) {
+            return decltype(b)::value == 0 ? q6_bound(sc_0, d0) : q6_bound(sc_1, d1);
+          });
         }
-        const float rowsum = sum_lane_groups(p0 + p1);
+        if (f0 == kBadBlock || (redo & 1u)) pp[0] = block_exact_lean(q0, sc_0, d0, xs);
+        if (f1 == kBadBlock || (redo & 2u)) pp[1] = block_exact_lean(q1, sc_1, d1, xs + 256);
+        const float rowsum = sum_lane_groups(pp[0] + pp[1]);
         if (grp == 0u) lds_write_b32(part_at + 64u * t, __float_as_uint(rowsum));
       }
       token_slot_done<NTOK>(sbase, L, sc.by_slots, pr, nstages, lane, rows, y);
@@ -407,14 +453,26 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
 
     const float c0 = block_terms(q0, sc_0, d0, A[0], A[1], A[2], A[3], e0);
     const float c1 = block_terms(q1, sc_1, d1, A[4], A[5], A[6], A[7], e1);
-    float part0 = e0 != kBadBlock ? c0 : 0.0f;
-    float part1 = e1 != kBadBlock ? c1 : 0.0f;
-    if (e0 == kBadBlock || e1 == kBadBlock) {
-      const float* xb = x + 512u * st + 128u * half + 16u * sub;
-      if (e0 == kBadBlock) part0 = block_exact(q0, sc_0, d0, xb);
-      if (e1 == kBadBlock) part1 = block_exact(q1, sc_1, d1, xb + 256);
+    float pp[2] = {e0 != kBadBlock ? c0 : 0.0f, e1 != kBadBlock ? c1 : 0.0f};
+    const float* const xs = x + 512u * st + 128u * half + 16u * sub;
+    const uint32_t counts = __builtin_amdgcn_readfirstlane(cnt);
+    uint32_t redo = 0u;
+    if (counts != 0u) {
+      const uint32_t list = sbase + L.expo + L.side_off + 2u * kSideBytes * st;
+      add_listed<2>(list, counts, grp, pp, q6_owner, [&](auto b, uint32_t i) {
+        return decltype(b)::value == 0
+                   ? q6_side_weight(q0[0], q0[1], q0[2], q0[3], sc_0[0], sc_0[1], sc_0[2], sc_0[3],
+                                    d0, i)
+                   : q6_side_weight(q1[0], q1[1], q1[2], q1[3], sc_1[0], sc_1[1], sc_1[2], sc_1[3],
+                                    d1, i);
+      });
+      redo = rounded_redo<2>(list, counts, grp, pp, [&](auto b) {
+        return decltype(b)::value == 0 ? q6_bound(sc_0, d0) : q6_bound(sc_1, d1);
+      });
     }
-    const float rowsum = sum_lane_groups(part0 + part1);
+    if (e0 == kBadBlock || (redo & 1u)) pp[0] = block_exact(q0, sc_0, d0, xs);
+    if (e1 == kBadBlock || (redo & 2u)) pp[1] = block_exact(q1, sc_1, d1, xs + 256);
+    const float rowsum = sum_lane_groups(pp[0] + pp[1]);
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
     hand_off<1>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws);
@@ -454,7 +512,8 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
 // even nb (4-byte aligned rows and stages); in-tile offsets (16 rows) and the
 // descriptor sizes are 32-bit
 bool q6_shape_ok(uint32_t rows, uint32_t nb) {
-  return nb != 0 && (nb & 1u) == 0 && rows != 0 && (uint64_t)nb * kQ6Bytes * 16u <= 0x7fffffffu &&
+  return nb != 0 && (nb & 1u) == 0 && nb <= kMaxMetaBlocks && rows != 0 &&
+         (uint64_t)nb * kQ6Bytes * 16u <= 0x7fffffffu &&
          (uint64_t)nb * 1024u <= 0x7fffffffu &&
          (uint64_t)((rows + 15u) / 16u) * (nb / 2u) <= 0xffffffffu &&
          quotients_fit((rows + 15u) / 16u, nb / 2u);

@@ -3,7 +3,26 @@
 //
 // Activations.  Each 256-element block b of x is written in fixed point,
 // x_i = X_i * 2^(e_b - 30) with |X_i| <= 2^30 (e_b from the block's largest
-// |x|), and X_i = sum_d D_d * 256^d in four signed byte digits.  For every
+// |x|, which is below 2^e_b), and X_i = sum_d D_d * 256^d in four signed byte
+// digits.  Rounding costs at most 2^(e_b - 31), so an element of at least
+// 2^(e_b - 14) keeps a relative error of at most 2^-17 whatever its weight.
+// Smaller non-zero elements ("side" elements) are handled in one of two ways,
+// so that the dot stays within its bar of 2e-5 * sum|w x| for any weights:
+//
+//  * At most kSideMax of them: they are left out of the fixed point (X_i = 0,
+//    and out of the unit sums) and listed as (index, x) entries; the
+//    consuming kernel adds w_i * x_i for them with the exact per-weight
+//    decode.
+//  * More ("rounded" block, side count kSideRounded): they stay in the fixed
+//    point, rounded like the rest, and the block keeps, per 16-element chunk,
+//    the sum of their rounding errors |x_i - X_i 2^(e_b - 30)|.  The kernel
+//    bounds a row's error from those blocks by (largest |w| the block header
+//    allows) x (that sum), and compares it with the sum of |partial dot| over
+//    the row's stage, which is at most sum|w x| over the stage.  A row whose
+//    bound exceeds kRoundedTol of it recomputes its rounded blocks exactly.
+//
+// A block with an activation that is not finite or reaches 2^100 takes the
+// exact per-weight path whole.  For every
 // 16-element chunk of a block the workgroup keeps an A-operand "image" of
 // v_mfma_i32_16x16x64_i8 in LDS: A rows 4 p + d hold digit d of the chunk
 // that meets lane group p's weights and every other row is zero, so the
@@ -26,6 +45,7 @@
 #include "si_hip_internal.h"
 
 #include <cstdlib>
+#include <type_traits>
 
 namespace sihip {
 namespace mfma {
@@ -39,29 +59,57 @@ constexpr int kBufferWord3 = 0x00020000;  // raw dword access (CDNA buffer descr
 constexpr int kFixBits = 30;
 constexpr uint32_t kLdsBytes = 163840u;
 constexpr int kBadBlock = 0x40000000;  // exponent slot of a block taking the exact path
+// Side elements: non-zero |x| below 2^(e_b - kSideShift).  Each block and
+// activation vector has kSideBytes of LDS: up to kSideMax 8-byte entries
+// (element index, x bits), or, for a rounded block, 16 f32 error sums, the
+// one of chunk c at position 4 p + t for the chunk in MFMA t of lane group p
+// (the four of a lane group side by side).
+constexpr int kSideShift = 14;
+constexpr uint32_t kSideMax = 8;
+constexpr uint32_t kSideEntryBytes = 8;
+constexpr uint32_t kSideBytes = kSideMax * kSideEntryBytes;  // 64
+constexpr uint32_t kSideRounded = 0xffu;  // side count of a rounded block
+// A row's stage passes when (error bound) * 1.01 <= kRoundedTol *
+// (sum |partial| - error bound); 1.01 covers the f32 rounding of both sums.
+constexpr float kRoundedTol = 4e-6f;
 
 constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
 
 // LDS map of one workgroup (byte offsets): per-wave stage buffers; for each
 // of ntok activation vectors the digit images of all its blocks (a further
 // 4 KB after the last one, which dead blocks of a short last stage may
-// read), its unit sums [block][unit] (formats that need them) and its
-// exponents [block]; then a ring of `slots` tile slots: [slot][partial]
-// [token][16 rows] f32 partials, and per slot a completion count and the tile
-// index it currently belongs to.
+// read), its unit sums [block][unit] (formats that need them) and its block
+// metadata; then a ring of `slots` tile slots: [slot][partial][token][16 rows]
+// f32 partials, and per slot a completion count and the tile index it
+// currently belongs to.
+//
+// Block metadata of a vector (at expo + t expo_stride): the exponents
+// [block] (4 bytes each, at most kMaxMetaBlocks blocks), at +kCountOff the
+// side counts, one byte per block, and at +side_off the side areas
+// [block][kSideBytes].  The counts of the bps blocks of a stage sit at
+// kCountOff + 4 bps s, exactly kCountOff past the stage's exponents, so a
+// kernel reads both from one address register (bytes of blocks past the
+// matrix are not written; readers mask them).
+constexpr uint32_t kCountOff = 512;
+constexpr uint32_t kMaxMetaBlocks = kCountOff / 4u;
 struct Layout {
   uint32_t img, xsum, expo, part, cnt, owner, total;
-  uint32_t img_stride, xsum_stride, expo_stride;  // per activation vector
+  // per activation vector
+  uint32_t img_stride, xsum_stride, expo_stride;
+  uint32_t side_off, bps;  // side areas in the metadata; blocks per stage
 };
 __host__ __device__ constexpr Layout make_layout(uint32_t stage_bytes, uint32_t stage_blocks,
                                                  uint32_t xsum_per_block, uint32_t waves,
                                                  uint32_t depth, uint32_t nb, uint32_t slots,
                                                  uint32_t mats, uint32_t ntok = 1u) {
   Layout l{};
-  const uint32_t partials = (nb + stage_blocks - 1u) / stage_blocks * mats;  // per tile
+  const uint32_t nstages = (nb + stage_blocks - 1u) / stage_blocks;
+  const uint32_t partials = nstages * mats;  // per tile
+  l.bps = stage_blocks;
   l.img_stride = nb * 1024u;
   l.xsum_stride = nb * xsum_per_block;
-  l.expo_stride = (nb * 4u + 15u) & ~15u;
+  l.side_off = kCountOff + ((4u * stage_blocks * nstages + 15u) & ~15u);
+  l.expo_stride = l.side_off + nb * kSideBytes;
   l.img = waves * depth * stage_bytes;
   l.xsum = l.img + ntok * l.img_stride + 4096u;
   l.expo = l.xsum + (xsum_per_block ? ntok * l.xsum_stride + 128u : 0u);
@@ -70,6 +118,10 @@ __host__ __device__ constexpr Layout make_layout(uint32_t stage_bytes, uint32_t 
   l.owner = l.cnt + slots * 4u;
   l.total = l.owner + slots * 4u;
   return l;
+}
+// Offset of block b's side count in its vector's metadata.
+__host__ __device__ constexpr uint32_t count_pos(const Layout& L, uint32_t b) {
+  return kCountOff + 4u * L.bps * (b / L.bps) + b % L.bps;
 }
 
 // Lanes whose A rows carry digits: lane 16 g + n with n / 4 == g.
@@ -81,8 +133,27 @@ template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
 }
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, true);
+}
 constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
 constexpr int kRowBcast15 = 0x15f;
+
+// Word k (uniform, 0..3) of a 16-byte piece.
+__device__ __forceinline__ uint32_t word_of(const u32x4& p, uint32_t k) {
+  return k == 0u ? p[0] : k == 1u ? p[1] : k == 2u ? p[2] : p[3];
+}
+// Byte k (uniform, 0..15) of a 16-byte piece.
+__device__ __forceinline__ uint32_t byte_of(const u32x4& p, uint32_t k) {
+  return (word_of(p, k >> 2) >> (8u * (k & 3u))) & 0xffu;
+}
+
+// The stage's side counts, one byte per block, with the bytes of blocks at
+// or past `nlive` cleared.
+__device__ __forceinline__ uint32_t live_counts(uint32_t word, uint32_t nlive) {
+  return nlive >= 4u ? word : word & ((1u << (8u * nlive)) - 1u);
+}
 
 __device__ __forceinline__ void lds_wait() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
 
@@ -95,6 +166,9 @@ __device__ __forceinline__ void lds_write_b64(uint32_t addr, u32x2 v) {
 __device__ __forceinline__ void lds_write_b32(uint32_t addr, uint32_t v) {
   asm volatile("ds_write_b32 %0, %1" : : "v"(addr), "v"(v) : "memory");
 }
+__device__ __forceinline__ void lds_write_b8(uint32_t addr, uint32_t v) {
+  asm volatile("ds_write_b8 %0, %1" : : "v"(addr), "v"(v) : "memory");
+}
 // LDS atomic add; returns the previous value.
 __device__ __forceinline__ uint32_t lds_add_rtn(uint32_t addr, uint32_t v) {
   uint32_t old;
@@ -104,6 +178,16 @@ __device__ __forceinline__ uint32_t lds_add_rtn(uint32_t addr, uint32_t v) {
 __device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
   uint32_t v;
   asm volatile("ds_read_b32 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ uint32_t lds_read_u16(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_u16 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
+  return v;
+}
+__device__ __forceinline__ u32x2 lds_read_b64(uint32_t addr) {
+  u32x2 v;
+  asm volatile("ds_read_b64 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
   return v;
 }
 
@@ -165,14 +249,116 @@ __device__ __forceinline__ void copy_x(uint8_t* smem, uint32_t img, const float*
   }
 }
 
+// The fixed-point split of one lane's 16 activations (a 16-element chunk of a
+// block whose 16 lanes form one DPP row): the row's exponent e (largest |x|
+// below 2^e), the fixed-point values X (two's complement), the mask of side
+// elements, the f32 sum of all 16 and that of the side elements, the sum of
+// the side elements' rounding errors, and whether the chunk alone forces the
+// exact path.
+struct ChunkSplit {
+  int e;
+  uint32_t fx[16];
+  uint32_t smask;
+  float xsum, xsum_side, err_side;
+  bool bad;
+};
+__device__ __forceinline__ ChunkSplit split_chunk(const float (&xv)[16]) {
+  ChunkSplit r;
+  float amax = 0.0f, amin = __builtin_huge_valf();
+  r.xsum = 0.0f;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    amax = fmaxf(amax, fabsf(xv[k]));
+    amin = fminf(amin, fabsf(xv[k]));
+    r.xsum += xv[k];
+  }
+  // not finite or huge: a NaN shows in the sum (which cannot overflow below
+  // 2^100), an infinity in the maximum
+  r.bad = !(amax < 0x1p100f) || r.xsum != r.xsum;
+  amax = fmaxf(amax, dpp<kRowShr1>(amax));
+  amax = fmaxf(amax, dpp<kRowShr2>(amax));
+  amax = fmaxf(amax, dpp<kRowShr4>(amax));
+  amax = fmaxf(amax, dpp<kRowShr8>(amax));
+  amax = dpp<kRowBcast15>(amax);
+  r.e = __builtin_amdgcn_frexp_expf(amax);  // amax < 2^e; 0 for amax == 0
+  const float thr = __builtin_amdgcn_ldexpf(1.0f, r.e - kSideShift);
+#pragma unroll
+  for (int k = 0; k < 16; ++k)
+    r.fx[k] = (uint32_t)__float2int_rn(__builtin_amdgcn_ldexpf(xv[k], kFixBits - r.e));
+  r.smask = 0u;
+  r.xsum_side = r.err_side = 0.0f;
+  // (rare for dense activations: some |x| below the threshold, or a zero).
+  // The empty asm keeps the compiler from hoisting this work above the
+  // branch, into every block's build.
+  if (__builtin_amdgcn_ballot_w64(amin < thr) != 0u) {
+    float xs[16];
+    uint32_t fs[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      xs[k] = xv[k];
+      fs[k] = r.fx[k];
+      asm volatile("" : "+v"(xs[k]), "+v"(fs[k]));
+    }
+    // side: 0 < |x| < thr, as integers: bits(|x|) - 1 below bits(thr) - 1
+    const uint32_t tb = __float_as_uint(thr) - 1u;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      const bool side = ((__float_as_uint(xs[k]) & 0x7fffffffu) - 1u) < tb;
+      r.smask |= (uint32_t)side << k;
+      r.xsum_side += side ? xs[k] : 0.0f;
+      // |X| < 2^16 for a side element, so (float)X and the difference are exact
+      const float err =
+          fabsf(xs[k] - __builtin_amdgcn_ldexpf((float)(int)fs[k], r.e - kFixBits));
+      r.err_side += side ? err : 0.0f;
+    }
+  }
+  return r;
+}
+
+// Side list of one block from its 16 lanes (one DPP row, lane n holding
+// elements 16 n .. 16 n + 15 in `xv`): returns the block's side count (the
+// same in every lane of the row); when it is at most kSideMax and `write`,
+// the lanes store their entries (element index, x bits) in element order at
+// `list` (8 bytes each).
+__device__ __forceinline__ uint32_t side_list(const float (&xv)[16], uint32_t smask, uint32_t n,
+                                              uint32_t list, bool write) {
+  const uint32_t own = __builtin_popcount(smask);
+  uint32_t incl = own;  // inclusive prefix count over the row
+  incl += dpp_u<kRowShr1>(incl);
+  incl += dpp_u<kRowShr2>(incl);
+  incl += dpp_u<kRowShr4>(incl);
+  incl += dpp_u<kRowShr8>(incl);
+  const uint32_t total = dpp_u<kRowBcast15>(incl);
+  if (write && smask != 0u && total <= kSideMax) {
+    uint32_t pos = incl - own;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) {
+      if ((smask >> k) & 1u) {
+        lds_write_b64(list + kSideEntryBytes * pos, u32x2{16u * n + (uint32_t)k,
+                                                           __float_as_uint(xv[k])});
+        ++pos;
+      }
+    }
+  }
+  return total;
+}
+
+// The biased digit words of a chunk: X + 0x80808080, with X = 0 for side
+// elements that go to the block's side list (`listed`).
+__device__ __forceinline__ void biased_values(const ChunkSplit& cs, bool listed, uint32_t (&u)[16]) {
+#pragma unroll
+  for (int k = 0; k < 16; ++k)
+    u[k] = ((listed && ((cs.smask >> k) & 1u)) ? 0u : cs.fx[k]) + 0x80808080u;
+}
+
 // Turns the copied blocks of activation vector `tok` into digit images in
-// place, plus exponents and, when the layout keeps them, the f32 sums of each
-// 32-element unit.  The caller has
-// waited for the copies.  CHUNK_SLOT(c) gives the byte offset, inside the
-// block's 1 KB, of the A row 4 p (digit 0) of MFMA t that holds chunk c
-// (elements 16 c .. 16 c + 15): 256 t + 64 p.  A block whose activations are
-// not all finite and below 2^100, or that has a non-zero 16-element chunk more
-// than 2^13 below its largest activation, gets exponent kBadBlock.
+// place, plus exponents, side lists or error sums, side counts and, when the
+// layout keeps them, the f32 sums of each 32-element unit (listed side
+// elements left out).  The caller has waited for the copies.  CHUNK_SLOT(c)
+// gives the byte offset, inside the block's 1 KB, of the A row 4 p (digit 0)
+// of MFMA t that holds chunk c (elements 16 c .. 16 c + 15): 256 t + 64 p.  A
+// block with an activation that is not finite or reaches 2^100 gets exponent
+// kBadBlock and side count 0.
 template <int WAVES, typename ChunkSlot>
 __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, uint32_t nb,
                                              uint32_t wave, uint32_t grp, uint32_t n,
@@ -182,6 +368,7 @@ __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, ui
   const uint32_t img = L.img + tok * L.img_stride;
   const uint32_t xsb = L.xsum + tok * L.xsum_stride;
   const uint32_t exb = L.expo + tok * L.expo_stride;
+  const uint32_t sdb = exb + L.side_off;
   for (uint32_t j = 0; j < npass; ++j) {
     if (4u * (wave + WAVES * j) >= nb) break;
     // lane (grp, n): elements 16n..16n+15 of block pb
@@ -194,51 +381,120 @@ __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, ui
     for (int k = 0; k < 4; ++k)
 #pragma unroll
       for (int c = 0; c < 4; ++c) xv[4 * k + c] = __uint_as_float(xq[k][c]);
-    float amax = 0.0f, xsum = 0.0f;
-    bool bad = false;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) {
-      const float av = fabsf(xv[k]);
-      amax = fmaxf(amax, av);
-      bad |= !(av < 0x1p100f);
-      xsum += xv[k];
-    }
-    const float cmax = amax;  // this lane's 16-element chunk
-    amax = fmaxf(amax, dpp<kRowShr1>(amax));
-    amax = fmaxf(amax, dpp<kRowShr2>(amax));
-    amax = fmaxf(amax, dpp<kRowShr4>(amax));
-    amax = fmaxf(amax, dpp<kRowShr8>(amax));
-    amax = dpp<kRowBcast15>(amax);
-    // A chunk far below the block's largest activation would keep too few
-    // significant bits in the block's fixed point; such blocks (outliers
-    // next to small activations) take the exact path too.
-    bad |= cmax > 0.0f && cmax < amax * 0x1p-13f;
-    const int e = __builtin_amdgcn_frexp_expf(amax);  // amax < 2^e; 0 for amax == 0
+    const ChunkSplit cs = split_chunk(xv);
+    const bool store = pb < nb;
+    const bool bad_blk = (__builtin_amdgcn_ballot_w64(cs.bad) >> (16u * grp)) & 0xffffull;
+    const uint32_t list = sbase + sdb + kSideBytes * pb;
+    const uint32_t nside = __builtin_amdgcn_ballot_w64(cs.smask != 0u)
+                               ? side_list(xv, cs.smask, n, list, store && !bad_blk)
+                               : 0u;
+    const bool rounded = !bad_blk && nside > kSideMax;
     uint32_t u[16];
-#pragma unroll
-    for (int k = 0; k < 16; ++k)
-      u[k] = (uint32_t)__float2int_rn(__builtin_amdgcn_ldexpf(xv[k], kFixBits - e)) + 0x80808080u;
+    biased_values(cs, !rounded, u);
     uint32_t dg[4][4];  // [element quad][digit]
 #pragma unroll
-    for (int k = 0; k < 4; ++k)
-      transpose_digits(u[4 * k], u[4 * k + 1], u[4 * k + 2], u[4 * k + 3], dg[k]);
+    for (int k = 0; k < 4; ++k) transpose_digits(u[4 * k], u[4 * k + 1], u[4 * k + 2], u[4 * k + 3], dg[k]);
     // all lanes of the group have read the block before any lane writes it
-    const uint32_t ib = sbase + img + 1024u * pbc + chunk_slot(n);
-    const bool store = pb < nb;
+    const uint32_t slot = chunk_slot(n);
+    const uint32_t ib = sbase + img + 1024u * pbc + slot;
     if (store) {
 #pragma unroll
       for (int d = 0; d < 4; ++d)
         lds_write_b128(ib + 16u * d, u32x4{dg[0][d], dg[1][d], dg[2][d], dg[3][d]});
+      if (rounded)  // position 4 p + t
+        lds_write_b32(list + 4u * (4u * ((slot >> 6) & 3u) + (slot >> 8)),
+                      __float_as_uint(cs.err_side));
     }
     if (want_sums) {
+      float xsum = rounded ? cs.xsum : cs.xsum - cs.xsum_side;
       xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit n / 2
       if (store && (n & 1u))
         lds_write_b32(sbase + xsb + 32u * pb + 4u * (n >> 1), __float_as_uint(xsum));
     }
-    const bool bad_blk = (__builtin_amdgcn_ballot_w64(bad) >> (16u * grp)) & 0xffffull;
-    if (store && n == 0u)
-      lds_write_b32(sbase + exb + 4u * pb, (uint32_t)(bad_blk ? kBadBlock : e - kFixBits));
+    if (store && n == 0u) {
+      lds_write_b32(sbase + exb + 4u * pb, (uint32_t)(bad_blk ? kBadBlock : cs.e - kFixBits));
+      lds_write_b8(sbase + exb + count_pos(L, pb), bad_blk ? 0u : rounded ? kSideRounded : nside);
+    }
   }
+}
+
+// Whether the row of this lane passes the rounded-block check of a stage:
+// `err` the lane's error bound from its rounded blocks, `abs_part` its sum of
+// |partial dot| over all blocks of the stage (both summed over the four lane
+// groups of the row here).  sum |partial| - err is at most the row's
+// sum |w x| over the stage.
+__device__ __forceinline__ bool rounded_ok(float err, float abs_part) {
+  const float e = sum_lane_groups(err), a = sum_lane_groups(abs_part);
+  return e * 1.01f <= kRoundedTol * (a - e);
+}
+// Sum of a rounded block's error sums over the four chunks of lane group p.
+__device__ __forceinline__ float rounded_err(uint32_t list, uint32_t p) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(list + 16u * p) : "memory");
+  return (__uint_as_float(v[0]) + __uint_as_float(v[1])) +
+         (__uint_as_float(v[2]) + __uint_as_float(v[3]));
+}
+
+// f(integral_constant<int, I>) for I = 0 .. N-1, so that register arrays are
+// indexed with constants.
+template <int N, int I = 0, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for<N, I + 1>(f);
+  }
+}
+
+// Side elements and rounded blocks of a stage of NB blocks for one activation
+// vector, in a kernel whose lane group `grp` holds a 64-element share of
+// every block (part[b]: the lane's partial dot of block b).  `list`: the side
+// area of the stage's first block; `counts`: the blocks' side counts, one byte
+// each (0 for blocks on the exact path or past the matrix).
+//
+// add_listed adds w_i x_i for the listed side elements; functors (called with
+// integral_constant<int, b>): owner(i), the lane group that holds the weights
+// of element i; side_w(b, i), the exact weight of element i of block b in the
+// lane's row (valid in lane group owner(i)).
+template <int NB, typename Owner, typename SideW>
+__device__ __forceinline__ void add_listed(uint32_t list, uint32_t counts, uint32_t grp,
+                                           float (&part)[NB], Owner owner, SideW side_w) {
+  static_for<NB>([&](auto bc) {
+    constexpr int b = decltype(bc)::value;
+    uint32_t c = (counts >> (8 * b)) & 0xffu;
+    if (c == kSideRounded) c = 0u;
+    for (uint32_t k = 0; k < c; ++k) {
+      // (the entry stays in vector registers: the same in every lane, and
+      // scalar registers are scarce in the kernels that call this)
+      const u32x2 ent = lds_read_b64(list + kSideBytes * b + kSideEntryBytes * k);
+      const uint32_t i = ent[0];
+      const float wv = side_w(bc, i);
+      if (grp == owner(i)) part[b] = fmaf(wv, __uint_as_float(ent[1]), part[b]);
+    }
+  });
+}
+
+// Bit b of the result: byte b of the counts marks a rounded block.
+__device__ __forceinline__ uint32_t rounded_mask(uint32_t counts) {
+  const uint32_t r = counts & (counts >> 1) & (counts >> 2) & (counts >> 3) & (counts >> 4) &
+                     (counts >> 5) & (counts >> 6) & (counts >> 7) & 0x01010101u;
+  return (r & 1u) | ((r >> 7) & 2u) | ((r >> 14) & 4u) | ((r >> 21) & 8u);
+}
+
+// The rounded blocks this lane must recompute exactly: all of the stage's
+// rounded blocks when its row fails the check (rounded_ok), else none.
+// bound(b): the largest |w| the lane's share of block b can hold.
+template <int NB, typename Bound>
+__device__ __forceinline__ uint32_t rounded_redo(uint32_t list, uint32_t counts, uint32_t grp,
+                                                 const float (&part)[NB], Bound bound) {
+  const uint32_t rmask = rounded_mask(counts);
+  if (rmask == 0u) return 0u;
+  float err = 0.0f, a = 0.0f;
+  static_for<NB>([&](auto bc) {
+    constexpr int b = decltype(bc)::value;
+    if ((rmask >> b) & 1u) err = fmaf(bound(bc), rounded_err(list + kSideBytes * b, grp), err);
+    a += fabsf(part[b]);
+  });
+  return rounded_ok(err, a) ? 0u : rmask;
 }
 
 // Slot ring set-up: every slot empty and owned by local tile == its index.
