@@ -269,6 +269,25 @@ int si_hip_quant_matvec_device_repeat(si_hip_context *ctx,
                                       size_t n_weights, size_t rows, size_t columns,
                                       const float *d_input, float *d_output, size_t iterations);
 
+/* ---- matvec that allocates nothing -------------------------------------
+ * No counterpart in the reference.  For callers that cannot allocate device
+ * memory: code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc.  y = W x for one Q4_K / Q5_K / Q6_K matrix of `rows` x
+ * `columns` whose packed GGUF bytes (`weight_bytes`, exactly rows * columns /
+ * 256 blocks) are at device address `weights`; d_input / d_output are device
+ * buffers of `columns` / `rows` floats; `stream` is a hipStream_t (NULL: the
+ * null stream), and the call only enqueues on it.  No context is needed.
+ * The kernels' cross-workgroup workspace is a file-scope device array of
+ * SI_HIP_NOALLOC_WORKSPACE_BYTES per GPU (held until the process ends), set
+ * up on the first call on each device and left in its rest state by every
+ * call; calls that overlap on one GPU race on it.  rows above
+ * SI_HIP_NOALLOC_MAX_ROWS (the tiles whose counters it holds) are rejected. */
+#define SI_HIP_NOALLOC_WORKSPACE_BYTES (2u << 20)
+#define SI_HIP_NOALLOC_MAX_ROWS 4194048u
+int si_hip_quant_matvec_noalloc(uint32_t ggml_type, const void *weights, size_t weight_bytes,
+                                size_t rows, size_t columns, const float *d_input,
+                                float *d_output, void *stream);
+
 /* ---- captured submission (HIP graphs) ------------------------------------
  * No counterpart in the reference: every Metal call there commits its command
  * buffer and waits (metal.rs:2320-2337).  For callers that repeat the same

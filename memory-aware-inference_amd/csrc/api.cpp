@@ -467,6 +467,11 @@ int si_hip_context_new(int device_ordinal, si_hip_context **out) {
                 "workspace clear");
     SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "workspace clear");
   }
+  // the device's workspace of si_hip_quant_matvec_noalloc (no allocation;
+  // done here so that callers of that entry point under graph capture find
+  // it ready)
+  int rc = sihip::noalloc_setup(ctx->stream);
+  if (rc) return rc;
   *out = ctx.release();
   return ok();
 }

@@ -63,6 +63,10 @@ __host__ __device__ __forceinline__ uint32_t argmax_candidate_index(uint64_t c, 
   return rule == kArgmaxFirstGreater ? 0xffffffffu - lo : lo;
 }
 
+// noalloc.hip: sets up the current device's workspace of
+// si_hip_quant_matvec_noalloc (once per device; `stream` not under capture).
+int noalloc_setup(hipStream_t stream);
+
 // kernels_generic.hip
 hipError_t launch_matvec_generic(uint32_t type, const uint8_t* w, const float* x, float* y,
                                  uint32_t rows, uint32_t cols, uint32_t batch, hipStream_t s);
