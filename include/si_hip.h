@@ -253,6 +253,11 @@ int si_hip_matvec_argmax_device(si_hip_context *ctx, const si_hip_quant_weight *
                                 size_t rows, size_t columns, const float *d_input,
                                 uint32_t rule, float *d_logits, uint64_t *d_result);
 uint32_t si_hip_argmax_result_index(uint64_t packed, uint32_t rule);
+/* q4_k_embedding_tensor (metal.rs:3785-3810) for n_tokens device-resident
+ * ids.  The table checks run here; the ids are checked by the kernel: an id
+ * beyond the rows the table holds yields a row of NaNs, and the next
+ * synchronisation (si_hip_synchronize or any synchronous call) returns
+ * SI_HIP_ERR_DEVICE. */
 int si_hip_embedding_device(si_hip_context *ctx, const si_hip_quant_weight *table,
                             size_t shape_columns, size_t shape_rows, const uint32_t *d_ids,
                             size_t n_tokens, float *d_output);
@@ -309,6 +314,20 @@ void si_hip_graph_free(si_hip_graph *graph);
 /* ---- kernel selection (the reference picks variants via SI_QK_* env) --- */
 #define SI_HIP_KERNEL_AUTO 0u     /* tuned gfx950 kernels where they apply */
 #define SI_HIP_KERNEL_GENERIC 1u  /* one wavefront per row, exact per-weight decode */
+/* Failure reporting.  Kernels that cannot finish their work correctly -- a
+ * bounded cross-wave or cross-workgroup wait that gave up, a device-side
+ * token id beyond the table -- still end normally, and report the failure
+ * through a host-visible word of the context; the next synchronisation
+ * returns SI_HIP_ERR_DEVICE (all device work since the previous one is then
+ * invalid) and puts the context's workspace back into its rest state.
+ *
+ * Test hook, no counterpart in the reference: with polls > 0 the bounded
+ * waits of the split-tile combine and of the argmax reduction take every
+ * entry for missing and give up after `polls` polls, so that tests can drive
+ * the reporting path while every kernel still ends; 0 restores normal
+ * waits. */
+int si_hip_debug_set_wait_give_up(si_hip_context *ctx, uint32_t polls);
+
 int si_hip_set_kernel_policy(si_hip_context *ctx, uint32_t policy);
 
 /* ---- telemetry (metal.rs:2312-2442) ------------------------------------ */

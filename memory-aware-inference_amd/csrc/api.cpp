@@ -84,6 +84,12 @@ bool checked_mul(size_t a, size_t b, size_t *out) {
   return true;
 }
 
+bool checked_add(size_t a, size_t b, size_t *out) {
+  if (b > SIZE_MAX - a) return false;
+  *out = a + b;
+  return true;
+}
+
 // rows * (columns/256) * block_bytes with the reference's overflow checks.
 int expected_weight_bytes(size_t rows, size_t columns, size_t block_bytes, const char *label,
                           size_t *out) {
@@ -155,6 +161,12 @@ struct si_hip_context {
   size_t stage_aux_bytes = 0;
   // cross-workgroup combine area of the matrix-core kernels (kept zeroed)
   sihip::Workspace ws;
+  // the host-visible word kernels report failures in (sihip::DeviceError),
+  // its device address (in the workspace's report slot) and the test hook's
+  // poll count (0 outside tests)
+  volatile uint32_t *dev_error = nullptr;
+  uint64_t dev_error_addr = 0;
+  uint32_t give_up_polls = 0;
   hipEvent_t events[16] = {};
   // graph capture: while `capturing`, the *_device calls go to capture_stream,
   // where HIP records them instead of running them
@@ -214,6 +226,51 @@ int grow(si_hip_context *ctx, void **buf, size_t *cap, size_t need) {
   return SI_HIP_OK;
 }
 
+// The workspace's rest state on the context's stream, waited for: counters
+// zero, entries empty, then the reserved words (the error word's address and
+// the test hook's poll count).
+int reset_workspace(si_hip_context *ctx) {
+  uint8_t *p = static_cast<uint8_t *>(ctx->ws.ptr);
+  static_assert(sihip::kWorkspaceReportSlot + 8 == sihip::kWorkspaceGiveUpWord &&
+                    sihip::kWorkspaceGiveUpWord + 4 == sihip::kWorkspaceArgmaxCounter,
+                "reserved words in one 16-byte run");
+  const uint32_t reserved[4] = {(uint32_t)ctx->dev_error_addr, (uint32_t)(ctx->dev_error_addr >> 32),
+                                ctx->give_up_polls, 0u};
+  SIHIP_CHECK(hipMemsetAsync(p, 0, sihip::kWorkspaceCounterBytes, ctx->stream), "workspace clear");
+  SIHIP_CHECK(hipMemsetD32Async(p + sihip::kWorkspaceCounterBytes, (int)sihip::kWorkspaceEmpty,
+                                (sihip::kWorkspaceBytes - sihip::kWorkspaceCounterBytes) / 4,
+                                ctx->stream),
+              "workspace clear");
+  SIHIP_CHECK(hipMemcpyAsync(p + sihip::kWorkspaceReportSlot, reserved, sizeof reserved,
+                             hipMemcpyHostToDevice, ctx->stream),
+              "workspace clear");
+  SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "workspace clear");
+  return SI_HIP_OK;
+}
+
+const char *device_error_text(uint32_t code) {
+  switch (code) {
+    case sihip::kDevErrSlotWait: return "a kernel gave up waiting for a tile's LDS slot";
+    case sihip::kDevErrCombineWait: return "a kernel gave up waiting for a split tile's partial sums";
+    case sihip::kDevErrArgmaxWait: return "a kernel gave up waiting for a workgroup's argmax candidate";
+    case sihip::kDevErrTokenId: return "an embedding token id lies beyond the table";
+    default: return "a kernel reported an unknown failure";
+  }
+}
+
+// After the stream has drained: a failure a kernel reported since the last
+// check fails the call (the work since then is not valid) and puts the
+// workspace back into its rest state for the next commands.
+int check_device_error(si_hip_context *ctx) {
+  const uint32_t code = ctx->dev_error ? *ctx->dev_error : 0u;
+  if (code == 0u) return SI_HIP_OK;
+  *ctx->dev_error = 0u;
+  int rc = reset_workspace(ctx);
+  if (rc) return rc;
+  return fail(SI_HIP_ERR_DEVICE, "%s (code %u); the device work since the last synchronisation "
+              "is not valid", device_error_text(code), code);
+}
+
 int wait_stream(si_hip_context *ctx, const char *what) {
   ctx->submitted.fetch_add(1);
   const auto t0 = std::chrono::steady_clock::now();
@@ -223,7 +280,7 @@ int wait_stream(si_hip_context *ctx, const char *what) {
   ctx->wait_nanos.fetch_add(
       (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count());
   if (e != hipSuccess) return fail(SI_HIP_ERR_DEVICE, "HIP %s failed: %s", what, hipGetErrorString(e));
-  return SI_HIP_OK;
+  return check_device_error(ctx);
 }
 
 // ---------------------------------------------------------------------------
@@ -456,16 +513,17 @@ int si_hip_context_new(int device_ordinal, si_hip_context **out) {
     ctx->ws.scratch = reinterpret_cast<float *>(static_cast<uint8_t *>(p) + sihip::kWorkspaceBytes);
     ctx->ws.scratch_bytes = sihip::kWorkspaceScratchBytes;
     ctx->tel->note_alloc(total);
-    // counters zero, entries empty; set on the context's own (non-blocking)
-    // stream before any kernel
-    SIHIP_CHECK(hipMemsetAsync(p, 0, sihip::kWorkspaceCounterBytes, ctx->stream),
-                "workspace clear");
-    SIHIP_CHECK(hipMemsetD32Async(static_cast<uint8_t *>(p) + sihip::kWorkspaceCounterBytes,
-                                  (int)sihip::kWorkspaceEmpty,
-                                  (sihip::kWorkspaceBytes - sihip::kWorkspaceCounterBytes) / 4,
-                                  ctx->stream),
-                "workspace clear");
-    SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "workspace clear");
+    void *word = nullptr, *word_dev = nullptr;
+    if (hipHostMalloc(&word, 64, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess)
+      return fail(SI_HIP_ERR_OUT_OF_MEMORY, "HIP could not allocate the device error word");
+    ctx->dev_error = static_cast<volatile uint32_t *>(word);
+    *ctx->dev_error = 0u;
+    SIHIP_CHECK(hipHostGetDevicePointer(&word_dev, word, 0), "error word mapping");
+    ctx->dev_error_addr = (uint64_t)(uintptr_t)word_dev;
+    // rest state, set on the context's own (non-blocking) stream before any
+    // kernel
+    int rc = reset_workspace(ctx.get());
+    if (rc) return rc;
   }
   // the device's workspace of si_hip_quant_matvec_noalloc (no allocation;
   // done here so that callers of that entry point under graph capture find
@@ -484,6 +542,7 @@ void si_hip_context_free(si_hip_context *ctx) {
     if (p) (void)hipFree(p);
   ctx->tel->note_free(ctx->stage_in_bytes + ctx->stage_out_bytes + ctx->stage_weights_bytes +
                       ctx->stage_aux_bytes + ctx->ws.bytes + ctx->ws.scratch_bytes);
+  if (ctx->dev_error) (void)hipHostFree(const_cast<uint32_t *>(ctx->dev_error));
   for (auto &ev : ctx->events)
     if (ev) (void)hipEventDestroy(ev);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -916,32 +975,49 @@ int si_hip_q4_k_embedding_row(si_hip_context *ctx, const uint8_t *row, size_t ro
 }
 
 namespace {
-int validate_embedding_table(const si_hip_quant_weight *t, size_t cols, size_t rows) {
+// q4_k_embedding_tensor's checks (src/metal.rs:3785-3810) in its order: the
+// tensor type, the token id and the dimension, the row's start and end
+// offsets, then that row alone against the payload (a table shorter than its
+// shape still serves the rows it holds); q4_k_embedding_row's dimension check
+// (metal.rs:3735-3737) and the u32 launch limit follow.
+int validate_embedding_row(const si_hip_quant_weight *t, size_t cols, size_t rows, size_t id) {
   if (!t) return fail(SI_HIP_ERR_NULL, "embedding table handle is null");
   if (t->ggml_type != SI_HIP_GGML_TYPE_Q4_K)
     return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "Q4_K embedding requires a rank-2 Q4_K tensor");
-  if (cols == 0 || cols % 256 != 0) return fail(SI_HIP_ERR_DIMENSIONS, "Q4_K embedding token id or dimension is invalid");
-  size_t row_bytes = cols / 256 * 144, total;
-  if (!checked_mul(rows, row_bytes, &total)) return fail(SI_HIP_ERR_OVERFLOW, "Q4_K embedding row offset overflows");
-  if (total > t->bytes) return fail(SI_HIP_ERR_BYTE_LENGTH, "Q4_K embedding tensor payload is shorter than its shape");
-  if (cols > UINT32_MAX || rows > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "embedding dimension exceeds HIP limits");
+  if (id >= rows || cols % 256 != 0)
+    return fail(SI_HIP_ERR_RANGE, "Q4_K embedding token id or dimension is invalid");
+  const size_t row_bytes = cols / 256 * 144;
+  size_t start = 0, end = 0;
+  if (!checked_mul(id, row_bytes, &start)) return fail(SI_HIP_ERR_OVERFLOW, "Q4_K embedding row offset overflows");
+  if (!checked_add(start, row_bytes, &end)) return fail(SI_HIP_ERR_OVERFLOW, "Q4_K embedding row end overflows");
+  if (end > t->bytes)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "Q4_K embedding tensor payload is shorter than its shape");
+  if (cols == 0) return fail(SI_HIP_ERR_DIMENSIONS, "Q4_K embedding dimension is invalid");
+  if (cols > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "embedding dimension exceeds HIP limits");
   return SI_HIP_OK;
+}
+
+// The rows of the table a kernel may read: those of its shape that its
+// payload holds whole.
+uint32_t embedding_table_rows(const si_hip_quant_weight *t, size_t cols, size_t rows) {
+  const size_t held = t->bytes / (cols / 256 * 144);
+  return (uint32_t)std::min<size_t>({rows, held, (size_t)UINT32_MAX});
 }
 }  // namespace
 
 int si_hip_q4_k_embedding_tokens(si_hip_context *ctx, const si_hip_quant_weight *t, size_t cols,
                                  size_t rows, const uint32_t *ids, size_t n, float *out) {
-  int rc = validate_embedding_table(t, cols, rows);
-  if (rc) return rc;
   if (n == 0) return fail(SI_HIP_ERR_DIMENSIONS, "Q4_K embedding needs at least one token id");
   if (!ids) return fail(SI_HIP_ERR_NULL, "token id buffer is null");
-  for (size_t i = 0; i < n; ++i)
-    if (ids[i] >= rows) return fail(SI_HIP_ERR_RANGE, "Q4_K embedding token id or dimension is invalid");
+  for (size_t i = 0; i < n; ++i) {
+    int rc = validate_embedding_row(t, cols, rows, ids[i]);
+    if (rc) return rc;
+  }
   if (n > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "too many token ids");
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!out) return fail(SI_HIP_ERR_NULL, "Q4_K embedding output is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
-  rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, n * sizeof(uint32_t));
+  int rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, n * sizeof(uint32_t));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, n * cols * sizeof(float));
   if (rc) return rc;
@@ -950,7 +1026,7 @@ int si_hip_q4_k_embedding_tokens(si_hip_context *ctx, const si_hip_quant_weight 
   hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, t->data(),
                                        static_cast<const uint32_t *>(ctx->stage_in),
                                        static_cast<float *>(ctx->stage_out), (uint32_t)n, (uint32_t)cols,
-                                       ctx->stream);
+                                       ctx->stream, embedding_table_rows(t, cols, rows), ctx->ws.ptr);
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
   SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, n * cols * sizeof(float), hipMemcpyDeviceToHost,
                              ctx->stream),
@@ -962,9 +1038,8 @@ int si_hip_q4_k_embedding_tokens(si_hip_context *ctx, const si_hip_quant_weight 
 
 int si_hip_q4_k_embedding_tensor(si_hip_context *ctx, const si_hip_quant_weight *t, size_t cols,
                                  size_t rows, size_t token_id, float *out) {
-  int rc = validate_embedding_table(t, cols, rows);
+  int rc = validate_embedding_row(t, cols, rows, token_id);
   if (rc) return rc;
-  if (token_id >= rows) return fail(SI_HIP_ERR_RANGE, "Q4_K embedding token id or dimension is invalid");
   const uint32_t id = (uint32_t)token_id;
   return si_hip_q4_k_embedding_tokens(ctx, t, cols, rows, &id, 1, out);
 }
@@ -1045,7 +1120,29 @@ int validate_head(const si_hip_quant_weight *w, size_t rows, size_t cols, size_t
     return fail(SI_HIP_ERR_BYTE_LENGTH, "%s output head byte length is invalid", label);
   if (rule != SI_HIP_ARGMAX_LAST_FINITE && rule != SI_HIP_ARGMAX_FIRST_GREATER)
     return fail(SI_HIP_ERR_RANGE, "unknown argmax tie rule %u", rule);
+  if (rows >= sihip::kArgmaxMaxRows)
+    return fail(SI_HIP_ERR_OVERFLOW, "%s output head rows exceed the argmax's %u", label,
+                (unsigned)sihip::kArgmaxMaxRows);
   return check_u32(rows, cols, label);
+}
+// The head's logits and greedy argmax on `stream`: the Q6_K matrix-core
+// kernel with the argmax fused into it, else the matvec, then the argmax
+// kernel.
+int dispatch_head(si_hip_context *ctx, const si_hip_quant_weight *w, const float *d_in,
+                  float *d_logits, uint32_t rows, uint32_t cols, uint32_t rule, uint64_t *d_result,
+                  hipStream_t stream) {
+  hipError_t e = hipErrorInvalidValue;
+  if (ctx->policy == SI_HIP_KERNEL_AUTO && w->ggml_type == SI_HIP_GGML_TYPE_Q6_K &&
+      sihip::launch_q6k_matvec_argmax_mfma(w->data(), d_in, d_logits, rows, cols, rule, d_result,
+                                           ctx->ws, stream, &e)) {
+    if (e != hipSuccess) return hip_fail(e, "output head launch");
+    return SI_HIP_OK;
+  }
+  int rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_logits, rows, cols, 1, stream);
+  if (rc) return rc;
+  e = sihip::launch_argmax(d_logits, rows, rule, ctx->ws, d_result, stream);
+  if (e != hipSuccess) return hip_fail(e, "argmax launch");
+  return SI_HIP_OK;
 }
 }  // namespace
 
@@ -1067,11 +1164,9 @@ int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_qua
               "input copy");
   float *d_logits = static_cast<float *>(ctx->stage_out);
   uint64_t *aux = static_cast<uint64_t *>(ctx->stage_aux);
-  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), static_cast<const float *>(ctx->stage_in),
-                       d_logits, (uint32_t)rows, (uint32_t)cols, 1, ctx->stream);
+  rc = dispatch_head(ctx, w, static_cast<const float *>(ctx->stage_in), d_logits, (uint32_t)rows,
+                     (uint32_t)cols, rule, aux, ctx->stream);
   if (rc) return rc;
-  hipError_t e = sihip::launch_argmax(d_logits, (uint32_t)rows, rule, ctx->ws, aux, ctx->stream);
-  if (e != hipSuccess) return hip_fail(e, "argmax launch");
   uint64_t packed = 0;
   SIHIP_CHECK(hipMemcpyAsync(&packed, aux, sizeof packed, hipMemcpyDeviceToHost, ctx->stream), "argmax copy");
   if (logits)
@@ -1368,6 +1463,8 @@ int si_hip_copy_from_device(si_hip_context *ctx, void *dst, const void *src, siz
   if (!ctx || !dst || !src) return fail(SI_HIP_ERR_NULL, "copy argument is null");
   SIHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "copy from device");
   SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "copy from device");
+  int rc = check_device_error(ctx);
+  if (rc) return rc;
   return ok();
 }
 
@@ -1501,11 +1598,9 @@ int si_hip_matvec_argmax_device(si_hip_context *ctx, const si_hip_quant_weight *
   if (rc) return rc;
   if (!ctx || !d_in || !d_logits || !d_result) return fail(SI_HIP_ERR_NULL, "device head argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
-  rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_logits, (uint32_t)rows, (uint32_t)cols, 1, device_stream(ctx));
+  rc = dispatch_head(ctx, w, d_in, d_logits, (uint32_t)rows, (uint32_t)cols, rule, d_result,
+                     device_stream(ctx));
   if (rc) return rc;
-  hipError_t e =
-      sihip::launch_argmax(d_logits, (uint32_t)rows, rule, ctx->ws, d_result, device_stream(ctx));
-  if (e != hipSuccess) return hip_fail(e, "argmax launch");
   ctx->async_submitted.fetch_add(1);
   return ok();
 }
@@ -1516,13 +1611,19 @@ uint32_t si_hip_argmax_result_index(uint64_t packed, uint32_t rule) {
 
 int si_hip_embedding_device(si_hip_context *ctx, const si_hip_quant_weight *t, size_t cols,
                             size_t rows, const uint32_t *d_ids, size_t n, float *d_out) {
-  int rc = validate_embedding_table(t, cols, rows);
+  // the ids live on the device: the table checks here (those of row 0, which
+  // every non-empty table passes), the ids' in the kernel, which gives an id
+  // beyond the rows the table holds a NaN row and reports it at the next
+  // synchronisation
+  if (rows == 0) return fail(SI_HIP_ERR_RANGE, "Q4_K embedding token id or dimension is invalid");
+  int rc = validate_embedding_row(t, cols, rows, 0);
   if (rc) return rc;
   if (n == 0 || n > UINT32_MAX) return fail(SI_HIP_ERR_DIMENSIONS, "embedding token count is invalid");
   if (!ctx || !d_ids || !d_out) return fail(SI_HIP_ERR_NULL, "device embedding argument is null");
   std::lock_guard<std::mutex> lock(ctx->mu);
   hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, t->data(), d_ids, d_out, (uint32_t)n,
-                                       (uint32_t)cols, device_stream(ctx));
+                                       (uint32_t)cols, device_stream(ctx),
+                                       embedding_table_rows(t, cols, rows), ctx->ws.ptr);
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
   ctx->async_submitted.fetch_add(1);
   return ok();
@@ -1600,6 +1701,17 @@ void si_hip_graph_free(si_hip_graph *graph) {
   if (graph->exec) (void)hipGraphExecDestroy(graph->exec);
   if (graph->graph) (void)hipGraphDestroy(graph->graph);
   delete graph;
+}
+
+int si_hip_debug_set_wait_give_up(si_hip_context *ctx, uint32_t polls) {
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  std::lock_guard<std::mutex> lock(ctx->mu);
+  if (ctx->capturing) return fail(SI_HIP_ERR_STATE, "the wait hook cannot change during a graph capture");
+  SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "wait hook");
+  ctx->give_up_polls = polls;
+  int rc = reset_workspace(ctx);
+  if (rc) return rc;
+  return ok();
 }
 
 int si_hip_set_kernel_policy(si_hip_context *ctx, uint32_t policy) {

@@ -107,12 +107,15 @@ __global__ __launch_bounds__(256) void fused_gate_up_generic_kernel(
 
 // Exact dequantisation of whole blocks: one thread per 32-weight unit.
 // `row_index` (optional) maps output row r to source row row_index[r]
-// (the embedding gather); otherwise output row r is source row r.
+// (the embedding gather); otherwise output row r is source row r.  An index
+// of table_rows or more reads nothing: its output row is NaN and the kernel
+// reports kDevErrTokenId through the workspace `ws` (when not null).
 template <uint32_t T>
 __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict__ w,
                                                       const uint32_t* __restrict__ row_index,
                                                       float* __restrict__ out, uint32_t out_rows,
-                                                      uint32_t cols) {
+                                                      uint32_t cols, uint32_t table_rows,
+                                                      void* ws) {
   constexpr uint32_t BB = BlockBytes<T>::value;
   const uint32_t nb = cols / kBlockElems;
   const uint64_t units_total = (uint64_t)out_rows * nb * 8u;
@@ -124,7 +127,13 @@ __global__ __launch_bounds__(256) void dequant_kernel(const uint8_t* __restrict_
   const uint32_t unit = rem & 7u;
   const uint64_t src_row = row_index ? row_index[r] : r;
   float v[32];
-  decode_unit_exact<T>(w + (src_row * nb + blk) * BB, unit, v);
+  if (src_row < table_rows) {
+    decode_unit_exact<T>(w + (src_row * nb + blk) * BB, unit, v);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 32; ++i) v[i] = __builtin_nanf("");
+    if (ws && blk == 0u && unit == 0u) report_device_error(ws, kDevErrTokenId);
+  }
   uint32_t col0;
   if constexpr (T == kTypeQ6K) {
     col0 = blk * 256u + (unit >> 2) * 128u + (unit & 3u) * 32u;
@@ -174,21 +183,22 @@ hipError_t launch_fused_gate_up_generic(const uint8_t* gate, const uint8_t* up, 
 }
 
 hipError_t launch_dequant(uint32_t type, const uint8_t* w, const uint32_t* row_index, float* out,
-                          uint32_t out_rows, uint32_t cols, hipStream_t s) {
+                          uint32_t out_rows, uint32_t cols, hipStream_t s, uint32_t table_rows,
+                          void* ws) {
   const uint64_t units = (uint64_t)out_rows * (cols / kBlockElems) * 8u;
   const dim3 grid((uint32_t)((units + 255) / 256));
   switch (type) {
     case kTypeQ4K:
       hipLaunchKernelGGL(dequant_kernel<kTypeQ4K>, grid, dim3(256), 0, s, w, row_index, out,
-                         out_rows, cols);
+                         out_rows, cols, table_rows, ws);
       break;
     case kTypeQ5K:
       hipLaunchKernelGGL(dequant_kernel<kTypeQ5K>, grid, dim3(256), 0, s, w, row_index, out,
-                         out_rows, cols);
+                         out_rows, cols, table_rows, ws);
       break;
     case kTypeQ6K:
       hipLaunchKernelGGL(dequant_kernel<kTypeQ6K>, grid, dim3(256), 0, s, w, row_index, out,
-                         out_rows, cols);
+                         out_rows, cols, table_rows, ws);
       break;
     default:
       return hipErrorInvalidValue;

@@ -524,6 +524,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   i32x4 A[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) A[t] = i32x4{0, 0, 0, 0};
+  uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
   for (uint32_t j = 0; j < my_pairs; ++j) {
     const Pair pr = DEPTH == 1 ? pr_next : pair_at(sc, wave + j * WAVES, tstages);
     const uint32_t s = MATS > 1 && pr.r >= nstages ? pr.r - nstages : pr.r;  // stage
@@ -595,7 +596,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
         }
         rs[t] = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
       }
-      hand_off_tokens<NTOK>(sbase, L, sc.by_slots, pr, tstages, rs, lane, rows, y);
+      hand_off_tokens<NTOK>(sbase, L, sc.by_slots, pr, tstages, rs, lane, rows, y, fail);
       continue;
     }
     u32x2 xs[4];
@@ -642,8 +643,9 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     const float rowsum = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
-    hand_off<MATS>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws);
+    hand_off<MATS>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws, fail);
   }
+  if (fail != 0u) report_device_error(wsp, fail);
 }
 
 // ---- Several activation vectors in the MFMA rows --------------------------
@@ -906,6 +908,7 @@ __device__ __forceinline__ float block_exact_row(uint32_t hp, const float* __res
 struct TokArgs {
   uint32_t slices, groups_per_slice, m_gps, m_parts;
   uint32_t slots, m_slots;
+  void* wsp;  // the workspace, for failure reports
 };
 
 // LDS map: per-wave stage buffers; the images of ng groups of nbl blocks
@@ -1121,6 +1124,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
   //    4 g + grp, row n
   const uint32_t hb0 = sbase + wave * kStage + 16u * n;
   const uint32_t qb0 = hb0 + 256u * (1u + (grp >> 1)) + 8u * (grp & 1u);
+  uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
   for (uint32_t j = 0; j < my_pairs; ++j) {
     const Pair pr = pr_next;
     const uint32_t s = pr.r, sl = s - s0;  // stage, and its place in the image range
@@ -1214,7 +1218,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
     }
     if (!sliced) {
       hand_off_lane_tokens(sbase, L, FastDiv{ta.slots, ta.m_slots}, pr, nstages, part[0], lane,
-                           rows, ntok, y);
+                           rows, ntok, y, fail);
       continue;
     }
     // the stage's partial sums of the tile's rows, for tok_reduce
@@ -1227,6 +1231,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       }
     }
   }
+  if (fail != 0u) report_device_error(ta.wsp, fail);
 }
 
 // y[t * rows + row] = sum over the stages s of part[(s * nv + t) * rows + row],
@@ -1288,6 +1293,7 @@ bool launch_tokens_td(const uint8_t* w, const float* x, float* y, uint32_t rows,
   }
   ta.m_gps = div_magic(ta.groups_per_slice);
   ta.m_slots = div_magic(ta.slots);
+  ta.wsp = ws.ptr;
   // block and tile indices divided by GS
   if ((uint64_t)(grid + ntiles) * ta.groups_per_slice >= (1ull << 32)) return false;
   if (lds > kLdsBytes) return false;

@@ -32,6 +32,7 @@
 // 13: its chunks are read as two pieces and realigned with v_alignbyte.
 // Scheduling, the LDS slot ring and the finishing wave are the Q4_K
 // kernel's (mfma_common.h).
+#include "argmax_device.h"
 #include "mfma_common.h"
 #include "si_hip_tuned.h"
 
@@ -233,13 +234,23 @@ __device__ __forceinline__ float q6_bound(const int (&sc)[4], float d) {
 // of ga.count matrices of one K, one after the other (every matrix but the
 // last a whole number of tiles); tile t reads the matrix whose tiles reach
 // past t.
-template <int WAVES, int DEPTH, int NTOK, bool GROUPED>
+//
+// ARGMAX (one vector, one matrix): the greedy argmax of y under tie rule
+// aa.rule, fused: each workgroup keeps the best candidate of the rows it
+// stores, and the workgroups reduce theirs through the workspace's argmax
+// area into *aa.result (argmax_device.h).
+struct ArgmaxArgs {
+  uint64_t* result;
+  uint32_t rule;
+};
+template <int WAVES, int DEPTH, int NTOK, bool GROUPED, bool ARGMAX = false>
 __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
                                                               uint32_t nb, void* __restrict__ wsp,
                                                               SchedArgs sa, uint32_t prefetch,
-                                                              GroupArgs ga) {
+                                                              GroupArgs ga, ArgmaxArgs aa) {
+  static_assert(!ARGMAX || (NTOK == 1 && !GROUPED), "argmax over one matrix and vector");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t slots = sa.packed & 0xffu;
   const Layout L = layout(WAVES, DEPTH, nb, slots, NTOK);
@@ -366,6 +377,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   i32x4 A[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) A[t] = i32x4{0, 0, 0, 0};
+  uint64_t best = 0u;  // ARGMAX: the best candidate of the rows this lane stored
+  uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
   for (uint32_t j = 0; j < my_pairs; ++j) {
     const Pair pr = pair_at(sc, wave + j * WAVES, nstages);
     const uint32_t st = pr.r;
@@ -408,7 +421,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
       // the decoded stage meets every vector in turn (vector 0's images and
       // exponents are already in A, e0, e1); each vector's row sums go
       // straight to the tile's slot
-      const uint32_t part_at = token_slot(sbase, L, sc.by_slots, pr, nstages, NTOK, lane);
+      const uint32_t part_at = token_slot(sbase, L, sc.by_slots, pr, nstages, NTOK, lane, fail);
 #pragma unroll 1
       for (uint32_t t = 0; t < (uint32_t)NTOK; ++t) {
         int f0 = e0, f1 = e1;
@@ -475,14 +488,29 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     const float rowsum = sum_lane_groups(pp[0] + pp[1]);
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
-    hand_off<1>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws);
+    hand_off<1, ARGMAX>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws, fail,
+                        &best, aa.rule);
+  }
+  if (fail != 0u) report_device_error(wsp, fail);
+  if constexpr (ARGMAX) {
+    // the workgroup's best, once every wave is done with the LDS, then the
+    // grid's through the workspace
+    best = wave_max_u64(best);
+    __syncthreads();
+    uint64_t* const wave_best = reinterpret_cast<uint64_t*>(smem);
+    if (lane == 0u) wave_best[wave] = best;
+    __syncthreads();
+    if (wave == 0u) {
+      const uint64_t m = lane < (uint32_t)WAVES ? wave_best[lane] : 0u;
+      argmax_publish_wave(wave_max_u64(m), wsp, aa.result, lane);
+    }
   }
 }
 
-template <int W, int D, int NT = 1, bool G = false>
+template <int W, int D, int NT = 1, bool G = false, bool AM = false>
 bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                const Workspace& ws, hipStream_t s, hipError_t* err,
-               const GroupArgs& ga = GroupArgs{}) {
+               const GroupArgs& ga = GroupArgs{}, const ArgmaxArgs& aa = ArgmaxArgs{}) {
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = (nb + 1u) / 2u;
   // several vectors: whole tiles only
@@ -496,15 +524,18 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
   const uint32_t lds = layout(W, D, nb, slots, NT).total + (D == 1 && prefetch ? 256u : 0u);
   SchedArgs sa;
   if (lds > kLdsBytes || !make_sched_args(ntiles, nstages, slots, ls, &sa)) return false;
+  // the argmax: an entry per workgroup, the waves' candidates at the LDS start
+  if (AM && (grid > kArgmaxMaxGroups || rows >= kArgmaxMaxRows || ws.bytes < kWorkspaceBytes))
+    return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, NT, G>),
+      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, NT, G, AM>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, NT, G>), dim3(grid), dim3(W * 64), lds, s, w, x, y,
-                     rows, nb, ws.ptr, sa, D == 1 ? prefetch : 0u, ga);
+  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, NT, G, AM>), dim3(grid), dim3(W * 64), lds, s, w, x,
+                     y, rows, nb, ws.ptr, sa, D == 1 ? prefetch : 0u, ga, aa);
   *err = hipGetLastError();
   return true;
 }
@@ -535,6 +566,16 @@ bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
   }
   return launch_wd<12, 1>(w, x, y, rows, nb, ws, s, err) || launch_wd<10, 1>(w, x, y, rows, nb, ws, s, err) ||
          launch_wd<8, 1>(w, x, y, rows, nb, ws, s, err) || launch_wd<4, 1>(w, x, y, rows, nb, ws, s, err);
+}
+
+bool launch_q6k_matvec_argmax_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                                   uint32_t cols, uint32_t rule, uint64_t* result,
+                                   const Workspace& ws, hipStream_t s, hipError_t* err) {
+  const uint32_t nb = cols / kBlockElems;
+  if (!q6_shape_ok(rows, nb)) return false;
+  const ArgmaxArgs aa{result, rule};
+  return launch_wd<12, 1, 1, false, true>(w, x, y, rows, nb, ws, s, err, GroupArgs{}, aa) ||
+         launch_wd<8, 1, 1, false, true>(w, x, y, rows, nb, ws, s, err, GroupArgs{}, aa);
 }
 
 // batch >= 2 vectors: four, three or two per pass over the weights while

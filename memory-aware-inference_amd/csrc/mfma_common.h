@@ -692,24 +692,41 @@ __device__ __forceinline__ void store_coherent(float* p, float v) {
 __device__ __forceinline__ float load_coherent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// Waits until ring slot word `owner_at` names local tile lt.  The wait is
+// bounded (about 2^24 polls, seconds): a wave that gives up sets `fail` to
+// kDevErrSlotWait and goes on, its results then invalid.  (Kernels report a
+// set `fail` once, at their end: report_device_error.)
+__device__ __forceinline__ void wait_slot(uint32_t owner_at, uint32_t lt, uint32_t& fail) {
+  uint32_t spin = 0;
+  for (; lds_read_b32(owner_at) != lt && spin < (1u << 24); ++spin) __builtin_amdgcn_s_sleep(1);
+  if (__builtin_amdgcn_readfirstlane(spin) == (1u << 24)) fail = kDevErrSlotWait;
+}
+
 // Hands partial pr.r (of tparts = MATS * nparts per tile) of tile pr.tile to
 // the tile's LDS slot, waiting while an earlier tile still holds it.  The wave
 // that completes the workgroup's share of the tile sums that share in partial
 // order and stores the rows -- y[row] = sum, or with MATS == 2 silu(sum of
 // partials < nparts) * (sum of the rest) -- or, for a split tile, publishes
-// the sums and, if it completes the tile, combines all shares.
-template <int MATS>
+// the sums and, if it completes the tile, combines all shares.  ARGMAX: every
+// row stored also enters *best (argmax_candidate under `rule`).
+template <int MATS, bool ARGMAX = false>
 __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32_t slots,
                                          const Sched& sc, const SchedArgs& sa, const Pair& pr,
                                          uint32_t nparts,
                                          float rowsum, uint32_t lane, uint32_t rows,
-                                         float* __restrict__ y, SplitWs ws) {
+                                         float* __restrict__ y, SplitWs ws, uint32_t& fail,
+                                         uint64_t* best = nullptr, uint32_t rule = 0u) {
+  auto store_row = [&](uint32_t row, float v) {
+    y[row] = v;
+    if constexpr (ARGMAX) {
+      const uint64_t c = argmax_candidate(v, row, rule);
+      *best = c > *best ? c : *best;
+    }
+  };
   const uint32_t grp = lane >> 4, n = lane & 15u;
   const uint32_t tparts = MATS * nparts;
   const uint32_t slot = pr.lt - quo(pr.lt, sc.by_slots) * slots;
-  for (uint32_t spin = 0;
-       lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
-    __builtin_amdgcn_s_sleep(1);
+  wait_slot(sbase + L.owner + 4u * slot, pr.lt, fail);
   if (grp == 0u)
     lds_write_b32(sbase + L.part + 64u * (slot * tparts + pr.r) + 4u * n, __float_as_uint(rowsum));
   uint32_t old = 0u;
@@ -727,7 +744,7 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
   }
   const uint32_t row = pr.tile * 16u + n;
   if (pr.lo == 0u && pr.hi == tparts) {
-    if (grp == 0u && row < rows) y[row] = MATS > 1 ? silu_times(sum, sum2) : sum;
+    if (grp == 0u && row < rows) store_row(row, MATS > 1 ? silu_times(sum, sum2) : sum);
   } else {
     // Publish the share's sums, then count the share; no fence orders the
     // two: the workgroup that completes the count waits for each entry to
@@ -736,6 +753,12 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
     // lane group k reads the entry of share g0 + k of each batch of four, the
     // first batch before the count goes out, so the workgroup that completes
     // it waits about one memory round trip for the other shares.
+    // (The lane's indices are taken afresh here, behind a compiler barrier,
+    // so that no address of this rare path is kept live through the caller's
+    // main loop.)
+    uint32_t ln = lane;
+    asm volatile("" : "+v"(ln));
+    const uint32_t grp = ln >> 4, n = ln & 15u;
     const uint32_t t = pr.tile - sc.split_base;  // leftover tile index
     const uint32_t e = 2u * blockIdx.x + (t == sc.t_a ? 0u : 1u);
     if (grp == 0u) {
@@ -767,6 +790,7 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
     uint32_t off = entry(g0 + grp);
     float v = 0.0f, v2 = 0.0f;
     fetch(off, g0 + grp, v, v2);
+    const uint32_t force = __builtin_amdgcn_readfirstlane(give_up_polls(ws.cnt));
     // (the count goes out after those reads, so waiting for it -- and for
     // every older memory operation of the wave -- takes one round trip)
     uint32_t before = 0u;
@@ -782,12 +806,18 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
           off = entry(wg);
           fetch(off, wg, v, v2);
         }
-        // wait (bounded) until every entry of the batch has landed
-        for (uint32_t spin = 0; spin < (1u << 22); ++spin) {
+        // wait (bounded: about 2^22 polls, or the test hook's count) until
+        // every entry of the batch has landed; on giving up, set `fail` and
+        // add what is there
+        for (uint32_t spin = 0;; ++spin) {
           const bool missing = off != kNoEntry && wg != blockIdx.x &&
-                               (__float_as_uint(v) == kPartEmpty ||
+                               (force != 0u || __float_as_uint(v) == kPartEmpty ||
                                 (MATS > 1 && __float_as_uint(v2) == kPartEmpty));
           if (!__builtin_amdgcn_ballot_w64(missing)) break;
+          if (spin == (force != 0u ? force : (1u << 22))) {
+            fail = kDevErrCombineWait;
+            break;
+          }
           __builtin_amdgcn_s_sleep(1);
           if (missing) fetch(off, wg, v, v2);
         }
@@ -807,7 +837,7 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
           if (MATS > 1) store_coherent(ws.part + off + 16u, __uint_as_float(kPartEmpty));
         }
       }
-      if (grp == 0u && row < rows) y[row] = MATS > 1 ? silu_times(g, u) : g;
+      if (grp == 0u && row < rows) store_row(row, MATS > 1 ? silu_times(g, u) : g);
       if (lane == 0u)
         (void)__hip_atomic_exchange(ws.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
@@ -881,12 +911,11 @@ inline LaunchShape launch_shape(uint32_t ntiles, uint32_t tparts, uint32_t waves
 // completes the tile, adds the partials in order and stores the rows.
 __device__ __forceinline__ uint32_t token_slot(uint32_t sbase, const Layout& L,
                                                const FastDiv& by_slots, const Pair& pr,
-                                               uint32_t tparts, uint32_t ntok, uint32_t lane) {
+                                               uint32_t tparts, uint32_t ntok, uint32_t lane,
+                                               uint32_t& fail) {
   const uint32_t slots = by_slots.d;
   const uint32_t slot = pr.lt - quo(pr.lt, by_slots) * slots;
-  for (uint32_t spin = 0;
-       lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
-    __builtin_amdgcn_s_sleep(1);
+  wait_slot(sbase + L.owner + 4u * slot, pr.lt, fail);
   return sbase + L.part + 64u * ntok * (slot * tparts + pr.r) + 4u * (lane & 15u);
 }
 template <int NTOK>
@@ -920,8 +949,8 @@ __device__ __forceinline__ void hand_off_tokens(uint32_t sbase, const Layout& L,
                                                 const FastDiv& by_slots, const Pair& pr,
                                                 uint32_t tparts, const float (&rowsum)[NTOK],
                                                 uint32_t lane, uint32_t rows,
-                                                float* __restrict__ y) {
-  const uint32_t base = token_slot(sbase, L, by_slots, pr, tparts, NTOK, lane);
+                                                float* __restrict__ y, uint32_t& fail) {
+  const uint32_t base = token_slot(sbase, L, by_slots, pr, tparts, NTOK, lane, fail);
   if ((lane >> 4) == 0u) {
 #pragma unroll
     for (int t = 0; t < NTOK; ++t) lds_write_b32(base + 64u * t, __float_as_uint(rowsum[t]));
@@ -936,13 +965,11 @@ __device__ __forceinline__ void hand_off_lane_tokens(uint32_t sbase, const Layou
                                                      const FastDiv& by_slots, const Pair& pr,
                                                      uint32_t tparts, float rowsum, uint32_t lane,
                                                      uint32_t rows, uint32_t ntok,
-                                                     float* __restrict__ y) {
+                                                     float* __restrict__ y, uint32_t& fail) {
   const uint32_t grp = lane >> 4, n = lane & 15u;
   const uint32_t slots = by_slots.d;
   const uint32_t slot = pr.lt - quo(pr.lt, by_slots) * slots;
-  for (uint32_t spin = 0;
-       lds_read_b32(sbase + L.owner + 4u * slot) != pr.lt && spin < (1u << 24); ++spin)
-    __builtin_amdgcn_s_sleep(1);
+  wait_slot(sbase + L.owner + 4u * slot, pr.lt, fail);
   // the slot's partial r holds [vector][16 rows], 256 bytes
   lds_write_b32(sbase + L.part + 256u * (slot * tparts + pr.r) + 4u * lane,
                 __float_as_uint(rowsum));

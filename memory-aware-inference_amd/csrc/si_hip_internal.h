@@ -25,10 +25,49 @@ constexpr size_t kWorkspaceCounterBytes = size_t(1) << 20;
 // a signalling-NaN pattern: no arithmetic result has it (results of
 // operations are quiet NaNs)
 constexpr uint32_t kWorkspaceEmpty = 0x7fbadbadu;
-// the argmax reduction's counter (the last counter word) and its 256 u64
-// entries (the last 4 KB)
+// Reserved words at the end of the counter region (the tile counters stop
+// 64 bytes before its end):
+//   kWorkspaceArgmaxCounter  the argmax reduction's counter
+//   kWorkspaceGiveUpWord     a test hook, zero otherwise: while it holds
+//                            n > 0, the bounded waits of the split-tile
+//                            combine and of the argmax reduction take every
+//                            entry for missing and give up after n polls
+//   kWorkspaceReportSlot     the device address (u64) of the owner's
+//                            host-visible error word, or 0 (no owner reads it)
+// and the argmax reduction's 512 u64 entries (the last 4 KB).
 constexpr size_t kWorkspaceArgmaxCounter = kWorkspaceCounterBytes - 4;
+constexpr size_t kWorkspaceGiveUpWord = kWorkspaceCounterBytes - 8;
+constexpr size_t kWorkspaceReportSlot = kWorkspaceCounterBytes - 16;
 constexpr size_t kWorkspaceArgmaxEntries = kWorkspaceBytes - 4096;
+constexpr uint32_t kArgmaxMaxGroups = 512;
+// Candidates index fewer rows than this, so that no candidate equals an entry
+// that holds none (both halves kWorkspaceEmpty).
+constexpr uint32_t kArgmaxMaxRows = 0x7fb00000u;
+
+// What a kernel reports through the error word when it cannot finish its work
+// correctly (it still ends normally).
+enum DeviceError : uint32_t {
+  kDevErrNone = 0,
+  kDevErrSlotWait = 1,     // a wave gave up waiting for its tile's LDS slot
+  kDevErrCombineWait = 2,  // a split tile's partial sums did not arrive
+  kDevErrArgmaxWait = 3,   // a workgroup's argmax candidate did not arrive
+  kDevErrTokenId = 4,      // an embedding token id beyond the table
+};
+
+// Stores `code` into the workspace owner's error word (a system-scope store
+// into host memory; the last report wins).  Taken only on failure paths.
+__device__ inline void report_device_error(void* ws, uint32_t code) {
+  uint64_t* slot = reinterpret_cast<uint64_t*>(static_cast<uint8_t*>(ws) + kWorkspaceReportSlot);
+  const uint64_t a = __hip_atomic_load(slot, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (a != 0u)
+    __hip_atomic_store(reinterpret_cast<uint32_t*>(a), code, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_SYSTEM);
+}
+// The test hook's poll count (0: the waits run their normal course).
+__device__ inline uint32_t give_up_polls(void* ws) {
+  uint32_t* w = reinterpret_cast<uint32_t*>(static_cast<uint8_t*>(ws) + kWorkspaceGiveUpWord);
+  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // silu(g) * u exactly as src/runtime.rs:4296-4298 / metal.rs:585 write it.
 __host__ __device__ __forceinline__ float silu_times(float g, float u) {
@@ -72,8 +111,12 @@ hipError_t launch_matvec_generic(uint32_t type, const uint8_t* w, const float* x
                                  uint32_t rows, uint32_t cols, uint32_t batch, hipStream_t s);
 hipError_t launch_fused_gate_up_generic(const uint8_t* gate, const uint8_t* up, const float* x,
                                         float* h, uint32_t rows, uint32_t cols, hipStream_t s);
+// Dequantises out_rows rows; with row_index, output row r is table row
+// row_index[r], and an index of table_rows or more gives a row of NaNs and
+// reports kDevErrTokenId through the workspace `ws` (when not null).
 hipError_t launch_dequant(uint32_t type, const uint8_t* w, const uint32_t* row_index, float* out,
-                          uint32_t out_rows, uint32_t cols, hipStream_t s);
+                          uint32_t out_rows, uint32_t cols, hipStream_t s,
+                          uint32_t table_rows = 0xffffffffu, void* ws = nullptr);
 
 // kernels_f32.hip: y = W x for a row-major F32 matrix; RMSNorm of `heads`
 // vectors of head_dim values, mode 0 (x * inv * w), 1 (x * inv * (1 + w)) or
@@ -83,7 +126,7 @@ hipError_t launch_f32_matvec(const float* w, const float* x, float* y, uint32_t 
 hipError_t launch_rms_norm(uint32_t mode, const float* x, const float* gate, const float* w,
                            float* y, uint32_t heads, uint32_t head_dim, float eps, hipStream_t s);
 
-// kernels_argmax.hip: max-loc over n < 2^31 logits in one launch, using the
+// kernels_argmax.hip: max-loc over n < kArgmaxMaxRows logits in one launch, using the
 // context workspace's argmax area; the winner lands in *result (packed
 // candidate, 0 when there is none).
 hipError_t launch_argmax(const float* logits, uint32_t n, uint32_t rule, const Workspace& ws,

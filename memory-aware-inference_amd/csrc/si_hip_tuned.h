@@ -13,7 +13,7 @@ namespace sihip {
 bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float* y, uint32_t rows,
                          uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
                          hipError_t* err);
-// Q4_K, one vector, K <= 8192, on the matrix cores.
+// Q4_K, one vector, on the matrix cores (K up to 128 blocks of 256).
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
 // Q4_K, batch >= 2 vectors (batch-major x and y): up to four per pass over the
@@ -39,6 +39,12 @@ bool launch_matvec_group(uint32_t type, const uint8_t* const* w, const uint32_t*
 // weights), on the matrix cores.
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
+// The Q6_K matvec with the greedy argmax of its output fused (rule: an
+// ArgmaxRule): y gets the logits, *result the packed winning candidate
+// (0 when no logit qualifies).
+bool launch_q6k_matvec_argmax_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                                   uint32_t cols, uint32_t rule, uint64_t* result,
+                                   const Workspace& ws, hipStream_t s, hipError_t* err);
 bool launch_q6k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
                             hipError_t* err);

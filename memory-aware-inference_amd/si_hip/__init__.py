@@ -131,6 +131,7 @@ _SIGS = {
     "si_hip_graph_calls": (_U64, [_P]),
     "si_hip_graph_free": (None, [_P]),
     "si_hip_set_kernel_policy": (_I, [_P, _U32]),
+    "si_hip_debug_set_wait_give_up": (_I, [_P, _U32]),
     "si_hip_current_allocated_bytes": (_U64, [_P]),
     "si_hip_peak_allocated_bytes": (_U64, [_P]),
     "si_hip_peak_active_weight_bytes": (_U64, [_P]),
@@ -366,6 +367,11 @@ class HipContext:
 
     def set_kernel_policy(self, policy: int) -> None:
         _check(lib().si_hip_set_kernel_policy(self._h, policy))
+
+    def debug_set_wait_give_up(self, polls: int) -> None:
+        """Test hook: the kernels' bounded waits give up after `polls` polls
+        (0 restores normal waits)."""
+        _check(lib().si_hip_debug_set_wait_give_up(self._h, polls))
 
     # ---- weights
     def upload_quant_weight_private(self, weight_bytes, ggml_type: int) -> QuantWeight:
