@@ -45,9 +45,12 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
                 copies: int = NCOPIES, seed: int = 17, detail: bool = False) -> dict:
     nbytes = rows * (cols // 256) * si_hip.BLOCK_BYTES[ggml_type]
     weights = []
+    host0 = None  # copy 0's host bytes, for the borrowed-bytes timing
     for c in range(copies):
         w = si_hip.synth_matrix(ggml_type, seed=seed + c, rows=rows, cols=cols, threads=16)
         weights.append(ctx.upload_quant_weight_private(w, ggml_type))
+        if c == 0 and detail:
+            host0 = w
         del w
     x = si_hip.synth_normal(seed, cols)
     d_x = ctx.device_alloc(cols * 4)
@@ -73,7 +76,7 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
     extra = {"graph_us_per_call": round(graph_ms * 1000.0, 3),
              "graph_gb_per_s": round(nbytes / (graph_ms * 1e-3) / 1e9, 1)}
     if detail:
-        extra.update(call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, steps))
+        extra.update(call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, steps, host0))
     ctx.device_free(d_x)
     ctx.device_free(d_y)
     for w in weights:
@@ -119,10 +122,13 @@ def time_graph_repeat(ctx, lib, harr, copies, rows, cols, d_x, d_y, steps: int,
     return ms / (reps * per_graph)
 
 
-def call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, samples: int) -> dict:
+def call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, samples: int,
+                host_bytes=None) -> dict:
     """Per-call device time of isolated calls (events around each call, the
     stream drained in between: p10/p50/p90), and host wall time per call of
-    the synchronous host-pointer API (x copied in, y copied out, one wait)."""
+    the synchronous host-pointer API (x copied in through pinned staging, y
+    copied out, one wait): on a retained weight, and on borrowed host bytes
+    (q4_k_matvec) once they are resident in HBM."""
     import ctypes as C
     per = []
     copies = len(weights)
@@ -144,14 +150,35 @@ def call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, samples: int) 
     for i in range(n_wall):
         ctx.gguf_quant_matvec_weight(weights[i % copies], rows, cols, x)
     wall = (time.perf_counter() - t0) / n_wall * 1e6
-    return {"isolated_call_us": {"p10": round(float(np.percentile(per, 10)), 3),
+    borrowed = {}
+    if host_bytes is not None and host_bytes.size * 2 <= si_hip.DEFAULT_RESIDENCY_BUDGET:
+        ctx.residency_evict()
+        s0 = ctx.residency_stats()
+        t0 = time.perf_counter()
+        ctx.q4_k_matvec(host_bytes, rows, cols, x)  # first call: the bytes go to HBM
+        first = (time.perf_counter() - t0) * 1e6
+        for _ in range(5):
+            ctx.q4_k_matvec(host_bytes, rows, cols, x)
+        t0 = time.perf_counter()
+        for _ in range(n_wall):
+            ctx.q4_k_matvec(host_bytes, rows, cols, x)
+        bw = (time.perf_counter() - t0) / n_wall * 1e6
+        s1 = ctx.residency_stats()
+        borrowed = {"borrowed_bytes_host_wall_us_per_call": round(bw, 2),
+                    "borrowed_bytes_first_call_us": round(first, 1),
+                    "borrowed_bytes_note": (
+                        f"q4_k_matvec on host bytes: {s1['uploads'] - s0['uploads']} weight "
+                        f"copy to HBM over {n_wall + 6} calls, {s1['hits'] - s0['hits']} "
+                        "resident hits")}
+        ctx.residency_evict()
+    return {**borrowed, "isolated_call_us": {"p10": round(float(np.percentile(per, 10)), 3),
                                  "p50": round(float(np.percentile(per, 50)), 3),
                                  "p90": round(float(np.percentile(per, 90)), 3),
                                  "samples": samples},
             "host_wall_us_per_call": round(wall, 2),
-            "host_wall_note": "synchronous C-ABI call with host x and y (H2D copy of x, "
-                              "kernel, D2H copy of y, stream wait), averaged over "
-                              f"{n_wall} calls"}
+            "host_wall_note": "synchronous C-ABI call on a retained weight with host x and "
+                              "y (x through pinned staging, kernel, y back, stream wait), "
+                              f"averaged over {n_wall} calls"}
 
 
 def _timed(ctx, fn, steps: int, warmup: int) -> float:
@@ -176,6 +203,7 @@ def _rate(nbytes: int, ms: float) -> dict:
 
 
 CONFIG_NAMES = ("mlp", "q5k", "head", "embedding", "many", "aggregate")
+DEFAULT_CONFIGS = ("mlp", "q5k", "head", "embedding", "many")  # the aggregate uploads 10 GB
 
 
 def run_configs(ctx, steps: int, warmup: int, only=CONFIG_NAMES) -> dict:
@@ -440,9 +468,12 @@ def main() -> int:
     ap.add_argument("--sweep", action="store_true", help="also time the batch-1 shape sweep")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--configs", nargs="?", const=",".join(CONFIG_NAMES), default=None,
-                    help="also time BASELINE configs 3-5: a comma list of "
-                         f"{','.join(CONFIG_NAMES)} (default: all)")
+    ap.add_argument("--configs", nargs="?", const=",".join(CONFIG_NAMES),
+                    default=",".join(DEFAULT_CONFIGS),
+                    help="BASELINE configs 3-5 timed after the headline: a comma list of "
+                         f"{','.join(CONFIG_NAMES)} (default: {','.join(DEFAULT_CONFIGS)}; "
+                         "the flag alone: all)")
+    ap.add_argument("--no-configs", action="store_true", help="time the headline only")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time device-to-device copies of the matrix size (the yardstick "
                          "that scales HBM traffic counters)")
@@ -470,7 +501,10 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k weights (u8 packed) x f32 activations, f32 accumulate",
+        "dtype": ("q4_k weights (u8 packed; 4-bit quants, 6-bit scales) x activations as "
+                  "block fixed point (per 256-element block: an exponent and 30-bit integers "
+                  "in four int8 digits; tiny or non-finite elements exact in f32), int8 MFMA "
+                  "with int32 accumulate, f32 combine of block sums"),
         "data": "synthetic (seeded generator, BASELINE.json config 2)",
         "config": {"workload": "Q4_K matvec N=17408 x K=5120, batch 1", "rows": rows,
                    "cols": cols, "batch": 1, "weight_copies": NCOPIES,
@@ -484,6 +518,10 @@ def main() -> int:
         "host_wall_us_per_call": head["host_wall_us_per_call"],
         "host_wall_note": head["host_wall_note"],
     }
+    for k in ("borrowed_bytes_host_wall_us_per_call", "borrowed_bytes_first_call_us",
+              "borrowed_bytes_note"):
+        if k in head:
+            out[k] = head[k]
     if args.copy_probe:
         nbytes = head["bytes_per_call"]
         src, dst = ctx.device_alloc(nbytes), ctx.device_alloc(nbytes)
@@ -509,13 +547,17 @@ def main() -> int:
             log(f"  sweep {r}x{c}: {res['us_per_call']} us, {res['gb_per_s']} GB/s")
             sweep.append(res)
         out["sweep"] = sweep
-    if args.configs:
+    if args.configs and not args.no_configs:
         only = tuple(c for c in args.configs.split(",") if c)
         bad = [c for c in only if c not in CONFIG_NAMES]
         if bad:
             print(f"unknown config(s) {bad}; choose from {CONFIG_NAMES}", file=sys.stderr)
             return 2
         out["configs"] = run_configs(ctx, args.steps, args.warmup, only)
+        # config 1: the matrix the reference's CPU path is quoted on
+        c1 = time_matvec(ctx, 12, 4096, 5120, args.steps, args.warmup)
+        out["configs"]["q4k_matvec_4096x5120"] = {k: c1[k] for k in (
+            "bytes_per_call", "us_per_call", "gb_per_s", "frac_of_peak")}
     ctx.close()
     if not args.no_cpu:
         log("timing the CPU baseline")
@@ -525,6 +567,8 @@ def main() -> int:
                     os.cpu_count() or 1, 64)
         log(f"timing the CPU baseline on {cores} threads")
         out["cpu_baseline_all_cores"] = cpu_baseline(rows, cols, args.cpu_seconds, threads=cores)
+        log("timing the CPU baseline at config 1 (4096x5120)")
+        out["cpu_baseline_config1"] = cpu_baseline(4096, 5120, args.cpu_seconds / 2)
     print(json.dumps(out), flush=True)
     return 0
 

@@ -203,7 +203,9 @@ int si_hip_gguf_quant_matmul_many_weight(si_hip_context *ctx, const si_hip_quant
 /* Qwen35Runtime::logits' head matvec (qwen35_runtime.rs:2132-2192) followed
  * by argmax (runtime.rs:4301-4309, or the first-wins rule of
  * qwen35_runtime.rs:2237-2244), on the device; only the token id (and,
- * when logits is non-NULL, the logits) come back. */
+ * when logits is non-NULL, the logits) come back.  A Q6_K head runs as one
+ * launch with the argmax fused into the matvec (which then stores no logits
+ * when logits is NULL). */
 int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_quant_weight *head,
                                            size_t rows, size_t columns, const float *input,
                                            size_t input_len, uint32_t rule, uint32_t *token,
@@ -338,6 +340,39 @@ void si_hip_reset_peaks(si_hip_context *ctx);
 /* sample_allocated (metal.rs:2374-2378): peak = max(peak, current). */
 void si_hip_sample_allocated(si_hip_context *ctx);
 int si_hip_get_command_stats(const si_hip_context *ctx, si_hip_command_stats *out);
+
+/* ---- residency of borrowed weight bytes -----------------------------------
+ * The reference's byte-slice entry points (q4_k_matvec / q5_k / q6_k,
+ * gguf_quant_matvec_bytes, gguf_quant_matvec_many_bytes, q4_k_fused_gate_up,
+ * gguf_quant_matmul_many_bytes, f32_matvec_bytes / f32_matvec_many; metal.rs
+ * 3357-4100, 4652-4775) bind the caller's host bytes to the GPU without a
+ * copy (unified memory, new_buffer_with_bytes_no_copy).  MI355X executes from
+ * HBM, so a context keeps an HBM copy of each borrowed byte range, keyed by
+ * (host address, length), and evicts the least recently used ranges beyond a
+ * byte budget; the GGUF store's tensor calls borrow the mapped file this way.
+ * A resident range is copied again when its fingerprint changes: the length
+ * and 64 windows of 64 bytes spread evenly over the range.  Bytes changed in
+ * place outside those windows go unseen: after changing borrowed bytes in
+ * place, call si_hip_residency_evict.  Resident bytes count as allocated
+ * device memory (si_hip_current_allocated_bytes).  No counterpart in the
+ * reference. */
+#define SI_HIP_DEFAULT_RESIDENCY_BUDGET (16ull << 30)
+typedef struct si_hip_residency_stats {
+  uint64_t hits;            /* ranges found resident and unchanged */
+  uint64_t uploads;         /* ranges copied: first use, changed, or not kept */
+  uint64_t uploaded_bytes;  /* bytes of those copies */
+  uint64_t evictions;
+  uint64_t resident_ranges;
+  uint64_t resident_bytes;
+  uint64_t budget_bytes;
+} si_hip_residency_stats;
+/* 0 turns residency off (every call copies its bytes); a smaller budget
+ * evicts at once. */
+int si_hip_set_residency_budget(si_hip_context *ctx, uint64_t bytes);
+/* Drops every resident range that overlaps [host_bytes, host_bytes + len)
+ * (len 0: every range). */
+int si_hip_residency_evict(si_hip_context *ctx, const void *host_bytes, size_t len);
+int si_hip_get_residency_stats(si_hip_context *ctx, si_hip_residency_stats *out);
 
 #ifdef __cplusplus
 }

@@ -16,12 +16,14 @@
 #include <cmath>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <memory>
 #include <mutex>
 #include <string>
 #include <vector>
 
 #include "si_hip_internal.h"
+#include "si_hip_shared.h"
 #include "si_hip_tuned.h"
 
 namespace {
@@ -142,6 +144,35 @@ struct DeviceBuffer {
   }
 };
 
+// Pinned host memory that the synchronous host-pointer calls stage their
+// inputs and outputs through (a bump region per call).
+struct PinnedStage {
+  uint8_t *ptr = nullptr;
+  size_t cap = 0;
+  size_t used = 0;
+};
+// An output copy waiting for its call's synchronisation: `bytes` from the
+// pinned staging at `src` to the caller's `dst`.
+struct PendingOut {
+  void *dst;
+  const void *src;
+  size_t bytes;
+};
+
+// HBM copies of borrowed host byte ranges, keyed by (host address, length).
+struct Resident {
+  std::shared_ptr<DeviceBuffer> buf;
+  uint64_t fingerprint = 0;
+  uint64_t used = 0;  // the call that last used it
+};
+struct Residency {
+  std::map<std::pair<uintptr_t, size_t>, Resident> ranges;
+  uint64_t budget = SI_HIP_DEFAULT_RESIDENCY_BUDGET;
+  uint64_t bytes = 0;
+  uint64_t tick = 0;
+  si_hip_residency_stats stats{};
+};
+
 }  // namespace
 
 struct si_hip_context {
@@ -167,6 +198,13 @@ struct si_hip_context {
   volatile uint32_t *dev_error = nullptr;
   uint64_t dev_error_addr = 0;
   uint32_t give_up_polls = 0;
+  // pinned staging of the synchronous calls' inputs and outputs; buffers
+  // outgrown during a call are freed after its synchronisation
+  PinnedStage pin_in, pin_out;
+  std::vector<PendingOut> pending;
+  std::vector<void *> pin_retired;
+  // borrowed weight bytes kept resident in HBM
+  Residency res;
   hipEvent_t events[16] = {};
   // graph capture: while `capturing`, the *_device calls go to capture_stream,
   // where HIP records them instead of running them
@@ -226,6 +264,83 @@ int grow(si_hip_context *ctx, void **buf, size_t *cap, size_t need) {
   return SI_HIP_OK;
 }
 
+// ---- pinned staging of host inputs and outputs ---------------------------------
+// Pageable host memory is copied through the runtime's own bounce buffers,
+// several times slower than DMA from pinned memory: the synchronous calls
+// copy their inputs into the context's pinned staging and read their outputs
+// from it after the wait.  Large transfers go direct.
+constexpr size_t kPinnedMaxCopy = size_t(16) << 20;
+
+uint8_t *pin_take(si_hip_context *ctx, PinnedStage &st, size_t bytes) {
+  const size_t chunk = (bytes + 255) & ~size_t(255);
+  if (st.used + chunk > st.cap) {
+    const size_t cap = std::max({st.used + chunk, 2 * st.cap, size_t(1) << 20});
+    void *p = nullptr;
+    if (hipHostMalloc(&p, cap, hipHostMallocDefault) != hipSuccess) return nullptr;
+    // chunks already handed out in this call stay valid until its wait
+    if (st.ptr) ctx->pin_retired.push_back(st.ptr);
+    st.ptr = static_cast<uint8_t *>(p);
+    st.cap = cap;
+    st.used = 0;
+  }
+  uint8_t *r = st.ptr + st.used;
+  st.used += chunk;
+  return r;
+}
+
+hipError_t copy_in(si_hip_context *ctx, void *dev, const void *host, size_t bytes) {
+  if (bytes == 0) return hipSuccess;
+  if (bytes <= kPinnedMaxCopy) {
+    uint8_t *p = pin_take(ctx, ctx->pin_in, bytes);
+    if (!p) return hipErrorOutOfMemory;
+    std::memcpy(p, host, bytes);
+    return hipMemcpyAsync(dev, p, bytes, hipMemcpyHostToDevice, ctx->stream);
+  }
+  return hipMemcpyAsync(dev, host, bytes, hipMemcpyHostToDevice, ctx->stream);
+}
+
+hipError_t copy_out(si_hip_context *ctx, void *host, const void *dev, size_t bytes) {
+  if (bytes == 0) return hipSuccess;
+  if (bytes <= kPinnedMaxCopy) {
+    uint8_t *p = pin_take(ctx, ctx->pin_out, bytes);
+    if (!p) return hipErrorOutOfMemory;
+    ctx->pending.push_back({host, p, bytes});
+    return hipMemcpyAsync(p, dev, bytes, hipMemcpyDeviceToHost, ctx->stream);
+  }
+  return hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, ctx->stream);
+}
+
+// After the stream has drained: outputs to the caller, staging reset.
+void finish_staging(si_hip_context *ctx, bool deliver) {
+  if (deliver)
+    for (const PendingOut &o : ctx->pending) std::memcpy(o.dst, o.src, o.bytes);
+  ctx->pending.clear();
+  ctx->pin_in.used = ctx->pin_out.used = 0;
+  for (void *p : ctx->pin_retired) (void)hipHostFree(p);
+  ctx->pin_retired.clear();
+}
+
+// The context's lock for one call.  A synchronous call that returns before
+// its wait (an error after some copies were enqueued) leaves staging in use:
+// the scope then drains the stream and drops the undelivered outputs.
+class CallScope {
+ public:
+  explicit CallScope(si_hip_context *ctx) : ctx_(ctx), lock_(ctx->mu) {}
+  ~CallScope() {
+    if (!ctx_->pending.empty() || ctx_->pin_in.used || ctx_->pin_out.used ||
+        !ctx_->pin_retired.empty()) {
+      (void)hipStreamSynchronize(ctx_->stream);
+      finish_staging(ctx_, false);
+    }
+  }
+  CallScope(const CallScope &) = delete;
+  CallScope &operator=(const CallScope &) = delete;
+
+ private:
+  si_hip_context *ctx_;
+  std::lock_guard<std::mutex> lock_;
+};
+
 // The workspace's rest state on the context's stream, waited for: counters
 // zero, entries empty, then the reserved words (the error word's address and
 // the test hook's poll count).
@@ -279,7 +394,11 @@ int wait_stream(si_hip_context *ctx, const char *what) {
   ctx->waited.fetch_add(1);
   ctx->wait_nanos.fetch_add(
       (uint64_t)std::chrono::duration_cast<std::chrono::nanoseconds>(t1 - t0).count());
-  if (e != hipSuccess) return fail(SI_HIP_ERR_DEVICE, "HIP %s failed: %s", what, hipGetErrorString(e));
+  if (e != hipSuccess) {
+    finish_staging(ctx, false);
+    return fail(SI_HIP_ERR_DEVICE, "HIP %s failed: %s", what, hipGetErrorString(e));
+  }
+  finish_staging(ctx, true);
   return check_device_error(ctx);
 }
 
@@ -380,27 +499,137 @@ int run_matvec_host(si_hip_context *ctx, uint32_t type, const uint8_t *dev_w, si
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, out_bytes);
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, input, in_bytes, hipMemcpyHostToDevice, ctx->stream),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, input, in_bytes),
               "input copy");
   rc = dispatch_matvec(ctx, type, dev_w, static_cast<const float *>(ctx->stage_in),
                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)columns,
                        (uint32_t)batch, ctx->stream);
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(output, ctx->stage_out, out_bytes, hipMemcpyDeviceToHost, ctx->stream),
+  SIHIP_CHECK(copy_out(ctx, output, ctx->stage_out, out_bytes),
               "output copy");
   rc = wait_stream(ctx, what);
   if (rc) return rc;
   return ok();
 }
 
-// Per-call upload of host bytes (the mapped/no-copy path of the reference).
-int stage_weights(si_hip_context *ctx, const uint8_t *bytes, size_t len, const uint8_t **dev) {
-  int rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, len);
-  if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_weights, bytes, len, hipMemcpyHostToDevice, ctx->stream),
-              "weight copy");
-  *dev = static_cast<const uint8_t *>(ctx->stage_weights);
+// ---- borrowed weight bytes ----------------------------------------------------
+// Length and 64 evenly spread 64-byte windows, mixed (a change detector for
+// resident ranges, not a content hash).
+uint64_t fingerprint(const uint8_t *p, size_t len) {
+  auto mix = [](uint64_t h) {
+    h ^= h >> 33;
+    h *= 0xff51afd7ed558ccdull;
+    h ^= h >> 33;
+    h *= 0xc4ceb9fe1a85ec53ull;
+    return h ^ (h >> 33);
+  };
+  uint64_t h = mix(0x9e3779b97f4a7c15ull ^ len);
+  constexpr size_t kWin = 64, kWindows = 64;
+  if (len <= kWin * kWindows) {
+    for (size_t i = 0; i < len; i += 8) {
+      uint64_t v = 0;
+      std::memcpy(&v, p + i, std::min<size_t>(8, len - i));
+      h = mix(h ^ v);
+    }
+    return h;
+  }
+  for (size_t w = 0; w < kWindows; ++w) {
+    const size_t off = (len - kWin) / (kWindows - 1) * w;
+    for (size_t i = 0; i < kWin; i += 8) {
+      uint64_t v;
+      std::memcpy(&v, p + off + i, 8);
+      h = mix(h ^ v);
+    }
+  }
+  return h;
+}
+
+void evict_range(si_hip_context *ctx, std::map<std::pair<uintptr_t, size_t>, Resident>::iterator it) {
+  ctx->res.bytes -= it->first.second;
+  ctx->res.stats.evictions += 1;
+  ctx->res.ranges.erase(it);  // the last reference frees the HBM copy
+}
+
+// HBM addresses of n borrowed host byte ranges for one call, enqueued on the
+// context's stream: resident copies (copied again when changed), new ones
+// under the budget, or -- residency off or the call's ranges over the budget
+// -- one staging copy per call.
+int borrow_weights(si_hip_context *ctx, size_t n, const uint8_t *const *ptrs, const size_t *lens,
+                   const uint8_t **devs, bool keep = true) {
+  Residency &R = ctx->res;
+  uint64_t total = 0;
+  for (size_t i = 0; i < n; ++i) total += lens[i];
+  if (!keep || R.budget == 0 || total > R.budget) {
+    size_t staged = 0;
+    for (size_t i = 0; i < n; ++i) staged += (lens[i] + 255) & ~size_t(255);
+    int rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, staged);
+    if (rc) return rc;
+    size_t off = 0;
+    for (size_t i = 0; i < n; ++i) {
+      uint8_t *d = static_cast<uint8_t *>(ctx->stage_weights) + off;
+      SIHIP_CHECK(hipMemcpyAsync(d, ptrs[i], lens[i], hipMemcpyHostToDevice, ctx->stream),
+                  "weight copy");
+      devs[i] = d;
+      off += (lens[i] + 255) & ~size_t(255);
+      R.stats.uploads += 1;
+      R.stats.uploaded_bytes += lens[i];
+    }
+    return SI_HIP_OK;
+  }
+  const uint64_t now = ++R.tick;
+  for (size_t i = 0; i < n; ++i) {
+    const auto key = std::make_pair((uintptr_t)ptrs[i], lens[i]);
+    const uint64_t fp = fingerprint(ptrs[i], lens[i]);
+    auto it = R.ranges.find(key);
+    if (it != R.ranges.end()) {
+      Resident &r = it->second;
+      r.used = now;
+      if (r.fingerprint == fp) {
+        R.stats.hits += 1;
+      } else {
+        SIHIP_CHECK(hipMemcpyAsync(r.buf->ptr, ptrs[i], lens[i], hipMemcpyHostToDevice, ctx->stream),
+                    "weight copy");
+        r.fingerprint = fp;
+        R.stats.uploads += 1;
+        R.stats.uploaded_bytes += lens[i];
+      }
+      devs[i] = static_cast<const uint8_t *>(r.buf->ptr);
+      continue;
+    }
+    // room under the budget: the least recently used ranges this call does
+    // not use (the call's own ranges fit: total <= budget)
+    while (R.bytes + lens[i] > R.budget) {
+      auto victim = R.ranges.end();
+      for (auto j = R.ranges.begin(); j != R.ranges.end(); ++j)
+        if (j->second.used != now && (victim == R.ranges.end() || j->second.used < victim->second.used))
+          victim = j;
+      if (victim == R.ranges.end()) break;
+      evict_range(ctx, victim);
+    }
+    auto buf = std::make_shared<DeviceBuffer>();
+    if (hipMalloc(&buf->ptr, lens[i]) != hipSuccess) {
+      buf->ptr = nullptr;
+      return fail(SI_HIP_ERR_OUT_OF_MEMORY, "HIP could not allocate %zu bytes for borrowed weights",
+                  lens[i]);
+    }
+    buf->bytes = lens[i];
+    buf->tel = ctx->tel;
+    ctx->tel->note_alloc(lens[i]);
+    SIHIP_CHECK(hipMemcpyAsync(buf->ptr, ptrs[i], lens[i], hipMemcpyHostToDevice, ctx->stream),
+                "weight copy");
+    devs[i] = static_cast<const uint8_t *>(buf->ptr);
+    R.ranges.emplace(key, Resident{std::move(buf), fp, now});
+    R.bytes += lens[i];
+    R.stats.uploads += 1;
+    R.stats.uploaded_bytes += lens[i];
+  }
   return SI_HIP_OK;
+}
+
+// One borrowed range (keep = false: a per-call staging copy).
+int stage_weights(si_hip_context *ctx, const uint8_t *bytes, size_t len, const uint8_t **dev,
+                  bool keep = true) {
+  return borrow_weights(ctx, 1, &bytes, &len, dev, keep);
 }
 
 int typed_matvec(si_hip_context *ctx, uint32_t type, const uint8_t *weight_bytes,
@@ -411,7 +640,7 @@ int typed_matvec(si_hip_context *ctx, uint32_t type, const uint8_t *weight_bytes
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!weight_bytes || !input || !output) return fail(SI_HIP_ERR_NULL, "%s matvec buffer is null", label);
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   const uint8_t *dev_w = nullptr;
   rc = stage_weights(ctx, weight_bytes, weight_len, &dev_w);
   if (rc) return rc;
@@ -543,6 +772,10 @@ void si_hip_context_free(si_hip_context *ctx) {
   ctx->tel->note_free(ctx->stage_in_bytes + ctx->stage_out_bytes + ctx->stage_weights_bytes +
                       ctx->stage_aux_bytes + ctx->ws.bytes + ctx->ws.scratch_bytes);
   if (ctx->dev_error) (void)hipHostFree(const_cast<uint32_t *>(ctx->dev_error));
+  finish_staging(ctx, false);
+  for (PinnedStage *st : {&ctx->pin_in, &ctx->pin_out})
+    if (st->ptr) (void)hipHostFree(st->ptr);
+  ctx->res.ranges.clear();
   for (auto &ev : ctx->events)
     if (ev) (void)hipEventDestroy(ev);
   if (ctx->stream) (void)hipStreamDestroy(ctx->stream);
@@ -623,6 +856,36 @@ int si_hip_gguf_quant_matvec_bytes(si_hip_context *ctx, uint32_t type, const uin
   return typed_matvec(ctx, type, wb, wl, rows, cols, in, in_len, out);
 }
 
+}  // extern "C"
+
+int sihip::quant_matvec_tensor_range(si_hip_context *ctx, uint32_t type, const uint8_t *tensor,
+                                     size_t tensor_len, size_t offset, size_t len, size_t rows,
+                                     size_t cols, const float *in, size_t in_len, float *out) {
+  if (block_bytes_of(type) == 0)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "unsupported staged quantized weight type");
+  const char *label = type_label(type);
+  int rc = validate_matvec(type, len, rows, cols, in_len, label);
+  if (rc) return rc;
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!tensor || !in || !out) return fail(SI_HIP_ERR_NULL, "%s matvec buffer is null", label);
+  if (offset > tensor_len || len > tensor_len - offset)
+    return fail(SI_HIP_ERR_RANGE, "%s row range is invalid", label);
+  CallScope scope(ctx);
+  const uint8_t *dev = nullptr;
+  if (tensor_len <= ctx->res.budget) {
+    rc = stage_weights(ctx, tensor, tensor_len, &dev);
+    dev += offset;
+  } else {
+    rc = stage_weights(ctx, tensor + offset, len, &dev);
+  }
+  if (rc) return rc;
+  char what[64];
+  snprintf(what, sizeof what, "%s matvec command", label);
+  return run_matvec_host(ctx, type, dev, rows, cols, 1, in, out, what);
+}
+
+extern "C" {
+
 int si_hip_gguf_quant_matvec_many_bytes(si_hip_context *ctx, const uint32_t *types,
                                         const uint8_t *const *bytes, const size_t *lens,
                                         const size_t *rows, const size_t *columns, size_t count,
@@ -635,8 +898,6 @@ int si_hip_gguf_quant_matvec_many_bytes(si_hip_context *ctx, const uint32_t *typ
   const size_t cols = columns[0];
   if (cols == 0 || in_len != cols)
     return fail(SI_HIP_ERR_DIMENSIONS, "staged quantized matvec group input length is invalid");
-  size_t staged = 0;
-  std::vector<size_t> offs(count);
   for (size_t i = 0; i < count; ++i) {
     if (rows[i] == 0 || columns[i] != cols || cols % 256 != 0)
       return fail(SI_HIP_ERR_DIMENSIONS, "staged quantized matvec group shapes differ");
@@ -647,8 +908,6 @@ int si_hip_gguf_quant_matvec_many_bytes(si_hip_context *ctx, const uint32_t *typ
       return fail(SI_HIP_ERR_OVERFLOW, "staged quantized matvec group byte length overflows");
     if (expected != lens[i])
       return fail(SI_HIP_ERR_BYTE_LENGTH, "staged quantized matvec tensor byte length is invalid");
-    offs[i] = staged;
-    staged += (lens[i] + 255) & ~(size_t)255;  // each matrix 256-byte aligned in the staging buffer
   }
   if (cols > UINT32_MAX)
     return fail(SI_HIP_ERR_OVERFLOW, "staged grouped quantized columns exceed HIP limits");
@@ -663,21 +922,15 @@ int si_hip_gguf_quant_matvec_many_bytes(si_hip_context *ctx, const uint32_t *typ
   for (size_t i = 0; i < count; ++i)
     if (!bytes[i] || !outputs[i])
       return fail(SI_HIP_ERR_NULL, "staged grouped matvec buffer %zu is null", i);
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  int rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, staged);
+  CallScope scope(ctx);
+  std::vector<const uint8_t *> dev(count);
+  int rc = borrow_weights(ctx, count, bytes, lens, dev.data());
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, total_rows * sizeof(float));
   if (rc) return rc;
-  std::vector<const uint8_t *> dev(count);
-  for (size_t i = 0; i < count; ++i) {
-    uint8_t *d = static_cast<uint8_t *>(ctx->stage_weights) + offs[i];
-    SIHIP_CHECK(hipMemcpyAsync(d, bytes[i], lens[i], hipMemcpyHostToDevice, ctx->stream),
-                "weight copy");
-    dev[i] = d;
-  }
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
   float *dst = static_cast<float *>(ctx->stage_out);
   rc = dispatch_matvec_group(ctx, types, dev.data(), rows, count,
@@ -686,8 +939,7 @@ int si_hip_gguf_quant_matvec_many_bytes(si_hip_context *ctx, const uint32_t *typ
   if (rc) return rc;
   size_t off = 0;
   for (size_t i = 0; i < count; ++i) {
-    SIHIP_CHECK(hipMemcpyAsync(outputs[i], dst + off, rows[i] * sizeof(float), hipMemcpyDeviceToHost,
-                               ctx->stream),
+    SIHIP_CHECK(copy_out(ctx, outputs[i], dst + off, rows[i] * sizeof(float)),
                 "output copy");
     off += rows[i];
   }
@@ -714,7 +966,7 @@ int si_hip_gguf_quant_matvec_weight(si_hip_context *ctx, const si_hip_quant_weig
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!in || !out) return fail(SI_HIP_ERR_NULL, "%s matvec buffer is null", label);
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   char what[64];
   snprintf(what, sizeof what, "%s retained matvec command", label);
   return run_matvec_host(ctx, w->ggml_type, w->data(), rows, cols, 1, in, out, what);
@@ -747,7 +999,7 @@ int si_hip_gguf_quant_matvec_tensor_rows(si_hip_context *ctx, const si_hip_quant
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!in || !out) return fail(SI_HIP_ERR_NULL, "%s matvec buffer is null", label);
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   char what[64];
   snprintf(what, sizeof what, "%s matvec command", label);
   return run_matvec_host(ctx, t->ggml_type, t->data() + byte_start, row_count, shape_cols, 1, in,
@@ -782,12 +1034,12 @@ int si_hip_gguf_quant_matvec_many_weights(si_hip_context *ctx,
   }
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!in) return fail(SI_HIP_ERR_NULL, "grouped matvec input is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   int rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, total_rows * sizeof(float));
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
   float *dst = static_cast<float *>(ctx->stage_out);
   rc = dispatch_weight_group(ctx, weights, rows, count, static_cast<const float *>(ctx->stage_in),
@@ -795,8 +1047,7 @@ int si_hip_gguf_quant_matvec_many_weights(si_hip_context *ctx,
   if (rc) return rc;
   size_t off = 0;
   for (size_t i = 0; i < count; ++i) {
-    SIHIP_CHECK(hipMemcpyAsync(outputs[i], dst + off, rows[i] * sizeof(float), hipMemcpyDeviceToHost,
-                               ctx->stream),
+    SIHIP_CHECK(copy_out(ctx, outputs[i], dst + off, rows[i] * sizeof(float)),
                 "output copy");
     off += rows[i];
   }
@@ -822,22 +1073,22 @@ int si_hip_q4_k_fused_gate_up(si_hip_context *ctx, const uint8_t *gate, size_t g
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!gate || !up || !in || !out) return fail(SI_HIP_ERR_NULL, "Q4_K fused gate/up buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, 2 * expected);
+  CallScope scope(ctx);
+  const uint8_t *const borrowed[2] = {gate, up};
+  const size_t blens[2] = {expected, expected};
+  const uint8_t *dgu[2] = {nullptr, nullptr};
+  rc = borrow_weights(ctx, 2, borrowed, blens, dgu);
   if (rc) return rc;
-  uint8_t *dw = static_cast<uint8_t *>(ctx->stage_weights);
-  SIHIP_CHECK(hipMemcpyAsync(dw, gate, expected, hipMemcpyHostToDevice, ctx->stream), "gate copy");
-  SIHIP_CHECK(hipMemcpyAsync(dw + expected, up, expected, hipMemcpyHostToDevice, ctx->stream), "up copy");
   rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, rows * sizeof(float));
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
-  rc = dispatch_gate_up(ctx, dw, dw + expected, static_cast<const float *>(ctx->stage_in),
+  rc = dispatch_gate_up(ctx, dgu[0], dgu[1], static_cast<const float *>(ctx->stage_in),
                         static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, rows * sizeof(float)),
               "output copy");
   rc = wait_stream(ctx, "Q4_K fused gate/up command");
   if (rc) return rc;
@@ -870,17 +1121,17 @@ int si_hip_q4_k_fused_gate_up_weights(si_hip_context *ctx, const si_hip_quant_we
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!in || !out) return fail(SI_HIP_ERR_NULL, "Q4_K fused gate/up buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, rows * sizeof(float));
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
   rc = dispatch_gate_up(ctx, g->data(), u->data(), static_cast<const float *>(ctx->stage_in),
                         static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, rows * sizeof(float)),
               "output copy");
   rc = wait_stream(ctx, "retained Q4_K fused gate/up command");
   if (rc) return rc;
@@ -924,14 +1175,14 @@ int si_hip_gguf_quant_fused_mlp_weights(si_hip_context *ctx, const si_hip_quant_
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!in || !out) return fail(SI_HIP_ERR_NULL, "fused MLP buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_aux, &ctx->stage_aux_bytes, gate_rows * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, down_rows * sizeof(float));
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
   float *hidden = static_cast<float *>(ctx->stage_aux);
   rc = dispatch_gate_up(ctx, g->data(), u->data(), static_cast<const float *>(ctx->stage_in), hidden,
@@ -940,8 +1191,7 @@ int si_hip_gguf_quant_fused_mlp_weights(si_hip_context *ctx, const si_hip_quant_
   rc = dispatch_matvec(ctx, d->ggml_type, d->data(), hidden, static_cast<float *>(ctx->stage_out),
                        (uint32_t)down_rows, (uint32_t)gate_rows, 1, ctx->stream);
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, down_rows * sizeof(float), hipMemcpyDeviceToHost,
-                             ctx->stream),
+  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, down_rows * sizeof(float)),
               "output copy");
   char what[64];
   snprintf(what, sizeof what, "fused MLP %s command", type_label(d->ggml_type));
@@ -958,16 +1208,16 @@ int si_hip_q4_k_embedding_row(si_hip_context *ctx, const uint8_t *row, size_t ro
   if (cols > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "embedding dimension exceeds HIP limits");
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!row || !out) return fail(SI_HIP_ERR_NULL, "Q4_K embedding buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   const uint8_t *dev = nullptr;
-  int rc = stage_weights(ctx, row, row_len, &dev);
+  int rc = stage_weights(ctx, row, row_len, &dev, false);
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, cols * sizeof(float));
   if (rc) return rc;
   hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, dev, nullptr,
                                        static_cast<float *>(ctx->stage_out), 1, (uint32_t)cols, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
-  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, cols * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, cols * sizeof(float)),
               "output copy");
   rc = wait_stream(ctx, "Q4_K embedding command");
   if (rc) return rc;
@@ -1016,20 +1266,19 @@ int si_hip_q4_k_embedding_tokens(si_hip_context *ctx, const si_hip_quant_weight 
   if (n > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "too many token ids");
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!out) return fail(SI_HIP_ERR_NULL, "Q4_K embedding output is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   int rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, n * sizeof(uint32_t));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, n * cols * sizeof(float));
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, ids, n * sizeof(uint32_t), hipMemcpyHostToDevice, ctx->stream),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, ids, n * sizeof(uint32_t)),
               "token id copy");
   hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, t->data(),
                                        static_cast<const uint32_t *>(ctx->stage_in),
                                        static_cast<float *>(ctx->stage_out), (uint32_t)n, (uint32_t)cols,
                                        ctx->stream, embedding_table_rows(t, cols, rows), ctx->ws.ptr);
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
-  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, n * cols * sizeof(float), hipMemcpyDeviceToHost,
-                             ctx->stream),
+  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, n * cols * sizeof(float)),
               "output copy");
   rc = wait_stream(ctx, "Q4_K embedding command");
   if (rc) return rc;
@@ -1081,7 +1330,7 @@ int si_hip_gguf_quant_matmul_many_bytes(si_hip_context *ctx, uint32_t type, cons
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!wb || !inputs || !outputs) return fail(SI_HIP_ERR_NULL, "batched matvec buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   const uint8_t *dev_w = nullptr;
   rc = stage_weights(ctx, wb, wl, &dev_w);
   if (rc) return rc;
@@ -1098,7 +1347,7 @@ int si_hip_gguf_quant_matmul_many_weight(si_hip_context *ctx, const si_hip_quant
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!inputs || !outputs) return fail(SI_HIP_ERR_NULL, "batched matvec buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   return run_matvec_host(ctx, w->ggml_type, w->data(), rows, cols, batch, inputs, outputs,
                          "retained batched quantized matvec command");
 }
@@ -1126,15 +1375,15 @@ int validate_head(const si_hip_quant_weight *w, size_t rows, size_t cols, size_t
   return check_u32(rows, cols, label);
 }
 // The head's logits and greedy argmax on `stream`: the Q6_K matrix-core
-// kernel with the argmax fused into it, else the matvec, then the argmax
-// kernel.
+// kernel with the argmax fused into it (storing the logits only when
+// `logits_wanted`), else the matvec into d_logits, then the argmax kernel.
 int dispatch_head(si_hip_context *ctx, const si_hip_quant_weight *w, const float *d_in,
-                  float *d_logits, uint32_t rows, uint32_t cols, uint32_t rule, uint64_t *d_result,
-                  hipStream_t stream) {
+                  float *d_logits, bool logits_wanted, uint32_t rows, uint32_t cols,
+                  uint32_t rule, uint64_t *d_result, hipStream_t stream) {
   hipError_t e = hipErrorInvalidValue;
   if (ctx->policy == SI_HIP_KERNEL_AUTO && w->ggml_type == SI_HIP_GGML_TYPE_Q6_K &&
-      sihip::launch_q6k_matvec_argmax_mfma(w->data(), d_in, d_logits, rows, cols, rule, d_result,
-                                           ctx->ws, stream, &e)) {
+      sihip::launch_q6k_matvec_argmax_mfma(w->data(), d_in, logits_wanted ? d_logits : nullptr,
+                                           rows, cols, rule, d_result, ctx->ws, stream, &e)) {
     if (e != hipSuccess) return hip_fail(e, "output head launch");
     return SI_HIP_OK;
   }
@@ -1153,24 +1402,24 @@ int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_qua
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!in || !token) return fail(SI_HIP_ERR_NULL, "output head buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, rows * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_aux, &ctx->stage_aux_bytes, sizeof(uint64_t));
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, in, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
   float *d_logits = static_cast<float *>(ctx->stage_out);
   uint64_t *aux = static_cast<uint64_t *>(ctx->stage_aux);
-  rc = dispatch_head(ctx, w, static_cast<const float *>(ctx->stage_in), d_logits, (uint32_t)rows,
-                     (uint32_t)cols, rule, aux, ctx->stream);
+  rc = dispatch_head(ctx, w, static_cast<const float *>(ctx->stage_in), d_logits, logits != nullptr,
+                     (uint32_t)rows, (uint32_t)cols, rule, aux, ctx->stream);
   if (rc) return rc;
   uint64_t packed = 0;
-  SIHIP_CHECK(hipMemcpyAsync(&packed, aux, sizeof packed, hipMemcpyDeviceToHost, ctx->stream), "argmax copy");
+  SIHIP_CHECK(copy_out(ctx, &packed, aux, sizeof packed), "argmax copy");
   if (logits)
-    SIHIP_CHECK(hipMemcpyAsync(logits, d_logits, rows * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+    SIHIP_CHECK(copy_out(ctx, logits, d_logits, rows * sizeof(float)),
                 "logits copy");
   rc = wait_stream(ctx, "output head argmax command");
   if (rc) return rc;
@@ -1202,20 +1451,20 @@ int run_f32_matvec_host(si_hip_context *ctx, const float *w, size_t rows, size_t
                         const float *x, float *y) {
   const size_t wb = rows * cols * sizeof(float);
   const size_t xb = cols * sizeof(float), yb = rows * sizeof(float);
-  int rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, wb);
+  const uint8_t *dw = nullptr;
+  int rc = stage_weights(ctx, reinterpret_cast<const uint8_t *>(w), wb, &dw);
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, xb);
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, yb);
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_weights, w, wb, hipMemcpyHostToDevice, ctx->stream), "weight copy");
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, x, xb, hipMemcpyHostToDevice, ctx->stream), "input copy");
-  hipError_t e = sihip::launch_f32_matvec(static_cast<const float *>(ctx->stage_weights),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, x, xb), "input copy");
+  hipError_t e = sihip::launch_f32_matvec(reinterpret_cast<const float *>(dw),
                                           static_cast<const float *>(ctx->stage_in),
                                           static_cast<float *>(ctx->stage_out), (uint32_t)rows,
                                           (uint32_t)cols, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "F32 matvec launch");
-  SIHIP_CHECK(hipMemcpyAsync(y, ctx->stage_out, yb, hipMemcpyDeviceToHost, ctx->stream), "output copy");
+  SIHIP_CHECK(copy_out(ctx, y, ctx->stage_out, yb), "output copy");
   rc = wait_stream(ctx, "F32 matvec command");
   if (rc) return rc;
   return ok();
@@ -1253,14 +1502,14 @@ int run_rms_host(si_hip_context *ctx, uint32_t mode, const float *x, const float
   if (rc) return rc;
   float *dx = static_cast<float *>(ctx->stage_in);
   float *dg = mode == 2 ? dx + n : nullptr;
-  SIHIP_CHECK(hipMemcpyAsync(dx, x, xb, hipMemcpyHostToDevice, ctx->stream), "input copy");
-  if (dg) SIHIP_CHECK(hipMemcpyAsync(dg, gate, xb, hipMemcpyHostToDevice, ctx->stream), "gate copy");
+  SIHIP_CHECK(copy_in(ctx, dx, x, xb), "input copy");
+  if (dg) SIHIP_CHECK(copy_in(ctx, dg, gate, xb), "gate copy");
   SIHIP_CHECK(hipMemcpyAsync(ctx->stage_aux, w, wb, hipMemcpyHostToDevice, ctx->stream), "weight copy");
   hipError_t e = sihip::launch_rms_norm(mode, dx, dg, static_cast<const float *>(ctx->stage_aux),
                                         static_cast<float *>(ctx->stage_out), (uint32_t)heads,
                                         (uint32_t)head_dim, eps, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "RMSNorm launch");
-  SIHIP_CHECK(hipMemcpyAsync(y, ctx->stage_out, xb, hipMemcpyDeviceToHost, ctx->stream), "output copy");
+  SIHIP_CHECK(copy_out(ctx, y, ctx->stage_out, xb), "output copy");
   rc = wait_stream(ctx, "RMSNorm command");
   if (rc) return rc;
   return ok();
@@ -1273,7 +1522,7 @@ int si_hip_f32_matvec(si_hip_context *ctx, const float *w, size_t values, size_t
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!w || !x || !y) return fail(SI_HIP_ERR_NULL, "F32 matvec buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   return run_f32_matvec_host(ctx, w, rows, cols, x, y);
 }
 
@@ -1295,7 +1544,7 @@ int si_hip_f32_matvec_device(si_hip_context *ctx, const float *d_w, size_t rows,
   int rc = validate_f32_matvec(rows * cols, rows, cols, cols);
   if (rc) return rc;
   if (!ctx || !d_w || !d_x || !d_y) return fail(SI_HIP_ERR_NULL, "device F32 matvec argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   hipError_t e = sihip::launch_f32_matvec(d_w, d_x, d_y, (uint32_t)rows, (uint32_t)cols,
                                           device_stream(ctx));
   if (e != hipSuccess) return hip_fail(e, "F32 matvec launch");
@@ -1310,36 +1559,38 @@ int si_hip_f32_matvec_many(si_hip_context *ctx, const float *const *ws, const si
   // f32_matvec_many_gguf_tensors, metal.rs:4780-4870)
   if (count == 0) return fail(SI_HIP_ERR_EMPTY, "F32 matvec group requires at least one matrix");
   if (!ws || !rows || !ys) return fail(SI_HIP_ERR_NULL, "F32 matvec group argument is null");
-  size_t wtotal = 0, ytotal = 0;
+  size_t ytotal = 0;
   for (size_t i = 0; i < count; ++i) {
     int rc = validate_f32_matvec(rows[i] * cols, rows[i], cols, x_len);
     if (rc) return rc;
     if (!ws[i] || !ys[i]) return fail(SI_HIP_ERR_NULL, "F32 matvec buffer is null");
-    wtotal += rows[i] * cols;
     ytotal += rows[i];
   }
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!x) return fail(SI_HIP_ERR_NULL, "F32 matvec buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  int rc = grow(ctx, &ctx->stage_weights, &ctx->stage_weights_bytes, wtotal * sizeof(float));
+  CallScope scope(ctx);
+  std::vector<const uint8_t *> wptr(count), dws(count);
+  std::vector<size_t> wlen(count);
+  for (size_t i = 0; i < count; ++i) {
+    wptr[i] = reinterpret_cast<const uint8_t *>(ws[i]);
+    wlen[i] = rows[i] * cols * sizeof(float);
+  }
+  int rc = borrow_weights(ctx, count, wptr.data(), wlen.data(), dws.data());
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_in, &ctx->stage_in_bytes, cols * sizeof(float));
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, ytotal * sizeof(float));
   if (rc) return rc;
-  SIHIP_CHECK(hipMemcpyAsync(ctx->stage_in, x, cols * sizeof(float), hipMemcpyHostToDevice, ctx->stream),
+  SIHIP_CHECK(copy_in(ctx, ctx->stage_in, x, cols * sizeof(float)),
               "input copy");
-  float *dw = static_cast<float *>(ctx->stage_weights), *dy = static_cast<float *>(ctx->stage_out);
+  float *dy = static_cast<float *>(ctx->stage_out);
   for (size_t i = 0; i < count; ++i) {
-    SIHIP_CHECK(hipMemcpyAsync(dw, ws[i], rows[i] * cols * sizeof(float), hipMemcpyHostToDevice,
-                               ctx->stream),
-                "weight copy");
-    hipError_t e = sihip::launch_f32_matvec(dw, static_cast<const float *>(ctx->stage_in), dy,
+    hipError_t e = sihip::launch_f32_matvec(reinterpret_cast<const float *>(dws[i]),
+                                            static_cast<const float *>(ctx->stage_in), dy,
                                             (uint32_t)rows[i], (uint32_t)cols, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "F32 matvec launch");
-    SIHIP_CHECK(hipMemcpyAsync(ys[i], dy, rows[i] * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+    SIHIP_CHECK(copy_out(ctx, ys[i], dy, rows[i] * sizeof(float)),
                 "output copy");
-    dw += rows[i] * cols;
     dy += rows[i];
   }
   rc = wait_stream(ctx, "F32 matvec group command");
@@ -1353,7 +1604,7 @@ int si_hip_rms_norm(si_hip_context *ctx, const float *x, size_t x_len, const flo
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!x || !w || !y) return fail(SI_HIP_ERR_NULL, "RMSNorm buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   return run_rms_host(ctx, 0, x, nullptr, w, 1, x_len, eps, y);
 }
 
@@ -1363,7 +1614,7 @@ int si_hip_rms_norm_heads(si_hip_context *ctx, const float *x, size_t x_len, con
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!x || !w || !y) return fail(SI_HIP_ERR_NULL, "head RMSNorm buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   return run_rms_host(ctx, 1, x, nullptr, w, heads, head_dim, eps, y);
 }
 
@@ -1374,7 +1625,7 @@ int si_hip_rms_norm_gated(si_hip_context *ctx, const float *x, size_t x_len, con
   if (rc) return rc;
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!x || !gate || !w || !y) return fail(SI_HIP_ERR_NULL, "Gated RMSNorm buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   return run_rms_host(ctx, 2, x, gate, w, heads, head_dim, eps, y);
 }
 
@@ -1388,7 +1639,7 @@ int si_hip_rms_norm_device(si_hip_context *ctx, uint32_t mode, const float *d_x,
   if (mode == 0 && heads != 1) return fail(SI_HIP_ERR_DIMENSIONS, "RMSNorm input and weight must have equal non-zero length");
   if (!ctx || !d_x || !d_w || !d_y || (mode == 2 && !d_gate))
     return fail(SI_HIP_ERR_NULL, "device RMSNorm argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   hipError_t e = sihip::launch_rms_norm(mode, d_x, d_gate, d_w, d_y, (uint32_t)heads,
                                         (uint32_t)head_dim, eps, device_stream(ctx));
   if (e != hipSuccess) return hip_fail(e, "RMSNorm launch");
@@ -1411,9 +1662,9 @@ int si_hip_dequantize(si_hip_context *ctx, uint32_t type, const uint8_t *bytes, 
   if (elements / 256 > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "%s block count exceeds HIP limits", label);
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (!bytes || !out) return fail(SI_HIP_ERR_NULL, "dequantize buffer is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   const uint8_t *dev = nullptr;
-  int rc = stage_weights(ctx, bytes, len, &dev);
+  int rc = stage_weights(ctx, bytes, len, &dev, false);
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, elements * sizeof(float));
   if (rc) return rc;
@@ -1421,7 +1672,7 @@ int si_hip_dequantize(si_hip_context *ctx, uint32_t type, const uint8_t *bytes, 
   hipError_t e = sihip::launch_dequant(type, dev, nullptr, static_cast<float *>(ctx->stage_out),
                                        (uint32_t)(elements / 256), 256, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "dequantize launch");
-  SIHIP_CHECK(hipMemcpyAsync(out, ctx->stage_out, elements * sizeof(float), hipMemcpyDeviceToHost, ctx->stream),
+  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, elements * sizeof(float)),
               "output copy");
   rc = wait_stream(ctx, "dequantize command");
   if (rc) return rc;
@@ -1454,6 +1705,7 @@ int si_hip_device_free(si_hip_context *ctx, void *p) {
 
 int si_hip_copy_to_device(si_hip_context *ctx, void *dst, const void *src, size_t bytes) {
   if (!ctx || !dst || !src) return fail(SI_HIP_ERR_NULL, "copy argument is null");
+  CallScope scope(ctx);
   SIHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream), "copy to device");
   SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "copy to device");
   return ok();
@@ -1461,6 +1713,7 @@ int si_hip_copy_to_device(si_hip_context *ctx, void *dst, const void *src, size_
 
 int si_hip_copy_from_device(si_hip_context *ctx, void *dst, const void *src, size_t bytes) {
   if (!ctx || !dst || !src) return fail(SI_HIP_ERR_NULL, "copy argument is null");
+  CallScope scope(ctx);
   SIHIP_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream), "copy from device");
   SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "copy from device");
   int rc = check_device_error(ctx);
@@ -1477,6 +1730,7 @@ int si_hip_copy_device(si_hip_context *ctx, void *dst, const void *src, size_t b
 
 int si_hip_synchronize(si_hip_context *ctx) {
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  CallScope scope(ctx);
   int rc = wait_stream(ctx, "synchronize");
   if (rc) return rc;
   return ok();
@@ -1496,7 +1750,7 @@ int si_hip_quant_matvec_device(si_hip_context *ctx, const si_hip_quant_weight *w
   int rc = validate_device_matvec(w, rows, cols, 1);
   if (rc) return rc;
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matvec argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, 1, device_stream(ctx));
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);
@@ -1516,7 +1770,7 @@ int si_hip_quant_matvec_many_device(si_hip_context *ctx, const si_hip_quant_weig
   }
   if (total > 0xffffffffu) return fail(SI_HIP_ERR_DIMENSIONS, "grouped quantized matvec rows overflow");
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matvec argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   int rc = dispatch_weight_group(ctx, ws, rows, count, d_in, d_out, (uint32_t)cols,
                                  device_stream(ctx));
   if (rc) return rc;
@@ -1535,7 +1789,7 @@ int si_hip_quant_matvec_device_repeat(si_hip_context *ctx, const si_hip_quant_we
       return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "repeat weights must share one type");
   }
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matvec argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   for (size_t i = 0; i < iters; ++i) {
     const si_hip_quant_weight *w = ws[i % n];
     int rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, 1, device_stream(ctx));
@@ -1554,7 +1808,7 @@ int si_hip_q4_k_fused_gate_up_device(si_hip_context *ctx, const si_hip_quant_wei
                                     "retained Q4_K fused gate/up byte length is invalid");
   if (rc) return rc;
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device gate/up argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   rc = dispatch_gate_up(ctx, g->data(), u->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols, device_stream(ctx));
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);
@@ -1568,7 +1822,7 @@ int si_hip_fused_mlp_device(si_hip_context *ctx, const si_hip_quant_weight *g,
   int rc = validate_mlp(g, u, d, gate_rows, cols, down_rows, cols);
   if (rc) return rc;
   if (!ctx || !d_in || !d_hidden || !d_out) return fail(SI_HIP_ERR_NULL, "device MLP argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   rc = dispatch_gate_up(ctx, g->data(), u->data(), d_in, d_hidden, (uint32_t)gate_rows, (uint32_t)cols, device_stream(ctx));
   if (rc) return rc;
   rc = dispatch_matvec(ctx, d->ggml_type, d->data(), d_hidden, d_out, (uint32_t)down_rows,
@@ -1583,7 +1837,7 @@ int si_hip_matmul_many_device(si_hip_context *ctx, const si_hip_quant_weight *w,
   int rc = validate_device_matvec(w, rows, cols, batch);
   if (rc) return rc;
   if (!ctx || !d_in || !d_out) return fail(SI_HIP_ERR_NULL, "device matmul argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_out, (uint32_t)rows, (uint32_t)cols,
                        (uint32_t)batch, device_stream(ctx));
   if (rc) return rc;
@@ -1597,8 +1851,8 @@ int si_hip_matvec_argmax_device(si_hip_context *ctx, const si_hip_quant_weight *
   int rc = validate_head(w, rows, cols, cols, rule);
   if (rc) return rc;
   if (!ctx || !d_in || !d_logits || !d_result) return fail(SI_HIP_ERR_NULL, "device head argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
-  rc = dispatch_head(ctx, w, d_in, d_logits, (uint32_t)rows, (uint32_t)cols, rule, d_result,
+  CallScope scope(ctx);
+  rc = dispatch_head(ctx, w, d_in, d_logits, true, (uint32_t)rows, (uint32_t)cols, rule, d_result,
                      device_stream(ctx));
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);
@@ -1620,7 +1874,7 @@ int si_hip_embedding_device(si_hip_context *ctx, const si_hip_quant_weight *t, s
   if (rc) return rc;
   if (n == 0 || n > UINT32_MAX) return fail(SI_HIP_ERR_DIMENSIONS, "embedding token count is invalid");
   if (!ctx || !d_ids || !d_out) return fail(SI_HIP_ERR_NULL, "device embedding argument is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, t->data(), d_ids, d_out, (uint32_t)n,
                                        (uint32_t)cols, device_stream(ctx),
                                        embedding_table_rows(t, cols, rows), ctx->ws.ptr);
@@ -1647,7 +1901,7 @@ int si_hip_event_elapsed_ms(si_hip_context *ctx, uint32_t a, uint32_t b, float *
 // ---- captured submission -------------------------------------------------------
 int si_hip_capture_begin(si_hip_context *ctx) {
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   if (ctx->capturing) return fail(SI_HIP_ERR_STATE, "a graph capture is already open");
   if (!ctx->capture_stream)
     SIHIP_CHECK(hipStreamCreateWithFlags(&ctx->capture_stream, hipStreamNonBlocking),
@@ -1662,7 +1916,7 @@ int si_hip_capture_begin(si_hip_context *ctx) {
 int si_hip_capture_end(si_hip_context *ctx, si_hip_graph **out) {
   if (!ctx || !out) return fail(SI_HIP_ERR_NULL, "capture_end argument is null");
   *out = nullptr;
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   if (!ctx->capturing) return fail(SI_HIP_ERR_STATE, "no graph capture is open");
   ctx->capturing = false;
   hipGraph_t g = nullptr;
@@ -1688,7 +1942,7 @@ int si_hip_graph_launch(si_hip_context *ctx, const si_hip_graph *graph) {
   if (graph->device != ctx->device)
     return fail(SI_HIP_ERR_RANGE, "graph was captured on device %d, context is on %d",
                 graph->device, ctx->device);
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   SIHIP_CHECK(hipGraphLaunch(graph->exec, ctx->stream), "graph launch");
   ctx->async_submitted.fetch_add(graph->calls);
   return ok();
@@ -1705,7 +1959,7 @@ void si_hip_graph_free(si_hip_graph *graph) {
 
 int si_hip_debug_set_wait_give_up(si_hip_context *ctx, uint32_t polls) {
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   if (ctx->capturing) return fail(SI_HIP_ERR_STATE, "the wait hook cannot change during a graph capture");
   SIHIP_CHECK(hipStreamSynchronize(ctx->stream), "wait hook");
   ctx->give_up_polls = polls;
@@ -1718,7 +1972,7 @@ int si_hip_set_kernel_policy(si_hip_context *ctx, uint32_t policy) {
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   if (policy != SI_HIP_KERNEL_AUTO && policy != SI_HIP_KERNEL_GENERIC)
     return fail(SI_HIP_ERR_RANGE, "unknown kernel policy %u", policy);
-  std::lock_guard<std::mutex> lock(ctx->mu);
+  CallScope scope(ctx);
   ctx->policy = policy;
   return ok();
 }
@@ -1747,6 +2001,43 @@ void si_hip_sample_allocated(si_hip_context *ctx) {
   while (now > prev && !ctx->tel->peak_allocated.compare_exchange_weak(prev, now)) {
   }
 }
+int si_hip_set_residency_budget(si_hip_context *ctx, uint64_t bytes) {
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  CallScope scope(ctx);
+  ctx->res.budget = bytes;
+  while (ctx->res.bytes > bytes) {
+    auto victim = ctx->res.ranges.begin();
+    for (auto j = ctx->res.ranges.begin(); j != ctx->res.ranges.end(); ++j)
+      if (j->second.used < victim->second.used) victim = j;
+    evict_range(ctx, victim);
+  }
+  return ok();
+}
+
+int si_hip_residency_evict(si_hip_context *ctx, const void *host_bytes, size_t len) {
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  CallScope scope(ctx);
+  const uintptr_t lo = (uintptr_t)host_bytes;
+  const uintptr_t hi = len == 0 ? UINTPTR_MAX : (len > UINTPTR_MAX - lo ? UINTPTR_MAX : lo + len);
+  for (auto it = ctx->res.ranges.begin(); it != ctx->res.ranges.end();) {
+    const uintptr_t a = it->first.first, b = a + it->first.second;
+    auto next = std::next(it);
+    if (len == 0 || (a < hi && lo < b)) evict_range(ctx, it);
+    it = next;
+  }
+  return ok();
+}
+
+int si_hip_get_residency_stats(si_hip_context *ctx, si_hip_residency_stats *out) {
+  if (!ctx || !out) return fail(SI_HIP_ERR_NULL, "residency stats argument is null");
+  CallScope scope(ctx);
+  *out = ctx->res.stats;
+  out->resident_ranges = ctx->res.ranges.size();
+  out->resident_bytes = ctx->res.bytes;
+  out->budget_bytes = ctx->res.budget;
+  return ok();
+}
+
 int si_hip_get_command_stats(const si_hip_context *ctx, si_hip_command_stats *out) {
   if (!ctx || !out) return fail(SI_HIP_ERR_NULL, "command stats argument is null");
   out->submitted = ctx->submitted.load();

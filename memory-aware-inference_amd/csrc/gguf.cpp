@@ -24,6 +24,7 @@
 #include <string>
 #include <vector>
 
+#include "si_hip_shared.h"
 #include "si_hip_status.h"
 
 namespace {
@@ -584,7 +585,8 @@ int si_hip_gguf_f32_matvec_many_tensors(si_hip_context *ctx, const si_hip_gguf *
 
 // Rows [row_start, row_start + row_count) of a rank-2 tensor of the store:
 // F32 through the F32 matvec, Q4_K / Q5_K / Q6_K through the quantized one
-// over the mapped row bytes (gguf_matvec_tensor_rows, metal.rs:5003-5015, with
+// over the mapped bytes, the whole tensor borrowed so that its row ranges
+// share one resident HBM copy (gguf_matvec_tensor_rows, metal.rs:5003-5015, with
 // q4_k_matvec_tensor_rows / quant_k_matvec_tensor_rows, 4346-4467, and
 // gguf_quant_matvec_tensor_rows, 4505-4527: their checks and messages).
 int si_hip_gguf_matvec_tensor_rows(si_hip_context *ctx, const si_hip_gguf *g, uint64_t index,
@@ -617,8 +619,9 @@ int si_hip_gguf_matvec_tensor_rows(si_hip_context *ctx, const si_hip_gguf *g, ui
   if (end < start) return set_error(SI_HIP_ERR_OVERFLOW, "%s row byte range overflows", label);
   if (end > t->data_end - t->data_start)
     return set_error(SI_HIP_ERR_BYTE_LENGTH, "%s tensor payload is shorter than its shape", label);
-  return si_hip_gguf_quant_matvec_bytes(ctx, ty, g->bytes + t->data_start + start, (size_t)len,
-                                        row_count, (size_t)cols, x, x_len, y);
+  return sihip::quant_matvec_tensor_range(ctx, ty, g->bytes + t->data_start,
+                                         (size_t)(t->data_end - t->data_start), (size_t)start,
+                                         (size_t)len, row_count, (size_t)cols, x, x_len, y);
 }
 
 // Several quantized matvecs over one input (gguf_quant_matvec_many_tensors,

@@ -708,7 +708,7 @@ __device__ __forceinline__ void wait_slot(uint32_t owner_at, uint32_t lt, uint32
 // order and stores the rows -- y[row] = sum, or with MATS == 2 silu(sum of
 // partials < nparts) * (sum of the rest) -- or, for a split tile, publishes
 // the sums and, if it completes the tile, combines all shares.  ARGMAX: every
-// row stored also enters *best (argmax_candidate under `rule`).
+// row also enters *best (argmax_candidate under `rule`), and y may be null.
 template <int MATS, bool ARGMAX = false>
 __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32_t slots,
                                          const Sched& sc, const SchedArgs& sa, const Pair& pr,
@@ -717,10 +717,12 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
                                          float* __restrict__ y, SplitWs ws, uint32_t& fail,
                                          uint64_t* best = nullptr, uint32_t rule = 0u) {
   auto store_row = [&](uint32_t row, float v) {
-    y[row] = v;
     if constexpr (ARGMAX) {
+      if (y) y[row] = v;  // a head whose logits are not wanted stores none
       const uint64_t c = argmax_candidate(v, row, rule);
       *best = c > *best ? c : *best;
+    } else {
+      y[row] = v;
     }
   };
   const uint32_t grp = lane >> 4, n = lane & 15u;

@@ -30,6 +30,7 @@ ARGMAX_LAST_FINITE = 0
 ARGMAX_FIRST_GREATER = 1
 KERNEL_AUTO = 0
 KERNEL_GENERIC = 1
+DEFAULT_RESIDENCY_BUDGET = 16 << 30  # SI_HIP_DEFAULT_RESIDENCY_BUDGET
 MAX_BATCH = 16
 
 STATUS = {
@@ -51,6 +52,12 @@ class HipError(RuntimeError):
 class CommandStats(C.Structure):
     _fields_ = [("submitted", C.c_uint64), ("async_submitted", C.c_uint64),
                 ("waited", C.c_uint64), ("wait_nanos", C.c_uint64)]
+
+
+class ResidencyStats(C.Structure):
+    _fields_ = [("hits", C.c_uint64), ("uploads", C.c_uint64), ("uploaded_bytes", C.c_uint64),
+                ("evictions", C.c_uint64), ("resident_ranges", C.c_uint64),
+                ("resident_bytes", C.c_uint64), ("budget_bytes", C.c_uint64)]
 
 
 class GgufValueC(C.Structure):
@@ -138,6 +145,9 @@ _SIGS = {
     "si_hip_reset_peaks": (None, [_P]),
     "si_hip_sample_allocated": (None, [_P]),
     "si_hip_get_command_stats": (_I, [_P, C.POINTER(CommandStats)]),
+    "si_hip_set_residency_budget": (_I, [_P, _U64]),
+    "si_hip_residency_evict": (_I, [_P, _P, _SZ]),
+    "si_hip_get_residency_stats": (_I, [_P, C.POINTER(ResidencyStats)]),
     # si_hip_f32.h
     "si_hip_f32_matvec": (_I, [_P, _FP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
     "si_hip_f32_matvec_bytes": (_I, [_P, _BP, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
@@ -668,6 +678,23 @@ class HipContext:
         s = CommandStats()
         _check(lib().si_hip_get_command_stats(self._h, C.byref(s)))
         return {k: int(getattr(s, k)) for k, _ in CommandStats._fields_}
+
+    # ---- residency of borrowed weight bytes
+    def set_residency_budget(self, nbytes: int) -> None:
+        _check(lib().si_hip_set_residency_budget(self._h, nbytes))
+
+    def residency_evict(self, host_bytes=None, nbytes: int = 0) -> None:
+        """Drops resident ranges overlapping the buffer (None: every range)."""
+        if host_bytes is None:
+            _check(lib().si_hip_residency_evict(self._h, None, 0))
+            return
+        b = _u8(host_bytes)
+        _check(lib().si_hip_residency_evict(self._h, b.ctypes.data_as(_P), nbytes or b.size))
+
+    def residency_stats(self) -> dict:
+        s = ResidencyStats()
+        _check(lib().si_hip_get_residency_stats(self._h, C.byref(s)))
+        return {k: int(getattr(s, k)) for k, _ in ResidencyStats._fields_}
 
     def __del__(self):
         try:
