@@ -412,6 +412,60 @@ __device__ __forceinline__ float k4_bound(const BlockQ4& w) {
                fmaf(ad, (float)(w.sco * QMAX), am * w.mno));
 }
 
+// One vector's partial dot of the lane's row over stage s (blocks 4 s ..
+// 4 s + nlive - 1): the MFMA digit sums, the side elements' exact products,
+// the rounded blocks' check, and the exact path for blocks that need it,
+// summed over the lane groups (every lane of a row gets the row's sum).
+template <int QB>
+__device__ __forceinline__ float stage_rowsum(const StageRegs<QB>& v, uint32_t sbase,
+                                              const Layout& L, uint32_t s, uint32_t nlive,
+                                              uint32_t grp, uint32_t n, i32x4 (&A)[8],
+                                              bool hi_units, int bsh, uint32_t rot_lo,
+                                              uint32_t rot_hi, const float* __restrict__ x) {
+  u32x2 xs[4];
+  i32x4 ex;
+  uint32_t cnt;
+  lds_read_sums(sbase + L.xsum + 128u * s + 8u * grp, sbase + L.expo + 16u * s, xs, ex, cnt);
+  float part[4];
+  bool bad_any = false;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    lds_read_images8(sbase + L.img + 4096u * s + 2048u * h + 16u * n, kActiveLanes, A);
+#pragma unroll
+    for (int b2 = 0; b2 < 2; ++b2) {
+      const int b = 2 * h + b2;
+      const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
+      const bool use = (uint32_t)b < nlive;
+      bad_any |= use && eb == kBadBlock;
+      const float c = block_dot(v.decode(b, hi_units, bsh, rot_lo, rot_hi), A[4 * b2],
+                                A[4 * b2 + 1], A[4 * b2 + 2], A[4 * b2 + 3], xs[b], eb);
+      part[b] = (use && eb != kBadBlock) ? c : 0.0f;
+    }
+  }
+  // side elements (lane group i / 64 holds element i), then the rounded
+  // blocks' check; blocks on the exact path, and rounded blocks of rows that
+  // fail the check, take the per-weight path
+  const uint32_t counts = live_counts(__builtin_amdgcn_readfirstlane(cnt), nlive);
+  uint32_t redo = 0u;
+  if (counts != 0u) {
+    const uint32_t list = sbase + L.expo + L.side_off + 4u * kSideBytes * s;
+    add_listed<4>(list, counts, grp, part, [](uint32_t i) { return i >> 6; },
+                  [&](auto b, uint32_t i) { return v.template side_weight<decltype(b)::value>(i); });
+    redo = rounded_redo<4>(list, counts, grp, part, [&](auto b) {
+      return k4_bound<QB == 5 ? 31 : 15>(
+          v.decode(decltype(b)::value, hi_units, bsh, rot_lo, rot_hi));
+    });
+  }
+  if (bad_any || redo != 0u) {
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+      if (((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock) ||
+          ((redo >> b) & 1u))
+        part[b] = v.exact(b, hi_units, bsh, rot_lo, rot_hi, x + 256u * (4u * s + b) + 64u * grp);
+  }
+  return sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
+}
+
 // GROUPED: the rows are those of ga.count matrices with one K, one after the
 // other (every matrix but the last a whole number of 16-row tiles), and tile
 // t's weights are those of the matrix whose tiles reach past t.
@@ -599,48 +653,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       hand_off_tokens<NTOK>(sbase, L, sc.by_slots, pr, tstages, rs, lane, rows, y, fail);
       continue;
     }
-    u32x2 xs[4];
-    i32x4 ex;
-    uint32_t cnt;
-    lds_read_sums(sbase + L.xsum + 128u * s + 8u * grp, sbase + L.expo + 16u * s, xs, ex, cnt);
-    float part[4];
-    bool bad_any = false;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      lds_read_images8(sbase + L.img + 4096u * s + 2048u * h + 16u * n, kActiveLanes, A);
-#pragma unroll
-      for (int b2 = 0; b2 < 2; ++b2) {
-        const int b = 2 * h + b2;
-        const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
-        const bool use = (uint32_t)b < nlive;
-        bad_any |= use && eb == kBadBlock;
-        const float c = block_dot(v.decode(b, hi_units, bsh, rot_lo, rot_hi), A[4 * b2],
-                                  A[4 * b2 + 1], A[4 * b2 + 2], A[4 * b2 + 3], xs[b], eb);
-        part[b] = (use && eb != kBadBlock) ? c : 0.0f;
-      }
-    }
-    // side elements (lane group i / 64 holds element i), then the rounded
-    // blocks' check; blocks on the exact path, and rounded blocks of rows that
-    // fail the check, take the per-weight path
-    const uint32_t counts = live_counts(__builtin_amdgcn_readfirstlane(cnt), nlive);
-    uint32_t redo = 0u;
-    if (counts != 0u) {
-      const uint32_t list = sbase + L.expo + L.side_off + 4u * kSideBytes * s;
-      add_listed<4>(list, counts, grp, part, [](uint32_t i) { return i >> 6; },
-                    [&](auto b, uint32_t i) { return v.template side_weight<decltype(b)::value>(i); });
-      redo = rounded_redo<4>(list, counts, grp, part, [&](auto b) {
-        return k4_bound<QB == 5 ? 31 : 15>(
-            v.decode(decltype(b)::value, hi_units, bsh, rot_lo, rot_hi));
-      });
-    }
-    if (bad_any || redo != 0u) {
-#pragma unroll
-      for (int b = 0; b < 4; ++b)
-        if (((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock) ||
-            ((redo >> b) & 1u))
-          part[b] = v.exact(b, hi_units, bsh, rot_lo, rot_hi, x + 256u * (4u * s + b) + 64u * grp);
-    }
-    const float rowsum = sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
+    const float rowsum =
+        stage_rowsum(v, sbase, L, s, nlive, grp, n, A, hi_units, bsh, rot_lo, rot_hi, x);
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
     hand_off<MATS>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws, fail);
