@@ -77,6 +77,7 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
              "graph_gb_per_s": round(nbytes / (graph_ms * 1e-3) / 1e9, 1)}
     if detail:
         extra.update(call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, steps, host0))
+        extra["floor"] = stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps, warmup)
     ctx.device_free(d_x)
     ctx.device_free(d_y)
     for w in weights:
@@ -87,6 +88,41 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
            "us_per_call": round(us, 3), "gb_per_s": round(gbs, 1),
            "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
     out.update(extra)
+    return out
+
+
+def stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps: int, warmup: int) -> dict:
+    """Back-to-back launches of si_hip_stream_probe over the same resident
+    copies: the matvec kernel's weight copies alone (its grid, 12 waves per
+    CU, 16-row x 64-byte buffer->LDS copies, one stage in flight per wave), the
+    same with the nontemporal bit, and an empty kernel of the launch shape.
+    The matvec cannot beat the first on this copy path."""
+    out = {}
+    per_graph = copies * max(1, GRAPH_CALLS // copies)
+    reps = max(1, steps // per_graph)
+    for mode, name in ((0, "copies_us"), (1, "copies_nontemporal_us"), (2, "empty_launch_us")):
+        # recorded into a HIP graph and replayed, so that host launch cost
+        # does not pace the short launches
+        ctx.capture_begin()
+        rc = lib.si_hip_stream_probe(ctx.handle, harr, copies, rows, cols, mode, per_graph)
+        graph = ctx.capture_end()
+        if rc:
+            graph.free()
+            raise si_hip.HipError(rc, si_hip.last_error())
+        for _ in range(max(1, warmup // per_graph)):
+            graph.launch()
+        ctx.synchronize()
+        ctx.event_record(0)
+        for _ in range(reps):
+            graph.launch()
+        ctx.event_record(1)
+        us = ctx.event_elapsed_ms(0, 1) * 1000.0 / (reps * per_graph)
+        ctx.synchronize()
+        graph.free()
+        out[name] = round(us, 3)
+    out["copies_frac_of_peak"] = round(nbytes / (out["copies_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    out["note"] = ("si_hip_stream_probe: the matvec's weight copies without arithmetic, "
+                   "back to back over the same resident copies, replayed from a HIP graph")
     return out
 
 
@@ -518,7 +554,7 @@ def main() -> int:
         "host_wall_us_per_call": head["host_wall_us_per_call"],
         "host_wall_note": head["host_wall_note"],
     }
-    for k in ("borrowed_bytes_host_wall_us_per_call", "borrowed_bytes_first_call_us",
+    for k in ("floor", "borrowed_bytes_host_wall_us_per_call", "borrowed_bytes_first_call_us",
               "borrowed_bytes_note"):
         if k in head:
             out[k] = head[k]

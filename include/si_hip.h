@@ -264,6 +264,17 @@ int si_hip_embedding_device(si_hip_context *ctx, const si_hip_quant_weight *tabl
                             size_t shape_columns, size_t shape_rows, const uint32_t *d_ids,
                             size_t n_tokens, float *d_output);
 
+/* Measurement probe, no counterpart in the reference (it is not part of the
+ * path): `iters` back-to-back launches on the compute stream, launch i
+ * reading weights[i % n] (Q4_K or Q5_K, rows x columns) with the weight
+ * copies of the one-vector matrix-core kernel -- its grid, twelve waves per
+ * CU, 16-row x 64-byte buffer->LDS copies, one stage in flight per wave --
+ * and no arithmetic.  mode 0: the kernels' default cache policy; 1: the
+ * nontemporal bit; 2: an empty kernel of the same launch shape.  Timed with
+ * the event slots, it bounds what the matvec can reach on its copy path. */
+int si_hip_stream_probe(si_hip_context *ctx, const si_hip_quant_weight *const *weights, size_t n,
+                        size_t rows, size_t columns, uint32_t mode, size_t iters);
+
 /* Timing on the compute stream: 16 event slots. */
 int si_hip_event_record(si_hip_context *ctx, uint32_t slot);
 int si_hip_event_elapsed_ms(si_hip_context *ctx, uint32_t start_slot, uint32_t end_slot,

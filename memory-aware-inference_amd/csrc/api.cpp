@@ -1799,6 +1799,32 @@ int si_hip_quant_matvec_device_repeat(si_hip_context *ctx, const si_hip_quant_we
   return ok();
 }
 
+int si_hip_stream_probe(si_hip_context *ctx, const si_hip_quant_weight *const *ws, size_t n,
+                        size_t rows, size_t cols, uint32_t mode, size_t iters) {
+  if (!ws || n == 0) return fail(SI_HIP_ERR_NULL, "stream probe needs at least one weight");
+  if (mode > sihip::kProbeEmpty) return fail(SI_HIP_ERR_RANGE, "unknown stream probe mode %u", mode);
+  for (size_t i = 0; i < n; ++i) {
+    int rc = validate_device_matvec(ws[i], rows, cols, 1);
+    if (rc) return rc;
+    if (ws[i]->ggml_type != SI_HIP_GGML_TYPE_Q4_K && ws[i]->ggml_type != SI_HIP_GGML_TYPE_Q5_K)
+      return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "the stream probe reads Q4_K or Q5_K weights");
+  }
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  int cus = 0;
+  SIHIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, ctx->device),
+              "device query");
+  CallScope scope(ctx);
+  for (size_t i = 0; i < iters; ++i) {
+    const si_hip_quant_weight *w = ws[i % n];
+    hipError_t e = sihip::launch_stream_probe(mode, w->data(), (uint32_t)rows, (uint32_t)cols,
+                                              (uint32_t)block_bytes_of(w->ggml_type),
+                                              (uint32_t)cus, device_stream(ctx));
+    if (e != hipSuccess) return hip_fail(e, "stream probe launch");
+  }
+  ctx->async_submitted.fetch_add(iters);
+  return ok();
+}
+
 int si_hip_q4_k_fused_gate_up_device(si_hip_context *ctx, const si_hip_quant_weight *g,
                                      const si_hip_quant_weight *u, size_t rows, size_t cols,
                                      const float *d_in, float *d_out) {

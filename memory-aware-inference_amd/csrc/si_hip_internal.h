@@ -126,6 +126,16 @@ hipError_t launch_f32_matvec(const float* w, const float* x, float* y, uint32_t 
 hipError_t launch_rms_norm(uint32_t mode, const float* x, const float* gate, const float* w,
                            float* y, uint32_t heads, uint32_t head_dim, float eps, hipStream_t s);
 
+// kernels_probe.hip: one launch of the matrix-core kernels' weight stream
+// alone (Q4_K / Q5_K blocks of block_bytes, a grid of min(tiles, cus)).
+enum ProbeMode : uint32_t {
+  kProbeDefault = 0,      // the kernels' copies, default cache policy
+  kProbeNontemporal = 1,  // the same with the nontemporal bit
+  kProbeEmpty = 2,        // the launch shape with no work
+};
+hipError_t launch_stream_probe(uint32_t mode, const uint8_t* w, uint32_t rows, uint32_t cols,
+                               uint32_t block_bytes, uint32_t cus, hipStream_t s);
+
 // kernels_argmax.hip: max-loc over n < kArgmaxMaxRows logits in one launch, using the
 // context workspace's argmax area; the winner lands in *result (packed
 // candidate, 0 when there is none).

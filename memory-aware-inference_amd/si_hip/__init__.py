@@ -132,6 +132,7 @@ _SIGS = {
     "si_hip_event_record": (_I, [_P, _U32]),
     "si_hip_event_elapsed_ms": (_I, [_P, _U32, _U32, C.POINTER(C.c_float)]),
     "si_hip_quant_matvec_device_repeat": (_I, [_P, C.POINTER(_P), _SZ, _SZ, _SZ, _P, _P, _SZ]),
+    "si_hip_stream_probe": (_I, [_P, C.POINTER(_P), _SZ, _SZ, _SZ, _U32, _SZ]),
     "si_hip_capture_begin": (_I, [_P]),
     "si_hip_capture_end": (_I, [_P, C.POINTER(_P)]),
     "si_hip_graph_launch": (_I, [_P, _P]),
