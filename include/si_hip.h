@@ -174,7 +174,24 @@ int si_hip_gguf_quant_fused_mlp_weights(si_hip_context *ctx, const si_hip_quant_
                                         size_t columns, size_t down_rows, const float *input,
                                         size_t input_len, float *output);
 
+/* q4_k_matvec_tensor_rows / q5_k / q6_k and gguf_quant_matvec_tensor_rows
+ * (metal.rs:4346-4527) on a GgufTensorView: its name, type, GGUF shape
+ * [columns, rows] (n_dims entries) and borrowed payload bytes, with the
+ * reference's checks and messages.  The whole payload is what stays resident
+ * (see residency below), so calls on different row ranges share one copy. */
+int si_hip_gguf_quant_matvec_view_rows(si_hip_context *ctx, const char *name, uint32_t ggml_type,
+                                       const uint64_t *shape, uint32_t n_dims,
+                                       const uint8_t *payload, size_t payload_len,
+                                       size_t row_start, size_t row_count, const float *input,
+                                       size_t input_len, float *output);
+
 /* ---- embedding (bit-exact dequantisation of table rows) --------------- */
+/* q4_k_embedding_tensor (metal.rs:3785-3810) on a GgufTensorView (type,
+ * shape, borrowed payload): the reference's checks in order; the table stays
+ * resident when it fits the residency budget, else the row alone is copied. */
+int si_hip_q4_k_embedding_view(si_hip_context *ctx, uint32_t ggml_type, const uint64_t *shape,
+                               uint32_t n_dims, const uint8_t *payload, size_t payload_len,
+                               size_t token_id, float *output);
 /* q4_k_embedding_row (metal.rs:3734-3783) */
 int si_hip_q4_k_embedding_row(si_hip_context *ctx, const uint8_t *row_bytes, size_t row_len,
                               size_t columns, float *output);

@@ -886,6 +886,38 @@ int sihip::quant_matvec_tensor_range(si_hip_context *ctx, uint32_t type, const u
 
 extern "C" {
 
+int si_hip_gguf_quant_matvec_view_rows(si_hip_context *ctx, const char *name, uint32_t type,
+                                       const uint64_t *shape, uint32_t n_dims,
+                                       const uint8_t *payload, size_t payload_len,
+                                       size_t row_start, size_t row_count, const float *in,
+                                       size_t in_len, float *out) {
+  // gguf_quant_matvec_tensor_rows (metal.rs:4505-4527), then the checks of
+  // q4_k_matvec_tensor_rows / quant_k_matvec_tensor_rows (4346-4467) in order
+  if (block_bytes_of(type) == 0)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "GGUF tensor %s has unsupported quantized type %u",
+                name ? name : "", type);
+  const char *label = type_label(type);
+  if (n_dims != 2 || !shape)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "%s matvec requires a rank-2 %s tensor", label, label);
+  const uint64_t cols = shape[0], rows = shape[1];
+  if (row_count == 0 || row_start >= rows || row_count > rows - row_start)
+    return fail(SI_HIP_ERR_RANGE, "%s row range is invalid", label);
+  if (cols % 256 != 0 || in_len != cols)
+    return fail(SI_HIP_ERR_DIMENSIONS, "%s tensor columns or input length is invalid", label);
+  const size_t row_bytes = (size_t)cols / 256 * block_bytes_of(type);
+  size_t start = 0, len = 0, end = 0;
+  if (!checked_mul(row_start, row_bytes, &start))
+    return fail(SI_HIP_ERR_OVERFLOW, "%s row byte range overflows", label);
+  if (!checked_mul(row_count, row_bytes, &len))
+    return fail(SI_HIP_ERR_OVERFLOW, "%s row byte length overflows", label);
+  if (!checked_add(start, len, &end))
+    return fail(SI_HIP_ERR_OVERFLOW, "%s row byte range overflows", label);
+  if (end > payload_len)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "%s tensor payload is shorter than its shape", label);
+  return sihip::quant_matvec_tensor_range(ctx, type, payload, payload_len, start, len, row_count,
+                                          (size_t)cols, in, in_len, out);
+}
+
 int si_hip_gguf_quant_matvec_many_bytes(si_hip_context *ctx, const uint32_t *types,
                                         const uint8_t *const *bytes, const size_t *lens,
                                         const size_t *rows, const size_t *columns, size_t count,
@@ -1280,6 +1312,47 @@ int si_hip_q4_k_embedding_tokens(si_hip_context *ctx, const si_hip_quant_weight 
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
   SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, n * cols * sizeof(float)),
               "output copy");
+  rc = wait_stream(ctx, "Q4_K embedding command");
+  if (rc) return rc;
+  return ok();
+}
+
+int si_hip_q4_k_embedding_view(si_hip_context *ctx, uint32_t type, const uint64_t *shape,
+                               uint32_t n_dims, const uint8_t *payload, size_t payload_len,
+                               size_t token_id, float *out) {
+  // q4_k_embedding_tensor (metal.rs:3785-3810) in its order, then
+  // q4_k_embedding_row's checks (3734-3741)
+  if (type != SI_HIP_GGML_TYPE_Q4_K || n_dims != 2 || !shape)
+    return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "Q4_K embedding requires a rank-2 Q4_K tensor");
+  const uint64_t cols = shape[0], rows = shape[1];
+  if (token_id >= rows || cols % 256 != 0)
+    return fail(SI_HIP_ERR_RANGE, "Q4_K embedding token id or dimension is invalid");
+  const size_t row_bytes = (size_t)cols / 256 * 144;
+  size_t start = 0, end = 0;
+  if (!checked_mul(token_id, row_bytes, &start))
+    return fail(SI_HIP_ERR_OVERFLOW, "Q4_K embedding row offset overflows");
+  if (!checked_add(start, row_bytes, &end)) return fail(SI_HIP_ERR_OVERFLOW, "Q4_K embedding row end overflows");
+  if (end > payload_len)
+    return fail(SI_HIP_ERR_BYTE_LENGTH, "Q4_K embedding tensor payload is shorter than its shape");
+  if (cols == 0) return fail(SI_HIP_ERR_DIMENSIONS, "Q4_K embedding dimension is invalid");
+  if (cols > UINT32_MAX) return fail(SI_HIP_ERR_OVERFLOW, "embedding dimension exceeds HIP limits");
+  if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
+  if (!payload || !out) return fail(SI_HIP_ERR_NULL, "Q4_K embedding buffer is null");
+  CallScope scope(ctx);
+  // the whole table stays resident when it fits the budget (later lookups
+  // copy nothing); otherwise the row alone is copied
+  const bool whole = payload_len <= ctx->res.budget;
+  const uint8_t *dev = nullptr;
+  int rc = whole ? stage_weights(ctx, payload, payload_len, &dev)
+                 : stage_weights(ctx, payload + start, row_bytes, &dev, false);
+  if (rc) return rc;
+  rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, (size_t)cols * sizeof(float));
+  if (rc) return rc;
+  hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, whole ? dev + start : dev, nullptr,
+                                       static_cast<float *>(ctx->stage_out), 1, (uint32_t)cols,
+                                       ctx->stream);
+  if (e != hipSuccess) return hip_fail(e, "embedding launch");
+  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, (size_t)cols * sizeof(float)), "output copy");
   rc = wait_stream(ctx, "Q4_K embedding command");
   if (rc) return rc;
   return ok();

@@ -8,6 +8,7 @@
 // order, the last one to the end of the file.  Error messages are the
 // reference's.  Files are mapped read-only (GgufModelStore::open,
 // model.rs:625-666); nothing is copied until a tensor is uploaded.
+#include "si_hip.h"
 #include "si_hip_f32.h"
 #include "si_hip_gguf.h"
 
@@ -596,32 +597,10 @@ int si_hip_gguf_matvec_tensor_rows(si_hip_context *ctx, const si_hip_gguf *g, ui
   if (!t) return g ? SI_HIP_ERR_RANGE : SI_HIP_ERR_NULL;
   if (t->ggml_type == 0)
     return si_hip_gguf_f32_matvec_tensor_rows(ctx, g, index, row_start, row_count, x, x_len, y);
-  const uint32_t ty = t->ggml_type;
-  if (ty != 12 && ty != 13 && ty != 14)
-    return set_error(SI_HIP_ERR_UNSUPPORTED_TYPE, "GGUF tensor %s has unsupported quantized type %u",
-                     t->name.c_str(), ty);
-  const char *label = ty == 12 ? "Q4_K" : ty == 13 ? "Q5_K" : "Q6_K";
-  const uint64_t bb = ty == 12 ? 144u : ty == 13 ? 176u : 210u;
-  if (t->shape.size() != 2)
-    return set_error(SI_HIP_ERR_UNSUPPORTED_TYPE, "%s matvec requires a rank-2 %s tensor", label, label);
-  const uint64_t cols = t->shape[0], rows = t->shape[1];
-  if (row_count == 0 || row_start >= rows || row_count > rows - row_start)
-    return set_error(SI_HIP_ERR_RANGE, "%s row range is invalid", label);
-  if (cols % 256 != 0 || x_len != cols)
-    return set_error(SI_HIP_ERR_DIMENSIONS, "%s tensor columns or input length is invalid", label);
-  const uint64_t row_bytes = cols / 256 * bb;
-  uint64_t start, len, end;
-  if (!checked_mul(row_start, row_bytes, &start))
-    return set_error(SI_HIP_ERR_OVERFLOW, "%s row byte range overflows", label);
-  if (!checked_mul(row_count, row_bytes, &len))
-    return set_error(SI_HIP_ERR_OVERFLOW, "%s row byte length overflows", label);
-  end = start + len;
-  if (end < start) return set_error(SI_HIP_ERR_OVERFLOW, "%s row byte range overflows", label);
-  if (end > t->data_end - t->data_start)
-    return set_error(SI_HIP_ERR_BYTE_LENGTH, "%s tensor payload is shorter than its shape", label);
-  return sihip::quant_matvec_tensor_range(ctx, ty, g->bytes + t->data_start,
-                                         (size_t)(t->data_end - t->data_start), (size_t)start,
-                                         (size_t)len, row_count, (size_t)cols, x, x_len, y);
+  return si_hip_gguf_quant_matvec_view_rows(ctx, t->name.c_str(), t->ggml_type, t->shape.data(),
+                                            (uint32_t)t->shape.size(), g->bytes + t->data_start,
+                                            (size_t)(t->data_end - t->data_start), row_start,
+                                            row_count, x, x_len, y);
 }
 
 // Several quantized matvecs over one input (gguf_quant_matvec_many_tensors,

@@ -108,6 +108,9 @@ _SIGS = {
     "si_hip_q4_k_fused_gate_up_weights": (_I, [_P, _P, _P, _SZ, _SZ, _FP, _SZ, _FP]),
     "si_hip_gguf_quant_fused_mlp_weights": (_I, [_P, _P, _P, _P, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
     "si_hip_q4_k_embedding_row": (_I, [_P, _BP, _SZ, _SZ, _FP]),
+    "si_hip_q4_k_embedding_view": (_I, [_P, _U32, C.POINTER(_U64), _U32, _BP, _SZ, _SZ, _FP]),
+    "si_hip_gguf_quant_matvec_view_rows": (_I, [_P, C.c_char_p, _U32, C.POINTER(_U64), _U32, _BP,
+                                                _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
     "si_hip_q4_k_embedding_tensor": (_I, [_P, _P, _SZ, _SZ, _SZ, _FP]),
     "si_hip_q4_k_embedding_tokens": (_I, [_P, _P, _SZ, _SZ, _U32P, _SZ, _FP]),
     "si_hip_gguf_quant_matmul_many_bytes": (_I, [_P, _U32, _BP, _SZ, _SZ, _SZ, _SZ, _FP, _SZ, _FP]),
@@ -512,6 +515,28 @@ class HipContext:
         y = np.empty(max(columns, 1), dtype=np.float32)
         _check(lib().si_hip_q4_k_embedding_row(self._h, _bp(b), b.size, columns, _fp(y)))
         return y[:columns]
+
+    def q4_k_embedding_view(self, ggml_type: int, shape: Sequence[int], payload,
+                            token_id: int) -> np.ndarray:
+        """q4_k_embedding_tensor over a GgufTensorView (type, shape, borrowed
+        payload bytes)."""
+        b = _u8(payload)
+        sh = (_U64 * len(shape))(*shape)
+        y = np.empty(max(int(shape[0]) if shape else 1, 1), dtype=np.float32)
+        _check(lib().si_hip_q4_k_embedding_view(self._h, ggml_type, sh, len(shape), _bp(b), b.size,
+                                                token_id, _fp(y)))
+        return y[:int(shape[0])]
+
+    def gguf_quant_matvec_view_rows(self, name: str, ggml_type: int, shape: Sequence[int],
+                                    payload, row_start: int, row_count: int, input) -> np.ndarray:
+        """gguf_quant_matvec_tensor_rows over a GgufTensorView."""
+        b, x = _u8(payload), _f32(input)
+        sh = (_U64 * len(shape))(*shape)
+        y = np.empty(max(row_count, 1), dtype=np.float32)
+        _check(lib().si_hip_gguf_quant_matvec_view_rows(self._h, name.encode(), ggml_type, sh,
+                                                        len(shape), _bp(b), b.size, row_start,
+                                                        row_count, _fp(x), x.size, _fp(y)))
+        return y[:row_count]
 
     def q4_k_embedding_tensor(self, table: QuantWeight, shape: Sequence[int],
                               token_id: int) -> np.ndarray:

@@ -157,6 +157,74 @@ def test_embedding_row_and_dequantize_rejections():
     assert L.si_hip_dequantize(NULL, 7, _bp(w), 144, 256, _fp(y)) == -5
 
 
+def _shape(*dims):
+    return (C.c_uint64 * len(dims))(*dims), len(dims)
+
+
+def test_view_rows_rejections_match_reference_order():
+    """gguf_quant_matvec_tensor_rows then quant_k_matvec_tensor_rows
+    (src/metal.rs:4346-4527): each check, in the reference's order, on a
+    GgufTensorView given as (name, type, shape, payload)."""
+    L = lib()
+    w = np.zeros(10 * 144 * 4, np.uint8)
+    x = _x(1024)
+    y = _x(16)
+
+    def call(t, shape, payload_len, start, count, xl=1024, name=b"blk.0.ffn_up.weight"):
+        sh, n = shape
+        rc = L.si_hip_gguf_quant_matvec_view_rows(NULL, name, t, sh, n, _bp(w), payload_len, start,
+                                                  count, _fp(x), xl, _fp(y))
+        return rc, si_hip.last_error()
+
+    assert call(2, _shape(1024, 10), w.size, 0, 1) == (
+        -5, "GGUF tensor blk.0.ffn_up.weight has unsupported quantized type 2")
+    assert call(12, _shape(1024, 10, 1), w.size, 0, 1) == (
+        -5, "Q4_K matvec requires a rank-2 Q4_K tensor")
+    assert call(14, _shape(1024, 10), w.size, 10, 1) == (-7, "Q6_K row range is invalid")
+    assert call(13, _shape(1024, 10), w.size, 3, 8) == (-7, "Q5_K row range is invalid")
+    assert call(12, _shape(1024, 10), w.size, 0, 0) == (-7, "Q4_K row range is invalid")
+    assert call(12, _shape(1000, 10), w.size, 0, 1) == (
+        -2, "Q4_K tensor columns or input length is invalid")
+    assert call(12, _shape(1024, 10), w.size, 0, 1, xl=1023) == (
+        -2, "Q4_K tensor columns or input length is invalid")
+    # a payload that holds rows 0..8 of 10: row 9 is past it, rows 0..8 pass the
+    # checks (and then need a context)
+    assert call(12, _shape(1024, 10), 9 * 576, 9, 1) == (
+        -3, "Q4_K tensor payload is shorter than its shape")
+    assert call(12, _shape(1024, 10), 9 * 576, 0, 9)[0] == -1
+    big = (1 << 64) // 576 + 1
+    assert call(12, _shape(1024, big + 5), w.size, big, 1) == (
+        -4, "Q4_K row byte range overflows")
+
+
+def test_embedding_view_rejections_match_reference_order():
+    """q4_k_embedding_tensor (src/metal.rs:3785-3810), then
+    q4_k_embedding_row's dimension check: a table shorter than its shape
+    still serves the rows it holds."""
+    L = lib()
+    t = np.zeros(16 * 144, np.uint8)
+    y = _x(256)
+
+    def call(ty, shape, payload_len, token):
+        sh, n = shape
+        rc = L.si_hip_q4_k_embedding_view(NULL, ty, sh, n, _bp(t), payload_len, token, _fp(y))
+        return rc, si_hip.last_error()
+
+    assert call(14, _shape(256, 16), t.size, 0) == (-5, "Q4_K embedding requires a rank-2 Q4_K tensor")
+    assert call(12, _shape(256, 16, 1), t.size, 0) == (
+        -5, "Q4_K embedding requires a rank-2 Q4_K tensor")
+    assert call(12, _shape(256, 16), t.size, 16) == (-7, "Q4_K embedding token id or dimension is invalid")
+    assert call(12, _shape(257, 16), t.size, 0) == (-7, "Q4_K embedding token id or dimension is invalid")
+    assert call(12, _shape(256, 16), 10 * 144, 12) == (
+        -3, "Q4_K embedding tensor payload is shorter than its shape")
+    assert call(12, _shape(256, 16), 10 * 144, 9)[0] == -1  # held: reaches the context check
+    assert call(12, _shape(0, 16), t.size, 0) == (-2, "Q4_K embedding dimension is invalid")
+    big = (1 << 64) // 576  # 1024 columns: 576-byte rows
+    assert call(12, _shape(1024, big * 2), t.size, big + 1) == (
+        -4, "Q4_K embedding row offset overflows")
+    assert call(12, _shape(1024, big * 2), t.size, big) == (-4, "Q4_K embedding row end overflows")
+
+
 def test_weight_upload_rejections_without_gpu():
     L = lib()
     out = C.c_void_p()

@@ -153,3 +153,42 @@ def test_store_row_ranges_share_one_resident_tensor(rctx):
         assert_dot_close(c, y64, ab, what="store rows")
     finally:
         g.close()
+
+
+def test_view_rows_match_store_and_share_residency(rctx):
+    """gguf_quant_matvec_tensor_rows over a GgufTensorView (the payload bytes
+    a caller holds): the same bits as the store's call on the same rows, and
+    row ranges of one payload share one resident copy."""
+    rows, cols, mats, data = _kquant_file(31)
+    g = GgufFile(data=data)
+    x = si_hip.synth_normal(32, cols)
+    try:
+        for name, t in (("q4", Q4), ("q5", Q5), ("q6", Q6)):
+            payload = np.ascontiguousarray(mats[name])
+            s0 = rctx.residency_stats()
+            a = rctx.gguf_quant_matvec_view_rows(name, t, (cols, rows), payload, 3, 50, x)
+            b = rctx.gguf_quant_matvec_view_rows(name, t, (cols, rows), payload, 53, rows - 53, x)
+            d = _delta(s0, rctx.residency_stats())
+            assert d["uploads"] == 1 and d["hits"] == 1
+            whole = g.matvec_tensor_rows(rctx, name, 0, rows, x)
+            assert same_bits(np.concatenate([a, b]), whole[3:])
+    finally:
+        g.close()
+
+
+def test_embedding_view_is_bit_exact_and_resident(rctx):
+    rows, cols = 512, 1024
+    table = si_hip.synth_matrix(Q4, seed=8500, rows=rows, cols=cols)
+    rb = cols // 256 * 144
+    s0 = rctx.residency_stats()
+    for tok in (0, 17, rows - 1):
+        got = rctx.q4_k_embedding_view(Q4, (cols, rows), table, tok)
+        exp = O.dequantize(Q4, table[tok * rb:(tok + 1) * rb], cols)
+        assert np.array_equal(got.view(np.uint32), exp.view(np.uint32)), tok
+    d = _delta(s0, rctx.residency_stats())
+    assert d["uploads"] == 1 and d["hits"] == 2  # the table went to HBM once
+    # with residency off, the row alone is copied (same bits)
+    rctx.set_residency_budget(0)
+    got = rctx.q4_k_embedding_view(Q4, (cols, rows), table, 17)
+    exp = O.dequantize(Q4, table[17 * rb:18 * rb], cols)
+    assert np.array_equal(got.view(np.uint32), exp.view(np.uint32))
