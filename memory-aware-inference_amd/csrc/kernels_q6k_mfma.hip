@@ -239,29 +239,45 @@ __device__ __forceinline__ float q6_bound(const int (&sc)[4], float d) {
 // aa.rule, fused: each workgroup keeps the best candidate of the rows it
 // stores, and the workgroups reduce theirs through the workspace's argmax
 // area into *aa.result (argmax_device.h).
+//
+// SLICED (one vector, one matrix): a K-sliced launch (SliceArgs,
+// mfma_common.h); the LDS holds the images and metadata of the workgroup's
+// slice only, stage r of the matrix at local stage r - r_lo.
 struct ArgmaxArgs {
   uint64_t* result;
   uint32_t rule;
 };
-template <int WAVES, int DEPTH, int NTOK, bool GROUPED, bool ARGMAX = false>
+template <int WAVES, int DEPTH, int NTOK, bool GROUPED, bool ARGMAX = false, bool SLICED = false>
 __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
                                                               uint32_t nb, void* __restrict__ wsp,
                                                               SchedArgs sa, uint32_t prefetch,
-                                                              GroupArgs ga, ArgmaxArgs aa) {
+                                                              GroupArgs ga, ArgmaxArgs aa,
+                                                              SliceArgs sla) {
   static_assert(!ARGMAX || (NTOK == 1 && !GROUPED), "argmax over one matrix and vector");
+  static_assert(!SLICED || (NTOK == 1 && !GROUPED && !ARGMAX), "slices of one matrix and vector");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t slots = sa.packed & 0xffu;
-  const Layout L = layout(WAVES, DEPTH, nb, slots, NTOK);
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t nstages = (nb + 1u) / 2u;
+  // the schedule: whole and split tiles (sc), or K slices (ss)
+  Sched sc{};
+  SliceSched ss{};
+  if constexpr (SLICED)
+    ss = make_slice_sched(ntiles, sla, sa);
+  else
+    sc = make_sched(ntiles, nstages, WAVES, sa);
+  // the stages whose images the LDS holds: [st0, st0 + nst), local index st - st0
+  const uint32_t st0 = SLICED ? ss.r_lo : 0u;
+  const uint32_t nbl = SLICED ? 2u * ss.ns : nb;
+  const Layout L = layout(WAVES, DEPTH, SLICED ? 2u * ss.pstride : nb, slots, NTOK);
   const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t grp = lane >> 4, n = lane & 15u;
   const uint32_t half = grp >> 1, sub = grp & 1u;
   const uint32_t row_bytes = nb * kQ6Bytes;
-  const uint32_t ntiles = (rows + 15u) / 16u;
-  const uint32_t nstages = (nb + 1u) / 2u;
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
   uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
 
@@ -269,7 +285,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   //    img + t img_stride + 1024 b)
 #pragma unroll
   for (int t = 0; t < NTOK; ++t)
-    copy_x<WAVES>(smem, L.img + t * L.img_stride, x + (size_t)t * nb * kBlockElems, nb, wave,
+    copy_x<WAVES>(smem, L.img + t * L.img_stride,
+                  x + (size_t)t * nb * kBlockElems + (size_t)2u * st0 * kBlockElems, nbl, wave,
                   lane);
 
   // 2. this wave's pairs k = wave, wave + WAVES, ... of the workgroup's pairs
@@ -278,8 +295,13 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   //    piece 4 i + l / 16 of row l % 16; the 16 lanes whose piece would be the
   //    28th re-read the 27th (same addresses, no extra traffic).  All copies
   //    lie inside the stage's 420 bytes of their row.
-  const Sched sc = make_sched(ntiles, nstages, WAVES, sa);
-  const uint32_t npairs = sc.npairs;
+  auto pair_of = [&](uint32_t k) -> Pair {
+    if constexpr (SLICED)
+      return pair_at(ss, k);
+    else
+      return pair_at(sc, k, nstages);
+  };
+  const uint32_t npairs = SLICED ? ss.npairs : sc.npairs;
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t voff_last = n * row_bytes + (grp < 2u ? 16u * (24u + grp) : kLastPiece);
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
@@ -302,7 +324,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     return wm + (size_t)row0 * row_bytes + kStageRowBytes * pr.r;
   };
   auto issue = [&](uint32_t j) {
-    const Pair pr = pair_at(sc, wave + j * WAVES, nstages);
+    const Pair pr = pair_of(wave + j * WAVES);
     const uint32_t st = pr.r;
     uint32_t nrows;
     const uint8_t* sb = tile_at(pr, nrows);
@@ -328,7 +350,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   // reads.  Their copies then find the lines in L2.
   const uint32_t npf = DEPTH == 1 && my_pairs > 1u ? min(min(prefetch, 2u), my_pairs - 1u) : 0u;
   for (uint32_t j = 1; j <= npf; ++j) {
-    const Pair pr = pair_at(sc, wave + j * WAVES, nstages);
+    const Pair pr = pair_of(wave + j * WAVES);
     uint32_t nrows;
     const uint8_t* sb = tile_at(pr, nrows);
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -361,7 +383,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   // chunk c = 8 h + 2 t + s: MFMA t of lane group 2 h + s
 #pragma unroll
   for (int t = 0; t < NTOK; ++t)
-    build_images<WAVES>(sbase, L, nb, wave, grp, n, [](uint32_t c) {
+    build_images<WAVES>(sbase, L, nbl, wave, grp, n, [](uint32_t c) {
       return 256u * ((c >> 1) & 3u) + 64u * (2u * (c >> 3) + (c & 1u));
     }, t);
   lds_wait();
@@ -380,8 +402,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   uint64_t best = 0u;  // ARGMAX: the best candidate of the rows this lane stored
   uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
   for (uint32_t j = 0; j < my_pairs; ++j) {
-    const Pair pr = pair_at(sc, wave + j * WAVES, nstages);
-    const uint32_t st = pr.r;
+    const Pair pr = pair_of(wave + j * WAVES);
+    const uint32_t st = pr.r, ls = st - st0;  // matrix stage, LDS stage
     const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
     if (DEPTH >= 3 && later >= 2u)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kCopies));
@@ -393,10 +415,10 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     u32x4 v[13];
     lds_read_stage(qa0 + buf, qh0 + buf, sc0 + buf, v);
     if (j + DEPTH < my_pairs) issue(j + DEPTH);  // the buffer just read is free again
-    lds_read_images(sbase + L.img + 2048u * st + 16u * n, kActiveLanes, A);
+    lds_read_images(sbase + L.img + 2048u * ls + 16u * n, kActiveLanes, A);
     u32x2 ex;
     uint32_t cnt;
-    lds_read_expo(sbase + L.expo + 8u * st, ex, cnt);
+    lds_read_expo(sbase + L.expo + 8u * ls, ex, cnt);
     const int e0 = __builtin_amdgcn_readfirstlane(ex[0]);
     const int e1 = __builtin_amdgcn_readfirstlane(ex[1]);
 
@@ -471,7 +493,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     const uint32_t counts = __builtin_amdgcn_readfirstlane(cnt);
     uint32_t redo = 0u;
     if (counts != 0u) {
-      const uint32_t list = sbase + L.expo + L.side_off + 2u * kSideBytes * st;
+      const uint32_t list = sbase + L.expo + L.side_off + 2u * kSideBytes * ls;
       add_listed<2>(list, counts, grp, pp, q6_owner, [&](auto b, uint32_t i) {
         return decltype(b)::value == 0
                    ? q6_side_weight(q0[0], q0[1], q0[2], q0[3], sc_0[0], sc_0[1], sc_0[2], sc_0[3],
@@ -488,8 +510,11 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     const float rowsum = sum_lane_groups(pp[0] + pp[1]);
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
-    hand_off<1, ARGMAX>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws, fail,
-                        &best, aa.rule);
+    if constexpr (SLICED)
+      hand_off_slice(sbase, L, ss, pr, rowsum, lane, rows, y, ws, fail);
+    else
+      hand_off<1, ARGMAX>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws, fail,
+                          &best, aa.rule);
   }
   if (fail != 0u) report_device_error(wsp, fail);
   if constexpr (ARGMAX) {
@@ -535,9 +560,81 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
     return true;
   }
   hipLaunchKernelGGL((q6k_matvec_mfma<W, D, NT, G, AM>), dim3(grid), dim3(W * 64), lds, s, w, x,
-                     y, rows, nb, ws.ptr, sa, D == 1 ? prefetch : 0u, ga, aa);
+                     y, rows, nb, ws.ptr, sa, D == 1 ? prefetch : 0u, ga, aa, SliceArgs{});
   *err = hipGetLastError();
   return true;
+}
+
+// A K-sliced launch in S slices (false when the shape or the LDS does not fit).
+template <int W, int D>
+bool launch_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+                   uint32_t S, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t nstages = nb / 2u;
+  SliceShape sh;
+  if (!slice_shape(ntiles, nstages, S, (uint32_t)cu_count(), ws.bytes, &sh)) return false;
+  const uint32_t slots = ring_slots(W, D, sh.tiles_per_group, sh.ns_max);
+  static const int pf_env = env_int("SI_HIP_Q6K_PREFETCH", -1);
+  const uint32_t prefetch = D == 1 && pf_env > 0 ? (uint32_t)pf_env : 0u;
+  const uint32_t lds = layout(W, D, 2u * sh.ns_max, slots).total + (prefetch ? 256u : 0u);
+  if (lds > kLdsBytes || slots > 0xffu || sh.groups > 0xffffu) return false;
+  SchedArgs sa{};
+  sa.packed = (sh.groups << 16) | slots;
+  sa.m_slots = div_magic(slots);
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, 1, false, false, true>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
+  if (attr != hipSuccess) {
+    *err = attr;
+    return true;
+  }
+  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, 1, false, false, true>), dim3(sh.groups), dim3(W * 64),
+                     lds, s, w, x, y, rows, nb, ws.ptr, sa, prefetch, GroupArgs{}, ArgmaxArgs{},
+                     sh.args);
+  *err = hipGetLastError();
+  return true;
+}
+
+// Slices for a one-vector launch, or 0.  A workgroup builds the images of
+// the blocks it reads before its first stage, about 0.07-0.1 us per block,
+// and only its first stages (one per wave, plus a pair touched into L2) are
+// in flight meanwhile; slicing shrinks the build S-fold but rounds each
+// slice's stages and each workgroup's tiles up.  Measured (MI355X, us):
+//   rows x cols      unsliced  S = 2   S = 4
+//   640 x 17408        12.1     11.0     8.3
+//   2560 x 17408       18.4     19.1    15.2
+//   2048 x 16384       13.3     10.8    10.0
+//   512 x 12288        10.9      8.3     7.3
+//   4096 x 14336       16.2     17.0    16.3
+//   5120 x 17408       24.5     27.2    25.7
+//   8192 x 28672       57.0     52.4    56.0
+//   2048 x 32768       50.4     20.2
+//   2560 x 9728         9.5              9.7
+// So: four slices when the unsliced launch's busiest workgroup has at most
+// two rounds of pairs (24; its build is then exposed) and slicing adds it
+// none or the rows are long (48 blocks or more); with more pairs, only when
+// the unsliced images leave room for fewer than eight waves (very long
+// rows), in the fewest slices that add no pairs to the busiest workgroup.
+uint32_t q6_slices(uint32_t ntiles, uint32_t nb, size_t ws_bytes) {
+  static const int env = env_int("SI_HIP_Q6K_SLICES", -1);
+  if (env >= 0) return (uint32_t)env;
+  const uint32_t nst = nb / 2u;
+  if (nst < 16u) return 0u;
+  const uint64_t cus = (uint64_t)cu_count();
+  // the unsliced launch's busiest workgroup (launch_shape's choice at 12 waves)
+  const LaunchShape ls = launch_shape(ntiles, nst, 12u, ws_bytes, 1u);
+  const uint64_t g1 = ls.groups;
+  const uint64_t q = ntiles / g1, lp = (ntiles - q * g1) * nst;
+  const uint64_t most0 = ls.split ? q * nst + (lp + g1 - 1u) / g1 : (ntiles + g1 - 1u) / g1 * nst;
+  auto most = [&](uint32_t S) {  // the busiest sliced workgroup's pairs
+    const uint64_t gs = std::min<uint64_t>(ntiles, cus / S);
+    return (ntiles + gs - 1u) / gs * ((nst + S - 1u) / S);
+  };
+  if (most0 <= 24u) return most(4u) <= most0 || nb >= 48u ? 4u : 0u;
+  if (layout(8u, 1u, nb, 2u).total <= kLdsBytes) return 0u;
+  for (uint32_t S : {2u, 4u})
+    if (most(S) <= most0) return S;
+  return 0u;
 }
 
 // even nb (4-byte aligned rows and stages); in-tile offsets (16 rows) and the
@@ -564,6 +661,10 @@ bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
     case 4: return launch_wd<6, 2>(w, x, y, rows, nb, ws, s, err);
     default: break;
   }
+  const uint32_t S = q6_slices((rows + 15u) / 16u, nb, ws.bytes);
+  if (S >= 2u && (launch_sliced<12, 1>(w, x, y, rows, nb, S, ws, s, err) ||
+                  launch_sliced<8, 1>(w, x, y, rows, nb, S, ws, s, err)))
+    return true;
   return launch_wd<12, 1>(w, x, y, rows, nb, ws, s, err) || launch_wd<10, 1>(w, x, y, rows, nb, ws, s, err) ||
          launch_wd<8, 1>(w, x, y, rows, nb, ws, s, err) || launch_wd<4, 1>(w, x, y, rows, nb, ws, s, err);
 }

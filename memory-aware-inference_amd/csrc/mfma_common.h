@@ -850,6 +850,165 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
   }
 }
 
+// K-sliced launches, for matrices of few tiles and long rows (a down
+// projection): the stages of every tile are cut into S slices as even as the
+// stage count allows, and workgroup g = S tg + s works on slice s of the tiles
+// tg, tg + Gs, tg + 2 Gs, ... (Gs = G / S).  A workgroup then holds the
+// activation images of its slice only, so it builds a 1 / S share of them
+// before its first stage.  The S slice sums of a tile meet in the workspace:
+// the wave that completes a slice publishes its 16 sums in entry
+// tile * S + s and counts them on the tile's counter, and the wave that
+// completes the count adds the S entries in slice order and stores the rows
+// (deterministic).  Launch constants: S, Gs, the slices' stage counts
+// (ns_lo, and ns_lo + 1 for slices s < rem) and their division constants.
+struct SliceArgs {
+  uint32_t slices, m_slices, tgroups, m_tgroups;
+  uint32_t ns_lo, rem, m_ns_lo, m_ns_hi;
+};
+struct SliceSched {
+  uint32_t s, tg, r_lo, ns, npairs;
+  uint32_t slices, tgroups;
+  uint32_t pstride;  // partials per ring slot: the longest slice's stage count
+  FastDiv by_ns, by_slots;
+};
+__device__ __forceinline__ SliceSched make_slice_sched(uint32_t ntiles, const SliceArgs& a,
+                                                       const SchedArgs& sa) {
+  SliceSched s;
+  const uint32_t g = blockIdx.x;
+  const uint32_t tg = quo(g, FastDiv{a.slices, a.m_slices});
+  const uint32_t sl = g - tg * a.slices;
+  const bool longer = sl < a.rem;
+  const uint32_t ntl =
+      tg < ntiles ? quo(ntiles - 1u - tg, FastDiv{a.tgroups, a.m_tgroups}) + 1u : 0u;
+  s.s = sl;
+  s.tg = tg;
+  s.ns = a.ns_lo + (longer ? 1u : 0u);
+  s.r_lo = sl * a.ns_lo + min(sl, a.rem);
+  s.npairs = ntl * s.ns;
+  s.slices = a.slices;
+  s.tgroups = a.tgroups;
+  s.pstride = a.ns_lo + (a.rem != 0u ? 1u : 0u);
+  s.by_ns = FastDiv{s.ns, longer ? a.m_ns_hi : a.m_ns_lo};
+  s.by_slots = FastDiv{sa.packed & 0xffu, sa.m_slots};
+  return s;
+}
+// Pair k of a sliced workgroup: local tile lt = k / ns, stage r_lo + k % ns;
+// [lo, hi) is the slice.
+__device__ __forceinline__ Pair pair_at(const SliceSched& s, uint32_t k) {
+  Pair p;
+  const uint32_t lt = quo(k, s.by_ns);
+  p.tile = s.tg + s.tgroups * lt;
+  p.r = s.r_lo + (k - lt * s.ns);
+  p.lt = lt;
+  p.lo = s.r_lo;
+  p.hi = s.r_lo + s.ns;
+  return p;
+}
+
+// hand_off for a sliced launch (one matrix): the wave that completes the
+// workgroup's slice of the tile adds its partials in stage order, frees the
+// ring slot, publishes the 16 sums and counts them; the wave that completes
+// the tile's count of S adds the S entries in slice order (lane group k
+// reads slice k of each batch of four; the first batch is read before the
+// count goes out, so the last slice waits about one memory round trip),
+// stores the rows and returns the entries and the counter to their empty
+// state.  The wait for an entry is bounded like hand_off's.
+__device__ __forceinline__ void hand_off_slice(uint32_t sbase, const Layout& L,
+                                               const SliceSched& sc, const Pair& pr, float rowsum,
+                                               uint32_t lane, uint32_t rows, float* __restrict__ y,
+                                               SplitWs ws, uint32_t& fail) {
+  const uint32_t slots = sc.by_slots.d;
+  const uint32_t slot = pr.lt - quo(pr.lt, sc.by_slots) * slots;
+  wait_slot(sbase + L.owner + 4u * slot, pr.lt, fail);
+  const uint32_t pbase = sbase + L.part + 64u * sc.pstride * slot + 4u * (lane & 15u);
+  if ((lane >> 4) == 0u) lds_write_b32(pbase + 64u * (pr.r - pr.lo), __float_as_uint(rowsum));
+  uint32_t old = 0u;
+  if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);
+  const uint32_t done = __builtin_amdgcn_readlane(old, 0);
+  if (done != sc.ns - 1u) return;
+  float sum = 0.0f;
+  for (uint32_t k = 0; k < sc.ns; ++k) sum += __uint_as_float(lds_read_b32(pbase + 64u * k));
+  // the partials are in registers: the slot can take the workgroup's next tile
+  if (lane == 0u) {
+    lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
+    lds_write_b32(sbase + L.owner + 4u * slot, pr.lt + slots);
+  }
+  // (the lane's indices are taken afresh behind a compiler barrier, so that
+  // none of this path's addresses stays live through the caller's loop)
+  uint32_t ln = lane;
+  asm volatile("" : "+v"(ln));
+  const uint32_t grp = ln >> 4, n = ln & 15u;
+  const uint32_t S = sc.slices;
+  float* const ent = ws.part + (size_t)pr.tile * S * 16u + n;  // slice k at ent + 16 k
+  if (grp == 0u) store_coherent(ent + 16u * sc.s, sum);
+  auto fetch = [&](uint32_t k, float& v) {
+    if (k == sc.s)
+      v = sum;
+    else if (k < S)
+      v = load_coherent(ent + 16u * k);
+  };
+  float v = 0.0f;
+  fetch(grp, v);
+  const uint32_t force = __builtin_amdgcn_readfirstlane(give_up_polls(ws.cnt));
+  uint32_t before = 0u;
+  if (lane == 0u)
+    before = __hip_atomic_fetch_add(ws.cnt + pr.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  before = __builtin_amdgcn_readlane(before, 0);
+  if (before + 1u != S) return;
+  float total = 0.0f;
+  for (uint32_t base = 0; base < S; base += 4u) {
+    const uint32_t k = base + grp;
+    if (base != 0u) fetch(k, v);
+    for (uint32_t spin = 0;; ++spin) {
+      const bool missing =
+          k < S && k != sc.s && (force != 0u || __float_as_uint(v) == kPartEmpty);
+      if (!__builtin_amdgcn_ballot_w64(missing)) break;
+      if (spin == (force != 0u ? force : (1u << 22))) {
+        fail = kDevErrCombineWait;
+        break;
+      }
+      __builtin_amdgcn_s_sleep(1);
+      if (missing) fetch(k, v);
+    }
+#pragma unroll
+    for (uint32_t j = 0; j < 4u; ++j) {
+      const float vj = __shfl(v, (int)(n + 16u * j), 64);
+      if (base + j < S) total += vj;
+    }
+    if (k < S) store_coherent(ent + 16u * k, __uint_as_float(kPartEmpty));
+  }
+  const uint32_t row = pr.tile * 16u + n;
+  if (grp == 0u && row < rows) y[row] = total;
+  if (lane == 0u)
+    (void)__hip_atomic_exchange(ws.cnt + pr.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The launch constants of a sliced launch of ntiles tiles of nstages stages
+// in S slices over at most `cus` workgroups, or false when the shape does not
+// fit: every slice at least one stage, the tiles' counters and S entries each
+// inside the workspace (below the argmax area), the quotients exact.
+struct SliceShape {
+  uint32_t groups, tiles_per_group, ns_max;
+  SliceArgs args;
+};
+inline bool slice_shape(uint32_t ntiles, uint32_t nstages, uint32_t S, uint32_t cus,
+                        size_t ws_bytes, SliceShape* out) {
+  if (S < 2u || S > 64u || nstages < S || ntiles == 0u || cus < S) return false;
+  const uint32_t gs = min(ntiles, cus / S);
+  if ((size_t)ntiles * 4u + 64u > kCounterBytes ||
+      kCounterBytes + (size_t)ntiles * S * 64u + 4096u > ws_bytes)
+    return false;
+  const uint32_t ns_lo = nstages / S, rem = nstages % S;
+  out->groups = gs * S;
+  out->tiles_per_group = (ntiles + gs - 1u) / gs;
+  out->ns_max = ns_lo + (rem != 0u ? 1u : 0u);
+  // pair quotients: k < tiles_per_group * ns_max, times ns
+  if ((uint64_t)out->tiles_per_group * out->ns_max * out->ns_max >= (1ull << 32)) return false;
+  out->args = SliceArgs{S, div_magic(S), gs, div_magic(gs), ns_lo, rem, div_magic(ns_lo),
+                        div_magic(ns_lo + 1u)};
+  return true;
+}
+
 inline int env_int(const char* name, int fallback) {
   const char* v = std::getenv(name);
   return v ? std::atoi(v) : fallback;

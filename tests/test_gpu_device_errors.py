@@ -12,8 +12,9 @@ failure reports of kernels that cannot finish their work correctly.
   * the embedding checks in q4_k_embedding_tensor's order (src/metal.rs:
     3785-3810): a table shorter than its shape serves the rows it holds;
   * bounded waits driven to give up by the test hook (every kernel still
-    ends): the split-tile combine and the argmax reduction report, the call
-    fails with SI_HIP_ERR_DEVICE, and the next calls are correct again.
+    ends): the split-tile and K-slice combines and the argmax reduction
+    report, the call fails with SI_HIP_ERR_DEVICE, and the next calls are
+    correct again.
 """
 import ctypes as C
 import struct
@@ -225,6 +226,29 @@ def test_forced_give_up_in_split_combine_reports(give_up):
         assert e.value.status == -9 and "split tile" in e.value.message
         ctx.debug_set_wait_give_up(0)
         _, y64, ab = O.matvec(Q4, w, rows, cols, x, threads=8)
+        assert_dot_close(ctx.gguf_quant_matvec_weight(W, rows, cols, x), y64, ab,
+                         what="after the forced give-up")
+    finally:
+        W.free()
+
+
+def test_forced_give_up_in_sliced_combine_reports(give_up):
+    """2560 x 17408 Q6_K (a down projection) runs K-sliced: with the hook set,
+    the wave that completes a tile's count gives up waiting for the other
+    slices' sums after 16 polls and reports; with it cleared, the same call
+    is within its bound again (the entries and counters were restored)."""
+    ctx = give_up
+    rows, cols = 2560, 17408
+    w = si_hip.synth_matrix(Q6, seed=7650, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(7651, cols)
+    W = ctx.upload_quant_weight_private(w, Q6)
+    try:
+        log("forced give-up: sliced combine")
+        with pytest.raises(si_hip.HipError) as e:
+            ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        assert e.value.status == -9 and "split tile" in e.value.message
+        ctx.debug_set_wait_give_up(0)
+        _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
         assert_dot_close(ctx.gguf_quant_matvec_weight(W, rows, cols, x), y64, ab,
                          what="after the forced give-up")
     finally:

@@ -1,0 +1,129 @@
+"""GPU: Q6_K matvecs of long rows over few tiles (down projections), which
+run K-sliced: each workgroup takes one of S slices of every tile's stages
+and holds only that slice's activation images, and a tile's S slice sums
+meet in the workspace, added in slice order.
+
+The launch takes four slices when an unsliced launch would give its busiest
+workgroup at most 24 (tile, stage) pairs (K of 8192 or more), and two or
+four when the unsliced images would leave room for fewer than eight waves
+(K of about 23,000 or more) and slicing adds no pairs.  The bar is the north
+star's: every row within 2e-5 * sum|w*x| of the f64 dot, +-inf / NaN rows
+where per-weight f32 products give them, and the same bits on every call.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import si_hip
+from test_gpu_parity import _category, assert_dot_close, same_bits
+
+pytestmark = pytest.mark.gpu
+
+Q4, Q6 = 12, 14
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+# (rows, cols): one tile (nb 48: four slices of 6 stages); a partial last
+# tile and 25 stages (slices of 7, 6, 6, 6); 160 tiles of the down
+# projection's K (three per workgroup, slices of 9, 9, 8, 8); 40 tiles (a
+# tensor-parallel shard); the largest block count the matrix-core kernels
+# take (128: two slices of 32 stages); one tile of 108 blocks
+SHAPES = [(16, 12288), (1000, 12800), (2560, 17408), (640, 17408), (2048, 32768), (3, 27648)]
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_sliced_q6_k_within_tolerance(hip_ctx, rows, cols):
+    log(f"sliced q6_k {rows}x{cols}")
+    w = si_hip.synth_matrix(Q6, seed=rows * 7 + cols, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(rows + cols, cols)
+    _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, Q6)
+    try:
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        worst = assert_dot_close(y, y64, ab, what=f"{rows}x{cols}")
+        log(f"  worst error / bound = {worst:.4f}")
+        # deterministic: the slices are added in slice order on every call
+        assert same_bits(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x), y)
+    finally:
+        W.free()
+
+
+def test_sliced_special_activations_in_every_slice(hip_ctx):
+    """Each slice of a 16384-column row (32 stages, 8 per slice) holds one
+    kind of special block: huge values (fixed point would overflow), side
+    elements (tiny next to their block's maximum), subnormals, zeros; then one
+    infinite or NaN activation in one slice at a time."""
+    rows, cols = 200, 16384
+    w = si_hip.synth_matrix(Q6, seed=4242, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, Q6)
+    base = si_hip.synth_normal(4243, cols)
+    try:
+        x = base.copy()
+        x[100:140] = np.float32(3e30)            # slice 0
+        x[4096 + 7] = np.float32(1e-9)           # slice 1: side elements
+        x[4096 + 300:4096 + 303] = np.float32(-2e-10)
+        x[8192:8192 + 256] = np.float32(1e-41)   # slice 2: a subnormal block
+        x[12288 + 512:12288 + 768] = 0.0         # slice 3: a zero block
+        _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        assert_dot_close(y, y64, ab, what="special blocks")
+        for k, v in [(50, np.inf), (4200, -np.inf), (9000, np.nan), (16383, np.inf)]:
+            x = base.copy()
+            x[k] = v
+            y32, _, _ = O.matvec(Q6, w, rows, cols, x, threads=8)
+            y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+            assert np.array_equal(_category(y), _category(y32)), f"x[{k}] = {v}"
+    finally:
+        W.free()
+
+
+def test_sliced_and_split_launches_interleaved(hip_ctx):
+    """Sliced launches share the workspace's tile counters and entries with
+    the split launches of other shapes: each must find them reset, in any
+    order and at any grid size."""
+    cases = [(Q6, 2560, 17408), (Q4, 17408, 5120), (Q6, 16, 12288), (Q6, 151936 // 8, 5120),
+             (Q6, 5120, 17408), (Q4, 1600, 17408), (Q6, 1000, 12800), (Q6, 2048, 32768)]
+    mats = {}
+    for t, rows, cols in cases:
+        w = si_hip.synth_matrix(t, seed=rows + cols + t, rows=rows, cols=cols, threads=8)
+        x = si_hip.synth_normal(rows ^ cols, cols)
+        _, y64, ab = O.matvec(t, w, rows, cols, x, threads=8)
+        mats[(t, rows, cols)] = (hip_ctx.upload_quant_weight_private(w, t), x, y64, ab)
+    try:
+        for key in cases * 2:
+            W, x, y64, ab = mats[key]
+            t, rows, cols = key
+            y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+            assert_dot_close(y, y64, ab, what=f"type {t} {rows}x{cols}")
+    finally:
+        for W, *_ in mats.values():
+            W.free()
+
+
+def test_sliced_down_in_fused_mlp(hip_ctx):
+    """A fused MLP whose Q6_K down projection (17408 -> 2560) runs sliced:
+    the output against the oracle's down projection of the device's own
+    intermediate (bit-identical to the separate gate/up call's)."""
+    inter, hidden = 17408, 2560
+    g = si_hip.synth_matrix(Q4, seed=91, rows=inter, cols=hidden, threads=8)
+    u = si_hip.synth_matrix(Q4, seed=92, rows=inter, cols=hidden, threads=8)
+    d = si_hip.synth_matrix(Q6, seed=93, rows=hidden, cols=inter, threads=8)
+    x = si_hip.synth_normal(94, hidden)
+    G = hip_ctx.upload_quant_weight_private(g, Q4)
+    U = hip_ctx.upload_quant_weight_private(u, Q4)
+    D = hip_ctx.upload_quant_weight_private(d, Q6)
+    try:
+        h = hip_ctx.q4_k_fused_gate_up_weights(G, U, inter, hidden, x)
+        y = hip_ctx.gguf_quant_fused_mlp_weights(G, U, D, inter, hidden, hidden, x)
+        # the down projection of the device's own h, so only the down's error counts
+        _, y64, ab = O.matvec(Q6, d, hidden, inter, h, threads=8)
+        assert_dot_close(y, y64, ab, what="fused MLP down")
+    finally:
+        for m in (G, U, D):
+            m.free()
