@@ -127,3 +127,39 @@ def test_sliced_down_in_fused_mlp(hip_ctx):
     finally:
         for m in (G, U, D):
             m.free()
+
+
+def test_token_stage_combines_interleaved(hip_ctx):
+    """Q4_K matmul-many of 3 to 16 vectors (one workgroup per stage and tile
+    group, stage sums through the workspace's scratch) between K-sliced Q6_K
+    and split Q4_K launches that share the tile counters: every call matches
+    the oracle and repeats its own bits."""
+    mats = {}
+    for t, rows, cols in ((Q4, 17408, 5120), (Q4, 1040, 5120), (Q6, 2560, 17408),
+                          (Q4, 1600, 17408)):
+        w = si_hip.synth_matrix(t, seed=rows + cols, rows=rows, cols=cols, threads=8)
+        mats[(t, rows, cols)] = (w, hip_ctx.upload_quant_weight_private(w, t))
+    seq = [((Q4, 17408, 5120), 16), ((Q6, 2560, 17408), 1), ((Q4, 1040, 5120), 4),
+           ((Q4, 1600, 17408), 1), ((Q4, 17408, 5120), 3), ((Q4, 1040, 5120), 11)]
+    try:
+        first = {}
+        for rep in range(2):
+            for key, batch in seq:
+                t, rows, cols = key
+                w, W = mats[key]
+                X = si_hip.synth_normal(rows * batch + cols, batch * cols).reshape(batch, cols)
+                log(f"interleaved: type {t} {rows}x{cols} batch {batch}, pass {rep}")
+                if batch == 1:
+                    outs = [hip_ctx.gguf_quant_matvec_weight(W, rows, cols, X[0])]
+                else:
+                    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+                if rep == 0:
+                    for b in sorted({0, batch // 2, batch - 1}):
+                        _, y64, ab = O.matvec(t, w, rows, cols, X[b], threads=8)
+                        assert_dot_close(outs[b], y64, ab, what=f"{key} batch {batch} vector {b}")
+                    first[(key, batch)] = [o.copy() for o in outs]
+                else:
+                    assert all(same_bits(a, b) for a, b in zip(outs, first[(key, batch)]))
+    finally:
+        for _, W in mats.values():
+            W.free()
