@@ -42,7 +42,8 @@ def log(msg: str) -> None:
 
 
 def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: int,
-                copies: int = NCOPIES, seed: int = 17, detail: bool = False) -> dict:
+                copies: int = NCOPIES, seed: int = 17, detail: bool = False,
+                graph: bool = True) -> dict:
     nbytes = rows * (cols // 256) * si_hip.BLOCK_BYTES[ggml_type]
     weights = []
     host0 = None  # copy 0's host bytes, for the borrowed-bytes timing
@@ -72,9 +73,11 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
     ctx.event_record(1)
     ms = ctx.event_elapsed_ms(0, 1)
     ctx.synchronize()
-    graph_ms = time_graph_repeat(ctx, lib, harr, copies, rows, cols, d_x, d_y, steps, warmup)
-    extra = {"graph_us_per_call": round(graph_ms * 1000.0, 3),
-             "graph_gb_per_s": round(nbytes / (graph_ms * 1e-3) / 1e9, 1)}
+    extra = {}
+    if graph:
+        graph_ms = time_graph_repeat(ctx, lib, harr, copies, rows, cols, d_x, d_y, steps, warmup)
+        extra = {"graph_us_per_call": round(graph_ms * 1000.0, 3),
+                 "graph_gb_per_s": round(nbytes / (graph_ms * 1e-3) / 1e9, 1)}
     if detail:
         extra.update(call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, steps, host0))
         extra["floor"] = stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps, warmup)
@@ -95,12 +98,14 @@ def stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps: int, warmup:
     """Back-to-back launches of si_hip_stream_probe over the same resident
     copies: the matvec kernel's weight copies alone (its grid, 12 waves per
     CU, 16-row x 64-byte buffer->LDS copies, one stage in flight per wave), the
-    same with the nontemporal bit, and an empty kernel of the launch shape.
-    The matvec cannot beat the first on this copy path."""
+    same with the nontemporal bit, an empty kernel of the launch shape, and
+    the same stages read as 4-row x 256-byte copies.  The matvec cannot beat
+    the first on this copy path."""
     out = {}
     per_graph = copies * max(1, GRAPH_CALLS // copies)
     reps = max(1, steps // per_graph)
-    for mode, name in ((0, "copies_us"), (1, "copies_nontemporal_us"), (2, "empty_launch_us")):
+    for mode, name in ((0, "copies_us"), (1, "copies_nontemporal_us"), (2, "empty_launch_us"),
+                       (3, "copies_4x256_us")):
         # recorded into a HIP graph and replayed, so that host launch cost
         # does not pace the short launches
         ctx.capture_begin()
@@ -510,6 +515,9 @@ def main() -> int:
                          f"{','.join(CONFIG_NAMES)} (default: {','.join(DEFAULT_CONFIGS)}; "
                          "the flag alone: all)")
     ap.add_argument("--no-configs", action="store_true", help="time the headline only")
+    ap.add_argument("--back-to-back-only", action="store_true",
+                    help="time the headline's back-to-back calls alone (no graph, isolated, "
+                         "host-call or floor legs), for a kernel trace of exactly those calls")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time device-to-device copies of the matrix size (the yardstick "
                          "that scales HBM traffic counters)")
@@ -523,7 +531,8 @@ def main() -> int:
     ctx = si_hip.HipContext(0)
     rows, cols = 17408, 5120
     log(f"timing Q4_K {rows}x{cols}, {args.steps} steps, {NCOPIES} resident copies")
-    head = time_matvec(ctx, 12, rows, cols, args.steps, args.warmup, detail=True)
+    b2b = args.back_to_back_only
+    head = time_matvec(ctx, 12, rows, cols, args.steps, args.warmup, detail=not b2b, graph=not b2b)
     log(f"  {head['us_per_call']} us/call, {head['gb_per_s']} GB/s")
     out = {
         "metric": METRIC,
@@ -548,14 +557,10 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": head["gb_per_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": head["frac_of_peak"],
                      "traffic": profiled_traffic()},
-        "graph_us_per_call": head["graph_us_per_call"],
-        "graph_gb_per_s": head["graph_gb_per_s"],
-        "isolated_call_us": head["isolated_call_us"],
-        "host_wall_us_per_call": head["host_wall_us_per_call"],
-        "host_wall_note": head["host_wall_note"],
     }
-    for k in ("floor", "borrowed_bytes_host_wall_us_per_call", "borrowed_bytes_first_call_us",
-              "borrowed_bytes_note"):
+    for k in ("graph_us_per_call", "graph_gb_per_s", "isolated_call_us", "host_wall_us_per_call",
+              "host_wall_note", "floor", "borrowed_bytes_host_wall_us_per_call",
+              "borrowed_bytes_first_call_us", "borrowed_bytes_note"):
         if k in head:
             out[k] = head[k]
     if args.copy_probe:

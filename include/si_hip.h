@@ -287,8 +287,9 @@ int si_hip_embedding_device(si_hip_context *ctx, const si_hip_quant_weight *tabl
  * copies of the one-vector matrix-core kernel -- its grid, twelve waves per
  * CU, 16-row x 64-byte buffer->LDS copies, one stage in flight per wave --
  * and no arithmetic.  mode 0: the kernels' default cache policy; 1: the
- * nontemporal bit; 2: an empty kernel of the same launch shape.  Timed with
- * the event slots, it bounds what the matvec can reach on its copy path. */
+ * nontemporal bit; 2: an empty kernel of the same launch shape; 3: the same
+ * stages read as 4-row x 256-byte copies.  Timed with the event slots, it
+ * bounds what the matvec can reach on its copy path. */
 int si_hip_stream_probe(si_hip_context *ctx, const si_hip_quant_weight *const *weights, size_t n,
                         size_t rows, size_t columns, uint32_t mode, size_t iters);
 

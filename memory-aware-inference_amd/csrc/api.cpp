@@ -1875,7 +1875,7 @@ int si_hip_quant_matvec_device_repeat(si_hip_context *ctx, const si_hip_quant_we
 int si_hip_stream_probe(si_hip_context *ctx, const si_hip_quant_weight *const *ws, size_t n,
                         size_t rows, size_t cols, uint32_t mode, size_t iters) {
   if (!ws || n == 0) return fail(SI_HIP_ERR_NULL, "stream probe needs at least one weight");
-  if (mode > sihip::kProbeEmpty) return fail(SI_HIP_ERR_RANGE, "unknown stream probe mode %u", mode);
+  if (mode > sihip::kProbeWide) return fail(SI_HIP_ERR_RANGE, "unknown stream probe mode %u", mode);
   for (size_t i = 0; i < n; ++i) {
     int rc = validate_device_matvec(ws[i], rows, cols, 1);
     if (rc) return rc;

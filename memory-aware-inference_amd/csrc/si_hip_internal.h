@@ -132,6 +132,7 @@ enum ProbeMode : uint32_t {
   kProbeDefault = 0,      // the kernels' copies, default cache policy
   kProbeNontemporal = 1,  // the same with the nontemporal bit
   kProbeEmpty = 2,        // the launch shape with no work
+  kProbeWide = 3,         // the same stages as 4-row x 256-byte copies
 };
 hipError_t launch_stream_probe(uint32_t mode, const uint8_t* w, uint32_t rows, uint32_t cols,
                                uint32_t block_bytes, uint32_t cus, hipStream_t s);

@@ -22,10 +22,10 @@ def test_probe_modes(hip_ctx, t):
     W = [hip_ctx.upload_quant_weight_private(si_hip.synth_matrix(t, seed=9000 + i, rows=rows,
                                                                  cols=cols), t) for i in range(2)]
     try:
-        for mode in (0, 1, 2):
+        for mode in (0, 1, 2, 3):
             assert _probe(hip_ctx, W, rows, cols, mode) == 0, si_hip.last_error()
         hip_ctx.synchronize()
-        assert _probe(hip_ctx, W, rows, cols, 3) == -7
+        assert _probe(hip_ctx, W, rows, cols, 4) == -7
         assert _probe(hip_ctx, W, rows, cols + 256, 0) != 0  # byte length mismatch
     finally:
         for w in W:
