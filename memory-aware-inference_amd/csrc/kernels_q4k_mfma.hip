@@ -413,24 +413,26 @@ __device__ __forceinline__ float k4_bound(const BlockQ4& w) {
 }
 
 // One vector's partial dot of the lane's row over stage s (blocks 4 s ..
-// 4 s + nlive - 1): the MFMA digit sums, the side elements' exact products,
-// the rounded blocks' check, and the exact path for blocks that need it,
-// summed over the lane groups (every lane of a row gets the row's sum).
+// 4 s + nlive - 1), whose images and metadata sit at LDS stage ls: the MFMA
+// digit sums, the side elements' exact products, the rounded blocks' check,
+// and the exact path for blocks that need it, summed over the lane groups
+// (every lane of a row gets the row's sum).
 template <int QB>
 __device__ __forceinline__ float stage_rowsum(const StageRegs<QB>& v, uint32_t sbase,
-                                              const Layout& L, uint32_t s, uint32_t nlive,
-                                              uint32_t grp, uint32_t n, i32x4 (&A)[8],
-                                              bool hi_units, int bsh, uint32_t rot_lo,
-                                              uint32_t rot_hi, const float* __restrict__ x) {
+                                              const Layout& L, uint32_t ls, uint32_t s,
+                                              uint32_t nlive, uint32_t grp, uint32_t n,
+                                              i32x4 (&A)[8], bool hi_units, int bsh,
+                                              uint32_t rot_lo, uint32_t rot_hi,
+                                              const float* __restrict__ x) {
   u32x2 xs[4];
   i32x4 ex;
   uint32_t cnt;
-  lds_read_sums(sbase + L.xsum + 128u * s + 8u * grp, sbase + L.expo + 16u * s, xs, ex, cnt);
+  lds_read_sums(sbase + L.xsum + 128u * ls + 8u * grp, sbase + L.expo + 16u * ls, xs, ex, cnt);
   float part[4];
   bool bad_any = false;
 #pragma unroll
   for (int h = 0; h < 2; ++h) {
-    lds_read_images8(sbase + L.img + 4096u * s + 2048u * h + 16u * n, kActiveLanes, A);
+    lds_read_images8(sbase + L.img + 4096u * ls + 2048u * h + 16u * n, kActiveLanes, A);
 #pragma unroll
     for (int b2 = 0; b2 < 2; ++b2) {
       const int b = 2 * h + b2;
@@ -448,7 +450,7 @@ __device__ __forceinline__ float stage_rowsum(const StageRegs<QB>& v, uint32_t s
   const uint32_t counts = live_counts(__builtin_amdgcn_readfirstlane(cnt), nlive);
   uint32_t redo = 0u;
   if (counts != 0u) {
-    const uint32_t list = sbase + L.expo + L.side_off + 4u * kSideBytes * s;
+    const uint32_t list = sbase + L.expo + L.side_off + 4u * kSideBytes * ls;
     add_listed<4>(list, counts, grp, part, [](uint32_t i) { return i >> 6; },
                   [&](auto b, uint32_t i) { return v.template side_weight<decltype(b)::value>(i); });
     redo = rounded_redo<4>(list, counts, grp, part, [&](auto b) {
@@ -469,28 +471,44 @@ __device__ __forceinline__ float stage_rowsum(const StageRegs<QB>& v, uint32_t s
 // GROUPED: the rows are those of ga.count matrices with one K, one after the
 // other (every matrix but the last a whole number of 16-row tiles), and tile
 // t's weights are those of the matrix whose tiles reach past t.
-template <int WAVES, int DEPTH, int MATS, int NTOK, int QB, bool GROUPED>
+//
+// SLICED (one matrix, one vector): a K-sliced launch (SliceArgs,
+// mfma_common.h); the LDS holds the images and metadata of the workgroup's
+// slice only, stage s of the matrix at local stage s - r_lo.
+template <int WAVES, int DEPTH, int MATS, int NTOK, int QB, bool GROUPED, bool SLICED = false>
 __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const uint8_t* __restrict__ w2,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
                                                               uint32_t nb, void* __restrict__ wsp,
-                                                              SchedArgs sa, GroupArgs ga) {
+                                                              SchedArgs sa, GroupArgs ga,
+                                                              SliceArgs sla) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   static_assert(NTOK == 1 || MATS == 1, "several activation vectors: one matrix");
   static_assert(QB == 4 || QB == 5, "Q4_K or Q5_K");
+  static_assert(!SLICED || (MATS == 1 && NTOK == 1 && !GROUPED), "slices of one matrix and vector");
   const uint32_t slots = sa.packed & 0xffu;
   constexpr uint32_t kPieces = block_pieces(QB);        // 16-byte pieces per block
   constexpr uint32_t kStage = stage_bytes(QB);
-  const Layout L = layout(WAVES, DEPTH, nb, slots, MATS, NTOK, QB);
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t nstages = (nb + 3u) / 4u;
+  const uint32_t tstages = MATS * nstages;  // pairs (and partials) per tile
+  // the schedule: whole and split tiles (sc), or K slices (ss)
+  Sched sc{};
+  SliceSched ss{};
+  if constexpr (SLICED)
+    ss = make_slice_sched(ntiles, sla, sa);
+  else
+    sc = make_sched(ntiles, tstages, WAVES, sa);
+  // the stages whose images the LDS holds: from st0, nbl blocks
+  const uint32_t st0 = SLICED ? ss.r_lo : 0u;
+  const uint32_t nbl = SLICED ? min(4u * ss.ns, nb - 4u * st0) : nb;
+  const Layout L = layout(WAVES, DEPTH, SLICED ? 4u * ss.pstride : nb, slots, MATS, NTOK, QB);
   const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t grp = lane >> 4, n = lane & 15u;
   const uint32_t row_bytes = nb * block_bytes(QB);
-  const uint32_t ntiles = (rows + 15u) / 16u;
-  const uint32_t nstages = (nb + 3u) / 4u;
-  const uint32_t tstages = MATS * nstages;  // pairs (and partials) per tile
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
   uint8_t* const wstage = smem + wave * DEPTH * kStage;
 
@@ -498,7 +516,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   //    t of NTOK at img + t img_stride)
 #pragma unroll
   for (int t = 0; t < NTOK; ++t)
-    copy_x<WAVES>(smem, L.img + t * L.img_stride, x + (size_t)t * nb * kBlockElems, nb, wave,
+    copy_x<WAVES>(smem, L.img + t * L.img_stride,
+                  x + (size_t)t * nb * kBlockElems + (size_t)4u * st0 * kBlockElems, nbl, wave,
                   lane);
 
   // 2. this wave's pairs k = wave, wave + WAVES, ... of the workgroup's pairs
@@ -506,8 +525,13 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   //    matrix r / nstages), and the copies of its first DEPTH, pair j of the
   //    wave into buffer j % DEPTH.  Piece
   //    c = 64 i + lane of a stage is piece c / 16 of row c % 16's 576 bytes.
-  const Sched sc = make_sched(ntiles, tstages, WAVES, sa);
-  const uint32_t npairs = sc.npairs;
+  auto pair_of = [&](uint32_t k) -> Pair {
+    if constexpr (SLICED)
+      return pair_at(ss, k);
+    else
+      return pair_at(sc, k, tstages);
+  };
+  const uint32_t npairs = SLICED ? ss.npairs : sc.npairs;
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
   auto issue = [&](uint32_t j, const Pair& pr) {
@@ -539,10 +563,10 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   };
   // (with one stage in flight, the pair of the next stage, worked out when
   // its copy is issued, is kept for its turn)
-  Pair pr_next = pair_at(sc, wave, tstages);
+  Pair pr_next = pair_of(wave);
 #pragma unroll
   for (int j = 0; j < DEPTH; ++j)
-    if ((uint32_t)j < my_pairs) issue(j, j == 0 ? pr_next : pair_at(sc, wave + j * WAVES, tstages));
+    if ((uint32_t)j < my_pairs) issue(j, j == 0 ? pr_next : pair_of(wave + j * WAVES));
 
   // 3. ring slots, then (once the x copies have landed) digit images, unit
   //    sums and exponents
@@ -560,7 +584,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   // chunk c = 4 p + t: units 2p, 2p + 1 of lane group p, MFMA t
 #pragma unroll
   for (int t = 0; t < NTOK; ++t)
-    build_images<WAVES>(sbase, L, nb, wave, grp, n,
+    build_images<WAVES>(sbase, L, nbl, wave, grp, n,
                         [](uint32_t c) { return 256u * (c & 3u) + 64u * (c >> 2); }, t);
   lds_wait();
   __builtin_amdgcn_s_barrier();
@@ -580,7 +604,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   for (int t = 0; t < 8; ++t) A[t] = i32x4{0, 0, 0, 0};
   uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
   for (uint32_t j = 0; j < my_pairs; ++j) {
-    const Pair pr = DEPTH == 1 ? pr_next : pair_at(sc, wave + j * WAVES, tstages);
+    const Pair pr = DEPTH == 1 ? pr_next : pair_of(wave + j * WAVES);
     const uint32_t s = MATS > 1 && pr.r >= nstages ? pr.r - nstages : pr.r;  // stage
     const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
     if (DEPTH >= 3 && later >= 2u)
@@ -593,7 +617,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     StageRegs<QB> v;
     v.read(hb0 + buf, qb0 + buf);
     if (j + DEPTH < my_pairs) {  // the buffer just read is free again
-      const Pair pn = pair_at(sc, wave + (j + DEPTH) * WAVES, tstages);
+      const Pair pn = pair_of(wave + (j + DEPTH) * WAVES);
       issue(j + DEPTH, pn);
       if (DEPTH == 1) pr_next = pn;
     }
@@ -653,11 +677,14 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       hand_off_tokens<NTOK>(sbase, L, sc.by_slots, pr, tstages, rs, lane, rows, y, fail);
       continue;
     }
-    const float rowsum =
-        stage_rowsum(v, sbase, L, s, nlive, grp, n, A, hi_units, bsh, rot_lo, rot_hi, x);
+    const float rowsum = stage_rowsum(v, sbase, L, s - st0, s, nlive, grp, n, A, hi_units, bsh,
+                                      rot_lo, rot_hi, x);
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
-    hand_off<MATS>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws, fail);
+    if constexpr (SLICED)
+      hand_off_slice(sbase, L, ss, pr, rowsum, lane, rows, y, ws, fail);
+    else
+      hand_off<MATS>(sbase, L, slots, sc, sa, pr, nstages, rowsum, lane, rows, y, ws, fail);
   }
   if (fail != 0u) report_device_error(wsp, fail);
 }
@@ -1365,9 +1392,99 @@ bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, ui
     return true;
   }
   hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT, QB, G>), dim3(grid), dim3(W * 64), lds, s, w,
-                     w2, x, y, rows, nb, ws.ptr, sa, ga);
+                     w2, x, y, rows, nb, ws.ptr, sa, ga, SliceArgs{});
   *err = hipGetLastError();
   return true;
+}
+
+// A K-sliced launch of one vector in S slices (false when the shape or the
+// LDS does not fit).  The slice's blocks, not the row's, bound the LDS
+// metadata, so rows longer than the unsliced kernels take run here.
+template <int W, int D, int QB>
+bool launch_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+                   uint32_t S, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t nstages = (nb + 3u) / 4u;
+  if (rows == 0u || nb == 0u || (uint64_t)nb * block_bytes(QB) * 16u > 0x7fffffffu) return false;
+  SliceShape sh;
+  if (!slice_shape(ntiles, nstages, S, (uint32_t)cu_count(), ws.bytes, &sh)) return false;
+  if (4u * sh.ns_max > kMaxMetaBlocks) return false;
+  const uint32_t slots = ring_slots(W, D, sh.tiles_per_group, sh.ns_max);
+  const uint32_t lds = layout(W, D, 4u * sh.ns_max, slots, 1u, 1u, QB).total;
+  if (lds > kLdsBytes || slots > 0xffu || sh.groups > 0xffffu) return false;
+  SchedArgs sa{};
+  sa.packed = (sh.groups << 16) | slots;
+  sa.m_slots = div_magic(slots);
+  static const hipError_t attr = hipFuncSetAttribute(
+      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, 1, 1, QB, false, true>),
+      hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
+  if (attr != hipSuccess) {
+    *err = attr;
+    return true;
+  }
+  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, 1, 1, QB, false, true>), dim3(sh.groups),
+                     dim3(W * 64), lds, s, w, nullptr, x, y, rows, nb, ws.ptr, sa, GroupArgs{},
+                     sh.args);
+  *err = hipGetLastError();
+  return true;
+}
+
+// Slices for a one-vector Q4_K / Q5_K launch, or 0.  The same rule as the
+// Q6_K kernel's (q6_slices), measured on this kernel (MI355X, us):
+//   type  rows x cols    unsliced  S = 2   S = 4   S = 8
+//   Q4_K  5120 x 17408     18.3     18.3    16.5    21.5
+//   Q4_K  2048 x 16384     12.4     10.0     9.0    10.2
+//   Q4_K  640 x 17408      11.5      9.3     8.0     8.5
+//   Q4_K  8192 x 28672    140.0     38.1    34.9    41.1   (unsliced: 4 waves)
+//   Q4_K  2560 x 34816     75.7     22.8    18.8    18.2   (unsliced: generic kernel)
+//   Q4_K  2560 x 9728       8.6      9.1     8.6     9.7
+//   Q4_K  17408 x 5120     13.6     17.7    22.7
+//   Q4_K  5120 x 5120       7.7      8.1     8.8
+//   Q5_K  5120 x 17408     25.6     23.9    22.1    27.0
+//   Q5_K  5120 x 5120       9.2     11.2    11.7
+// So: rows of fewer than 8 stages (K < 8192) stay whole; four slices when
+// the unsliced launch's busiest workgroup has at most two rounds of pairs
+// (24) and slicing adds it none or the rows are long (48 blocks or more);
+// with more pairs, only rows whose images leave room for fewer than eight
+// waves (or exceed the LDS metadata), in four slices, else two, when that
+// adds no pairs.  Rows longer than the unsliced kernels take must slice.
+uint32_t q4_slices(uint32_t ntiles, uint32_t nb, size_t ws_bytes, int qb) {
+  static const int env = env_int("SI_HIP_Q4K_SLICES", -1);
+  if (env >= 0) return (uint32_t)env;
+  const uint32_t nst = (nb + 3u) / 4u;
+  if (nst < 8u) return 0u;
+  const uint64_t cus = (uint64_t)cu_count();
+  auto most = [&](uint32_t S) {  // the busiest sliced workgroup's pairs
+    const uint64_t gs = std::min<uint64_t>(ntiles, cus / S);
+    return (ntiles + gs - 1u) / gs * ((nst + S - 1u) / S);
+  };
+  if (nb > kMaxMetaBlocks) return 4u;
+  // the unsliced launch's busiest workgroup (launch_shape's choice at the
+  // kernel's wave count)
+  const LaunchShape ls = launch_shape(ntiles, nst, qb == 5 ? 8u : 12u, ws_bytes, 1u);
+  const uint64_t g1 = ls.groups;
+  const uint64_t q = ntiles / g1, lp = (ntiles - q * g1) * nst;
+  const uint64_t most0 = ls.split ? q * nst + (lp + g1 - 1u) / g1 : (ntiles + g1 - 1u) / g1 * nst;
+  if (most0 <= 24u) return most(4u) <= most0 || nb >= 48u ? 4u : 0u;
+  if (layout(8u, 1u, nb, 2u, 1u, 1u, qb).total <= kLdsBytes) return 0u;
+  for (uint32_t S : {4u, 2u})
+    if (most(S) <= most0) return S;
+  return 0u;
+}
+
+// The sliced launch, when q4_slices asks for one.
+template <int QB>
+bool try_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t cols,
+                const Workspace& ws, hipStream_t s, hipError_t* err) {
+  const uint32_t nb = cols / kBlockElems;
+  if (rows == 0u || nb == 0u) return false;
+  const uint32_t S = q4_slices((rows + 15u) / 16u, nb, ws.bytes, QB);
+  if (S < 2u) return false;
+  if constexpr (QB == 4) {  // (Q5_K's weight registers leave room for 8 waves)
+    if (launch_sliced<12, 1, QB>(w, x, y, rows, nb, S, ws, s, err)) return true;
+  }
+  return launch_sliced<8, 1, QB>(w, x, y, rows, nb, S, ws, s, err) ||
+         launch_sliced<4, 1, QB>(w, x, y, rows, nb, S, ws, s, err);
 }
 
 // NT activation vectors (batch-major x and y) in one pass over the weights.
@@ -1447,6 +1564,7 @@ bool matmul_passes(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
 
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  if (try_sliced<4>(w, x, y, rows, cols, ws, s, err)) return true;
   if (!shape_ok(rows, cols, 1u, 4)) return false;
   const uint32_t nb = cols / kBlockElems;
   static const int cfg = env_int("SI_HIP_Q4K_MFMA_CFG", 0);
@@ -1499,6 +1617,7 @@ bool launch_matvec_group(uint32_t type, const uint8_t* const* w, const uint32_t*
 
 bool launch_q5k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  if (try_sliced<5>(w, x, y, rows, cols, ws, s, err)) return true;
   if (!shape_ok(rows, cols, 1u, 5)) return false;
   return launch_q5k_one(w, x, y, rows, cols / kBlockElems, ws, s, err);
 }

@@ -13,7 +13,8 @@ namespace sihip {
 bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float* y, uint32_t rows,
                          uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
                          hipError_t* err);
-// Q4_K, one vector, on the matrix cores (K up to 128 blocks of 256).
+// Q4_K, one vector, on the matrix cores (K up to 512 blocks of 256; rows of
+// more than 128 blocks, and long rows over few tiles, in K slices).
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
 // Q4_K, batch >= 2 vectors (batch-major x and y): up to four per pass over the

@@ -159,10 +159,10 @@ def test_fused_gate_up_nonfinite_activations(hip_ctx, policy):
 
 @pytest.mark.parametrize("cols", [27648, 31744])
 def test_nonfinite_activations_beyond_the_matrix_core_budget(hip_ctx, cols):
-    """Q4_K with K past the matrix-core kernel's LDS budget (31744) and just
-    inside it (27648): an infinite activation gives +-inf rows by weight sign
-    (NaN where a product is 0 * inf), as the reference's per-weight products
-    do."""
+    """Q4_K with K of 27648 and 31744 (one tile: the launch is K-sliced, each
+    workgroup holding a quarter of the row's images): an infinite activation
+    gives +-inf rows by weight sign (NaN where a product is 0 * inf), as the
+    reference's per-weight products do."""
     rows = 16
     w = si_hip.synth_matrix(12, seed=cols, rows=rows, cols=cols)
     W = hip_ctx.upload_quant_weight_private(w, 12)

@@ -1,12 +1,13 @@
-"""GPU: Q6_K matvecs of long rows over few tiles (down projections), which
-run K-sliced: each workgroup takes one of S slices of every tile's stages
-and holds only that slice's activation images, and a tile's S slice sums
-meet in the workspace, added in slice order.
+"""GPU: Q4_K, Q5_K and Q6_K matvecs of long rows over few tiles (down
+projections), which run K-sliced: each workgroup takes one of S slices of
+every tile's stages and holds only that slice's activation images, and a
+tile's S slice sums meet in the workspace, added in slice order.
 
 The launch takes four slices when an unsliced launch would give its busiest
 workgroup at most 24 (tile, stage) pairs (K of 8192 or more), and two or
 four when the unsliced images would leave room for fewer than eight waves
-(K of about 23,000 or more) and slicing adds no pairs.  The bar is the north
+and slicing adds no pairs; Q4_K and Q5_K rows longer than the unsliced
+kernels take (more than 128 blocks) always slice.  The bar is the north
 star's: every row within 2e-5 * sum|w*x| of the f64 dot, +-inf / NaN rows
 where per-weight f32 products give them, and the same bits on every call.
 """
@@ -21,7 +22,7 @@ from test_gpu_parity import _category, assert_dot_close, same_bits
 
 pytestmark = pytest.mark.gpu
 
-Q4, Q6 = 12, 14
+Q4, Q5, Q6 = 12, 13, 14
 
 
 def log(msg):
@@ -50,6 +51,58 @@ def test_sliced_q6_k_within_tolerance(hip_ctx, rows, cols):
         log(f"  worst error / bound = {worst:.4f}")
         # deterministic: the slices are added in slice order on every call
         assert same_bits(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x), y)
+    finally:
+        W.free()
+
+
+# Q4_K / Q5_K: the BASELINE down shape (17 stages: slices of 5, 4, 4, 4);
+# 136 blocks (past the unsliced kernels' 128); 129 blocks, odd, whose last
+# slice ends in a partial stage; 13 stages over a partial last tile; one tile
+# of 256 blocks (slices of 64 blocks)
+Q45_SHAPES = [(Q4, 5120, 17408), (Q4, 2560, 34816), (Q5, 100, 33024), (Q4, 1000, 12800),
+              (Q5, 5120, 17408), (Q4, 3, 65536), (Q4, 640, 17408)]
+
+
+@pytest.mark.parametrize("t,rows,cols", Q45_SHAPES)
+def test_sliced_q4_q5_within_tolerance(hip_ctx, t, rows, cols):
+    log(f"sliced type {t} {rows}x{cols}")
+    w = si_hip.synth_matrix(t, seed=rows * 5 + cols + t, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(rows + cols + t, cols)
+    _, y64, ab = O.matvec(t, w, rows, cols, x, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, t)
+    try:
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        worst = assert_dot_close(y, y64, ab, what=f"type {t} {rows}x{cols}")
+        log(f"  worst error / bound = {worst:.4f}")
+        assert same_bits(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x), y)
+    finally:
+        W.free()
+
+
+@pytest.mark.parametrize("t", [Q4, Q5])
+def test_sliced_q4_q5_special_activations(hip_ctx, t):
+    """Huge, side, subnormal and zero blocks in different slices of a
+    16384-column row, then one infinite or NaN activation at a time."""
+    rows, cols = 200, 16384
+    w = si_hip.synth_matrix(t, seed=4300 + t, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, t)
+    base = si_hip.synth_normal(4301, cols)
+    try:
+        x = base.copy()
+        x[100:140] = np.float32(3e30)
+        x[4096 + 7] = np.float32(1e-9)
+        x[4096 + 300:4096 + 303] = np.float32(-2e-10)
+        x[8192:8192 + 256] = np.float32(1e-41)
+        x[12288 + 512:12288 + 768] = 0.0
+        _, y64, ab = O.matvec(t, w, rows, cols, x, threads=8)
+        assert_dot_close(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x), y64, ab,
+                         what="special blocks")
+        for k, v in [(50, np.inf), (4200, -np.inf), (9000, np.nan), (16383, np.inf)]:
+            x = base.copy()
+            x[k] = v
+            y32, _, _ = O.matvec(t, w, rows, cols, x, threads=8)
+            y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+            assert np.array_equal(_category(y), _category(y32)), f"x[{k}] = {v}"
     finally:
         W.free()
 
