@@ -11,7 +11,7 @@ stream, each call reading the next copy.  The CPU baseline times the
 oracle's restatement of the reference CPU path (quant.rs dequantisation
 followed by the sequential f32 host dot) on the host cores.
 
-  python bench.py [--steps K] [--warmup W] [--gpus 1] [--sweep] [--no-cpu]
+  python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu]
 """
 from __future__ import annotations
 
@@ -243,12 +243,13 @@ def _rate(nbytes: int, ms: float) -> dict:
             "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-CONFIG_NAMES = ("mlp", "q5k", "head", "embedding", "many", "aggregate")
-DEFAULT_CONFIGS = ("mlp", "q5k", "head", "embedding", "many")  # the aggregate uploads 10 GB
+CONFIG_NAMES = ("sweep", "mlp", "q5k", "head", "embedding", "many", "aggregate")
+# (the aggregate uploads 10 GB)
+DEFAULT_CONFIGS = ("sweep", "mlp", "q5k", "head", "embedding", "many")
 
 
 def run_configs(ctx, steps: int, warmup: int, only=CONFIG_NAMES) -> dict:
-    """BASELINE configs 3-5 on the HBM-resident device path (synthetic data);
+    """BASELINE configs 2-5 on the HBM-resident device path (synthetic data);
     `only` picks some of CONFIG_NAMES."""
     import ctypes as C
     lib = si_hip.lib()
@@ -271,6 +272,15 @@ def run_configs(ctx, steps: int, warmup: int, only=CONFIG_NAMES) -> dict:
         return rows * (cols // 256) * si_hip.BLOCK_BYTES[t]
 
     N, K = 17408, 5120
+    if "sweep" in only:
+        # config 2: the batch-1 Q4_K shapes other than the headline's
+        sweep = {}
+        for r, c in ((5120, 5120), (5120, 17408), (1024, 5120)):
+            m = time_matvec(ctx, Q4, r, c, steps, warmup)
+            log(f"configs: sweep {r}x{c}: {m['us_per_call']} us, {m['gb_per_s']} GB/s")
+            sweep[f"{r}x{c}"] = {k: m[k] for k in ("bytes_per_call", "us_per_call", "gb_per_s",
+                                                  "frac_of_peak")}
+        res["q4k_sweep"] = sweep
     if "mlp" in only:
         res.update(_config_mlp(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K))
     if {"q5k", "head", "embedding"} & set(only):
@@ -506,12 +516,11 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--sweep", action="store_true", help="also time the batch-1 shape sweep")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--configs", nargs="?", const=",".join(CONFIG_NAMES),
                     default=",".join(DEFAULT_CONFIGS),
-                    help="BASELINE configs 3-5 timed after the headline: a comma list of "
+                    help="BASELINE configs 2-5 timed after the headline: a comma list of "
                          f"{','.join(CONFIG_NAMES)} (default: {','.join(DEFAULT_CONFIGS)}; "
                          "the flag alone: all)")
     ap.add_argument("--no-configs", action="store_true", help="time the headline only")
@@ -581,13 +590,6 @@ def main() -> int:
         out["copy_probe"] = {"bytes_read_per_copy": nbytes, "us_per_copy": round(us, 3),
                              "gb_per_s_read": round(nbytes / (us * 1e-6) / 1e9, 1)}
         log(f"  copy probe {nbytes} B: {us:.3f} us")
-    if args.sweep:
-        sweep = []
-        for r, c in ((5120, 5120), (17408, 5120), (5120, 17408), (1024, 5120)):
-            res = time_matvec(ctx, 12, r, c, args.steps, args.warmup)
-            log(f"  sweep {r}x{c}: {res['us_per_call']} us, {res['gb_per_s']} GB/s")
-            sweep.append(res)
-        out["sweep"] = sweep
     if args.configs and not args.no_configs:
         only = tuple(c for c in args.configs.split(",") if c)
         bad = [c for c in only if c not in CONFIG_NAMES]
