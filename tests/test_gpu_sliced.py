@@ -216,3 +216,73 @@ def test_token_stage_combines_interleaved(hip_ctx):
     finally:
         for _, W in mats.values():
             W.free()
+
+
+def test_sliced_launches_in_a_graph(hip_ctx):
+    """K-sliced Q4_K and Q6_K matvecs and a split Q4_K matvec recorded in one
+    HIP graph and replayed three times, with eager sliced and split launches
+    on the same workspace between the replays: every replay equals the eager
+    run bit for bit (the tile counters and entries are left clean by every
+    launch; no memset is recorded)."""
+    import ctypes as C
+    lib = si_hip.lib()
+    P = C.c_void_p
+    shapes = [(Q4, 5120, 17408), (Q6, 2560, 17408), (Q4, 17408, 5120), (Q4, 2560, 34816)]
+    mats, ins, outs = [], [], []
+    for t, rows, cols in shapes:
+        w = si_hip.synth_matrix(t, seed=rows + cols + 7 * t, rows=rows, cols=cols, threads=8)
+        mats.append((w, hip_ctx.upload_quant_weight_private(w, t)))
+        x = si_hip.synth_normal(rows * 3 + cols, cols)
+        d_x = hip_ctx.device_alloc(cols * 4)
+        hip_ctx.to_device(d_x, x)
+        ins.append((x, d_x))
+        outs.append(hip_ctx.device_alloc(rows * 4))
+    d_e = hip_ctx.device_alloc(17408 * 4)
+    h = hip_ctx.handle
+
+    def enqueue():
+        for (t, rows, cols), (_, W), (_, d_x), d_y in zip(shapes, mats, ins, outs):
+            rc = lib.si_hip_quant_matvec_device(h, W.handle, rows, cols, P(d_x), P(d_y))
+            assert rc == 0, si_hip.last_error()
+
+    def results():
+        hip_ctx.synchronize()
+        return [hip_ctx.from_device(d_y, rows) for (_, rows, _), d_y in zip(shapes, outs)]
+
+    def clear():
+        for (_, rows, _), d_y in zip(shapes, outs):
+            hip_ctx.to_device(d_y, np.full(rows, np.nan, np.float32))
+
+    try:
+        enqueue()
+        ref = results()
+        for (t, rows, cols), (w, _), (x, _), y in zip(shapes, mats, ins, ref):
+            _, y64, ab = O.matvec(t, w, rows, cols, x, threads=8)
+            assert_dot_close(y, y64, ab, what=f"eager type {t} {rows}x{cols}")
+        log("sliced graph: capture")
+        hip_ctx.capture_begin()
+        enqueue()
+        graph = hip_ctx.capture_end()
+        try:
+            for rep in range(3):
+                clear()
+                # eager sliced and split launches on the same workspace
+                for k in (1, 2):
+                    (t, rows, cols), (_, W), (_, d_x) = shapes[k], mats[k], ins[k]
+                    assert lib.si_hip_quant_matvec_device(h, W.handle, rows, cols, P(d_x),
+                                                          P(d_e)) == 0
+                hip_ctx.synchronize()
+                log(f"sliced graph replay {rep}")
+                graph.launch()
+                for a, b in zip(results(), ref):
+                    assert same_bits(a, b), f"replay {rep} differs"
+        finally:
+            graph.free()
+    finally:
+        for _, W in mats:
+            W.free()
+        for _, d_x in ins:
+            hip_ctx.device_free(d_x)
+        for d_y in outs:
+            hip_ctx.device_free(d_y)
+        hip_ctx.device_free(d_e)

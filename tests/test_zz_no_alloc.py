@@ -1,8 +1,8 @@
 """GPU: si_hip_quant_matvec_noalloc (the matvec that allocates nothing)
 against si_hip_quant_matvec_device, through the C ABI.
 
-The two run the same kernels; the no-alloc one combines split tiles in its
-static device workspace instead of a context's.  Results must be bit-identical
+The two run the same kernels; the no-alloc one combines split tiles and K
+slices in its static device workspace instead of a context's.  Results must be bit-identical
 (the combine order is fixed for a given grid), and therefore within the
 oracle's 2e-5 * sum|w*x| bar.  Each type runs two calls in a row, the second
 on a smaller matrix, so the second finds the workspace as the first left it.
@@ -21,6 +21,9 @@ CASES = [  # (type, (rows, cols) of the first call, (rows, cols) of the second)
     (12, (17408, 5120), (1024, 5120)),
     (13, (5120, 5120), (300, 2304)),
     (14, (20011, 5120), (5120, 17408)),
+    # K-sliced launches (the slices' sums meet in the workspace's entries)
+    (12, (5120, 17408), (640, 17408)),
+    (14, (2560, 17408), (16, 12288)),
 ]
 
 
