@@ -51,8 +51,9 @@ static_assert(16u * (kRowPieces - 1u) <= kStageRowBytes && kLastPiece % 4u == 0u
 static_assert(16u * kRowPieces <= kCopies * 64u, "copies cover every piece");
 
 __host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
-                                            uint32_t slots, uint32_t ntok = 1u) {
-  return make_layout(kStageBytes, 2u, 0u, waves, depth, nb, slots, 1u, ntok);
+                                            uint32_t slots, uint32_t ntok = 1u,
+                                            uint32_t sums = 1u) {
+  return make_layout(kStageBytes, 2u, 0u, waves, depth, nb, slots, sums, ntok);
 }
 
 // The lane's 13 pieces of a stage buffer (piece q of row n at 256 q + 16 n;
@@ -243,11 +244,21 @@ __device__ __forceinline__ float q6_bound(const int (&sc)[4], float d) {
 // SLICED (one vector, one matrix): a K-sliced launch (SliceArgs,
 // mfma_common.h); the LDS holds the images and metadata of the workgroup's
 // slice only, stage r of the matrix at local stage r - r_lo.
+//
+// PAIRED (one vector, one matrix of an odd block count nr): the launch sees
+// rows / 2 rows of nb = 2 nr blocks, row r being rows 2 r and 2 r + 1 of the
+// matrix one after the other.  Such a pair of rows starts on a 4-byte
+// boundary (the rows themselves alternate by 2 bytes), so the two-block
+// stages and their copies are the even case's.  Block b of a launch row
+// meets x block b mod nr (x sits twice in the image area); the sums of its
+// blocks b < nr go to y[2 r] and the rest to y[2 r + 1], the stage that
+// holds blocks nr - 1 and nr handing one sum to each.
 struct ArgmaxArgs {
   uint64_t* result;
   uint32_t rule;
 };
-template <int WAVES, int DEPTH, int NTOK, bool GROUPED, bool ARGMAX = false, bool SLICED = false>
+template <int WAVES, int DEPTH, int NTOK, bool GROUPED, bool ARGMAX = false, bool SLICED = false,
+          bool PAIRED = false>
 __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
@@ -257,6 +268,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
                                                               SliceArgs sla) {
   static_assert(!ARGMAX || (NTOK == 1 && !GROUPED), "argmax over one matrix and vector");
   static_assert(!SLICED || (NTOK == 1 && !GROUPED && !ARGMAX), "slices of one matrix and vector");
+  static_assert(!PAIRED || (NTOK == 1 && !GROUPED && !SLICED), "row pairs of one matrix");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t slots = sa.packed & 0xffu;
   const uint32_t ntiles = (rows + 15u) / 16u;
@@ -271,7 +283,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   // the stages whose images the LDS holds: [st0, st0 + nst), local index st - st0
   const uint32_t st0 = SLICED ? ss.r_lo : 0u;
   const uint32_t nbl = SLICED ? 2u * ss.ns : nb;
-  const Layout L = layout(WAVES, DEPTH, SLICED ? 2u * ss.pstride : nb, slots, NTOK);
+  const Layout L = layout(WAVES, DEPTH, SLICED ? 2u * ss.pstride : nb, slots, NTOK, PAIRED ? 2u : 1u);
+  const uint32_t nr = nb / 2u;  // PAIRED: blocks of one matrix row
   const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
@@ -283,11 +296,15 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
 
   // 1. x into the image area, natural order (block b of vector t at
   //    img + t img_stride + 1024 b)
+  if constexpr (PAIRED) {
+    copy_x<WAVES>(smem, L.img, x, nb, wave, lane, nr);  // x twice over
+  } else {
 #pragma unroll
-  for (int t = 0; t < NTOK; ++t)
-    copy_x<WAVES>(smem, L.img + t * L.img_stride,
-                  x + (size_t)t * nb * kBlockElems + (size_t)2u * st0 * kBlockElems, nbl, wave,
-                  lane);
+    for (int t = 0; t < NTOK; ++t)
+      copy_x<WAVES>(smem, L.img + t * L.img_stride,
+                    x + (size_t)t * nb * kBlockElems + (size_t)2u * st0 * kBlockElems, nbl, wave,
+                    lane);
+  }
 
   // 2. this wave's pairs k = wave, wave + WAVES, ... of the workgroup's pairs
   //    (pair_at: a tile and its stage) and the copies of its first DEPTH, pair
@@ -505,6 +522,27 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
         return decltype(b)::value == 0 ? q6_bound(sc_0, d0) : q6_bound(sc_1, d1);
       });
     }
+    if constexpr (PAIRED) {
+      // the blocks' own x blocks (b mod nr) on the exact path, and each
+      // block's sum to its row of the pair
+      const uint32_t vb0 = 2u * st, vb1 = vb0 + 1u;
+      const float* const x0 = x + 256u * (vb0 < nr ? vb0 : vb0 - nr) + 128u * half + 16u * sub;
+      const float* const x1 = x + 256u * (vb1 < nr ? vb1 : vb1 - nr) + 128u * half + 16u * sub;
+      if (e0 == kBadBlock || (redo & 1u)) pp[0] = block_exact(q0, sc_0, d0, x0);
+      if (e1 == kBadBlock || (redo & 2u)) pp[1] = block_exact(q1, sc_1, d1, x1);
+      float ra = 0.0f, rb = 0.0f;
+      if (vb1 < nr) {
+        ra = sum_lane_groups(pp[0] + pp[1]);
+      } else if (vb0 >= nr) {
+        rb = sum_lane_groups(pp[0] + pp[1]);
+      } else {
+        ra = sum_lane_groups(pp[0]);
+        rb = sum_lane_groups(pp[1]);
+      }
+      hand_off<1, ARGMAX, true>(sbase, L, slots, sc, sa, pr, nstages, ra, lane, rows, y, ws, fail,
+                                &best, aa.rule, rb);
+      continue;
+    }
     if (e0 == kBadBlock || (redo & 1u)) pp[0] = block_exact(q0, sc_0, d0, xs);
     if (e1 == kBadBlock || (redo & 2u)) pp[1] = block_exact(q1, sc_1, d1, xs + 256);
     const float rowsum = sum_lane_groups(pp[0] + pp[1]);
@@ -532,35 +570,39 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   }
 }
 
-template <int W, int D, int NT = 1, bool G = false, bool AM = false>
+// P: rows and nb are the launch's (row pairs of a matrix of nb / 2 blocks).
+template <int W, int D, int NT = 1, bool G = false, bool AM = false, bool P = false>
 bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                const Workspace& ws, hipStream_t s, hipError_t* err,
                const GroupArgs& ga = GroupArgs{}, const ArgmaxArgs& aa = ArgmaxArgs{}) {
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = (nb + 1u) / 2u;
   // several vectors: whole tiles only
-  const LaunchShape ls = launch_shape(ntiles, nstages, W, NT == 1 ? ws.bytes : 0u, 1u);
+  const LaunchShape ls = launch_shape(ntiles, nstages, W, NT == 1 ? ws.bytes : 0u, P ? 2u : 1u);
   const uint32_t grid = ls.groups;
-  const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, nstages);
+  const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, P ? 2u * nstages : nstages);
   // One pair touched ahead pays where the image build is long (the 68-block
   // down projection: 1 us of 22); with 20 blocks (the output head) it costs.
   static const int pf_env = env_int("SI_HIP_Q6K_PREFETCH", -1);
   const uint32_t prefetch = pf_env >= 0 ? (uint32_t)pf_env : (nb >= 48u ? 1u : 0u);
-  const uint32_t lds = layout(W, D, nb, slots, NT).total + (D == 1 && prefetch ? 256u : 0u);
+  const uint32_t lds =
+      layout(W, D, nb, slots, NT, P ? 2u : 1u).total + (D == 1 && prefetch ? 256u : 0u);
   SchedArgs sa;
   if (lds > kLdsBytes || !make_sched_args(ntiles, nstages, slots, ls, &sa)) return false;
   // the argmax: an entry per workgroup, the waves' candidates at the LDS start
-  if (AM && (grid > kArgmaxMaxGroups || rows >= kArgmaxMaxRows || ws.bytes < kWorkspaceBytes))
+  if (AM && (grid > kArgmaxMaxGroups || (P ? 2u : 1u) * (uint64_t)rows >= kArgmaxMaxRows ||
+             ws.bytes < kWorkspaceBytes))
     return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, NT, G, AM>),
+      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, NT, G, AM, false, P>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, NT, G, AM>), dim3(grid), dim3(W * 64), lds, s, w, x,
-                     y, rows, nb, ws.ptr, sa, D == 1 ? prefetch : 0u, ga, aa, SliceArgs{});
+  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, NT, G, AM, false, P>), dim3(grid), dim3(W * 64), lds,
+                     s, w, x, y, rows, nb, ws.ptr, sa, D == 1 ? prefetch : 0u, ga, aa,
+                     SliceArgs{});
   *err = hipGetLastError();
   return true;
 }
@@ -637,6 +679,13 @@ uint32_t q6_slices(uint32_t ntiles, uint32_t nb, size_t ws_bytes) {
   return 0u;
 }
 
+// An odd block count over an even row count runs as row pairs (PAIRED) of
+// 2 nb blocks.
+bool q6_shape_ok(uint32_t rows, uint32_t nb);
+bool paired_ok(uint32_t rows, uint32_t nb) {
+  return (nb & 1u) == 1u && rows >= 2u && (rows & 1u) == 0u && q6_shape_ok(rows / 2u, 2u * nb);
+}
+
 // even nb (4-byte aligned rows and stages); in-tile offsets (16 rows) and the
 // descriptor sizes are 32-bit
 bool q6_shape_ok(uint32_t rows, uint32_t nb) {
@@ -652,6 +701,11 @@ bool q6_shape_ok(uint32_t rows, uint32_t nb) {
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t nb = cols / kBlockElems;
+  if (paired_ok(rows, nb))
+    return launch_wd<12, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
+           launch_wd<10, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
+           launch_wd<8, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
+           launch_wd<4, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err);
   if (!q6_shape_ok(rows, nb)) return false;
   static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
   switch (cfg) {
@@ -673,8 +727,13 @@ bool launch_q6k_matvec_argmax_mfma(const uint8_t* w, const float* x, float* y, u
                                    uint32_t cols, uint32_t rule, uint64_t* result,
                                    const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t nb = cols / kBlockElems;
-  if (!q6_shape_ok(rows, nb)) return false;
   const ArgmaxArgs aa{result, rule};
+  if (paired_ok(rows, nb))
+    return launch_wd<12, 1, 1, false, true, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err,
+                                                  GroupArgs{}, aa) ||
+           launch_wd<8, 1, 1, false, true, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err,
+                                                 GroupArgs{}, aa);
+  if (!q6_shape_ok(rows, nb)) return false;
   return launch_wd<12, 1, 1, false, true>(w, x, y, rows, nb, ws, s, err, GroupArgs{}, aa) ||
          launch_wd<8, 1, 1, false, true>(w, x, y, rows, nb, ws, s, err, GroupArgs{}, aa);
 }

@@ -230,21 +230,26 @@ __device__ __forceinline__ float sum_lane_groups(float v) {
 
 // Copy of x (nb blocks of 256 f32) into the image area in natural order
 // (block b at img + 1024 b): pass j of wave v copies blocks 4 (v + WAVES j)
-// .. +3, one 64-lane 16-byte copy each.
+// .. +3, one 64-lane 16-byte copy each -- the blocks build_images has the
+// same wave convert, so that a wave's own wait covers what it converts.
+// src_nb != 0: the image holds nb = 2 src_nb blocks, block b being x block
+// b mod src_nb (x twice over).
 template <int WAVES>
 __device__ __forceinline__ void copy_x(uint8_t* smem, uint32_t img, const float* x, uint32_t nb,
-                                       uint32_t wave, uint32_t lane) {
+                                       uint32_t wave, uint32_t lane, uint32_t src_nb = 0u) {
+  const uint32_t xn = src_nb != 0u ? src_nb : nb;
   const uint32_t npass = (nb + 4u * WAVES - 1u) / (4u * WAVES);
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(x), 0, (int)(nb * 1024u), kBufferWord3);
+      const_cast<float*>(x), 0, (int)(xn * 1024u), kBufferWord3);
   for (uint32_t j = 0; j < npass; ++j) {
     const uint32_t b0 = 4u * (wave + WAVES * j);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t b = b0 + i;
+      const uint32_t sb = b >= xn ? b - xn : b;
       if (b < nb)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(smem + img + 1024u * b), 16,
-                                                  1024u * b + 16u * lane, 0, 0, 0);
+                                                  1024u * sb + 16u * lane, 0, 0, 0);
     }
   }
 }
@@ -709,13 +714,22 @@ __device__ __forceinline__ void wait_slot(uint32_t owner_at, uint32_t lt, uint32
 // partials < nparts) * (sum of the rest) -- or, for a split tile, publishes
 // the sums and, if it completes the tile, combines all shares.  ARGMAX: every
 // row also enters *best (argmax_candidate under `rule`), and y may be null.
-template <int MATS, bool ARGMAX = false>
+//
+// PAIRED (one matrix whose rows are taken in pairs, row r of the launch being
+// rows 2 r and 2 r + 1 of y): each of the tile's nparts pairs hands two
+// partials, rowsum for row 2 r at slot partial pr.r and rowsum2 for row
+// 2 r + 1 at partial nparts + pr.r; the two sums are added and stored apart.
+template <int MATS, bool ARGMAX = false, bool PAIRED = false>
 __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32_t slots,
                                          const Sched& sc, const SchedArgs& sa, const Pair& pr,
                                          uint32_t nparts,
                                          float rowsum, uint32_t lane, uint32_t rows,
                                          float* __restrict__ y, SplitWs ws, uint32_t& fail,
-                                         uint64_t* best = nullptr, uint32_t rule = 0u) {
+                                         uint64_t* best = nullptr, uint32_t rule = 0u,
+                                         float rowsum2 = 0.0f) {
+  static_assert(!PAIRED || MATS == 1, "paired rows of one matrix");
+  constexpr bool kTwo = MATS > 1 || PAIRED;  // two sums per row of the tile
+  constexpr uint32_t kSums = kTwo ? 2u : 1u;
   auto store_row = [&](uint32_t row, float v) {
     if constexpr (ARGMAX) {
       if (y) y[row] = v;  // a head whose logits are not wanted stores none
@@ -725,12 +739,27 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
       y[row] = v;
     }
   };
+  // the finished rows: y[row] = sum (MATS 1), silu(sum) * sum2 (MATS 2), or
+  // y[2 row] = sum and y[2 row + 1] = sum2 (PAIRED)
+  auto store_sums = [&](uint32_t row, float a, float b) {
+    if constexpr (PAIRED) {
+      store_row(2u * row, a);
+      store_row(2u * row + 1u, b);
+    } else {
+      store_row(row, MATS > 1 ? silu_times(a, b) : a);
+    }
+  };
   const uint32_t grp = lane >> 4, n = lane & 15u;
-  const uint32_t tparts = MATS * nparts;
+  const uint32_t tparts = PAIRED ? nparts : MATS * nparts;  // pairs per tile
+  const uint32_t sstride = kTwo ? 2u * nparts : nparts;      // LDS partials per slot
   const uint32_t slot = pr.lt - quo(pr.lt, sc.by_slots) * slots;
   wait_slot(sbase + L.owner + 4u * slot, pr.lt, fail);
-  if (grp == 0u)
-    lds_write_b32(sbase + L.part + 64u * (slot * tparts + pr.r) + 4u * n, __float_as_uint(rowsum));
+  if (grp == 0u) {
+    lds_write_b32(sbase + L.part + 64u * (slot * sstride + pr.r) + 4u * n, __float_as_uint(rowsum));
+    if constexpr (PAIRED)
+      lds_write_b32(sbase + L.part + 64u * (slot * sstride + nparts + pr.r) + 4u * n,
+                    __float_as_uint(rowsum2));
+  }
   uint32_t old = 0u;
   if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);  // one lane: no serialised atomics
   const uint32_t done = __builtin_amdgcn_readlane(old, 0);
@@ -738,15 +767,20 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
   float sum = 0.0f, sum2 = 0.0f;
   for (uint32_t st = pr.lo; st < pr.hi; ++st) {
     const float v =
-        __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * tparts + st) + 4u * n));
-    if (MATS == 1 || st < nparts)
+        __uint_as_float(lds_read_b32(sbase + L.part + 64u * (slot * sstride + st) + 4u * n));
+    if constexpr (PAIRED) {
       sum += v;
-    else
+      sum2 += __uint_as_float(
+          lds_read_b32(sbase + L.part + 64u * (slot * sstride + nparts + st) + 4u * n));
+    } else if (MATS == 1 || st < nparts) {
+      sum += v;
+    } else {
       sum2 += v;
+    }
   }
   const uint32_t row = pr.tile * 16u + n;
   if (pr.lo == 0u && pr.hi == tparts) {
-    if (grp == 0u && row < rows) store_row(row, MATS > 1 ? silu_times(sum, sum2) : sum);
+    if (grp == 0u && row < rows) store_sums(row, sum, sum2);
   } else {
     // Publish the share's sums, then count the share; no fence orders the
     // two: the workgroup that completes the count waits for each entry to
@@ -764,8 +798,8 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
     const uint32_t t = pr.tile - sc.split_base;  // leftover tile index
     const uint32_t e = 2u * blockIdx.x + (t == sc.t_a ? 0u : 1u);
     if (grp == 0u) {
-      store_coherent(ws.part + (e * MATS) * 16u + n, sum);
-      if (MATS > 1) store_coherent(ws.part + (e * MATS + 1u) * 16u + n, sum2);
+      store_coherent(ws.part + (e * kSums) * 16u + n, sum);
+      if (kTwo) store_coherent(ws.part + (e * kSums + 1u) * 16u + n, sum2);
     }
     const uint32_t g0 = range_of(sc, sa, t * tparts);
     const uint32_t g1 = range_of(sc, sa, t * tparts + tparts - 1u);
@@ -777,16 +811,16 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
       const uint32_t wa = range_start(sc, sa, wg);
       if (wa == range_start(sc, sa, wg + 1u)) return kNoEntry;  // no leftover pairs
       const uint32_t t0 = quo(wa, sc.by_parts);
-      return (2u * wg + (t == t0 ? 0u : 1u)) * MATS * 16u + n;
+      return (2u * wg + (t == t0 ? 0u : 1u)) * kSums * 16u + n;
     };
     // this workgroup's own share is taken from registers, not read back
     auto fetch = [&](uint32_t off, uint32_t wg, float& v, float& v2) {
       if (wg == blockIdx.x) {
         v = sum;
-        if (MATS > 1) v2 = sum2;
+        if (kTwo) v2 = sum2;
       } else if (off != kNoEntry) {
         v = load_coherent(ws.part + off);
-        if (MATS > 1) v2 = load_coherent(ws.part + off + 16u);
+        if (kTwo) v2 = load_coherent(ws.part + off + 16u);
       }
     };
     uint32_t off = entry(g0 + grp);
@@ -814,7 +848,7 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
         for (uint32_t spin = 0;; ++spin) {
           const bool missing = off != kNoEntry && wg != blockIdx.x &&
                                (force != 0u || __float_as_uint(v) == kPartEmpty ||
-                                (MATS > 1 && __float_as_uint(v2) == kPartEmpty));
+                                (kTwo && __float_as_uint(v2) == kPartEmpty));
           if (!__builtin_amdgcn_ballot_w64(missing)) break;
           if (spin == (force != 0u ? force : (1u << 22))) {
             fail = kDevErrCombineWait;
@@ -828,18 +862,18 @@ __device__ __forceinline__ void hand_off(uint32_t sbase, const Layout& L, uint32
 #pragma unroll
         for (uint32_t k = 0; k < 4u; ++k) {
           const float vk = __shfl(v, (int)(n + 16u * k), 64);
-          const float v2k = MATS > 1 ? __shfl(v2, (int)(n + 16u * k), 64) : 0.0f;
+          const float v2k = kTwo ? __shfl(v2, (int)(n + 16u * k), 64) : 0.0f;
           if ((have >> (16u * k)) & 1u) {
             g += vk;
-            if (MATS > 1) u += v2k;
+            if (kTwo) u += v2k;
           }
         }
         if (off != kNoEntry) {
           store_coherent(ws.part + off, __uint_as_float(kPartEmpty));
-          if (MATS > 1) store_coherent(ws.part + off + 16u, __uint_as_float(kPartEmpty));
+          if (kTwo) store_coherent(ws.part + off + 16u, __uint_as_float(kPartEmpty));
         }
       }
-      if (grp == 0u && row < rows) store_row(row, MATS > 1 ? silu_times(g, u) : g);
+      if (grp == 0u && row < rows) store_sums(row, g, u);
       if (lane == 0u)
         (void)__hip_atomic_exchange(ws.cnt + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }

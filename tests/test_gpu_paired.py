@@ -1,0 +1,140 @@
+"""GPU: Q6_K matvecs with an odd number of blocks per row.
+
+A Q6_K block is 210 bytes, so with an odd block count nb consecutive rows
+alternate between 4-byte aligned and 2 bytes off.  Such a matrix with an
+even row count runs on the matrix cores as row pairs: the launch sees
+rows / 2 rows of 2 nb blocks (rows 2 r and 2 r + 1 back to back, which
+start aligned), x sits twice in the image area, and each block's sum goes
+to its own row of the pair -- the stage holding blocks nb - 1 and nb hands
+one sum to each.  Odd row counts keep the generic kernel.
+
+Bar: rows within 2e-5 * sum|w*x| of the f64 dot, +-inf / NaN rows where
+per-weight f32 products give them, the same bits on every call, and the
+fused head's token equal to the oracle's under both tie rules.
+"""
+import sys
+
+import numpy as np
+import pytest
+
+import oracle_lib as O
+import si_hip
+from test_gpu_parity import _category, assert_dot_close, same_bits
+
+pytestmark = pytest.mark.gpu
+
+Q6 = 14
+
+
+def log(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+# (rows, cols): one block per row (the single stage straddles the pair);
+# 9 blocks over a partial tile of pairs (17 pairs); the Gemma-class head
+# width 5376 (21 blocks); the Llama-2-7B down projection (43 blocks); a head
+# of 32000 rows (a split launch of 1000 pair tiles); an odd row count (the
+# generic kernel)
+SHAPES = [(2, 256), (34, 2304), (1000, 5376), (4096, 11008), (32000, 5376), (41, 2304)]
+
+
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_odd_block_count_within_tolerance(hip_ctx, rows, cols):
+    log(f"odd-nb q6_k {rows}x{cols}")
+    w = si_hip.synth_matrix(Q6, seed=rows * 11 + cols, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(rows + 3 * cols, cols)
+    _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, Q6)
+    try:
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        worst = assert_dot_close(y, y64, ab, what=f"{rows}x{cols}")
+        log(f"  worst error / bound = {worst:.4f}")
+        assert same_bits(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x), y)
+    finally:
+        W.free()
+
+
+def test_odd_block_count_special_activations(hip_ctx):
+    """Huge, side, subnormal and zero blocks, and single non-finite
+    activations in the first block, the straddling stage's blocks (the last
+    block of the even row, the first of the odd row) and the last block."""
+    rows, cols = 64, 2304  # 9 blocks: the straddling stage holds block 8 and block 0
+    w = si_hip.synth_matrix(Q6, seed=4400, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, Q6)
+    base = si_hip.synth_normal(4401, cols)
+    try:
+        x = base.copy()
+        x[100:140] = np.float32(3e30)
+        x[300] = np.float32(1e-9)
+        x[310:313] = np.float32(-2e-10)
+        x[1024:1280] = np.float32(1e-41)
+        x[2048:2304] = 0.0
+        _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+        assert_dot_close(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x), y64, ab,
+                         what="special blocks")
+        for k, v in [(5, np.inf), (2100, -np.inf), (2303, np.nan), (700, np.inf)]:
+            x = base.copy()
+            x[k] = v
+            y32, _, _ = O.matvec(Q6, w, rows, cols, x, threads=8)
+            y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+            assert np.array_equal(_category(y), _category(y32)), f"x[{k}] = {v}"
+    finally:
+        W.free()
+
+
+@pytest.mark.parametrize("rows,cols", [(20000, 2304), (4098, 5376)])
+def test_odd_block_count_head_argmax(hip_ctx, rows, cols):
+    """The output head with the argmax fused into the paired launch: logits
+    equal the plain matvec's bit for bit and the token the oracle's, under
+    both tie rules; crafted ties across even and odd rows."""
+    w = si_hip.synth_matrix(Q6, seed=rows + cols, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(rows - cols, cols)
+    H = hip_ctx.upload_quant_weight_private(w, Q6)
+    try:
+        y = hip_ctx.gguf_quant_matvec_weight(H, rows, cols, x)
+        for rule, pick in ((si_hip.ARGMAX_LAST_FINITE, O.argmax_last_finite),
+                           (si_hip.ARGMAX_FIRST_GREATER, O.argmax_first_greater)):
+            tok, logits = hip_ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, x, rule=rule)
+            assert same_bits(logits, y)
+            assert tok == pick(y)
+        _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+        assert_dot_close(y, y64, ab, what="head logits")
+    finally:
+        H.free()
+    # ties: rows 7 (odd), 10 (even) and rows - 1 (odd) carry the same largest row
+    nb = cols // 256
+    blocks = np.asarray(w).reshape(rows, nb, 210).copy()
+    big = bytearray(210)
+    big[0:128] = b"\xff" * 128
+    big[128:192] = b"\xff" * 64
+    big[192:208] = bytes([127]) * 16
+    big[208:210] = np.float16(1.0).tobytes()
+    for r in (7, 10, rows - 1):
+        blocks[r, :] = np.frombuffer(bytes(big), np.uint8)
+    ones = np.ones(cols, np.float32)
+    H = hip_ctx.upload_quant_weight_private(blocks.tobytes(), Q6)
+    try:
+        last, logits = hip_ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, ones)
+        first, _ = hip_ctx.gguf_quant_matvec_argmax_weight(
+            H, rows, cols, ones, rule=si_hip.ARGMAX_FIRST_GREATER, want_logits=False)
+        assert logits[7] == logits[10] == logits[rows - 1] == logits.max()
+        assert (first, last) == (7, rows - 1)
+    finally:
+        H.free()
+
+
+def test_odd_block_count_matmul_many(hip_ctx):
+    """Several vectors over an odd-block matrix: one paired launch per
+    vector, each within its bound."""
+    rows, cols, batch = 1000, 5376, 3
+    w = si_hip.synth_matrix(Q6, seed=4500, rows=rows, cols=cols, threads=8)
+    X = si_hip.synth_normal(4501, batch * cols).reshape(batch, cols)
+    W = hip_ctx.upload_quant_weight_private(w, Q6)
+    try:
+        outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+        for b in range(batch):
+            _, y64, ab = O.matvec(Q6, w, rows, cols, X[b], threads=8)
+            assert_dot_close(outs[b], y64, ab, what=f"vector {b}")
+    finally:
+        W.free()
