@@ -286,3 +286,26 @@ def test_sliced_launches_in_a_graph(hip_ctx):
         for d_y in outs:
             hip_ctx.device_free(d_y)
         hip_ctx.device_free(d_e)
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_long_and_odd_rows(hip_ctx, seed):
+    """Seeded random types, row counts (even and odd, partial tiles) and block
+    counts (odd, long, past 128): one-vector matvecs that land on the
+    K-sliced, row-pair, split, whole-tile and generic launches, every row
+    within the oracle's bound and repeating its own bits."""
+    rng = np.random.default_rng(9500 + seed)
+    t = int(rng.choice([Q4, Q5, Q6]))
+    cols = 256 * int(rng.choice([9, 21, 43, 48, 50, 64, 68, 108, 129, 136]))
+    rows = int(rng.integers(1, 2000))
+    log(f"random long/odd seed={seed}: type {t} {rows}x{cols}")
+    w = si_hip.synth_matrix(t, seed=9600 + seed, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(9700 + seed, cols)
+    W = hip_ctx.upload_quant_weight_private(w, t)
+    try:
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        _, y64, ab = O.matvec(t, w, rows, cols, x, threads=8)
+        assert_dot_close(y, y64, ab, what=f"type {t} {rows}x{cols}")
+        assert same_bits(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x), y)
+    finally:
+        W.free()
