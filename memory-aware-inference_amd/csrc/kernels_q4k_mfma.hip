@@ -56,16 +56,26 @@ namespace {
 using namespace mfma;
 
 // Block bytes of the two formats this kernel reads (QB = quant bits): 144
-// (Q4_K) and 176 (Q5_K), both multiples of 16.  A stage is 16 rows x 4 blocks.
+// (Q4_K) and 176 (Q5_K), both multiples of 16.  A stage is 16 rows x SB
+// blocks (SB = 4, or 2 for the one-vector kernel's finer form): SB * 9 (or
+// 11) 16-byte pieces per row, moved by stage_copies 64-lane copies, the last
+// one's lanes past the row's pieces re-reading its last piece.
 __host__ __device__ constexpr uint32_t block_bytes(int qb) { return qb == 5 ? kQ5Bytes : kQ4Bytes; }
 __host__ __device__ constexpr uint32_t block_pieces(int qb) { return block_bytes(qb) / 16u; }
-__host__ __device__ constexpr uint32_t stage_bytes(int qb) { return 64u * block_bytes(qb); }
+__host__ __device__ constexpr uint32_t stage_copies(int qb, int sb = 4) {
+  return (16u * (uint32_t)sb * block_pieces(qb) + 63u) / 64u;
+}
+__host__ __device__ constexpr uint32_t stage_bytes(int qb, int sb = 4) {
+  return 1024u * stage_copies(qb, sb);
+}
+static_assert(stage_bytes(4) == 64u * kQ4Bytes && stage_bytes(5) == 64u * kQ5Bytes,
+              "four-block stages fill their copies exactly");
 
-// LDS map (make_layout): 4-block stages, 32 bytes of unit sums per block.
+// LDS map (make_layout): SB-block stages, 32 bytes of unit sums per block.
 __host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
                                             uint32_t slots, uint32_t mats, uint32_t ntok = 1u,
-                                            int qb = 4) {
-  return make_layout(stage_bytes(qb), 4u, 32u, waves, depth, nb, slots, mats, ntok);
+                                            int qb = 4, int sb = 4) {
+  return make_layout(stage_bytes(qb, sb), (uint32_t)sb, 32u, waves, depth, nb, slots, mats, ntok);
 }
 
 // The lane's header and two qs pieces of the four blocks of a stage buffer:
@@ -91,6 +101,21 @@ __device__ __forceinline__ void lds_read_weights(uint32_t hb, uint32_t qb, u32x4
       : "memory");
 }
 
+// The same for the two blocks of a two-block stage.
+__device__ __forceinline__ void lds_read_weights2(uint32_t hb, uint32_t qb, u32x4 (&v)[6]) {
+  asm volatile(
+      "ds_read_b128 %0, %6\n"
+      "ds_read_b128 %1, %7\n"
+      "ds_read_b128 %2, %7 offset:256\n"
+      "ds_read_b128 %3, %6 offset:2304\n"
+      "ds_read_b128 %4, %7 offset:2304\n"
+      "ds_read_b128 %5, %7 offset:2560\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5])
+      : "v"(hb), "v"(qb)
+      : "memory");
+}
+
 // Unit sums of the lane's two units in the four blocks (xb + 32 b), the
 // four block exponents (eb) and their four side counts (one byte each, at
 // eb + kCountOff).
@@ -108,6 +133,23 @@ __device__ __forceinline__ void lds_read_sums(uint32_t xb, uint32_t eb, u32x2 (&
       : "=&v"(xs[0]), "=&v"(xs[1]), "=&v"(xs[2]), "=&v"(xs[3]), "=&v"(ex), "=&v"(cnt)
       : "v"(xb), "v"(eb)
       : "memory");
+}
+// The same for the two blocks of a two-block stage (exponents in ex[0..1],
+// the two side counts in the low 16 bits of cnt).
+__device__ __forceinline__ void lds_read_sums2(uint32_t xb, uint32_t eb, u32x2 (&xs)[2], i32x4& ex,
+                                               uint32_t& cnt) {
+  static_assert(kCountOff == 512, "the offset below");
+  u32x2 e2;
+  asm volatile(
+      "ds_read_b64 %0, %4\n"
+      "ds_read_b64 %1, %4 offset:32\n"
+      "ds_read_b64 %2, %5\n"
+      "ds_read_u16 %3, %5 offset:512\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(xs[0]), "=&v"(xs[1]), "=&v"(e2), "=&v"(cnt)
+      : "v"(xb), "v"(eb)
+      : "memory");
+  ex = i32x4{(int)e2[0], (int)e2[1], 0, 0};
 }
 // The 8 A images of two blocks (block b, MFMA t at addr + 1024 b + 256 t),
 // read only by the lanes in `mask`; the other lanes keep their registers.
@@ -271,6 +313,26 @@ __device__ __forceinline__ void lds_read_weights5(uint32_t hb, uint32_t qb, u32x
       : "memory");
 }
 
+// The same for the two blocks of a two-block stage.
+__device__ __forceinline__ void lds_read_weights5x2(uint32_t hb, uint32_t qb, u32x4 (&v)[10]) {
+  asm volatile(
+      "ds_read_b128 %0, %10\n"
+      "ds_read_b128 %1, %10 offset:256\n"
+      "ds_read_b128 %2, %10 offset:512\n"
+      "ds_read_b128 %3, %11\n"
+      "ds_read_b128 %4, %11 offset:256\n"
+      "ds_read_b128 %5, %10 offset:2816\n"
+      "ds_read_b128 %6, %10 offset:3072\n"
+      "ds_read_b128 %7, %10 offset:3328\n"
+      "ds_read_b128 %8, %11 offset:2816\n"
+      "ds_read_b128 %9, %11 offset:3072\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+        "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9])
+      : "v"(hb), "v"(qb)
+      : "memory");
+}
+
 // 5-bit weights of units 2 grp (low nibbles + qh bit 2 grp) and 2 grp + 1
 // (high nibbles + bit 2 grp + 1) from 16 qs bytes and the matching 16 qh
 // bytes.  rot_lo / rot_hi rotate that qh bit of every byte to bit 4
@@ -355,17 +417,21 @@ __device__ __forceinline__ float side_weight_dec(BlockQ4 w, uint32_t i) {
   return k4_value_exact(d1, m1, q);
 }
 
-// The weights of a stage in registers, per format: Q4_K keeps (header, qs
-// piece a, qs piece b) per block, Q5_K adds the two qh pieces.
-template <int QB>
+// The weights of a stage of SB blocks in registers, per format: Q4_K keeps
+// (header, qs piece a, qs piece b) per block, Q5_K adds the two qh pieces.
+template <int QB, int SB = 4>
 struct StageRegs {
   static constexpr int kPer = QB == 5 ? 5 : 3;
-  u32x4 v[4 * kPer];
+  u32x4 v[SB * kPer];
   __device__ __forceinline__ void read(uint32_t hb, uint32_t qb) {
-    if constexpr (QB == 5)
+    if constexpr (QB == 5 && SB == 4)
       lds_read_weights5(hb, qb, v);
-    else
+    else if constexpr (QB == 5)
+      lds_read_weights5x2(hb, qb, v);
+    else if constexpr (SB == 4)
       lds_read_weights(hb, qb, v);
+    else
+      lds_read_weights2(hb, qb, v);
   }
   __device__ __forceinline__ BlockQ4 decode(int b, bool hi_units, int bsh, uint32_t rot_lo,
                                             uint32_t rot_hi) const {
@@ -412,27 +478,31 @@ __device__ __forceinline__ float k4_bound(const BlockQ4& w) {
                fmaf(ad, (float)(w.sco * QMAX), am * w.mno));
 }
 
-// One vector's partial dot of the lane's row over stage s (blocks 4 s ..
-// 4 s + nlive - 1), whose images and metadata sit at LDS stage ls: the MFMA
+// One vector's partial dot of the lane's row over stage s (blocks SB s ..
+// SB s + nlive - 1), whose images and metadata sit at LDS stage ls: the MFMA
 // digit sums, the side elements' exact products, the rounded blocks' check,
 // and the exact path for blocks that need it, summed over the lane groups
 // (every lane of a row gets the row's sum).
-template <int QB>
-__device__ __forceinline__ float stage_rowsum(const StageRegs<QB>& v, uint32_t sbase,
+template <int QB, int SB>
+__device__ __forceinline__ float stage_rowsum(const StageRegs<QB, SB>& v, uint32_t sbase,
                                               const Layout& L, uint32_t ls, uint32_t s,
                                               uint32_t nlive, uint32_t grp, uint32_t n,
                                               i32x4 (&A)[8], bool hi_units, int bsh,
                                               uint32_t rot_lo, uint32_t rot_hi,
                                               const float* __restrict__ x) {
-  u32x2 xs[4];
+  static_assert(SB == 4 || SB == 2, "four- or two-block stages");
+  u32x2 xs[SB];
   i32x4 ex;
   uint32_t cnt;
-  lds_read_sums(sbase + L.xsum + 128u * ls + 8u * grp, sbase + L.expo + 16u * ls, xs, ex, cnt);
-  float part[4];
+  if constexpr (SB == 4)
+    lds_read_sums(sbase + L.xsum + 128u * ls + 8u * grp, sbase + L.expo + 16u * ls, xs, ex, cnt);
+  else
+    lds_read_sums2(sbase + L.xsum + 64u * ls + 8u * grp, sbase + L.expo + 8u * ls, xs, ex, cnt);
+  float part[SB];
   bool bad_any = false;
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    lds_read_images8(sbase + L.img + 4096u * ls + 2048u * h + 16u * n, kActiveLanes, A);
+  for (int h = 0; h < SB / 2; ++h) {
+    lds_read_images8(sbase + L.img + 1024u * SB * ls + 2048u * h + 16u * n, kActiveLanes, A);
 #pragma unroll
     for (int b2 = 0; b2 < 2; ++b2) {
       const int b = 2 * h + b2;
@@ -450,22 +520,26 @@ __device__ __forceinline__ float stage_rowsum(const StageRegs<QB>& v, uint32_t s
   const uint32_t counts = live_counts(__builtin_amdgcn_readfirstlane(cnt), nlive);
   uint32_t redo = 0u;
   if (counts != 0u) {
-    const uint32_t list = sbase + L.expo + L.side_off + 4u * kSideBytes * ls;
-    add_listed<4>(list, counts, grp, part, [](uint32_t i) { return i >> 6; },
-                  [&](auto b, uint32_t i) { return v.template side_weight<decltype(b)::value>(i); });
-    redo = rounded_redo<4>(list, counts, grp, part, [&](auto b) {
+    const uint32_t list = sbase + L.expo + L.side_off + (uint32_t)SB * kSideBytes * ls;
+    add_listed<SB>(list, counts, grp, part, [](uint32_t i) { return i >> 6; },
+                   [&](auto b, uint32_t i) { return v.template side_weight<decltype(b)::value>(i); });
+    redo = rounded_redo<SB>(list, counts, grp, part, [&](auto b) {
       return k4_bound<QB == 5 ? 31 : 15>(
           v.decode(decltype(b)::value, hi_units, bsh, rot_lo, rot_hi));
     });
   }
   if (bad_any || redo != 0u) {
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+    for (int b = 0; b < SB; ++b)
       if (((uint32_t)b < nlive && __builtin_amdgcn_readfirstlane(ex[b]) == kBadBlock) ||
           ((redo >> b) & 1u))
-        part[b] = v.exact(b, hi_units, bsh, rot_lo, rot_hi, x + 256u * (4u * s + b) + 64u * grp);
+        part[b] = v.exact(b, hi_units, bsh, rot_lo, rot_hi,
+                          x + 256u * ((uint32_t)SB * s + b) + 64u * grp);
   }
-  return sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
+  if constexpr (SB == 4)
+    return sum_lane_groups((part[0] + part[1]) + (part[2] + part[3]));
+  else
+    return sum_lane_groups(part[0] + part[1]);
 }
 
 // GROUPED: the rows are those of ga.count matrices with one K, one after the
@@ -475,7 +549,10 @@ __device__ __forceinline__ float stage_rowsum(const StageRegs<QB>& v, uint32_t s
 // SLICED (one matrix, one vector): a K-sliced launch (SliceArgs,
 // mfma_common.h); the LDS holds the images and metadata of the workgroup's
 // slice only, stage s of the matrix at local stage s - r_lo.
-template <int WAVES, int DEPTH, int MATS, int NTOK, int QB, bool GROUPED, bool SLICED = false>
+// SB (one matrix, one vector): blocks per stage, 4, or 2 for shapes whose
+// workgroups have few pairs per wave (finer pairs, a shorter last one).
+template <int WAVES, int DEPTH, int MATS, int NTOK, int QB, bool GROUPED, bool SLICED = false,
+          int SB = 4>
 __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const uint8_t* __restrict__ w2,
                                                               const float* __restrict__ x,
@@ -487,11 +564,13 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   static_assert(NTOK == 1 || MATS == 1, "several activation vectors: one matrix");
   static_assert(QB == 4 || QB == 5, "Q4_K or Q5_K");
   static_assert(!SLICED || (MATS == 1 && NTOK == 1 && !GROUPED), "slices of one matrix and vector");
+  static_assert(SB == 4 || (SB == 2 && MATS == 1 && NTOK == 1), "two-block stages: one vector");
   const uint32_t slots = sa.packed & 0xffu;
-  constexpr uint32_t kPieces = block_pieces(QB);        // 16-byte pieces per block
-  constexpr uint32_t kStage = stage_bytes(QB);
+  constexpr uint32_t kPieces = stage_copies(QB, SB);    // copy instructions per stage
+  constexpr uint32_t kRowPieces = SB * block_pieces(QB);  // 16-byte pieces per row and stage
+  constexpr uint32_t kStage = stage_bytes(QB, SB);
   const uint32_t ntiles = (rows + 15u) / 16u;
-  const uint32_t nstages = (nb + 3u) / 4u;
+  const uint32_t nstages = (nb + SB - 1u) / SB;
   const uint32_t tstages = MATS * nstages;  // pairs (and partials) per tile
   // the schedule: whole and split tiles (sc), or K slices (ss)
   Sched sc{};
@@ -502,8 +581,9 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     sc = make_sched(ntiles, tstages, WAVES, sa);
   // the stages whose images the LDS holds: from st0, nbl blocks
   const uint32_t st0 = SLICED ? ss.r_lo : 0u;
-  const uint32_t nbl = SLICED ? min(4u * ss.ns, nb - 4u * st0) : nb;
-  const Layout L = layout(WAVES, DEPTH, SLICED ? 4u * ss.pstride : nb, slots, MATS, NTOK, QB);
+  const uint32_t nbl = SLICED ? min(SB * ss.ns, nb - SB * st0) : nb;
+  const Layout L =
+      layout(WAVES, DEPTH, SLICED ? SB * ss.pstride : nb, slots, MATS, NTOK, QB, SB);
   const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
@@ -517,7 +597,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
 #pragma unroll
   for (int t = 0; t < NTOK; ++t)
     copy_x<WAVES>(smem, L.img + t * L.img_stride,
-                  x + (size_t)t * nb * kBlockElems + (size_t)4u * st0 * kBlockElems, nbl, wave,
+                  x + (size_t)t * nb * kBlockElems + (size_t)SB * st0 * kBlockElems, nbl, wave,
                   lane);
 
   // 2. this wave's pairs k = wave, wave + WAVES, ... of the workgroup's pairs
@@ -550,16 +630,21 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
         }
     }
     const uint32_t nrows = min(16u, mrows - row0);
-    const uint8_t* sb = wm + (size_t)row0 * row_bytes + 4u * block_bytes(QB) * st;
+    const uint8_t* sb = wm + (size_t)row0 * row_bytes + SB * block_bytes(QB) * st;
     // the descriptor ends at the tile's last row: pieces past it read zero
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - 4u * block_bytes(QB) * st),
+        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - SB * block_bytes(QB) * st),
         kBufferWord3);
     uint8_t* dst = wstage + (j % DEPTH) * kStage;
 #pragma unroll
-    for (int i = 0; i < (int)kPieces; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * i), 16,
-                                                voff + 64u * i, 0, 0, 0);
+    for (int i = 0; i < (int)kPieces; ++i) {
+      // (a stage of SB = 2 ends inside its last copy: those lanes re-read the
+      // row's last piece, which adds no traffic)
+      const uint32_t off = 4u * (uint32_t)i + 3u < kRowPieces
+                               ? voff + 64u * i
+                               : n * row_bytes + 16u * min(4u * i + grp, kRowPieces - 1u);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * i), 16, off, 0, 0, 0);
+    }
   };
   // (with one stage in flight, the pair of the next stage, worked out when
   // its copy is issued, is kept for its turn)
@@ -614,14 +699,14 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     const uint32_t buf = (j % DEPTH) * kStage;
-    StageRegs<QB> v;
+    StageRegs<QB, SB> v;
     v.read(hb0 + buf, qb0 + buf);
     if (j + DEPTH < my_pairs) {  // the buffer just read is free again
       const Pair pn = pair_of(wave + (j + DEPTH) * WAVES);
       issue(j + DEPTH, pn);
       if (DEPTH == 1) pr_next = pn;
     }
-    const uint32_t nlive = min(4u, nb - 4u * s);
+    const uint32_t nlive = min((uint32_t)SB, nb - SB * s);
     if constexpr (NTOK > 1) {
       // the stage's weights are decoded once and meet every vector in turn
       BlockQ4 bw[4];
@@ -1371,28 +1456,28 @@ bool launch_tokens_groups(const uint8_t* w, const float* x, float* y, uint32_t r
          launch_tokens_td<6, 4>(w, x, y, rows, nb, ntok, ws, s, err);
 }
 
-template <int W, int D, int M, int NT = 1, int QB = 4, bool G = false>
+template <int W, int D, int M, int NT = 1, int QB = 4, bool G = false, int SB = 4>
 bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, uint32_t rows,
                uint32_t nb, const Workspace& ws, hipStream_t s, hipError_t* err,
                const GroupArgs& ga = GroupArgs{}) {
   const uint32_t ntiles = (rows + 15u) / 16u;
-  const uint32_t tstages = (nb + 3u) / 4u * M;
+  const uint32_t tstages = (nb + SB - 1u) / SB * M;
   // several vectors: whole tiles only
   const LaunchShape ls = launch_shape(ntiles, tstages, W, NT == 1 ? ws.bytes : 0u, M);
   const uint32_t grid = ls.groups;
   const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, tstages);
-  const uint32_t lds = layout(W, D, nb, slots, M, NT, QB).total;
+  const uint32_t lds = layout(W, D, nb, slots, M, NT, QB, SB).total;
   SchedArgs sa;
   if (lds > kLdsBytes || !make_sched_args(ntiles, tstages, slots, ls, &sa)) return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT, QB, G>),
+      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT, QB, G, false, SB>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT, QB, G>), dim3(grid), dim3(W * 64), lds, s, w,
-                     w2, x, y, rows, nb, ws.ptr, sa, ga, SliceArgs{});
+  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT, QB, G, false, SB>), dim3(grid), dim3(W * 64),
+                     lds, s, w, w2, x, y, rows, nb, ws.ptr, sa, ga, SliceArgs{});
   *err = hipGetLastError();
   return true;
 }
@@ -1440,45 +1525,150 @@ bool launch_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
 //   Q4_K  2560 x 9728       8.6      9.1     8.6     9.7
 //   Q4_K  17408 x 5120     13.6     17.7    22.7
 //   Q4_K  5120 x 5120       7.7      8.1     8.8
+//   Q4_K  8192 x 8192      11.5              15.6
+//   Q4_K  12288 x 8192     15.0              18.5
+//   Q4_K  4096 x 8192       8.9               9.4
+//   Q4_K  4096 x 12288     10.3              10.5            (unsliced: 8 waves)
 //   Q5_K  5120 x 17408     25.6     23.9    22.1    27.0
 //   Q5_K  5120 x 5120       9.2     11.2    11.7
 // So: rows of fewer than 8 stages (K < 8192) stay whole; four slices when
 // the unsliced launch's busiest workgroup has at most two rounds of pairs
-// (24) and slicing adds it none or the rows are long (48 blocks or more);
-// with more pairs, only rows whose images leave room for fewer than eight
-// waves (or exceed the LDS metadata), in four slices, else two, when that
-// adds no pairs.  Rows longer than the unsliced kernels take must slice.
-uint32_t q4_slices(uint32_t ntiles, uint32_t nb, size_t ws_bytes, int qb) {
+// (24) and slicing takes some of them (a tie keeps the whole rows) or the
+// rows are long (64 blocks or more); with more pairs, only rows whose
+// images leave room for fewer than eight waves (or exceed the LDS
+// metadata), in four slices, else two, when that adds no pairs.  Rows
+// longer than the unsliced kernels take must slice.
+// The (tile, stage) pairs of an unsliced launch's busiest workgroup, on
+// launch_shape's grid at the given wave count.
+uint64_t busiest_pairs(uint32_t ntiles, uint32_t tparts, uint32_t waves, size_t ws_bytes) {
+  const LaunchShape ls = launch_shape(ntiles, tparts, waves, ws_bytes, 1u);
+  const uint64_t g = ls.groups, q = ntiles / g, lp = (ntiles - q * g) * (uint64_t)tparts;
+  return ls.split ? q * tparts + (lp + g - 1u) / g : (ntiles + g - 1u) / g * tparts;
+}
+
+// Whether an unsliced one-vector launch of W waves and SB-block stages fits
+// the LDS.
+bool unsliced_fits(uint32_t ntiles, uint32_t nb, uint32_t waves, int qb, int sb,
+                   size_t ws_bytes) {
+  const uint32_t tparts = (nb + sb - 1u) / sb;
+  const LaunchShape ls = launch_shape(ntiles, tparts, waves, ws_bytes, 1u);
+  const uint32_t slots = ring_slots(waves, 1u, ls.tiles_per_group, tparts);
+  return layout(waves, 1u, nb, slots, 1u, 1u, qb, sb).total <= kLdsBytes;
+}
+
+struct SliceChoice {
+  uint32_t slices = 0;   // 0: unsliced
+  uint64_t most0 = 0;    // busiest unsliced workgroup's pairs (0: not weighed)
+  uint64_t most_s = 0;   // busiest sliced workgroup's pairs at `slices`
+  bool forced = false;   // SI_HIP_Q4K_SLICES fixed `slices`
+};
+
+SliceChoice q4_slices(uint32_t ntiles, uint32_t nb, size_t ws_bytes, int qb) {
+  SliceChoice c;
   static const int env = env_int("SI_HIP_Q4K_SLICES", -1);
-  if (env >= 0) return (uint32_t)env;
+  if (env >= 0) {
+    c.slices = (uint32_t)env;
+    c.forced = true;
+    return c;
+  }
   const uint32_t nst = (nb + 3u) / 4u;
-  if (nst < 8u) return 0u;
+  if (nst < 8u) return c;
   const uint64_t cus = (uint64_t)cu_count();
   auto most = [&](uint32_t S) {  // the busiest sliced workgroup's pairs
     const uint64_t gs = std::min<uint64_t>(ntiles, cus / S);
     return (ntiles + gs - 1u) / gs * ((nst + S - 1u) / S);
   };
-  if (nb > kMaxMetaBlocks) return 4u;
-  // the unsliced launch's busiest workgroup (launch_shape's choice at the
-  // kernel's wave count)
-  const LaunchShape ls = launch_shape(ntiles, nst, qb == 5 ? 8u : 12u, ws_bytes, 1u);
-  const uint64_t g1 = ls.groups;
-  const uint64_t q = ntiles / g1, lp = (ntiles - q * g1) * nst;
-  const uint64_t most0 = ls.split ? q * nst + (lp + g1 - 1u) / g1 : (ntiles + g1 - 1u) / g1 * nst;
-  if (most0 <= 24u) return most(4u) <= most0 || nb >= 48u ? 4u : 0u;
-  if (layout(8u, 1u, nb, 2u, 1u, 1u, qb).total <= kLdsBytes) return 0u;
+  if (nb > kMaxMetaBlocks) {
+    c.slices = 4u;
+    return c;
+  }
+  c.most0 = busiest_pairs(ntiles, nst, qb == 5 ? 8u : 12u, ws_bytes);
+  auto pick = [&](uint32_t S) {
+    c.slices = S;
+    c.most_s = most(S);
+    return c;
+  };
+  if (c.most0 <= 24u) return most(4u) < c.most0 || nb >= 64u ? pick(4u) : c;
+  if (layout(8u, 1u, nb, 2u, 1u, 1u, qb).total <= kLdsBytes) return c;
   for (uint32_t S : {4u, 2u})
-    if (most(S) <= most0) return S;
-  return 0u;
+    if (most(S) <= c.most0) return pick(S);
+  return c;
 }
 
-// The sliced launch, when q4_slices asks for one.
+// Whether one Q4_K / Q5_K vector runs as two-block stages (12 waves,
+// unsliced) rather than the slices of `sc` or four-block stages.  A stage of
+// two blocks halves each pair, so more waves share a short launch; it costs
+// more per block (twice the pairs, hand-offs and waits).  Measured on MI355X
+// (us; the four-block kernel unsliced at 12 waves, or at 8 where 12 do not
+// fit):
+//   type  rows x cols    4-block  sliced  2-block
+//   Q4_K  4096 x 4096       5.6      -       5.2
+//   Q4_K  8192 x 5120       8.0      -       7.5
+//   Q4_K  5120 x 5120       7.6      -       7.1
+//   Q4_K  1024 x 5120       6.1      -       5.6
+//   Q4_K  4096 x 8192       8.9     9.4      8.1
+//   Q4_K  8192 x 6144       8.6      -       9.1   (12 pairs per workgroup)
+//   Q4_K  8192 x 8192      11.5    15.6     12.4   (16)
+//   Q4_K  17408 x 5120     13.8      -      14.8   (22)
+//   Q4_K  4096 x 14336     11.8    13.6     11.4   (12 waves do not fit)
+//   Q4_K  2048 x 11008      -       8.4      8.9
+//   Q4_K  1024 x 17408     11.2     8.1     10.7
+//   Q5_K  5120 x 5120       9.1      -       7.9
+//   Q5_K  8192 x 8192      16.0    16.6     14.6
+//   Q5_K  17408 x 5120     18.0      -      18.1
+//   Q5_K  5120 x 17408     22.2    22.2     20.3
+//   Q5_K  2560 x 17408      -      15.0     15.7
+//   Q5_K  640 x 17408       -       8.7     11.4
+//   Q5_K  1024 x 8192       -       7.9      8.3
+// So Q4_K takes two-block stages when the four-block launch leaves waves
+// idle (fewer pairs per workgroup than waves) and the two-block one needs at
+// most two rounds, or when 12 waves of four-block stages do not fit (three
+// rounds); Q5_K, whose four-block stages leave registers for only 8 waves,
+// whenever 12 waves fit.  Slices stay where every unsliced workgroup would
+// build the whole row's activation images for a small share of the work:
+// at most a quarter as many tiles as CUs, rows of 64 blocks or more over
+// fewer tiles than CUs, and rows past 32 blocks whose busiest workgroup the
+// slices shorten.
+bool two_block_stages(uint32_t ntiles, uint32_t nb, size_t ws_bytes, int qb,
+                      const SliceChoice& sc) {
+  constexpr uint32_t kWaves = 12u;
+  if (sc.forced || !unsliced_fits(ntiles, nb, kWaves, qb, 2, ws_bytes)) return false;
+  const uint32_t cus = (uint32_t)cu_count();
+  if (sc.slices >= 2u && (ntiles <= cus / 4u || (nb >= 64u && ntiles < cus) ||
+                          (nb > 32u && sc.most_s < sc.most0)))
+    return false;
+  if (qb == 5) return true;
+  if (nb > 56u) return false;
+  const uint64_t rounds2 = (busiest_pairs(ntiles, (nb + 1u) / 2u, kWaves, ws_bytes) + kWaves - 1u) /
+                           kWaves;
+  if (!unsliced_fits(ntiles, nb, kWaves, qb, 4, ws_bytes)) return rounds2 <= 3u;
+  return rounds2 <= 2u && busiest_pairs(ntiles, (nb + 3u) / 4u, kWaves, ws_bytes) < kWaves;
+}
+
+// Whether the unsliced kernel of SB-block stages takes the shape (the
+// offsets, pair counts and quotients its schedule forms).
+bool shape_ok(uint32_t rows, uint32_t cols, uint32_t mats, int qb, uint32_t sb = 4u) {
+  const uint32_t nb = cols / kBlockElems;
+  const uint64_t pairs = (uint64_t)((rows + 15u) / 16u) * ((nb + sb - 1u) / sb) * mats;
+  return rows != 0 && nb != 0 && nb <= kMaxMetaBlocks &&
+         (uint64_t)nb * block_bytes(qb) * 16u <= 0x7fffffffu &&
+         (uint64_t)nb * 1024u <= 0x7fffffffu && pairs <= 0xffffffffu &&
+         quotients_fit((rows + 15u) / 16u, (nb + sb - 1u) / sb * mats);
+}
+
+// Two-block stages or the sliced launch, when two_block_stages or q4_slices
+// asks for one.
 template <int QB>
 bool try_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t cols,
                 const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t nb = cols / kBlockElems;
   if (rows == 0u || nb == 0u) return false;
-  const uint32_t S = q4_slices((rows + 15u) / 16u, nb, ws.bytes, QB);
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const SliceChoice sc = q4_slices(ntiles, nb, ws.bytes, QB);
+  if (shape_ok(rows, cols, 1u, QB, 2u) && two_block_stages(ntiles, nb, ws.bytes, QB, sc) &&
+      launch_wd<12, 1, 1, 1, QB, false, 2>(w, nullptr, x, y, rows, nb, ws, s, err))
+    return true;
+  const uint32_t S = sc.slices;
   if (S < 2u) return false;
   if constexpr (QB == 4) {  // (Q5_K's weight registers leave room for 8 waves)
     if (launch_sliced<12, 1, QB>(w, x, y, rows, nb, S, ws, s, err)) return true;
@@ -1496,19 +1686,19 @@ bool launch_tokens(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
          launch_wd<4, 1, 1, NT, QB>(w, nullptr, x, y, rows, nb, ws, s, err);
 }
 
-bool shape_ok(uint32_t rows, uint32_t cols, uint32_t mats, int qb) {
-  const uint32_t nb = cols / kBlockElems;
-  const uint64_t pairs = (uint64_t)((rows + 15u) / 16u) * ((nb + 3u) / 4u) * mats;
-  return rows != 0 && nb != 0 && nb <= kMaxMetaBlocks &&
-         (uint64_t)nb * block_bytes(qb) * 16u <= 0x7fffffffu &&
-         (uint64_t)nb * 1024u <= 0x7fffffffu && pairs <= 0xffffffffu &&
-         quotients_fit((rows + 15u) / 16u, (nb + 3u) / 4u * mats);
-}
 
-// One vector, Q5_K (8 waves: its 20 weight pieces per stage leave too few
-// registers for 12).
+// One vector, Q5_K in four-block stages (8 waves: their 20 weight pieces per
+// wave leave too few registers for 12).
 bool launch_q5k_one(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                     const Workspace& ws, hipStream_t s, hipError_t* err) {
+  static const int cfg = env_int("SI_HIP_Q5K_MFMA_CFG", 0);
+  switch (cfg) {
+    case 1: return launch_wd<8, 1, 1, 1, 5>(w, nullptr, x, y, rows, nb, ws, s, err);
+    case 2:
+      return shape_ok(rows, nb * kBlockElems, 1u, 5, 2u) &&
+             launch_wd<12, 1, 1, 1, 5, false, 2>(w, nullptr, x, y, rows, nb, ws, s, err);
+    default: break;
+  }
   return launch_wd<8, 1, 1, 1, 5>(w, nullptr, x, y, rows, nb, ws, s, err) ||
          launch_wd<4, 1, 1, 1, 5>(w, nullptr, x, y, rows, nb, ws, s, err);
 }
@@ -1545,7 +1735,7 @@ bool matmul_passes(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
       case 3: ok = launch_tokens<3, QB>(w, xb, yb, rows, nb, ws, s, err); break;
       case 2: ok = launch_tokens<2, QB>(w, xb, yb, rows, nb, ws, s, err); break;
       default:
-        ok = QB == 5 ? launch_q5k_one(w, xb, yb, rows, nb, ws, s, err)
+        ok = QB == 5 ? launch_q5k_matvec_mfma(w, xb, yb, rows, cols, ws, s, err)
                      : launch_q4k_matvec_mfma(w, xb, yb, rows, cols, ws, s, err);
         break;
     }
@@ -1564,11 +1754,14 @@ bool matmul_passes(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
 
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
-  if (try_sliced<4>(w, x, y, rows, cols, ws, s, err)) return true;
+  static const int cfg = env_int("SI_HIP_Q4K_MFMA_CFG", 0);
+  if (cfg == 0 && try_sliced<4>(w, x, y, rows, cols, ws, s, err)) return true;
   if (!shape_ok(rows, cols, 1u, 4)) return false;
   const uint32_t nb = cols / kBlockElems;
-  static const int cfg = env_int("SI_HIP_Q4K_MFMA_CFG", 0);
   switch (cfg) {
+    case 5:
+      return shape_ok(rows, cols, 1u, 4, 2u) &&
+             launch_wd<12, 1, 1, 1, 4, false, 2>(w, nullptr, x, y, rows, nb, ws, s, err);
     case 1: return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
     case 2: return launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
     case 3: return launch_wd<4, 3, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
@@ -1617,7 +1810,8 @@ bool launch_matvec_group(uint32_t type, const uint8_t* const* w, const uint32_t*
 
 bool launch_q5k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
-  if (try_sliced<5>(w, x, y, rows, cols, ws, s, err)) return true;
+  static const int cfg = env_int("SI_HIP_Q5K_MFMA_CFG", 0);
+  if (cfg == 0 && try_sliced<5>(w, x, y, rows, cols, ws, s, err)) return true;
   if (!shape_ok(rows, cols, 1u, 5)) return false;
   return launch_q5k_one(w, x, y, rows, cols / kBlockElems, ws, s, err);
 }

@@ -5,6 +5,7 @@ f32 dot within 2e-5 * sum|w*x| of the f64 value of the exact products;
 greedy argmax identical.  Tests that restate the reference's own Metal tests
 (src/metal.rs:7445-7602) keep their inputs and tolerances.
 """
+import gc
 import json
 import struct
 import sys
@@ -707,11 +708,20 @@ def test_grouped_matvecs_share_one_submission(hip_ctx):
     outs = hip_ctx.gguf_quant_matvec_many_weights(ws, [r for _, r in specs], cols, x)
     after = hip_ctx.command_stats()
     assert after["waited"] - before["waited"] == 1
+    # (one launch for the group; a lone matvec of the same matrix may take
+    # another stage form, so the two agree within the bound)
     for (t, r), raw, y in zip(specs, raws, outs):
-        assert np.array_equal(y, hip_ctx.gguf_quant_matvec_weight(ws[specs.index((t, r))], r, cols, x))
+        _, y64, ab = O.matvec(t, raw, r, cols, x)
+        assert_dot_close(y, y64, ab, what=f"grouped type {t}")
+        assert_dot_close(hip_ctx.gguf_quant_matvec_weight(ws[specs.index((t, r))], r, cols, x),
+                         y64, ab, what=f"lone type {t}")
 
 
 def test_telemetry_counts_weights(hip_ctx):
+    # weights of earlier tests held in reference cycles (a view and its
+    # tensor) are freed by the cyclic collector, which may otherwise run in
+    # the middle of this test's upload
+    gc.collect()
     hip_ctx.reset_peaks()
     base = hip_ctx.current_allocated_bytes()
     w = si_hip.synth_matrix(12, seed=1500, rows=128, cols=1024)

@@ -127,7 +127,8 @@ def test_fused_gate_up_group_and_matmul_bytes_are_resident(rctx):
     outs = rctx.gguf_quant_matvec_many_bytes([(Q4, g, rows, cols), (Q4, u, rows, cols)], x)
     d = _delta(s1, rctx.residency_stats())
     assert d["hits"] == 2 and d["uploads"] == 0
-    assert same_bits(outs[0], rctx.q4_k_matvec(g, rows, cols, x))
+    _, y64, ab = O.matvec(Q4, g, rows, cols, x)
+    assert_dot_close(outs[0], y64, ab, what="grouped bytes")
     X = si_hip.synth_normal(8403, 3 * cols).reshape(3, cols)
     s2 = rctx.residency_stats()
     m = rctx.gguf_quant_matmul_many_bytes(Q4, g, rows, cols, 3, X)
@@ -148,9 +149,11 @@ def test_store_row_ranges_share_one_resident_tensor(rctx):
         c = g.matvec_tensor_rows(rctx, "q4", 0, rows, x)
         d = _delta(s0, rctx.residency_stats())
         assert d["uploads"] == 1 and d["hits"] == 2
-        assert same_bits(np.concatenate([a, b]), c)
+        # (a row range may take another launch form than the whole tensor:
+        # the same rows agree within the bound, not always to the bit)
         _, y64, ab = O.matvec(Q4, mats["q4"], rows, cols, x)
         assert_dot_close(c, y64, ab, what="store rows")
+        assert_dot_close(np.concatenate([a, b]), y64, ab, what="store row ranges")
     finally:
         g.close()
 
@@ -158,7 +161,8 @@ def test_store_row_ranges_share_one_resident_tensor(rctx):
 def test_view_rows_match_store_and_share_residency(rctx):
     """gguf_quant_matvec_tensor_rows over a GgufTensorView (the payload bytes
     a caller holds): the same bits as the store's call on the same rows, and
-    row ranges of one payload share one resident copy."""
+    row ranges of one payload share one resident copy (ranges of other row
+    counts within the bound)."""
     rows, cols, mats, data = _kquant_file(31)
     g = GgufFile(data=data)
     x = si_hip.synth_normal(32, cols)
@@ -171,7 +175,10 @@ def test_view_rows_match_store_and_share_residency(rctx):
             d = _delta(s0, rctx.residency_stats())
             assert d["uploads"] == 1 and d["hits"] == 1
             whole = g.matvec_tensor_rows(rctx, name, 0, rows, x)
-            assert same_bits(np.concatenate([a, b]), whole[3:])
+            _, y64, ab = O.matvec(t, mats[name], rows, cols, x)
+            assert_dot_close(np.concatenate([a, b]), y64[3:], ab[3:], what=f"{name} view rows")
+            assert same_bits(g.matvec_tensor_rows(rctx, name, 3, 50, x), a)
+            assert_dot_close(whole, y64, ab, what=f"{name} store rows")
     finally:
         g.close()
 

@@ -4,10 +4,12 @@ every tile's stages and holds only that slice's activation images, and a
 tile's S slice sums meet in the workspace, added in slice order.
 
 The launch takes four slices when an unsliced launch would give its busiest
-workgroup at most 24 (tile, stage) pairs (K of 8192 or more), and two or
+workgroup at most 24 (tile, stage) pairs (K of 8192 or more) and slicing
+takes some of them or the rows are long (64 blocks or more), and two or
 four when the unsliced images would leave room for fewer than eight waves
 and slicing adds no pairs; Q4_K and Q5_K rows longer than the unsliced
-kernels take (more than 128 blocks) always slice.  The bar is the north
+kernels take (more than 128 blocks) always slice.  (Q4_K / Q5_K shapes of
+many tiles run two-block stages instead; test_gpu_two_block.py.)  The bar is the north
 star's: every row within 2e-5 * sum|w*x| of the f64 dot, +-inf / NaN rows
 where per-weight f32 products give them, and the same bits on every call.
 """
@@ -57,10 +59,11 @@ def test_sliced_q6_k_within_tolerance(hip_ctx, rows, cols):
 
 # Q4_K / Q5_K: the BASELINE down shape (17 stages: slices of 5, 4, 4, 4);
 # 136 blocks (past the unsliced kernels' 128); 129 blocks, odd, whose last
-# slice ends in a partial stage; 13 stages over a partial last tile; one tile
-# of 256 blocks (slices of 64 blocks)
+# slice ends in a partial stage; 13 stages over a partial last tile; the
+# down shape's K over 64 tiles; one tile of 256 blocks (slices of 64
+# blocks); 40 tiles
 Q45_SHAPES = [(Q4, 5120, 17408), (Q4, 2560, 34816), (Q5, 100, 33024), (Q4, 1000, 12800),
-              (Q5, 5120, 17408), (Q4, 3, 65536), (Q4, 640, 17408)]
+              (Q5, 1024, 17408), (Q4, 3, 65536), (Q4, 640, 17408), (Q5, 640, 17408)]
 
 
 @pytest.mark.parametrize("t,rows,cols", Q45_SHAPES)
