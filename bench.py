@@ -236,6 +236,32 @@ def _timed(ctx, fn, steps: int, warmup: int) -> float:
     return ms / steps
 
 
+def _timed_graph(ctx, fn, per_graph: int, steps: int, warmup: int) -> float:
+    """Average ms per call of fn(i) when per_graph calls are recorded once
+    into a HIP graph and the graph is replayed back to back: the device time
+    of short calls without the Python and host launch cost of each call."""
+    ctx.capture_begin()
+    try:
+        for i in range(per_graph):
+            fn(i)
+    finally:
+        graph = ctx.capture_end()
+    try:
+        reps = max(1, steps // per_graph)
+        for _ in range(max(1, warmup // per_graph)):
+            graph.launch()
+        ctx.synchronize()
+        ctx.event_record(0)
+        for _ in range(reps):
+            graph.launch()
+        ctx.event_record(1)
+        ms = ctx.event_elapsed_ms(0, 1)
+        ctx.synchronize()
+    finally:
+        graph.free()
+    return ms / (reps * per_graph)
+
+
 def _rate(nbytes: int, ms: float) -> dict:
     us = ms * 1000.0
     gbs = nbytes / (us * 1e-6) / 1e9
@@ -328,9 +354,14 @@ def _config_mixed(ctx, lib, upload, dev_f32, bpc, steps, warmup, K, only) -> dic
     y = ctx.device_alloc(K * 4)
     if "q5k" in only:
         q5 = [upload(Q5, 400 + c, K, K) for c in range(8)]
-        ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_quant_matvec_device(
-            ctx.handle, q5[i % 8].handle, K, K, C.c_void_p(x), C.c_void_p(y))), steps, warmup)
-        res["q5k_matvec_5120x5120"] = _rate(bpc(Q5, K, K), ms)
+
+        def q5_call(i):
+            si_hip._check(lib.si_hip_quant_matvec_device(
+                ctx.handle, q5[i % 8].handle, K, K, C.c_void_p(x), C.c_void_p(y)))
+
+        res["q5k_matvec_5120x5120"] = _rate(bpc(Q5, K, K), _timed(ctx, q5_call, steps, warmup))
+        res["q5k_matvec_5120x5120"]["graph_us_per_call"] = round(
+            1000.0 * _timed_graph(ctx, q5_call, 64, steps, warmup), 3)
         for w in q5:
             w.free()
     V = 151936
@@ -349,9 +380,14 @@ def _config_mixed(ctx, lib, upload, dev_f32, bpc, steps, warmup, K, only) -> dic
         ids = ctx.device_alloc(64 * 4)
         ctx.to_device(ids, si_hip.synth_token_ids(421, 64, V).astype(np.uint32))
         emb = ctx.device_alloc(64 * K * 4)
-        ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_embedding_device(
-            ctx.handle, table.handle, K, V, C.c_void_p(ids), 64, C.c_void_p(emb))), steps, warmup)
-        res["q4k_embedding_64_tokens"] = _rate(64 * bpc(Q4, 1, K), ms)
+        def emb_call(i):
+            si_hip._check(lib.si_hip_embedding_device(
+                ctx.handle, table.handle, K, V, C.c_void_p(ids), 64, C.c_void_p(emb)))
+
+        res["q4k_embedding_64_tokens"] = _rate(64 * bpc(Q4, 1, K), _timed(ctx, emb_call, steps,
+                                                                          warmup))
+        res["q4k_embedding_64_tokens"]["graph_us_per_call"] = round(
+            1000.0 * _timed_graph(ctx, emb_call, 64, steps, warmup), 3)
         table.free()
         ctx.device_free(ids); ctx.device_free(emb)
     for p in (x, y):
@@ -386,8 +422,15 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     Xg = dev_f32(si_hip.synth_normal(511, K))
     Yg = ctx.device_alloc(sum(g_rows) * 4)
     g_bytes = sum(bpc(Q4, r, K) for r in g_rows)
-    ms_one = _timed(ctx, lambda i: ctx.quant_matvec_many_device(gws[i % 4], g_rows, K, Xg, Yg),
-                    steps, warmup)
+    g_handles = [(C.c_void_p * 3)(*[wq.handle.value for wq in grp]) for grp in gws]
+    g_rarr = (C.c_size_t * 3)(*g_rows)
+
+    def one_launch(i):
+        si_hip._check(lib.si_hip_quant_matvec_many_device(ctx.handle, g_handles[i % 4], g_rarr, 3,
+                                                          K, C.c_void_p(Xg), C.c_void_p(Yg)))
+
+    ms_one = _timed(ctx, one_launch, steps, warmup)
+    ms_one_graph = _timed_graph(ctx, one_launch, 64, steps, warmup)
 
     def per_matrix(i):
         off = 0
@@ -400,6 +443,8 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     res["grouped_q4k_6144+1024+1024x5120"] = {
         "bytes_per_call": g_bytes, "one_launch": _rate(g_bytes, ms_one),
         "launch_per_matrix": _rate(g_bytes, ms_each)}
+    res["grouped_q4k_6144+1024+1024x5120"]["one_launch"]["graph_us_per_call"] = round(
+        1000.0 * ms_one_graph, 3)
     for grp in gws:
         for wq in grp:
             wq.free()
@@ -515,7 +560,11 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
-    ap.add_argument("--warmup", type=int, default=20)
+    # (from an idle start the headline matvec needs about a thousand calls,
+    # some 13 ms, to reach its steady rate: the first hundred run ~6% slower)
+    ap.add_argument("--warmup", type=int, default=2000,
+                    help="untimed calls before each timed headline leg (the configs, timed "
+                         "after the headline on a warm GPU, take at most 100)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--configs", nargs="?", const=",".join(CONFIG_NAMES),
@@ -596,9 +645,10 @@ def main() -> int:
         if bad:
             print(f"unknown config(s) {bad}; choose from {CONFIG_NAMES}", file=sys.stderr)
             return 2
-        out["configs"] = run_configs(ctx, args.steps, args.warmup, only)
+        cfg_warmup = min(args.warmup, 100)
+        out["configs"] = run_configs(ctx, args.steps, cfg_warmup, only)
         # config 1: the matrix the reference's CPU path is quoted on
-        c1 = time_matvec(ctx, 12, 4096, 5120, args.steps, args.warmup)
+        c1 = time_matvec(ctx, 12, 4096, 5120, args.steps, cfg_warmup)
         out["configs"]["q4k_matvec_4096x5120"] = {k: c1[k] for k in (
             "bytes_per_call", "us_per_call", "gb_per_s", "frac_of_peak")}
     ctx.close()

@@ -403,20 +403,6 @@ __device__ __forceinline__ float block_exact_dec(const BlockQ4& w, const float* 
   return exact_dot16_bytes(w.hb, d1o, m1o, xs + 48, acc);
 }
 
-// Exact weight of element i (uniform) of a decoded block for the lane's row;
-// valid in lane group i / 64, which holds units 2 grp and 2 grp + 1.
-__device__ __forceinline__ float side_weight_dec(BlockQ4 w, uint32_t i) {
-  const uint32_t l = i & 31u;
-  const bool odd = (i >> 5) & 1u;
-  const i32x4 lo = l < 16u ? w.la : w.lb, hi = l < 16u ? w.ha : w.hb;
-  const i32x4 qv = odd ? hi : lo;
-  const uint32_t q =
-      byte_of(u32x4{(uint32_t)qv[0], (uint32_t)qv[1], (uint32_t)qv[2], (uint32_t)qv[3]}, l & 15u);
-  const float d1 = __fmul_rn(w.d, (float)(odd ? w.sco : w.sce));
-  const float m1 = __fmul_rn(w.dmin, odd ? w.mno : w.mne);
-  return k4_value_exact(d1, m1, q);
-}
-
 // The weights of a stage of SB blocks in registers, per format: Q4_K keeps
 // (header, qs piece a, qs piece b) per block, Q5_K adds the two qh pieces.
 template <int QB, int SB = 4>
@@ -448,27 +434,8 @@ struct StageRegs {
     else
       return block_exact(v[3 * b], v[3 * b + 1], v[3 * b + 2], hi_units, bsh, xs);
   }
-  // Exact weight (quant.rs:36-63, 90-122 rounding) of element i (uniform,
-  // 0..255) of block B in the lane's row.  Only lane group i / 64 holds the
-  // qs bytes of unit i / 32; other lanes return a value that is not used.
-  template <int B>
-  __device__ __forceinline__ float side_weight(uint32_t i) const {
-    const uint32_t u = i >> 5, l = i & 31u;
-    const u32x4 qa = v[kPer * B + kPer - 2], qb = v[kPer * B + kPer - 1];
-    uint32_t q = (byte_of(l < 16u ? qa : qb, l & 15u) >> (4u * (u & 1u))) & 0x0fu;
-    if constexpr (QB == 5) {
-      const u32x4 h0 = v[5 * B + 1], h1 = v[5 * B + 2];
-      q |= ((byte_of(l < 16u ? h0 : h1, l & 15u) >> u) & 1u) << 4;  // quant.rs:99-122
-    }
-    return k4_weight(v[kPer * B], u, q);
-  }
 };
 
-// Side elements of a stage's four blocks: for each entry (element i, x_i) of
-// block b's list (at list + 32 b, kSideMax entries per block), lane group
-// i / 64 adds w_i * x_i of its row to part[b].  `counts` holds the blocks'
-// side counts, one byte each (0 for blocks that take the exact path or lie
-// past the matrix); nearly always 0.
 // Largest |w| of the lane's two units of a decoded Q4_K (QMAX 15) or Q5_K
 // (QMAX 31) block: |d| sc QMAX + |dmin| m, the larger of the two units.
 template <int QMAX>
@@ -514,15 +481,12 @@ __device__ __forceinline__ float stage_rowsum(const StageRegs<QB, SB>& v, uint32
       part[b] = (use && eb != kBadBlock) ? c : 0.0f;
     }
   }
-  // side elements (lane group i / 64 holds element i), then the rounded
-  // blocks' check; blocks on the exact path, and rounded blocks of rows that
-  // fail the check, take the per-weight path
+  // the rounded blocks' check; blocks on the exact path, and rounded blocks
+  // of rows that fail the check, take the per-weight path
   const uint32_t counts = live_counts(__builtin_amdgcn_readfirstlane(cnt), nlive);
   uint32_t redo = 0u;
   if (counts != 0u) {
     const uint32_t list = sbase + L.expo + L.side_off + (uint32_t)SB * kSideBytes * ls;
-    add_listed<SB>(list, counts, grp, part, [](uint32_t i) { return i >> 6; },
-                   [&](auto b, uint32_t i) { return v.template side_weight<decltype(b)::value>(i); });
     redo = rounded_redo<SB>(list, counts, grp, part, [&](auto b) {
       return k4_bound<QB == 5 ? 31 : 15>(
           v.decode(decltype(b)::value, hi_units, bsh, rot_lo, rot_hi));
@@ -542,7 +506,7 @@ __device__ __forceinline__ float stage_rowsum(const StageRegs<QB, SB>& v, uint32
     return sum_lane_groups(part[0] + part[1]);
 }
 
-// GROUPED: the rows are those of ga.count matrices with one K, one after the
+// GROUPED: the rows are those of the group's matrices with one K, one after the
 // other (every matrix but the last a whole number of 16-row tiles), and tile
 // t's weights are those of the matrix whose tiles reach past t.
 //
@@ -565,6 +529,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   static_assert(QB == 4 || QB == 5, "Q4_K or Q5_K");
   static_assert(!SLICED || (MATS == 1 && NTOK == 1 && !GROUPED), "slices of one matrix and vector");
   static_assert(SB == 4 || (SB == 2 && MATS == 1 && NTOK == 1), "two-block stages: one vector");
+  if constexpr (GROUPED) load_group_args_early(ga);
   const uint32_t slots = sa.packed & 0xffu;
   constexpr uint32_t kPieces = stage_copies(QB, SB);    // copy instructions per stage
   constexpr uint32_t kRowPieces = SB * block_pieces(QB);  // 16-byte pieces per row and stage
@@ -623,7 +588,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       mrows = ga.rows[0];
 #pragma unroll
       for (uint32_t k = 1; k < kMaxGroup; ++k)
-        if (k < ga.count && pr.tile >= ga.tile_end[k - 1]) {
+        if (pr.tile >= ga.tile_end[k - 1]) {
           wm = ga.w[k];
           mrows = ga.rows[k];
           row0 = (pr.tile - ga.tile_end[k - 1]) * 16u;
@@ -743,8 +708,6 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
         if (counts != 0u) {
           const uint32_t list =
               sbase + L.expo + t * L.expo_stride + L.side_off + 4u * kSideBytes * s;
-          add_listed<4>(list, counts, grp, part, [](uint32_t i) { return i >> 6; },
-                        [&](auto b, uint32_t i) { return side_weight_dec(bw[decltype(b)::value], i); });
           redo = rounded_redo<4>(list, counts, grp, part, [&](auto b) {
             return k4_bound<QB == 5 ? 31 : 15>(bw[decltype(b)::value]);
           });
@@ -1780,7 +1743,7 @@ bool launch_matvec_group(uint32_t type, const uint8_t* const* w, const uint32_t*
                          const Workspace& ws, hipStream_t s, hipError_t* err) {
   if (count < 2u || count > kMaxGroup) return false;
   GroupArgs ga{};
-  ga.count = count;
+  for (uint32_t k = 0; k < kMaxGroup; ++k) ga.tile_end[k] = 0xffffffffu;
   uint64_t tiles = 0, total = 0;
   for (uint32_t k = 0; k < count; ++k) {
     if (rows[k] == 0u || (k + 1u < count && rows[k] % 16u != 0u)) return false;
@@ -1792,6 +1755,17 @@ bool launch_matvec_group(uint32_t type, const uint8_t* const* w, const uint32_t*
     ga.tile_end[k] = (uint32_t)tiles;
   }
   const uint32_t nb = cols / kBlockElems, trows = (uint32_t)total;
+  // two-block stages where one matrix of the group's rows would take them
+  static const int group_two_block = env_int("SI_HIP_GROUP_TWO_BLOCK", 1);
+  if (group_two_block != 0 && (type == kTypeQ4K || type == kTypeQ5K) && shape_ok(trows, cols, 1u, type == kTypeQ4K ? 4 : 5, 2u) &&
+      two_block_stages((uint32_t)tiles, nb, ws.bytes, type == kTypeQ4K ? 4 : 5, SliceChoice{})) {
+    if (type == kTypeQ4K &&
+        launch_wd<12, 1, 1, 1, 4, true, 2>(w[0], nullptr, x, y, trows, nb, ws, s, err, ga))
+      return true;
+    if (type == kTypeQ5K &&
+        launch_wd<12, 1, 1, 1, 5, true, 2>(w[0], nullptr, x, y, trows, nb, ws, s, err, ga))
+      return true;
+  }
   switch (type) {
     case kTypeQ4K:
       return shape_ok(trows, cols, 1u, 4) &&

@@ -209,20 +209,6 @@ __device__ __forceinline__ float block_exact_lean(const i32x4 (&q)[4], const int
   return acc;
 }
 
-// Exact weight (quant.rs:145-171 rounding) of element i = 128 h + 32 t + l
-// (uniform) of a block in the lane's row, from the lane's sets q and scales
-// sc; valid in lane group q6_owner(i) = 2 h + l / 16, which holds set t of
-// element i.
-__device__ __forceinline__ uint32_t q6_owner(uint32_t i) { return 2u * (i >> 7) + ((i & 31u) >> 4); }
-__device__ __forceinline__ float q6_side_weight(i32x4 q0, i32x4 q1, i32x4 q2, i32x4 q3, int s0,
-                                                int s1, int s2, int s3, float d, uint32_t i) {
-  const uint32_t t = (i >> 5) & 3u, l = i & 31u;
-  const i32x4 qt = t == 0u ? q0 : t == 1u ? q1 : t == 2u ? q2 : q3;
-  const int st = t == 0u ? s0 : t == 1u ? s1 : t == 2u ? s2 : s3;
-  const uint32_t qv =
-      byte_of(u32x4{(uint32_t)qt[0], (uint32_t)qt[1], (uint32_t)qt[2], (uint32_t)qt[3]}, l & 15u);
-  return k6_value_exact(d, st, (int)qv - 32);
-}
 // Largest |w| of the lane's share of a block: |d| * 32 * max |scale|.
 __device__ __forceinline__ float q6_bound(const int (&sc)[4], float d) {
   const int m = max(max(abs(sc[0]), abs(sc[1])), max(abs(sc[2]), abs(sc[3])));
@@ -232,7 +218,7 @@ __device__ __forceinline__ float q6_bound(const int (&sc)[4], float d) {
 // NTOK activation vectors (batch-major x and y) share each decoded stage:
 // vector t's images sit at img + t img_stride, and a launch with NTOK > 1
 // gives every workgroup whole tiles (no split).  GROUPED: the rows are those
-// of ga.count matrices of one K, one after the other (every matrix but the
+// of the group's matrices of one K, one after the other (every matrix but the
 // last a whole number of tiles); tile t reads the matrix whose tiles reach
 // past t.
 //
@@ -270,6 +256,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   static_assert(!SLICED || (NTOK == 1 && !GROUPED && !ARGMAX), "slices of one matrix and vector");
   static_assert(!PAIRED || (NTOK == 1 && !GROUPED && !SLICED), "row pairs of one matrix");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  if constexpr (GROUPED) load_group_args_early(ga);
   const uint32_t slots = sa.packed & 0xffu;
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = (nb + 1u) / 2u;
@@ -331,7 +318,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
       mrows = ga.rows[0];
 #pragma unroll
       for (uint32_t k = 1; k < kMaxGroup; ++k)
-        if (k < ga.count && pr.tile >= ga.tile_end[k - 1]) {
+        if (pr.tile >= ga.tile_end[k - 1]) {
           wm = ga.w[k];
           mrows = ga.rows[k];
           row0 = (pr.tile - ga.tile_end[k - 1]) * 16u;
@@ -483,13 +470,6 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
         if (counts != 0u) {
           const uint32_t list =
               sbase + L.expo + t * L.expo_stride + L.side_off + 2u * kSideBytes * st;
-          add_listed<2>(list, counts, grp, pp, q6_owner, [&](auto b, uint32_t i) {
-            return decltype(b)::value == 0
-                       ? q6_side_weight(q0[0], q0[1], q0[2], q0[3], sc_0[0], sc_0[1], sc_0[2],
-                                        sc_0[3], d0, i)
-                       : q6_side_weight(q1[0], q1[1], q1[2], q1[3], sc_1[0], sc_1[1], sc_1[2],
-                                        sc_1[3], d1, i);
-          });
           redo = rounded_redo<2>(list, counts, grp, pp, [&](auto b) {
             return decltype(b)::value == 0 ? q6_bound(sc_0, d0) : q6_bound(sc_1, d1);
           });
@@ -511,13 +491,6 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     uint32_t redo = 0u;
     if (counts != 0u) {
       const uint32_t list = sbase + L.expo + L.side_off + 2u * kSideBytes * ls;
-      add_listed<2>(list, counts, grp, pp, q6_owner, [&](auto b, uint32_t i) {
-        return decltype(b)::value == 0
-                   ? q6_side_weight(q0[0], q0[1], q0[2], q0[3], sc_0[0], sc_0[1], sc_0[2], sc_0[3],
-                                    d0, i)
-                   : q6_side_weight(q1[0], q1[1], q1[2], q1[3], sc_1[0], sc_1[1], sc_1[2], sc_1[3],
-                                    d1, i);
-      });
       redo = rounded_redo<2>(list, counts, grp, pp, [&](auto b) {
         return decltype(b)::value == 0 ? q6_bound(sc_0, d0) : q6_bound(sc_1, d1);
       });

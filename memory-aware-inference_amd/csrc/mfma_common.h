@@ -6,20 +6,19 @@
 // |x|, which is below 2^e_b), and X_i = sum_d D_d * 256^d in four signed byte
 // digits.  Rounding costs at most 2^(e_b - 31), so an element of at least
 // 2^(e_b - 14) keeps a relative error of at most 2^-17 whatever its weight.
-// Smaller non-zero elements ("side" elements) are handled in one of two ways,
-// so that the dot stays within its bar of 2e-5 * sum|w x| for any weights:
-//
-//  * At most kSideMax of them: they are left out of the fixed point (X_i = 0,
-//    and out of the unit sums) and listed as (index, x) entries; the
-//    consuming kernel adds w_i * x_i for them with the exact per-weight
-//    decode.
-//  * More ("rounded" block, side count kSideRounded): they stay in the fixed
-//    point, rounded like the rest, and the block keeps, per 16-element chunk,
-//    the sum of their rounding errors |x_i - X_i 2^(e_b - 30)|.  The kernel
-//    bounds a row's error from those blocks by (largest |w| the block header
-//    allows) x (that sum), and compares it with the sum of |partial dot| over
-//    the row's stage, which is at most sum|w x| over the stage.  A row whose
-//    bound exceeds kRoundedTol of it recomputes its rounded blocks exactly.
+// A block with smaller non-zero elements ("side" elements) is a "rounded"
+// block (side count kSideRounded), so that the dot stays within its bar of
+// 2e-5 * sum|w x| for any weights: the side elements stay in the fixed point,
+// rounded like the rest, and the block keeps, per 16-element chunk, the sum
+// of their rounding errors |x_i - X_i 2^(e_b - 30)|.  The kernel bounds a
+// row's error from those blocks by (largest |w| the block header allows) x
+// (that sum), and compares it with the sum of |partial dot| over the row's
+// stage, which is at most sum|w x| over the stage.  A row whose bound exceeds
+// kRoundedTol of it recomputes its rounded blocks exactly.  (The
+// vectors-in-rows kernel, q4k_tokens_mfma, builds its own images and lists
+// up to kSideMax side elements of a block as (index, x) entries instead,
+// adding w_i * x_i for them with the exact per-weight decode: a rounded
+// block there holds back the next stage's copy until its rows are checked.)
 //
 // A block with an activation that is not finite or reaches 2^100 takes the
 // exact per-weight path whole.  For every
@@ -60,10 +59,10 @@ constexpr int kFixBits = 30;
 constexpr uint32_t kLdsBytes = 163840u;
 constexpr int kBadBlock = 0x40000000;  // exponent slot of a block taking the exact path
 // Side elements: non-zero |x| below 2^(e_b - kSideShift).  Each block and
-// activation vector has kSideBytes of LDS: up to kSideMax 8-byte entries
-// (element index, x bits), or, for a rounded block, 16 f32 error sums, the
-// one of chunk c at position 4 p + t for the chunk in MFMA t of lane group p
-// (the four of a lane group side by side).
+// activation vector has kSideBytes of LDS: for a rounded block, 16 f32 error
+// sums, the one of chunk c at position 4 p + t for the chunk in MFMA t of
+// lane group p (the four of a lane group side by side); in q4k_tokens_mfma,
+// up to kSideMax 8-byte entries (element index, x bits) instead.
 constexpr int kSideShift = 14;
 constexpr uint32_t kSideMax = 8;
 constexpr uint32_t kSideEntryBytes = 8;
@@ -357,9 +356,9 @@ __device__ __forceinline__ void biased_values(const ChunkSplit& cs, bool listed,
 }
 
 // Turns the copied blocks of activation vector `tok` into digit images in
-// place, plus exponents, side lists or error sums, side counts and, when the
-// layout keeps them, the f32 sums of each 32-element unit (listed side
-// elements left out).  The caller has waited for the copies.  CHUNK_SLOT(c)
+// place, plus exponents, the error sums of rounded blocks, side counts
+// (kSideRounded or 0) and, when the layout keeps them, the f32 sums of each
+// 32-element unit.  The caller has waited for the copies.  CHUNK_SLOT(c)
 // gives the byte offset, inside the block's 1 KB, of the A row 4 p (digit 0)
 // of MFMA t that holds chunk c (elements 16 c .. 16 c + 15): 256 t + 64 p.  A
 // block with an activation that is not finite or reaches 2^100 gets exponent
@@ -390,12 +389,10 @@ __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, ui
     const bool store = pb < nb;
     const bool bad_blk = (__builtin_amdgcn_ballot_w64(cs.bad) >> (16u * grp)) & 0xffffull;
     const uint32_t list = sbase + sdb + kSideBytes * pb;
-    const uint32_t nside = __builtin_amdgcn_ballot_w64(cs.smask != 0u)
-                               ? side_list(xv, cs.smask, n, list, store && !bad_blk)
-                               : 0u;
-    const bool rounded = !bad_blk && nside > kSideMax;
+    const bool rounded =
+        !bad_blk && ((__builtin_amdgcn_ballot_w64(cs.smask != 0u) >> (16u * grp)) & 0xffffull);
     uint32_t u[16];
-    biased_values(cs, !rounded, u);
+    biased_values(cs, false, u);
     uint32_t dg[4][4];  // [element quad][digit]
 #pragma unroll
     for (int k = 0; k < 4; ++k) transpose_digits(u[4 * k], u[4 * k + 1], u[4 * k + 2], u[4 * k + 3], dg[k]);
@@ -411,14 +408,14 @@ __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, ui
                       __float_as_uint(cs.err_side));
     }
     if (want_sums) {
-      float xsum = rounded ? cs.xsum : cs.xsum - cs.xsum_side;
+      float xsum = cs.xsum;
       xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit n / 2
       if (store && (n & 1u))
         lds_write_b32(sbase + xsb + 32u * pb + 4u * (n >> 1), __float_as_uint(xsum));
     }
     if (store && n == 0u) {
       lds_write_b32(sbase + exb + 4u * pb, (uint32_t)(bad_blk ? kBadBlock : cs.e - kFixBits));
-      lds_write_b8(sbase + exb + count_pos(L, pb), bad_blk ? 0u : rounded ? kSideRounded : nside);
+      lds_write_b8(sbase + exb + count_pos(L, pb), rounded ? kSideRounded : 0u);
     }
   }
 }
@@ -450,34 +447,11 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Side elements and rounded blocks of a stage of NB blocks for one activation
-// vector, in a kernel whose lane group `grp` holds a 64-element share of
-// every block (part[b]: the lane's partial dot of block b).  `list`: the side
-// area of the stage's first block; `counts`: the blocks' side counts, one byte
-// each (0 for blocks on the exact path or past the matrix).
-//
-// add_listed adds w_i x_i for the listed side elements; functors (called with
-// integral_constant<int, b>): owner(i), the lane group that holds the weights
-// of element i; side_w(b, i), the exact weight of element i of block b in the
-// lane's row (valid in lane group owner(i)).
-template <int NB, typename Owner, typename SideW>
-__device__ __forceinline__ void add_listed(uint32_t list, uint32_t counts, uint32_t grp,
-                                           float (&part)[NB], Owner owner, SideW side_w) {
-  static_for<NB>([&](auto bc) {
-    constexpr int b = decltype(bc)::value;
-    uint32_t c = (counts >> (8 * b)) & 0xffu;
-    if (c == kSideRounded) c = 0u;
-    for (uint32_t k = 0; k < c; ++k) {
-      // (the entry stays in vector registers: the same in every lane, and
-      // scalar registers are scarce in the kernels that call this)
-      const u32x2 ent = lds_read_b64(list + kSideBytes * b + kSideEntryBytes * k);
-      const uint32_t i = ent[0];
-      const float wv = side_w(bc, i);
-      if (grp == owner(i)) part[b] = fmaf(wv, __uint_as_float(ent[1]), part[b]);
-    }
-  });
-}
-
+// Rounded blocks of a stage of NB blocks for one activation vector, in a
+// kernel whose lane group `grp` holds a 64-element share of every block
+// (part[b]: the lane's partial dot of block b).  `list`: the side area of the
+// stage's first block; `counts`: the blocks' side counts, one byte each (0
+// for blocks on the exact path or past the matrix).
 // Bit b of the result: byte b of the counts marks a rounded block.
 __device__ __forceinline__ uint32_t rounded_mask(uint32_t counts) {
   const uint32_t r = counts & (counts >> 1) & (counts >> 2) & (counts >> 3) & (counts >> 4) &
@@ -538,16 +512,28 @@ struct SchedArgs {
 };
 
 // Several matrices of one K in one launch (grouped matvec): matrix k's packed
-// rows, its row count and the running count of 16-row tiles up to and
-// including it.  After SchedArgs, so kernels that do not read it keep their
-// first 64 bytes of arguments as they were.
+// rows, the running count of 16-row tiles up to and including it (past the
+// group's last matrix, UINT32_MAX, which no tile reaches) and its row count.
+// After SchedArgs, so kernels that do not read it keep their first 64 bytes
+// of arguments as they were; its 128 bytes are the next two 64-byte lines,
+// which the grouped kernels load beside the first.
 constexpr uint32_t kMaxGroup = 8;
 struct GroupArgs {
-  uint32_t count;
+  const uint8_t* w[kMaxGroup];
   uint32_t tile_end[kMaxGroup];
   uint32_t rows[kMaxGroup];
-  const uint8_t* w[kMaxGroup];
 };
+static_assert(sizeof(GroupArgs) == 128, "two argument lines");
+
+// A grouped kernel's first statement: the matrix table's loads go out with
+// those of the first argument line (the compiler would issue them once the
+// schedule is worked out, and their latency would then come before the
+// first weight copy).
+__device__ __forceinline__ void load_group_args_early(const GroupArgs& ga) {
+#pragma unroll
+  for (uint32_t k = 0; k < kMaxGroup; ++k)
+    asm volatile("" ::"s"(ga.w[k]), "s"(ga.rows[k]), "s"(ga.tile_end[k]));
+}
 
 // Work split.  With G workgroups and T tiles of S partials each, workgroup g
 // owns the whole tiles g, g + G, ...  When that leaves some workgroups a

@@ -1,19 +1,19 @@
 """CPU model of the matrix-core kernels' activation handling (no GPU).
 
 The kernels (memory-aware-inference_amd/csrc/mfma_common.h, split_chunk,
-side_list, build_images, rounded_redo) write each 256-element block of x as
-X * 2^(e - 30), X an integer of at most 30 bits and e the exponent of the
-block's largest |x| (largest |x| < 2^e).  Non-zero activations below
-2^(e - 14) are "side" elements:
+build_images, rounded_redo; side_list in the vectors-in-rows kernel) write
+each 256-element block of x as X * 2^(e - 30), X an integer of at most 30
+bits and e the exponent of the block's largest |x| (largest |x| < 2^e).
+Non-zero activations below 2^(e - 14) are "side" elements:
 
-  * at most 8 in a block: left out of X and added back with exact per-weight
-    products ("side" blocks);
+  * up to side_max of them in a block: left out of X and added back with
+    exact per-weight products ("side" blocks).  side_max is 8 in the
+    vectors-in-rows kernel (q4k_tokens_mfma) and 0 in the others;
   * more: kept in X, rounded like the rest ("rounded" blocks).  Per row and
-    stage of four blocks the kernel bounds their rounding error by
-    (largest |w| of the lane's 64-element share) x (sum of the side elements'
-    |rounding error| in that share), and compares it with the sum of the
-    shares' |partial dot|; a row that fails recomputes its rounded blocks
-    exactly.
+    stage the kernel bounds their rounding error by (largest |w| of the
+    lane's 64-element share) x (sum of the side elements' |rounding error|
+    in that share), and compares it with the sum of the shares' |partial
+    dot|; a row that fails recomputes its rounded blocks exactly.
 
 A block with a non-finite or huge activation takes the exact path.  This
 model restates those rules in numpy and measures the error they leave against
@@ -33,12 +33,14 @@ import si_hip
 
 BAR = 2e-5
 SIDE_SHIFT = 14
-SIDE_MAX = 8
+SIDE_MAX_TOKENS = 8  # q4k_tokens_mfma lists up to 8 side elements of a block
+SIDE_MAX_MATVEC = 0  # the other matrix-core kernels round every side block
+SIDE_MAXES = [SIDE_MAX_MATVEC, SIDE_MAX_TOKENS]
 TOL = 4e-6
 LIMIT = (2.0 ** -17 + TOL) / BAR  # 0.58
 
 
-def _block_split(v):
+def _block_split(v, side_max=SIDE_MAX_MATVEC):
     """(kind, fixed-point x) of one block, kind in fixed/side/rounded/exact."""
     a = np.abs(v)
     if not (np.all(np.isfinite(v)) and np.all(a < 2.0 ** 100)):
@@ -48,12 +50,12 @@ def _block_split(v):
     side = (v != 0) & (a < 2.0 ** (e - SIDE_SHIFT))
     if not side.any():
         return "fixed", fixed
-    if side.sum() <= SIDE_MAX:
+    if side.sum() <= side_max:
         return "side", np.where(side, v, fixed)
     return "rounded", fixed
 
 
-def model_dot(w, x, rule="side"):
+def model_dot(w, x, rule="side", side_max=SIDE_MAX_MATVEC, stage=4):
     """The kernel's activation handling for every row of w: returns
     (y as the kernel would compute it in exact arithmetic, per-block kinds,
     number of row-stages that recompute their rounded blocks)."""
@@ -63,7 +65,7 @@ def model_dot(w, x, rule="side"):
     kinds, xe = [], np.empty_like(xb)
     for b in range(nb):
         if rule == "side":
-            k, f = _block_split(xb[b])
+            k, f = _block_split(xb[b], side_max)
         else:  # the chunk rule
             v = xb[b]
             a = np.abs(v)
@@ -81,8 +83,8 @@ def model_dot(w, x, rule="side"):
     y = shares.sum(axis=(1, 2))
     redone = 0
     rounded = [b for b, k in enumerate(kinds) if k == "rounded"]
-    for s0 in range(0, nb, 4):
-        blocks = [b for b in rounded if s0 <= b < s0 + 4]
+    for s0 in range(0, nb, stage):
+        blocks = [b for b in rounded if s0 <= b < s0 + stage]
         if not blocks:
             continue
         # error bound of each row: max |w| of the share x its side-error sum
@@ -94,7 +96,7 @@ def model_dot(w, x, rule="side"):
             serr = (np.abs(v - xe[b]) * side).reshape(4, 64).sum(axis=1)  # per share
             wmax = np.abs(wb[:, b, :]).reshape(rows, 4, 64).max(axis=2)
             err += (wmax * serr).sum(axis=1)
-        a = np.abs(shares[:, s0:s0 + 4, :]).sum(axis=(1, 2))
+        a = np.abs(shares[:, s0:s0 + stage, :]).sum(axis=(1, 2))
         fail = ~(err * 1.01 <= TOL * (a - err))
         redone += int(fail.sum())
         for b in blocks:  # the failing rows' rounded blocks, exactly
@@ -102,8 +104,8 @@ def model_dot(w, x, rule="side"):
     return y, kinds, redone
 
 
-def error_ratio(w, x, rule="side"):
-    y, _, _ = model_dot(w, x, rule)
+def error_ratio(w, x, rule="side", side_max=SIDE_MAX_MATVEC, stage=4):
+    y, _, _ = model_dot(w, x, rule, side_max, stage)
     x64 = np.asarray(x, np.float32).astype(np.float64)
     err = np.abs(y - w @ x64)
     return float(np.max(err / (BAR * (np.abs(w) @ np.abs(x64)))))
@@ -121,13 +123,14 @@ def test_crafted_weights_are_zero_where_asked(t):
     _weights(t, 8, 1024, 5 + t)
 
 
+@pytest.mark.parametrize("side_max,stage", [(0, 4), (0, 2), (8, 4)])
 @pytest.mark.parametrize("t", [12, 13, 14])
 @pytest.mark.parametrize("case", crafted.CASES)
-def test_side_rule_meets_the_bar_on_crafted_inputs(t, case):
+def test_side_rule_meets_the_bar_on_crafted_inputs(t, case, side_max, stage):
     rows, cols = 24, 2048
     w = _weights(t, rows, cols, 40 + t)
     x = crafted.crafted_x(cols, case, 7 + t)
-    ratio = error_ratio(w, x)
+    ratio = error_ratio(w, x, side_max=side_max, stage=stage)
     assert ratio <= LIMIT, f"{case}: {ratio:.3g} of the bar"
 
 
@@ -157,22 +160,33 @@ def test_crafted_many_blocks_are_rounded_and_pass():
 
 def test_side_rule_routes_crafted_blocks():
     w = np.ones((2, 9 * 256))
-    _, kinds, _ = model_dot(w, crafted.crafted_x(9 * 256, "side", 3))
+    x = crafted.crafted_x(9 * 256, "side", 3)
+    _, kinds, _ = model_dot(w, x, side_max=SIDE_MAX_TOKENS)
     assert kinds == ["side"] * 9  # 1..8 side elements per block, all listed
+    _, kinds, redone = model_dot(w, x)
+    assert kinds == ["rounded"] * 9 and redone == 0  # the same blocks rounded pass
     _, kinds, _ = model_dot(w[:, :512], crafted.crafted_x(2 * 256, "edge", 3))
     assert kinds == ["fixed", "fixed"]
 
 
 def test_side_elements_are_rare_on_normal_activations():
-    """Share of N(0,1) blocks with side elements, and with more than the list
-    holds (rounded), over 20,000 blocks."""
+    """Share of N(0,1) blocks with side elements, over 20,000 blocks: listed
+    in the vectors-in-rows kernel (more than its list holds: rounded), rounded
+    in the others, whose rows then pass the check on random weights."""
     x = si_hip.synth_normal(12345, 20000 * 256)
-    kinds = [_block_split(v)[0] for v in x.astype(np.float64).reshape(-1, 256)]
+    blocks = x.astype(np.float64).reshape(-1, 256)
+    kinds = [_block_split(v, SIDE_MAX_TOKENS)[0] for v in blocks]
     side = kinds.count("side") / len(kinds)
     rounded = kinds.count("rounded") / len(kinds)
-    print(f"N(0,1) blocks: {side:.4f} with listed side elements, {rounded:.6f} rounded")
+    print(f"N(0,1) blocks: {side:.4f} with side elements, {rounded:.6f} past the list")
     assert 0.0 < side < 0.1
     assert rounded < 1e-4
+    assert [_block_split(v)[0] for v in blocks].count("rounded") / len(kinds) == side
+    raw = si_hip.synth_matrix(12, seed=11, rows=64, cols=64 * 256)
+    w = O.dequantize(12, raw, 64 * 64 * 256).reshape(64, -1).astype(np.float64)
+    for stage in (4, 2):
+        _, kinds, redone = model_dot(w, x[:64 * 256], stage=stage)
+        assert "rounded" in kinds and redone == 0
 
 
 def test_swiglu_intermediate_is_rounded_not_redone():
@@ -191,8 +205,9 @@ def test_swiglu_intermediate_is_rounded_not_redone():
     assert error_ratio(w, h) <= LIMIT
 
 
+@pytest.mark.parametrize("side_max", SIDE_MAXES)
 @pytest.mark.parametrize("seed", range(3))
-def test_side_rule_on_heavy_tailed_activations(seed):
+def test_side_rule_on_heavy_tailed_activations(seed, side_max):
     """Student-t activations with a few massive channels (the shape of real
     decoder activations) on random Q4_K weights."""
     rows, cols = 32, 4096
@@ -201,4 +216,4 @@ def test_side_rule_on_heavy_tailed_activations(seed):
     rng = np.random.default_rng(seed)
     x = rng.standard_t(2.0, cols)
     x[rng.choice(cols, 6, replace=False)] *= 1e4
-    assert error_ratio(w, x.astype(np.float32)) <= LIMIT
+    assert error_ratio(w, x.astype(np.float32), side_max=side_max) <= LIMIT

@@ -536,7 +536,9 @@ def test_q6_k_matmul_many_head_shape(hip_ctx):
 
 
 @pytest.mark.parametrize("types,rows,cols", [
-    ((12, 12, 12), (6144, 1024, 1024), 5120),   # one launch
+    ((12, 12, 12), (6144, 1024, 1024), 5120),   # one launch (two-block stages)
+    ((12, 12), (8192, 8192), 5120),             # one launch (four-block stages)
+    ((13, 13), (304, 200), 5376),               # Q5_K, one launch, an odd block count
     ((12, 12, 12), (16, 48, 33), 2304),         # one launch, ragged last matrix
     ((12,) * 8, (64,) * 7 + (100,), 1024),      # the largest group of one launch
     ((12, 12), (100, 64), 1024),                # first rows not whole tiles: one launch each
