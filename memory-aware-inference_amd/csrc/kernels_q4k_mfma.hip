@@ -1448,29 +1448,29 @@ bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, ui
 // A K-sliced launch of one vector in S slices (false when the shape or the
 // LDS does not fit).  The slice's blocks, not the row's, bound the LDS
 // metadata, so rows longer than the unsliced kernels take run here.
-template <int W, int D, int QB>
+template <int W, int D, int QB, int SB = 4>
 bool launch_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                    uint32_t S, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
-  const uint32_t nstages = (nb + 3u) / 4u;
+  const uint32_t nstages = (nb + SB - 1u) / SB;
   if (rows == 0u || nb == 0u || (uint64_t)nb * block_bytes(QB) * 16u > 0x7fffffffu) return false;
   SliceShape sh;
   if (!slice_shape(ntiles, nstages, S, (uint32_t)cu_count(), ws.bytes, &sh)) return false;
-  if (4u * sh.ns_max > kMaxMetaBlocks) return false;
+  if (SB * sh.ns_max > kMaxMetaBlocks) return false;
   const uint32_t slots = ring_slots(W, D, sh.tiles_per_group, sh.ns_max);
-  const uint32_t lds = layout(W, D, 4u * sh.ns_max, slots, 1u, 1u, QB).total;
+  const uint32_t lds = layout(W, D, SB * sh.ns_max, slots, 1u, 1u, QB, SB).total;
   if (lds > kLdsBytes || slots > 0xffu || sh.groups > 0xffffu) return false;
   SchedArgs sa{};
   sa.packed = (sh.groups << 16) | slots;
   sa.m_slots = div_magic(slots);
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, 1, 1, QB, false, true>),
+      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, 1, 1, QB, false, true, SB>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, 1, 1, QB, false, true>), dim3(sh.groups),
+  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, 1, 1, QB, false, true, SB>), dim3(sh.groups),
                      dim3(W * 64), lds, s, w, nullptr, x, y, rows, nb, ws.ptr, sa, GroupArgs{},
                      sh.args);
   *err = hipGetLastError();
@@ -1619,6 +1619,22 @@ bool shape_ok(uint32_t rows, uint32_t cols, uint32_t mats, int qb, uint32_t sb =
          quotients_fit((rows + 15u) / 16u, (nb + sb - 1u) / sb * mats);
 }
 
+// Whether a sliced launch takes two-block stages: when the busiest sliced
+// workgroup of four-block stages has fewer pairs than 12 waves, so that
+// waves would idle.  Measured on MI355X (us, S = 4, four- / two-block):
+// Q4_K 1024 x 17408 7.62 / 7.17, 640 x 17408 7.27 / 6.99, 2048 x 16384 8.39 /
+// 8.14, 1000 x 12800 7.07 / 6.69, 2048 x 11008 7.53 / 7.37; Q5_K 1024 x 17408
+// 8.48 / 7.77, 2048 x 16384 9.40 / 8.85; with more pairs four-block stages
+// win: Q4_K 2560 x 17408 9.94 / 11.95, 5120 x 17408 16.2 / 19.9.
+// SI_HIP_Q4K_SLICE_SB (2 or 4) fixes the choice.
+bool sliced_two_block(uint32_t ntiles, uint32_t nb, uint32_t S, size_t ws_bytes) {
+  static const int env = env_int("SI_HIP_Q4K_SLICE_SB", 0);
+  if (env == 2 || env == 4) return env == 2;
+  SliceShape sh;
+  if (!slice_shape(ntiles, (nb + 3u) / 4u, S, (uint32_t)cu_count(), ws_bytes, &sh)) return false;
+  return (uint64_t)sh.tiles_per_group * sh.ns_max < 12u;
+}
+
 // Two-block stages or the sliced launch, when two_block_stages or q4_slices
 // asks for one.
 template <int QB>
@@ -1633,6 +1649,9 @@ bool try_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, uint3
     return true;
   const uint32_t S = sc.slices;
   if (S < 2u) return false;
+  if (sliced_two_block(ntiles, nb, S, ws.bytes) &&
+      launch_sliced<12, 1, QB, 2>(w, x, y, rows, nb, S, ws, s, err))
+    return true;
   if constexpr (QB == 4) {  // (Q5_K's weight registers leave room for 8 waves)
     if (launch_sliced<12, 1, QB>(w, x, y, rows, nb, S, ws, s, err)) return true;
   }
