@@ -586,8 +586,13 @@ bool launch_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
                    uint32_t S, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = nb / 2u;
+  // even nb (4-byte aligned rows and stages); in-tile offsets (16 rows) and
+  // descriptor sizes are 32-bit; the slice's blocks bound the LDS metadata
+  if (rows == 0u || nb == 0u || (nb & 1u) != 0u || (uint64_t)nb * kQ6Bytes * 16u > 0x7fffffffu)
+    return false;
   SliceShape sh;
   if (!slice_shape(ntiles, nstages, S, (uint32_t)cu_count(), ws.bytes, &sh)) return false;
+  if (2u * sh.ns_max > kMaxMetaBlocks) return false;
   const uint32_t slots = ring_slots(W, D, sh.tiles_per_group, sh.ns_max);
   static const int pf_env = env_int("SI_HIP_Q6K_PREFETCH", -1);
   const uint32_t prefetch = D == 1 && pf_env > 0 ? (uint32_t)pf_env : 0u;
@@ -635,6 +640,11 @@ uint32_t q6_slices(uint32_t ntiles, uint32_t nb, size_t ws_bytes) {
   if (env >= 0) return (uint32_t)env;
   const uint32_t nst = nb / 2u;
   if (nst < 16u) return 0u;
+  if (nb > kMaxMetaBlocks) {  // rows longer than the unsliced kernel takes must slice
+    uint32_t S = 4u;
+    while (S < 64u && 2u * ((nst + S - 1u) / S) > kMaxMetaBlocks) S *= 2u;
+    return S;
+  }
   const uint64_t cus = (uint64_t)cu_count();
   // the unsliced launch's busiest workgroup (launch_shape's choice at 12 waves)
   const LaunchShape ls = launch_shape(ntiles, nst, 12u, ws_bytes, 1u);
@@ -679,8 +689,13 @@ bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
            launch_wd<10, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
            launch_wd<8, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
            launch_wd<4, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err);
-  if (!q6_shape_ok(rows, nb)) return false;
   static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
+  if (cfg == 0 && nb > kMaxMetaBlocks) {  // (q6_shape_ok takes none of these)
+    const uint32_t S = q6_slices((rows + 15u) / 16u, nb, ws.bytes);
+    return S >= 2u && (launch_sliced<12, 1>(w, x, y, rows, nb, S, ws, s, err) ||
+                       launch_sliced<8, 1>(w, x, y, rows, nb, S, ws, s, err));
+  }
+  if (!q6_shape_ok(rows, nb)) return false;
   switch (cfg) {
     case 1: return launch_wd<12, 1>(w, x, y, rows, nb, ws, s, err);
     case 2: return launch_wd<8, 2>(w, x, y, rows, nb, ws, s, err);

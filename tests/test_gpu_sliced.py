@@ -35,9 +35,12 @@ def log(msg):
 # (rows, cols): one tile (nb 48: four slices of 6 stages); a partial last
 # tile and 25 stages (slices of 7, 6, 6, 6); 160 tiles of the down
 # projection's K (three per workgroup, slices of 9, 9, 8, 8); 40 tiles (a
-# tensor-parallel shard); the largest block count the matrix-core kernels
-# take (128: two slices of 32 stages); one tile of 108 blocks
-SHAPES = [(16, 12288), (1000, 12800), (2560, 17408), (640, 17408), (2048, 32768), (3, 27648)]
+# tensor-parallel shard); the largest block count the unsliced kernel takes
+# (128: two slices of 32 stages); one tile of 108 blocks; rows past 128
+# blocks, which must slice (136 blocks: four slices of 17 stages; 256
+# blocks: four of 32)
+SHAPES = [(16, 12288), (1000, 12800), (2560, 17408), (640, 17408), (2048, 32768), (3, 27648),
+          (100, 34816), (2560, 34816), (40, 65536)]
 
 
 @pytest.mark.parametrize("rows,cols", SHAPES)
