@@ -1542,7 +1542,13 @@ SliceChoice q4_slices(uint32_t ntiles, uint32_t nb, size_t ws_bytes, int qb) {
     return (ntiles + gs - 1u) / gs * ((nst + S - 1u) / S);
   };
   if (nb > kMaxMetaBlocks) {
-    c.slices = 4u;
+    // rows longer than the unsliced kernels take must slice: the fewest
+    // slices (from four) whose images leave the stage buffers of 12 waves
+    // (Q4_K, 32 blocks) or 8 (Q5_K, 64 blocks) room in the LDS
+    const uint32_t cap = qb == 5 ? 16u : 8u;  // stages per slice
+    uint32_t S = 4u;
+    while (S < 64u && S < cus && (nst + S - 1u) / S > cap) S *= 2u;
+    c.slices = S;
     return c;
   }
   c.most0 = busiest_pairs(ntiles, nst, qb == 5 ? 8u : 12u, ws_bytes);

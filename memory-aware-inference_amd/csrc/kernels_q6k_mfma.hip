@@ -640,12 +640,15 @@ uint32_t q6_slices(uint32_t ntiles, uint32_t nb, size_t ws_bytes) {
   if (env >= 0) return (uint32_t)env;
   const uint32_t nst = nb / 2u;
   if (nst < 16u) return 0u;
-  if (nb > kMaxMetaBlocks) {  // rows longer than the unsliced kernel takes must slice
+  const uint64_t cus = (uint64_t)cu_count();
+  if (nb > kMaxMetaBlocks) {
+    // rows longer than the unsliced kernel takes must slice: the fewest
+    // slices (from four) whose images (64 blocks at most) leave the stage
+    // buffers of 12 waves room in the LDS
     uint32_t S = 4u;
-    while (S < 64u && 2u * ((nst + S - 1u) / S) > kMaxMetaBlocks) S *= 2u;
+    while (S < 64u && S < cus && (nst + S - 1u) / S > 32u) S *= 2u;
     return S;
   }
-  const uint64_t cus = (uint64_t)cu_count();
   // the unsliced launch's busiest workgroup (launch_shape's choice at 12 waves)
   const LaunchShape ls = launch_shape(ntiles, nst, 12u, ws_bytes, 1u);
   const uint64_t g1 = ls.groups;

@@ -13,8 +13,9 @@ namespace sihip {
 bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float* y, uint32_t rows,
                          uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
                          hipError_t* err);
-// Q4_K, one vector, on the matrix cores (K up to 512 blocks of 256; rows of
-// more than 128 blocks, and long rows over few tiles, in K slices).
+// Q4_K, one vector, on the matrix cores (rows of more than 128 blocks, and
+// long rows over few tiles, in K slices; up to 2048 blocks of 256, where 64
+// slices of at most 8 stages still fit the LDS).
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
 // Q4_K, batch >= 2 vectors (batch-major x and y): up to four per pass over the
