@@ -38,9 +38,9 @@ def log(msg):
 # tensor-parallel shard); the largest block count the unsliced kernel takes
 # (128: two slices of 32 stages); one tile of 108 blocks; rows past 128
 # blocks, which must slice (136 blocks: four slices of 17 stages; 256
-# blocks: four of 32)
+# blocks: four of 32; 548 blocks: sixteen of 18)
 SHAPES = [(16, 12288), (1000, 12800), (2560, 17408), (640, 17408), (2048, 32768), (3, 27648),
-          (100, 34816), (2560, 34816), (40, 65536)]
+          (100, 34816), (2560, 34816), (40, 65536), (17, 140288)]
 
 
 @pytest.mark.parametrize("rows,cols", SHAPES)
@@ -63,10 +63,12 @@ def test_sliced_q6_k_within_tolerance(hip_ctx, rows, cols):
 # Q4_K / Q5_K: the BASELINE down shape (17 stages: slices of 5, 4, 4, 4);
 # 136 blocks (past the unsliced kernels' 128); 129 blocks, odd, whose last
 # slice ends in a partial stage; 13 stages over a partial last tile; the
-# down shape's K over 64 tiles; one tile of 256 blocks (slices of 64
-# blocks); 40 tiles
+# down shape's K over 64 tiles; one tile of 256 blocks (slices of 32
+# blocks); 40 tiles; rows of 512 and 548 blocks over one tile (sixteen and
+# thirty-two slices)
 Q45_SHAPES = [(Q4, 5120, 17408), (Q4, 2560, 34816), (Q5, 100, 33024), (Q4, 1000, 12800),
-              (Q5, 1024, 17408), (Q4, 3, 65536), (Q4, 640, 17408), (Q5, 640, 17408)]
+              (Q5, 1024, 17408), (Q4, 3, 65536), (Q4, 640, 17408), (Q5, 640, 17408),
+              (Q4, 3, 131072), (Q4, 16, 140288), (Q5, 16, 140288)]
 
 
 @pytest.mark.parametrize("t,rows,cols", Q45_SHAPES)
