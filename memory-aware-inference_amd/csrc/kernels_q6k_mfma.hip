@@ -254,7 +254,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
                                                               SliceArgs sla) {
   static_assert(!ARGMAX || (NTOK == 1 && !GROUPED), "argmax over one matrix and vector");
   static_assert(!SLICED || (NTOK == 1 && !GROUPED && !ARGMAX), "slices of one matrix and vector");
-  static_assert(!PAIRED || (NTOK == 1 && !GROUPED && !SLICED), "row pairs of one matrix");
+  static_assert(!PAIRED || (NTOK == 1 && !GROUPED), "row pairs of one matrix");
+  static_assert(!(PAIRED && SLICED && ARGMAX), "sliced row pairs: no argmax");
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   if constexpr (GROUPED) load_group_args_early(ga);
   const uint32_t slots = sa.packed & 0xffu;
@@ -284,7 +285,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   // 1. x into the image area, natural order (block b of vector t at
   //    img + t img_stride + 1024 b)
   if constexpr (PAIRED) {
-    copy_x<WAVES>(smem, L.img, x, nb, wave, lane, nr);  // x twice over
+    // x twice over; a slice, the stretch of it that its stages meet
+    copy_x<WAVES>(smem, L.img, x, nbl, wave, lane, nr, 2u * st0);
   } else {
 #pragma unroll
     for (int t = 0; t < NTOK; ++t)
@@ -512,8 +514,11 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
         ra = sum_lane_groups(pp[0]);
         rb = sum_lane_groups(pp[1]);
       }
-      hand_off<1, ARGMAX, true>(sbase, L, slots, sc, sa, pr, nstages, ra, lane, rows, y, ws, fail,
-                                &best, aa.rule, rb);
+      if constexpr (SLICED)
+        hand_off_slice<true>(sbase, L, ss, pr, ra, lane, rows, y, ws, fail, rb);
+      else
+        hand_off<1, ARGMAX, true>(sbase, L, slots, sc, sa, pr, nstages, ra, lane, rows, y, ws,
+                                  fail, &best, aa.rule, rb);
       continue;
     }
     if (e0 == kBadBlock || (redo & 1u)) pp[0] = block_exact(q0, sc_0, d0, xs);
@@ -581,7 +586,8 @@ bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32
 }
 
 // A K-sliced launch in S slices (false when the shape or the LDS does not fit).
-template <int W, int D>
+// P: row pairs, rows and nb being the pairs' (rows / 2 rows of 2 nr blocks).
+template <int W, int D, bool P = false>
 bool launch_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                    uint32_t S, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
@@ -591,24 +597,26 @@ bool launch_sliced(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
   if (rows == 0u || nb == 0u || (nb & 1u) != 0u || (uint64_t)nb * kQ6Bytes * 16u > 0x7fffffffu)
     return false;
   SliceShape sh;
-  if (!slice_shape(ntiles, nstages, S, (uint32_t)cu_count(), ws.bytes, &sh)) return false;
+  if (!slice_shape(ntiles, nstages, S, (uint32_t)cu_count(), ws.bytes, &sh, P ? 128u : 64u))
+    return false;
   if (2u * sh.ns_max > kMaxMetaBlocks) return false;
   const uint32_t slots = ring_slots(W, D, sh.tiles_per_group, sh.ns_max);
   static const int pf_env = env_int("SI_HIP_Q6K_PREFETCH", -1);
   const uint32_t prefetch = D == 1 && pf_env > 0 ? (uint32_t)pf_env : 0u;
-  const uint32_t lds = layout(W, D, 2u * sh.ns_max, slots).total + (prefetch ? 256u : 0u);
+  const uint32_t lds =
+      layout(W, D, 2u * sh.ns_max, slots, 1u, P ? 2u : 1u).total + (prefetch ? 256u : 0u);
   if (lds > kLdsBytes || slots > 0xffu || sh.groups > 0xffffu) return false;
   SchedArgs sa{};
   sa.packed = (sh.groups << 16) | slots;
   sa.m_slots = div_magic(slots);
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, 1, false, false, true>),
+      reinterpret_cast<const void*>(&q6k_matvec_mfma<W, D, 1, false, false, true, P>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, 1, false, false, true>), dim3(sh.groups), dim3(W * 64),
+  hipLaunchKernelGGL((q6k_matvec_mfma<W, D, 1, false, false, true, P>), dim3(sh.groups), dim3(W * 64),
                      lds, s, w, x, y, rows, nb, ws.ptr, sa, prefetch, GroupArgs{}, ArgmaxArgs{},
                      sh.args);
   *err = hipGetLastError();
@@ -687,12 +695,21 @@ bool q6_shape_ok(uint32_t rows, uint32_t nb) {
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t nb = cols / kBlockElems;
+  static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
+  if (cfg == 0 && (nb & 1u) == 1u && rows >= 2u && (rows & 1u) == 0u) {
+    // row pairs, K-sliced by the rule of the even case (and always past 64
+    // blocks, where the pairs' rows exceed what the unsliced kernel takes)
+    const uint32_t prows = rows / 2u, pnb = 2u * nb;
+    const uint32_t S = q6_slices((prows + 15u) / 16u, pnb, ws.bytes);
+    if (S >= 2u && (launch_sliced<12, 1, true>(w, x, y, prows, pnb, S, ws, s, err) ||
+                    launch_sliced<8, 1, true>(w, x, y, prows, pnb, S, ws, s, err)))
+      return true;
+  }
   if (paired_ok(rows, nb))
     return launch_wd<12, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
            launch_wd<10, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
            launch_wd<8, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
            launch_wd<4, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err);
-  static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
   if (cfg == 0 && nb > kMaxMetaBlocks) {  // (q6_shape_ok takes none of these)
     const uint32_t S = q6_slices((rows + 15u) / 16u, nb, ws.bytes);
     return S >= 2u && (launch_sliced<12, 1>(w, x, y, rows, nb, S, ws, s, err) ||

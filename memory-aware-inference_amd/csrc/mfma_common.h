@@ -231,11 +231,13 @@ __device__ __forceinline__ float sum_lane_groups(float v) {
 // (block b at img + 1024 b): pass j of wave v copies blocks 4 (v + WAVES j)
 // .. +3, one 64-lane 16-byte copy each -- the blocks build_images has the
 // same wave convert, so that a wave's own wait covers what it converts.
-// src_nb != 0: the image holds nb = 2 src_nb blocks, block b being x block
-// b mod src_nb (x twice over).
+// src_nb != 0: the image holds blocks first .. first + nb - 1 of x twice
+// over (first + nb <= 2 src_nb), image block b being x block
+// (first + b) mod src_nb.
 template <int WAVES>
 __device__ __forceinline__ void copy_x(uint8_t* smem, uint32_t img, const float* x, uint32_t nb,
-                                       uint32_t wave, uint32_t lane, uint32_t src_nb = 0u) {
+                                       uint32_t wave, uint32_t lane, uint32_t src_nb = 0u,
+                                       uint32_t first = 0u) {
   const uint32_t xn = src_nb != 0u ? src_nb : nb;
   const uint32_t npass = (nb + 4u * WAVES - 1u) / (4u * WAVES);
   const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
@@ -244,8 +246,8 @@ __device__ __forceinline__ void copy_x(uint8_t* smem, uint32_t img, const float*
     const uint32_t b0 = 4u * (wave + WAVES * j);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const uint32_t b = b0 + i;
-      const uint32_t sb = b >= xn ? b - xn : b;
+      const uint32_t b = b0 + i, v = first + b;
+      const uint32_t sb = v >= xn ? v - xn : v;
       if (b < nb)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(smem + img + 1024u * b), 16,
                                                   1024u * sb + 16u * lane, 0, 0, 0);
@@ -932,22 +934,34 @@ __device__ __forceinline__ Pair pair_at(const SliceSched& s, uint32_t k) {
 // reads slice k of each batch of four; the first batch is read before the
 // count goes out, so the last slice waits about one memory round trip),
 // stores the rows and returns the entries and the counter to their empty
-// state.  The wait for an entry is bounded like hand_off's.
+// state.  The wait for an entry is bounded like hand_off's.  TWO (row pairs):
+// every row has two sums, rowsum for y[2 row] and rowsum2 for y[2 row + 1];
+// the LDS keeps 2 pstride partials per slot and an entry 32 floats (the
+// second sums at +16).
+template <bool TWO = false>
 __device__ __forceinline__ void hand_off_slice(uint32_t sbase, const Layout& L,
                                                const SliceSched& sc, const Pair& pr, float rowsum,
                                                uint32_t lane, uint32_t rows, float* __restrict__ y,
-                                               SplitWs ws, uint32_t& fail) {
+                                               SplitWs ws, uint32_t& fail, float rowsum2 = 0.0f) {
+  constexpr uint32_t kSums = TWO ? 2u : 1u;
   const uint32_t slots = sc.by_slots.d;
   const uint32_t slot = pr.lt - quo(pr.lt, sc.by_slots) * slots;
   wait_slot(sbase + L.owner + 4u * slot, pr.lt, fail);
-  const uint32_t pbase = sbase + L.part + 64u * sc.pstride * slot + 4u * (lane & 15u);
-  if ((lane >> 4) == 0u) lds_write_b32(pbase + 64u * (pr.r - pr.lo), __float_as_uint(rowsum));
+  const uint32_t pbase = sbase + L.part + 64u * kSums * sc.pstride * slot + 4u * (lane & 15u);
+  const uint32_t pbase2 = pbase + 64u * sc.pstride;  // TWO: the second sums
+  if ((lane >> 4) == 0u) {
+    lds_write_b32(pbase + 64u * (pr.r - pr.lo), __float_as_uint(rowsum));
+    if constexpr (TWO) lds_write_b32(pbase2 + 64u * (pr.r - pr.lo), __float_as_uint(rowsum2));
+  }
   uint32_t old = 0u;
   if (lane == 0u) old = lds_add_rtn(sbase + L.cnt + 4u * slot, 1u);
   const uint32_t done = __builtin_amdgcn_readlane(old, 0);
   if (done != sc.ns - 1u) return;
-  float sum = 0.0f;
-  for (uint32_t k = 0; k < sc.ns; ++k) sum += __uint_as_float(lds_read_b32(pbase + 64u * k));
+  float sum = 0.0f, sum2 = 0.0f;
+  for (uint32_t k = 0; k < sc.ns; ++k) {
+    sum += __uint_as_float(lds_read_b32(pbase + 64u * k));
+    if constexpr (TWO) sum2 += __uint_as_float(lds_read_b32(pbase2 + 64u * k));
+  }
   // the partials are in registers: the slot can take the workgroup's next tile
   if (lane == 0u) {
     lds_write_b32(sbase + L.cnt + 4u * slot, 0u);
@@ -959,46 +973,69 @@ __device__ __forceinline__ void hand_off_slice(uint32_t sbase, const Layout& L,
   asm volatile("" : "+v"(ln));
   const uint32_t grp = ln >> 4, n = ln & 15u;
   const uint32_t S = sc.slices;
-  float* const ent = ws.part + (size_t)pr.tile * S * 16u + n;  // slice k at ent + 16 k
-  if (grp == 0u) store_coherent(ent + 16u * sc.s, sum);
-  auto fetch = [&](uint32_t k, float& v) {
-    if (k == sc.s)
+  // slice k at ent + 16 kSums k (its second sums 16 floats on)
+  float* const ent = ws.part + (size_t)pr.tile * S * 16u * kSums + n;
+  if (grp == 0u) {
+    store_coherent(ent + 16u * kSums * sc.s, sum);
+    if constexpr (TWO) store_coherent(ent + 16u * kSums * sc.s + 16u, sum2);
+  }
+  auto fetch = [&](uint32_t k, float& v, float& v2) {
+    if (k == sc.s) {
       v = sum;
-    else if (k < S)
-      v = load_coherent(ent + 16u * k);
+      v2 = sum2;
+    } else if (k < S) {
+      v = load_coherent(ent + 16u * kSums * k);
+      if constexpr (TWO) v2 = load_coherent(ent + 16u * kSums * k + 16u);
+    }
   };
-  float v = 0.0f;
-  fetch(grp, v);
+  float v = 0.0f, v2 = 0.0f;
+  fetch(grp, v, v2);
   const uint32_t force = __builtin_amdgcn_readfirstlane(give_up_polls(ws.cnt));
   uint32_t before = 0u;
   if (lane == 0u)
     before = __hip_atomic_fetch_add(ws.cnt + pr.tile, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   before = __builtin_amdgcn_readlane(before, 0);
   if (before + 1u != S) return;
-  float total = 0.0f;
+  float total = 0.0f, total2 = 0.0f;
   for (uint32_t base = 0; base < S; base += 4u) {
     const uint32_t k = base + grp;
-    if (base != 0u) fetch(k, v);
+    if (base != 0u) fetch(k, v, v2);
     for (uint32_t spin = 0;; ++spin) {
       const bool missing =
-          k < S && k != sc.s && (force != 0u || __float_as_uint(v) == kPartEmpty);
+          k < S && k != sc.s &&
+          (force != 0u || __float_as_uint(v) == kPartEmpty ||
+           (TWO && __float_as_uint(v2) == kPartEmpty));
       if (!__builtin_amdgcn_ballot_w64(missing)) break;
       if (spin == (force != 0u ? force : (1u << 22))) {
         fail = kDevErrCombineWait;
         break;
       }
       __builtin_amdgcn_s_sleep(1);
-      if (missing) fetch(k, v);
+      if (missing) fetch(k, v, v2);
     }
 #pragma unroll
     for (uint32_t j = 0; j < 4u; ++j) {
       const float vj = __shfl(v, (int)(n + 16u * j), 64);
       if (base + j < S) total += vj;
+      if constexpr (TWO) {
+        const float wj = __shfl(v2, (int)(n + 16u * j), 64);
+        if (base + j < S) total2 += wj;
+      }
     }
-    if (k < S) store_coherent(ent + 16u * k, __uint_as_float(kPartEmpty));
+    if (k < S) {
+      store_coherent(ent + 16u * kSums * k, __uint_as_float(kPartEmpty));
+      if constexpr (TWO) store_coherent(ent + 16u * kSums * k + 16u, __uint_as_float(kPartEmpty));
+    }
   }
   const uint32_t row = pr.tile * 16u + n;
-  if (grp == 0u && row < rows) y[row] = total;
+  if (grp == 0u && row < rows) {
+    if constexpr (TWO) {
+      y[2u * row] = total;
+      y[2u * row + 1u] = total2;
+    } else {
+      y[row] = total;
+    }
+  }
   if (lane == 0u)
     (void)__hip_atomic_exchange(ws.cnt + pr.tile, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
@@ -1012,11 +1049,11 @@ struct SliceShape {
   SliceArgs args;
 };
 inline bool slice_shape(uint32_t ntiles, uint32_t nstages, uint32_t S, uint32_t cus,
-                        size_t ws_bytes, SliceShape* out) {
+                        size_t ws_bytes, SliceShape* out, uint32_t entry_bytes = 64u) {
   if (S < 2u || S > 64u || nstages < S || ntiles == 0u || cus < S) return false;
   const uint32_t gs = min(ntiles, cus / S);
   if ((size_t)ntiles * 4u + 64u > kCounterBytes ||
-      kCounterBytes + (size_t)ntiles * S * 64u + 4096u > ws_bytes)
+      kCounterBytes + (size_t)ntiles * S * entry_bytes + 4096u > ws_bytes)
     return false;
   const uint32_t ns_lo = nstages / S, rem = nstages % S;
   out->groups = gs * S;

@@ -6,7 +6,10 @@ even row count runs on the matrix cores as row pairs: the launch sees
 rows / 2 rows of 2 nb blocks (rows 2 r and 2 r + 1 back to back, which
 start aligned), x sits twice in the image area, and each block's sum goes
 to its own row of the pair -- the stage holding blocks nb - 1 and nb hands
-one sum to each.  Odd row counts keep the generic kernel.
+one sum to each.  Long pair rows over few tiles, and every pair row past 128
+blocks (nb > 64), run K-sliced: a workgroup holds the images of its slice's
+stretch of the doubled x, and the slice hand-off carries both sums of each
+row.  Odd row counts keep the generic kernel.
 
 Bar: rows within 2e-5 * sum|w*x| of the f64 dot, +-inf / NaN rows where
 per-weight f32 products give them, the same bits on every call, and the
@@ -33,10 +36,12 @@ def log(msg):
 
 # (rows, cols): one block per row (the single stage straddles the pair);
 # 9 blocks over a partial tile of pairs (17 pairs); the Gemma-class head
-# width 5376 (21 blocks); the Llama-2-7B down projection (43 blocks); a head
-# of 32000 rows (a split launch of 1000 pair tiles); an odd row count (the
-# generic kernel)
-SHAPES = [(2, 256), (34, 2304), (1000, 5376), (4096, 11008), (32000, 5376), (41, 2304)]
+# width 5376 (21 blocks); the Llama-2-7B down projection (43 blocks, K-sliced
+# pairs); a head of 32000 rows (a split launch of 1000 pair tiles); an odd
+# row count (the generic kernel); pair rows past 128 blocks, which must slice
+# (67, 65 and 129 blocks; 135 blocks: eight slices)
+SHAPES = [(2, 256), (34, 2304), (1000, 5376), (4096, 11008), (32000, 5376), (41, 2304),
+          (100, 17152), (2560, 16640), (2, 33024), (40, 34560)]
 
 
 @pytest.mark.parametrize("rows,cols", SHAPES)
@@ -83,23 +88,119 @@ def test_odd_block_count_special_activations(hip_ctx):
         W.free()
 
 
+def test_sliced_pairs_special_activations(hip_ctx):
+    """Huge, side, subnormal and zero blocks across the slices of 67-block
+    pair rows, including the straddling stage (blocks 66 and 67 of a pair
+    row), then one infinite or NaN activation at a time."""
+    rows, cols = 200, 17152
+    w = si_hip.synth_matrix(Q6, seed=4600, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, Q6)
+    base = si_hip.synth_normal(4601, cols)
+    try:
+        x = base.copy()
+        x[100:140] = np.float32(3e30)
+        x[4096 + 7] = np.float32(1e-9)
+        x[4096 + 300:4096 + 303] = np.float32(-2e-10)
+        x[8192:8192 + 256] = np.float32(1e-41)
+        x[cols - 256:] = 0.0
+        _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+        assert_dot_close(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x), y64, ab,
+                         what="special blocks")
+        for k, v in [(5, np.inf), (cols - 1, -np.inf), (9000, np.nan), (256 * 33 + 3, np.inf)]:
+            x = base.copy()
+            x[k] = v
+            y32, _, _ = O.matvec(Q6, w, rows, cols, x, threads=8)
+            y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+            assert np.array_equal(_category(y), _category(y32)), f"x[{k}] = {v}"
+    finally:
+        W.free()
+
+
+def test_sliced_pairs_in_a_graph(hip_ctx):
+    """Sliced row pairs (32-float workspace entries) and a plain sliced Q6_K
+    launch (16-float entries) on one workspace, recorded in a HIP graph and
+    replayed three times with eager launches between: every replay equals
+    the eager run bit for bit (both leave the entries empty)."""
+    import ctypes as C
+    lib = si_hip.lib()
+    P = C.c_void_p
+    shapes = [(4096, 11008), (2560, 17408), (100, 17152)]
+    mats, ins, outs = [], [], []
+    for rows, cols in shapes:
+        w = si_hip.synth_matrix(Q6, seed=rows + cols + 5, rows=rows, cols=cols, threads=8)
+        mats.append((w, hip_ctx.upload_quant_weight_private(w, Q6)))
+        x = si_hip.synth_normal(rows * 5 + cols, cols)
+        d_x = hip_ctx.device_alloc(cols * 4)
+        hip_ctx.to_device(d_x, x)
+        ins.append((x, d_x))
+        outs.append(hip_ctx.device_alloc(rows * 4))
+    d_e = hip_ctx.device_alloc(4096 * 4)
+    h = hip_ctx.handle
+
+    def enqueue():
+        for (rows, cols), (_, W), (_, d_x), d_y in zip(shapes, mats, ins, outs):
+            rc = lib.si_hip_quant_matvec_device(h, W.handle, rows, cols, P(d_x), P(d_y))
+            assert rc == 0, si_hip.last_error()
+
+    def results():
+        hip_ctx.synchronize()
+        return [hip_ctx.from_device(d_y, rows) for (rows, _), d_y in zip(shapes, outs)]
+
+    try:
+        enqueue()
+        ref = results()
+        for (rows, cols), (w, _), (x, _), y in zip(shapes, mats, ins, ref):
+            _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+            assert_dot_close(y, y64, ab, what=f"eager {rows}x{cols}")
+        hip_ctx.capture_begin()
+        enqueue()
+        graph = hip_ctx.capture_end()
+        try:
+            for rep in range(3):
+                for (rows, _), d_y in zip(shapes, outs):
+                    hip_ctx.to_device(d_y, np.full(rows, np.nan, np.float32))
+                (rows, cols), (_, W), (_, d_x) = shapes[0], mats[0], ins[0]
+                assert lib.si_hip_quant_matvec_device(h, W.handle, rows, cols, P(d_x), P(d_e)) == 0
+                hip_ctx.synchronize()
+                log(f"sliced pairs graph replay {rep}")
+                graph.launch()
+                for a, b in zip(results(), ref):
+                    assert same_bits(a, b), f"replay {rep} differs"
+        finally:
+            graph.free()
+    finally:
+        for _, W in mats:
+            W.free()
+        for _, d_x in ins:
+            hip_ctx.device_free(d_x)
+        for d_y in outs:
+            hip_ctx.device_free(d_y)
+        hip_ctx.device_free(d_e)
+
+
 @pytest.mark.parametrize("rows,cols", [(20000, 2304), (4098, 5376)])
 def test_odd_block_count_head_argmax(hip_ctx, rows, cols):
-    """The output head with the argmax fused into the paired launch: logits
-    equal the plain matvec's bit for bit and the token the oracle's, under
-    both tie rules; crafted ties across even and odd rows."""
+    """The output head with the argmax fused into the paired launch: the
+    token is the oracle's argmax of the logits the call returns, under both
+    tie rules, the logits repeat their bits and meet the bound (the plain
+    matvec of the same head may run K-sliced, so it agrees within the bound);
+    crafted ties across even and odd rows."""
     w = si_hip.synth_matrix(Q6, seed=rows + cols, rows=rows, cols=cols, threads=8)
     x = si_hip.synth_normal(rows - cols, cols)
     H = hip_ctx.upload_quant_weight_private(w, Q6)
     try:
         y = hip_ctx.gguf_quant_matvec_weight(H, rows, cols, x)
+        _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+        assert_dot_close(y, y64, ab, what="head logits")
+        first = None
         for rule, pick in ((si_hip.ARGMAX_LAST_FINITE, O.argmax_last_finite),
                            (si_hip.ARGMAX_FIRST_GREATER, O.argmax_first_greater)):
             tok, logits = hip_ctx.gguf_quant_matvec_argmax_weight(H, rows, cols, x, rule=rule)
-            assert same_bits(logits, y)
-            assert tok == pick(y)
-        _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
-        assert_dot_close(y, y64, ab, what="head logits")
+            assert tok == pick(logits)
+            assert_dot_close(logits, y64, ab, what="fused head logits")
+            if first is None:
+                first = logits
+            assert same_bits(logits, first)
     finally:
         H.free()
     # ties: rows 7 (odd), 10 (even) and rows - 1 (odd) carry the same largest row
