@@ -501,12 +501,21 @@ int run_matvec_host(si_hip_context *ctx, uint32_t type, const uint8_t *dev_w, si
   if (rc) return rc;
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, input, in_bytes),
               "input copy");
-  rc = dispatch_matvec(ctx, type, dev_w, static_cast<const float *>(ctx->stage_in),
-                       static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)columns,
-                       (uint32_t)batch, ctx->stream);
+  // the kernel stores the rows straight into pinned host staging (no copy
+  // back after it); larger outputs go through device staging
+  float *dev_out = static_cast<float *>(ctx->stage_out);
+  uint8_t *pinned_out = nullptr;
+  if (out_bytes <= kPinnedMaxCopy) {
+    pinned_out = pin_take(ctx, ctx->pin_out, out_bytes);
+    if (!pinned_out) return fail(SI_HIP_ERR_OUT_OF_MEMORY, "HIP could not allocate pinned staging");
+    ctx->pending.push_back({output, pinned_out, out_bytes});
+    dev_out = reinterpret_cast<float *>(pinned_out);
+  }
+  rc = dispatch_matvec(ctx, type, dev_w, static_cast<const float *>(ctx->stage_in), dev_out,
+                       (uint32_t)rows, (uint32_t)columns, (uint32_t)batch, ctx->stream);
   if (rc) return rc;
-  SIHIP_CHECK(copy_out(ctx, output, ctx->stage_out, out_bytes),
-              "output copy");
+  if (!pinned_out)
+    SIHIP_CHECK(copy_out(ctx, output, ctx->stage_out, out_bytes), "output copy");
   rc = wait_stream(ctx, what);
   if (rc) return rc;
   return ok();
