@@ -310,6 +310,28 @@ hipError_t copy_out(si_hip_context *ctx, void *host, const void *dev, size_t byt
   return hipMemcpyAsync(host, dev, bytes, hipMemcpyDeviceToHost, ctx->stream);
 }
 
+// Where a synchronous call's kernel stores an output: a pinned region when
+// the bytes fit there (the kernel's stores cross PCIe; the bytes reach the
+// caller's buffer after the stream wait, with no copy back), else the
+// device staging buffer, which `deliver` copies out.
+struct OutStage {
+  float *ptr;
+  bool pinned;
+};
+
+OutStage out_stage(si_hip_context *ctx, size_t bytes) {
+  if (bytes > 0 && bytes <= kPinnedMaxCopy)
+    if (uint8_t *p = pin_take(ctx, ctx->pin_out, bytes)) return {reinterpret_cast<float *>(p), true};
+  return {static_cast<float *>(ctx->stage_out), false};
+}
+
+// The `floats` values at o.ptr + off to the caller's buffer `host`.
+hipError_t deliver(si_hip_context *ctx, void *host, const OutStage &o, size_t off, size_t floats) {
+  if (!o.pinned) return copy_out(ctx, host, o.ptr + off, floats * sizeof(float));
+  if (floats) ctx->pending.push_back({host, o.ptr + off, floats * sizeof(float)});
+  return hipSuccess;
+}
+
 // After the stream has drained: outputs to the caller, staging reset.
 void finish_staging(si_hip_context *ctx, bool deliver) {
   if (deliver)
@@ -501,21 +523,11 @@ int run_matvec_host(si_hip_context *ctx, uint32_t type, const uint8_t *dev_w, si
   if (rc) return rc;
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, input, in_bytes),
               "input copy");
-  // the kernel stores the rows straight into pinned host staging (no copy
-  // back after it); larger outputs go through device staging
-  float *dev_out = static_cast<float *>(ctx->stage_out);
-  uint8_t *pinned_out = nullptr;
-  if (out_bytes <= kPinnedMaxCopy) {
-    pinned_out = pin_take(ctx, ctx->pin_out, out_bytes);
-    if (!pinned_out) return fail(SI_HIP_ERR_OUT_OF_MEMORY, "HIP could not allocate pinned staging");
-    ctx->pending.push_back({output, pinned_out, out_bytes});
-    dev_out = reinterpret_cast<float *>(pinned_out);
-  }
-  rc = dispatch_matvec(ctx, type, dev_w, static_cast<const float *>(ctx->stage_in), dev_out,
+  const OutStage o = out_stage(ctx, out_bytes);
+  rc = dispatch_matvec(ctx, type, dev_w, static_cast<const float *>(ctx->stage_in), o.ptr,
                        (uint32_t)rows, (uint32_t)columns, (uint32_t)batch, ctx->stream);
   if (rc) return rc;
-  if (!pinned_out)
-    SIHIP_CHECK(copy_out(ctx, output, ctx->stage_out, out_bytes), "output copy");
+  SIHIP_CHECK(deliver(ctx, output, o, 0, batch * rows), "output copy");
   rc = wait_stream(ctx, what);
   if (rc) return rc;
   return ok();
@@ -973,15 +985,14 @@ int si_hip_gguf_quant_matvec_many_bytes(si_hip_context *ctx, const uint32_t *typ
   if (rc) return rc;
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
-  float *dst = static_cast<float *>(ctx->stage_out);
+  const OutStage o = out_stage(ctx, total_rows * sizeof(float));
   rc = dispatch_matvec_group(ctx, types, dev.data(), rows, count,
-                             static_cast<const float *>(ctx->stage_in), dst, (uint32_t)cols,
+                             static_cast<const float *>(ctx->stage_in), o.ptr, (uint32_t)cols,
                              ctx->stream);
   if (rc) return rc;
   size_t off = 0;
   for (size_t i = 0; i < count; ++i) {
-    SIHIP_CHECK(copy_out(ctx, outputs[i], dst + off, rows[i] * sizeof(float)),
-                "output copy");
+    SIHIP_CHECK(deliver(ctx, outputs[i], o, off, rows[i]), "output copy");
     off += rows[i];
   }
   rc = wait_stream(ctx, "staged grouped quantized matvec command");
@@ -1082,14 +1093,13 @@ int si_hip_gguf_quant_matvec_many_weights(si_hip_context *ctx,
   if (rc) return rc;
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
-  float *dst = static_cast<float *>(ctx->stage_out);
+  const OutStage o = out_stage(ctx, total_rows * sizeof(float));
   rc = dispatch_weight_group(ctx, weights, rows, count, static_cast<const float *>(ctx->stage_in),
-                             dst, (uint32_t)cols, ctx->stream);
+                             o.ptr, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
   size_t off = 0;
   for (size_t i = 0; i < count; ++i) {
-    SIHIP_CHECK(copy_out(ctx, outputs[i], dst + off, rows[i] * sizeof(float)),
-                "output copy");
+    SIHIP_CHECK(deliver(ctx, outputs[i], o, off, rows[i]), "output copy");
     off += rows[i];
   }
   rc = wait_stream(ctx, "grouped quantized matvec command");
@@ -1126,11 +1136,11 @@ int si_hip_q4_k_fused_gate_up(si_hip_context *ctx, const uint8_t *gate, size_t g
   if (rc) return rc;
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
-  rc = dispatch_gate_up(ctx, dgu[0], dgu[1], static_cast<const float *>(ctx->stage_in),
-                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols, ctx->stream);
+  const OutStage o = out_stage(ctx, rows * sizeof(float));
+  rc = dispatch_gate_up(ctx, dgu[0], dgu[1], static_cast<const float *>(ctx->stage_in), o.ptr,
+                        (uint32_t)rows, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
-  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, rows * sizeof(float)),
-              "output copy");
+  SIHIP_CHECK(deliver(ctx, out, o, 0, rows), "output copy");
   rc = wait_stream(ctx, "Q4_K fused gate/up command");
   if (rc) return rc;
   return ok();
@@ -1169,11 +1179,11 @@ int si_hip_q4_k_fused_gate_up_weights(si_hip_context *ctx, const si_hip_quant_we
   if (rc) return rc;
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
-  rc = dispatch_gate_up(ctx, g->data(), u->data(), static_cast<const float *>(ctx->stage_in),
-                        static_cast<float *>(ctx->stage_out), (uint32_t)rows, (uint32_t)cols, ctx->stream);
+  const OutStage o = out_stage(ctx, rows * sizeof(float));
+  rc = dispatch_gate_up(ctx, g->data(), u->data(), static_cast<const float *>(ctx->stage_in), o.ptr,
+                        (uint32_t)rows, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
-  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, rows * sizeof(float)),
-              "output copy");
+  SIHIP_CHECK(deliver(ctx, out, o, 0, rows), "output copy");
   rc = wait_stream(ctx, "retained Q4_K fused gate/up command");
   if (rc) return rc;
   return ok();
@@ -1229,11 +1239,11 @@ int si_hip_gguf_quant_fused_mlp_weights(si_hip_context *ctx, const si_hip_quant_
   rc = dispatch_gate_up(ctx, g->data(), u->data(), static_cast<const float *>(ctx->stage_in), hidden,
                         (uint32_t)gate_rows, (uint32_t)cols, ctx->stream);
   if (rc) return rc;
-  rc = dispatch_matvec(ctx, d->ggml_type, d->data(), hidden, static_cast<float *>(ctx->stage_out),
-                       (uint32_t)down_rows, (uint32_t)gate_rows, 1, ctx->stream);
+  const OutStage o = out_stage(ctx, down_rows * sizeof(float));
+  rc = dispatch_matvec(ctx, d->ggml_type, d->data(), hidden, o.ptr, (uint32_t)down_rows,
+                       (uint32_t)gate_rows, 1, ctx->stream);
   if (rc) return rc;
-  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, down_rows * sizeof(float)),
-              "output copy");
+  SIHIP_CHECK(deliver(ctx, out, o, 0, down_rows), "output copy");
   char what[64];
   snprintf(what, sizeof what, "fused MLP %s command", type_label(d->ggml_type));
   rc = wait_stream(ctx, what);
@@ -1255,11 +1265,11 @@ int si_hip_q4_k_embedding_row(si_hip_context *ctx, const uint8_t *row, size_t ro
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, cols * sizeof(float));
   if (rc) return rc;
-  hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, dev, nullptr,
-                                       static_cast<float *>(ctx->stage_out), 1, (uint32_t)cols, ctx->stream);
+  const OutStage o = out_stage(ctx, cols * sizeof(float));
+  hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, dev, nullptr, o.ptr, 1, (uint32_t)cols,
+                                       ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
-  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, cols * sizeof(float)),
-              "output copy");
+  SIHIP_CHECK(deliver(ctx, out, o, 0, cols), "output copy");
   rc = wait_stream(ctx, "Q4_K embedding command");
   if (rc) return rc;
   return ok();
@@ -1314,13 +1324,13 @@ int si_hip_q4_k_embedding_tokens(si_hip_context *ctx, const si_hip_quant_weight 
   if (rc) return rc;
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, ids, n * sizeof(uint32_t)),
               "token id copy");
+  const OutStage o = out_stage(ctx, n * cols * sizeof(float));
   hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, t->data(),
-                                       static_cast<const uint32_t *>(ctx->stage_in),
-                                       static_cast<float *>(ctx->stage_out), (uint32_t)n, (uint32_t)cols,
-                                       ctx->stream, embedding_table_rows(t, cols, rows), ctx->ws.ptr);
+                                       static_cast<const uint32_t *>(ctx->stage_in), o.ptr,
+                                       (uint32_t)n, (uint32_t)cols, ctx->stream,
+                                       embedding_table_rows(t, cols, rows), ctx->ws.ptr);
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
-  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, n * cols * sizeof(float)),
-              "output copy");
+  SIHIP_CHECK(deliver(ctx, out, o, 0, n * cols), "output copy");
   rc = wait_stream(ctx, "Q4_K embedding command");
   if (rc) return rc;
   return ok();
@@ -1357,11 +1367,11 @@ int si_hip_q4_k_embedding_view(si_hip_context *ctx, uint32_t type, const uint64_
   if (rc) return rc;
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, (size_t)cols * sizeof(float));
   if (rc) return rc;
+  const OutStage o = out_stage(ctx, (size_t)cols * sizeof(float));
   hipError_t e = sihip::launch_dequant(SI_HIP_GGML_TYPE_Q4_K, whole ? dev + start : dev, nullptr,
-                                       static_cast<float *>(ctx->stage_out), 1, (uint32_t)cols,
-                                       ctx->stream);
+                                       o.ptr, 1, (uint32_t)cols, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "embedding launch");
-  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, (size_t)cols * sizeof(float)), "output copy");
+  SIHIP_CHECK(deliver(ctx, out, o, 0, cols), "output copy");
   rc = wait_stream(ctx, "Q4_K embedding command");
   if (rc) return rc;
   return ok();
@@ -1541,12 +1551,12 @@ int run_f32_matvec_host(si_hip_context *ctx, const float *w, size_t rows, size_t
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, yb);
   if (rc) return rc;
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, x, xb), "input copy");
+  const OutStage o = out_stage(ctx, yb);
   hipError_t e = sihip::launch_f32_matvec(reinterpret_cast<const float *>(dw),
-                                          static_cast<const float *>(ctx->stage_in),
-                                          static_cast<float *>(ctx->stage_out), (uint32_t)rows,
-                                          (uint32_t)cols, ctx->stream);
+                                          static_cast<const float *>(ctx->stage_in), o.ptr,
+                                          (uint32_t)rows, (uint32_t)cols, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "F32 matvec launch");
-  SIHIP_CHECK(copy_out(ctx, y, ctx->stage_out, yb), "output copy");
+  SIHIP_CHECK(deliver(ctx, y, o, 0, rows), "output copy");
   rc = wait_stream(ctx, "F32 matvec command");
   if (rc) return rc;
   return ok();
@@ -1587,11 +1597,11 @@ int run_rms_host(si_hip_context *ctx, uint32_t mode, const float *x, const float
   SIHIP_CHECK(copy_in(ctx, dx, x, xb), "input copy");
   if (dg) SIHIP_CHECK(copy_in(ctx, dg, gate, xb), "gate copy");
   SIHIP_CHECK(hipMemcpyAsync(ctx->stage_aux, w, wb, hipMemcpyHostToDevice, ctx->stream), "weight copy");
+  const OutStage o = out_stage(ctx, xb);
   hipError_t e = sihip::launch_rms_norm(mode, dx, dg, static_cast<const float *>(ctx->stage_aux),
-                                        static_cast<float *>(ctx->stage_out), (uint32_t)heads,
-                                        (uint32_t)head_dim, eps, ctx->stream);
+                                        o.ptr, (uint32_t)heads, (uint32_t)head_dim, eps, ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "RMSNorm launch");
-  SIHIP_CHECK(copy_out(ctx, y, ctx->stage_out, xb), "output copy");
+  SIHIP_CHECK(deliver(ctx, y, o, 0, n), "output copy");
   rc = wait_stream(ctx, "RMSNorm command");
   if (rc) return rc;
   return ok();
@@ -1665,15 +1675,15 @@ int si_hip_f32_matvec_many(si_hip_context *ctx, const float *const *ws, const si
   if (rc) return rc;
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, x, cols * sizeof(float)),
               "input copy");
-  float *dy = static_cast<float *>(ctx->stage_out);
+  const OutStage o = out_stage(ctx, ytotal * sizeof(float));
+  size_t off = 0;
   for (size_t i = 0; i < count; ++i) {
     hipError_t e = sihip::launch_f32_matvec(reinterpret_cast<const float *>(dws[i]),
-                                            static_cast<const float *>(ctx->stage_in), dy,
+                                            static_cast<const float *>(ctx->stage_in), o.ptr + off,
                                             (uint32_t)rows[i], (uint32_t)cols, ctx->stream);
     if (e != hipSuccess) return hip_fail(e, "F32 matvec launch");
-    SIHIP_CHECK(copy_out(ctx, ys[i], dy, rows[i] * sizeof(float)),
-                "output copy");
-    dy += rows[i];
+    SIHIP_CHECK(deliver(ctx, ys[i], o, off, rows[i]), "output copy");
+    off += rows[i];
   }
   rc = wait_stream(ctx, "F32 matvec group command");
   if (rc) return rc;
@@ -1751,11 +1761,11 @@ int si_hip_dequantize(si_hip_context *ctx, uint32_t type, const uint8_t *bytes, 
   rc = grow(ctx, &ctx->stage_out, &ctx->stage_out_bytes, elements * sizeof(float));
   if (rc) return rc;
   // treat the blocks as one row-major [blocks x 256] matrix
-  hipError_t e = sihip::launch_dequant(type, dev, nullptr, static_cast<float *>(ctx->stage_out),
-                                       (uint32_t)(elements / 256), 256, ctx->stream);
+  const OutStage o = out_stage(ctx, elements * sizeof(float));
+  hipError_t e = sihip::launch_dequant(type, dev, nullptr, o.ptr, (uint32_t)(elements / 256), 256,
+                                       ctx->stream);
   if (e != hipSuccess) return hip_fail(e, "dequantize launch");
-  SIHIP_CHECK(copy_out(ctx, out, ctx->stage_out, elements * sizeof(float)),
-              "output copy");
+  SIHIP_CHECK(deliver(ctx, out, o, 0, elements), "output copy");
   rc = wait_stream(ctx, "dequantize command");
   if (rc) return rc;
   return ok();
