@@ -72,6 +72,41 @@ __global__ __launch_bounds__(256) void matvec_generic_kernel(
   }
 }
 
+// One row of nb blocks by one workgroup: thread t decodes units t, t + 256,
+// ... exactly as quant.rs does, the four waves' sums meet in LDS.
+template <uint32_t T>
+__global__ __launch_bounds__(256) void row_dot_kernel(const uint8_t* __restrict__ w,
+                                                      const float* __restrict__ x,
+                                                      float* __restrict__ y, uint32_t cols) {
+  constexpr uint32_t BB = BlockBytes<T>::value;
+  __shared__ float part[4];
+  const uint32_t nb = cols / kBlockElems;
+  float acc = 0.0f;
+  for (uint32_t u = threadIdx.x; u < nb * 8u; u += 256u) {
+    float v[32];
+    decode_unit_exact<T>(w + (size_t)(u >> 3) * BB, u & 7u, v);
+    uint32_t col0;
+    if constexpr (T == kTypeQ6K) {
+      col0 = (u >> 3) * 256u + ((u & 7u) >> 2) * 128u + (u & 3u) * 32u;
+    } else {
+      col0 = (u >> 3) * 256u + (u & 7u) * 32u;
+    }
+    const float4* xv = reinterpret_cast<const float4*>(x + col0);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 xx = xv[i];
+      acc = fmaf(v[4 * i + 0], xx.x, acc);
+      acc = fmaf(v[4 * i + 1], xx.y, acc);
+      acc = fmaf(v[4 * i + 2], xx.z, acc);
+      acc = fmaf(v[4 * i + 3], xx.w, acc);
+    }
+  }
+  acc = wave_sum(acc);
+  if ((threadIdx.x & 63u) == 0u) part[threadIdx.x >> 6] = acc;
+  __syncthreads();
+  if (threadIdx.x == 0u) y[0] = (part[0] + part[1]) + (part[2] + part[3]);
+}
+
 // silu(g) * u with both projections Q4_K (si_q4_k_fused_gate_up, metal.rs:585).
 __global__ __launch_bounds__(256) void fused_gate_up_generic_kernel(
     const uint8_t* __restrict__ gate, const uint8_t* __restrict__ up, const float* __restrict__ x,
@@ -172,6 +207,24 @@ hipError_t launch_matvec_generic(uint32_t type, const uint8_t* w, const float* x
       return hipErrorInvalidValue;
   }
 #undef SIHIP_MV
+  return hipGetLastError();
+}
+
+hipError_t launch_row_dot(uint32_t type, const uint8_t* w, const float* x, float* y,
+                          uint32_t cols, hipStream_t s) {
+  switch (type) {
+    case kTypeQ4K:
+      hipLaunchKernelGGL(row_dot_kernel<kTypeQ4K>, dim3(1), dim3(256), 0, s, w, x, y, cols);
+      break;
+    case kTypeQ5K:
+      hipLaunchKernelGGL(row_dot_kernel<kTypeQ5K>, dim3(1), dim3(256), 0, s, w, x, y, cols);
+      break;
+    case kTypeQ6K:
+      hipLaunchKernelGGL(row_dot_kernel<kTypeQ6K>, dim3(1), dim3(256), 0, s, w, x, y, cols);
+      break;
+    default:
+      return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

@@ -692,24 +692,44 @@ bool q6_shape_ok(uint32_t rows, uint32_t nb) {
 
 }  // namespace
 
-bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
-                            uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
-  const uint32_t nb = cols / kBlockElems;
-  static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
-  if (cfg == 0 && (nb & 1u) == 1u && rows >= 2u && (rows & 1u) == 0u) {
-    // row pairs, K-sliced by the rule of the even case (and always past 64
-    // blocks, where the pairs' rows exceed what the unsliced kernel takes)
-    const uint32_t prows = rows / 2u, pnb = 2u * nb;
+namespace {
+// An odd block count nb over an even row count: row pairs, K-sliced by the
+// rule of the even case (and always past 64 blocks, where the pairs' rows
+// exceed what the unsliced kernel takes), else unsliced.
+bool launch_pairs(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+                  bool may_slice, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  if ((nb & 1u) == 0u || rows < 2u || (rows & 1u) == 1u) return false;
+  const uint32_t prows = rows / 2u, pnb = 2u * nb;
+  if (may_slice) {
     const uint32_t S = q6_slices((prows + 15u) / 16u, pnb, ws.bytes);
     if (S >= 2u && (launch_sliced<12, 1, true>(w, x, y, prows, pnb, S, ws, s, err) ||
                     launch_sliced<8, 1, true>(w, x, y, prows, pnb, S, ws, s, err)))
       return true;
   }
-  if (paired_ok(rows, nb))
-    return launch_wd<12, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
-           launch_wd<10, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
-           launch_wd<8, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err) ||
-           launch_wd<4, 1, 1, false, false, true>(w, x, y, rows / 2u, 2u * nb, ws, s, err);
+  return paired_ok(rows, nb) &&
+         (launch_wd<12, 1, 1, false, false, true>(w, x, y, prows, pnb, ws, s, err) ||
+          launch_wd<10, 1, 1, false, false, true>(w, x, y, prows, pnb, ws, s, err) ||
+          launch_wd<8, 1, 1, false, false, true>(w, x, y, prows, pnb, ws, s, err) ||
+          launch_wd<4, 1, 1, false, false, true>(w, x, y, prows, pnb, ws, s, err));
+}
+}  // namespace
+
+bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
+                            uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  const uint32_t nb = cols / kBlockElems;
+  static const int cfg = env_int("SI_HIP_Q6K_MFMA_CFG", 0);
+  if ((nb & 1u) == 1u && (rows & 1u) == 0u)
+    return launch_pairs(w, x, y, rows, nb, cfg == 0, ws, s, err);
+  if ((nb & 1u) == 1u && rows >= 3u && (uint64_t)rows * nb >= 65536u) {
+    // an odd row count as well: the pairs of all rows but the last, then the
+    // last row alone (one workgroup).  The second launch costs 3-5 us, so
+    // below 64K blocks the generic kernel (one wave per row) is faster.
+    if (!launch_pairs(w, x, y, rows - 1u, nb, cfg == 0, ws, s, err)) return false;
+    if (*err == hipSuccess)
+      *err = launch_row_dot(kTypeQ6K, w + (size_t)(rows - 1u) * nb * kQ6Bytes, x, y + (rows - 1u),
+                            cols, s);
+    return true;
+  }
   if (cfg == 0 && nb > kMaxMetaBlocks) {  // (q6_shape_ok takes none of these)
     const uint32_t S = q6_slices((rows + 15u) / 16u, nb, ws.bytes);
     return S >= 2u && (launch_sliced<12, 1>(w, x, y, rows, nb, S, ws, s, err) ||

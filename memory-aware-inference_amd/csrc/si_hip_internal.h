@@ -111,6 +111,10 @@ hipError_t launch_matvec_generic(uint32_t type, const uint8_t* w, const float* x
                                  uint32_t rows, uint32_t cols, uint32_t batch, hipStream_t s);
 hipError_t launch_fused_gate_up_generic(const uint8_t* gate, const uint8_t* up, const float* x,
                                         float* h, uint32_t rows, uint32_t cols, hipStream_t s);
+// y[0] = the dot of one row (w: its nb = cols / 256 blocks) with x, by one
+// workgroup.
+hipError_t launch_row_dot(uint32_t type, const uint8_t* w, const float* x, float* y,
+                          uint32_t cols, hipStream_t s);
 // Dequantises out_rows rows; with row_index, output row r is table row
 // row_index[r], and an index of table_rows or more gives a row of NaNs and
 // reports kDevErrTokenId through the workspace `ws` (when not null).

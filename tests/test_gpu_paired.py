@@ -9,7 +9,9 @@ to its own row of the pair -- the stage holding blocks nb - 1 and nb hands
 one sum to each.  Long pair rows over few tiles, and every pair row past 128
 blocks (nb > 64), run K-sliced: a workgroup holds the images of its slice's
 stretch of the doubled x, and the slice hand-off carries both sums of each
-row.  Odd row counts keep the generic kernel.
+row.  An odd row count over 64K blocks or more runs its first rows - 1 rows
+as pairs and the last row alone (one workgroup); smaller odd row counts run
+the generic kernel.
 
 Bar: rows within 2e-5 * sum|w*x| of the f64 dot, +-inf / NaN rows where
 per-weight f32 products give them, the same bits on every call, and the
@@ -37,11 +39,14 @@ def log(msg):
 # (rows, cols): one block per row (the single stage straddles the pair);
 # 9 blocks over a partial tile of pairs (17 pairs); the Gemma-class head
 # width 5376 (21 blocks); the Llama-2-7B down projection (43 blocks, K-sliced
-# pairs); a head of 32000 rows (a split launch of 1000 pair tiles); an odd
-# row count (the generic kernel); pair rows past 128 blocks, which must slice
-# (67, 65 and 129 blocks; 135 blocks: eight slices)
+# pairs); a head of 32000 rows (a split launch of 1000 pair tiles); odd row
+# counts (generic below 64K blocks: 41 rows, three rows of one block, one row;
+# pairs, then the last row alone: 4097 rows of sliced pairs, a 32001-row
+# head); pair rows past 128 blocks, which must slice (67, 65 and 129 blocks;
+# 135 blocks: eight slices), and the same with an odd row count
 SHAPES = [(2, 256), (34, 2304), (1000, 5376), (4096, 11008), (32000, 5376), (41, 2304),
-          (100, 17152), (2560, 16640), (2, 33024), (40, 34560)]
+          (3, 256), (4097, 11008), (32001, 5376), (1, 2304),
+          (100, 17152), (2560, 16640), (2, 33024), (40, 34560), (1001, 17152), (501, 34560)]
 
 
 @pytest.mark.parametrize("rows,cols", SHAPES)
@@ -116,15 +121,43 @@ def test_sliced_pairs_special_activations(hip_ctx):
         W.free()
 
 
+def test_odd_rows_split_special_activations(hip_ctx):
+    """An odd row count split into sliced pairs and the last row alone: huge,
+    side and zero blocks within the bound, then one infinite or NaN
+    activation at a time, every row (the last one's own launch included) in
+    the category that per-weight f32 products give."""
+    rows, cols = 1001, 17152
+    w = si_hip.synth_matrix(Q6, seed=4650, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, Q6)
+    base = si_hip.synth_normal(4651, cols)
+    try:
+        x = base.copy()
+        x[100:140] = np.float32(3e30)
+        x[4096 + 7] = np.float32(1e-9)
+        x[cols - 256:] = 0.0
+        _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        assert_dot_close(y, y64, ab, what="special blocks")
+        for k, v in [(5, np.inf), (cols - 1, np.nan), (256 * 40 + 3, -np.inf)]:
+            x = base.copy()
+            x[k] = v
+            y32, _, _ = O.matvec(Q6, w, rows, cols, x, threads=8)
+            y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+            assert np.array_equal(_category(y), _category(y32)), f"x[{k}] = {v}"
+    finally:
+        W.free()
+
+
 def test_sliced_pairs_in_a_graph(hip_ctx):
-    """Sliced row pairs (32-float workspace entries) and a plain sliced Q6_K
-    launch (16-float entries) on one workspace, recorded in a HIP graph and
+    """Sliced row pairs (32-float workspace entries), a plain sliced Q6_K
+    launch (16-float entries) and an odd row count (sliced pairs, then the
+    last row's generic launch) on one workspace, recorded in a HIP graph and
     replayed three times with eager launches between: every replay equals
     the eager run bit for bit (both leave the entries empty)."""
     import ctypes as C
     lib = si_hip.lib()
     P = C.c_void_p
-    shapes = [(4096, 11008), (2560, 17408), (100, 17152)]
+    shapes = [(4096, 11008), (2560, 17408), (100, 17152), (1001, 17152)]
     mats, ins, outs = [], [], []
     for rows, cols in shapes:
         w = si_hip.synth_matrix(Q6, seed=rows + cols + 5, rows=rows, cols=cols, threads=8)
