@@ -1469,14 +1469,21 @@ int validate_head(const si_hip_quant_weight *w, size_t rows, size_t cols, size_t
 // The head's logits and greedy argmax on `stream`: the Q6_K matrix-core
 // kernel with the argmax fused into it (storing the logits only when
 // `logits_wanted`), else the matvec into d_logits, then the argmax kernel.
+// The fused launch stores the logits (when wanted) at fused_logits, which
+// may be pinned host staging (that kernel never reads them back), and sets
+// *fused; the matvec + argmax_kernel pair stores them at d_logits (device
+// memory, which argmax_kernel reads).
 int dispatch_head(si_hip_context *ctx, const si_hip_quant_weight *w, const float *d_in,
-                  float *d_logits, bool logits_wanted, uint32_t rows, uint32_t cols,
-                  uint32_t rule, uint64_t *d_result, hipStream_t stream) {
+                  float *d_logits, float *fused_logits, bool logits_wanted, uint32_t rows,
+                  uint32_t cols, uint32_t rule, uint64_t *d_result, hipStream_t stream,
+                  bool *fused) {
   hipError_t e = hipErrorInvalidValue;
+  *fused = false;
   if (ctx->policy == SI_HIP_KERNEL_AUTO && w->ggml_type == SI_HIP_GGML_TYPE_Q6_K &&
-      sihip::launch_q6k_matvec_argmax_mfma(w->data(), d_in, logits_wanted ? d_logits : nullptr,
+      sihip::launch_q6k_matvec_argmax_mfma(w->data(), d_in, logits_wanted ? fused_logits : nullptr,
                                            rows, cols, rule, d_result, ctx->ws, stream, &e)) {
     if (e != hipSuccess) return hip_fail(e, "output head launch");
+    *fused = true;
     return SI_HIP_OK;
   }
   int rc = dispatch_matvec(ctx, w->ggml_type, w->data(), d_in, d_logits, rows, cols, 1, stream);
@@ -1504,15 +1511,28 @@ int si_hip_gguf_quant_matvec_argmax_weight(si_hip_context *ctx, const si_hip_qua
   SIHIP_CHECK(copy_in(ctx, ctx->stage_in, in, cols * sizeof(float)),
               "input copy");
   float *d_logits = static_cast<float *>(ctx->stage_out);
-  uint64_t *aux = static_cast<uint64_t *>(ctx->stage_aux);
-  rc = dispatch_head(ctx, w, static_cast<const float *>(ctx->stage_in), d_logits, logits != nullptr,
-                     (uint32_t)rows, (uint32_t)cols, rule, aux, ctx->stream);
+  // the packed token (a plain store of the reducing wave) and a fused
+  // launch's logits go straight into pinned staging when they fit there
+  const OutStage lo = logits ? out_stage(ctx, rows * sizeof(float)) : OutStage{d_logits, false};
+  uint8_t *pinned_token = pin_take(ctx, ctx->pin_out, sizeof(uint64_t));
+  uint64_t *aux = pinned_token ? reinterpret_cast<uint64_t *>(pinned_token)
+                               : static_cast<uint64_t *>(ctx->stage_aux);
+  bool fused = false;
+  rc = dispatch_head(ctx, w, static_cast<const float *>(ctx->stage_in), d_logits, lo.ptr,
+                     logits != nullptr, (uint32_t)rows, (uint32_t)cols, rule, aux, ctx->stream,
+                     &fused);
   if (rc) return rc;
   uint64_t packed = 0;
-  SIHIP_CHECK(copy_out(ctx, &packed, aux, sizeof packed), "argmax copy");
-  if (logits)
-    SIHIP_CHECK(copy_out(ctx, logits, d_logits, rows * sizeof(float)),
-                "logits copy");
+  if (pinned_token)
+    ctx->pending.push_back({&packed, pinned_token, sizeof packed});
+  else
+    SIHIP_CHECK(copy_out(ctx, &packed, aux, sizeof packed), "argmax copy");
+  if (logits) {
+    if (fused)
+      SIHIP_CHECK(deliver(ctx, logits, lo, 0, rows), "logits copy");
+    else
+      SIHIP_CHECK(copy_out(ctx, logits, d_logits, rows * sizeof(float)), "logits copy");
+  }
   rc = wait_stream(ctx, "output head argmax command");
   if (rc) return rc;
   if (packed == 0) {
@@ -1970,8 +1990,9 @@ int si_hip_matvec_argmax_device(si_hip_context *ctx, const si_hip_quant_weight *
   if (rc) return rc;
   if (!ctx || !d_in || !d_logits || !d_result) return fail(SI_HIP_ERR_NULL, "device head argument is null");
   CallScope scope(ctx);
-  rc = dispatch_head(ctx, w, d_in, d_logits, true, (uint32_t)rows, (uint32_t)cols, rule, d_result,
-                     device_stream(ctx));
+  bool fused = false;
+  rc = dispatch_head(ctx, w, d_in, d_logits, d_logits, true, (uint32_t)rows, (uint32_t)cols, rule,
+                     d_result, device_stream(ctx), &fused);
   if (rc) return rc;
   ctx->async_submitted.fetch_add(1);
   return ok();
