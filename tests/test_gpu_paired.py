@@ -272,3 +272,27 @@ def test_odd_block_count_matmul_many(hip_ctx):
             assert_dot_close(outs[b], y64, ab, what=f"vector {b}")
     finally:
         W.free()
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_odd_block_counts(hip_ctx, seed):
+    """Seeded random Q6_K shapes with odd block counts and row counts of either
+    parity up to 300K blocks: unsliced and sliced row pairs, the odd row
+    count's pairs plus one-workgroup last row, and the generic kernel below
+    64K blocks; every row within the oracle's bound and repeating its bits."""
+    rng = np.random.default_rng(9800 + seed)
+    nb = int(rng.choice([1, 9, 21, 43, 67, 135]))
+    rows = int(rng.integers(1, min(8000, 300000 // nb) + 1))
+    rows = rows | 1 if seed % 2 == 0 else max(2, rows & ~1)  # odd, then even row counts
+    cols = 256 * nb
+    log(f"random odd-nb q6_k seed={seed}: {rows}x{cols}")
+    w = si_hip.synth_matrix(Q6, seed=9850 + seed, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(9870 + seed, cols)
+    W = hip_ctx.upload_quant_weight_private(w, Q6)
+    try:
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        _, y64, ab = O.matvec(Q6, w, rows, cols, x, threads=8)
+        assert_dot_close(y, y64, ab, what=f"{rows}x{cols}")
+        assert same_bits(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x), y)
+    finally:
+        W.free()
