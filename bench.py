@@ -222,11 +222,18 @@ def call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, samples: int,
                               f"averaged over {n_wall} calls"}
 
 
-def _timed(ctx, fn, steps: int, warmup: int) -> float:
-    """Average ms per call of fn(i) enqueued back to back on the compute stream."""
-    for i in range(warmup):
-        fn(i)
-    ctx.synchronize()
+def _timed(ctx, fn, steps: int, warmup: int, warm_ms: float = 20.0) -> float:
+    """Average ms per call of fn(i) enqueued back to back on the compute stream,
+    after at least `warmup` untimed calls and warm_ms of them (a GPU left idle
+    by host work, e.g. weight uploads, clocks down and needs some 10 ms of
+    calls to come back)."""
+    t0 = time.perf_counter()
+    i = 0
+    while i < warmup or (time.perf_counter() - t0) * 1e3 < warm_ms:
+        for _ in range(25):
+            fn(i)
+            i += 1
+        ctx.synchronize()
     ctx.event_record(0)
     for i in range(steps):
         fn(i)
