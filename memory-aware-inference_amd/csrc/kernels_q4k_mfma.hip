@@ -447,8 +447,9 @@ __device__ __forceinline__ float k4_bound(const BlockQ4& w) {
 
 // One vector's partial dot of the lane's row over stage s (blocks SB s ..
 // SB s + nlive - 1), whose images and metadata sit at LDS stage ls: the MFMA
-// digit sums, the side elements' exact products, the rounded blocks' check,
-// and the exact path for blocks that need it, summed over the lane groups
+// digit sums, the rounded blocks' check (an exact recompute of them for a row
+// that fails it), and the exact path for blocks that need it, summed over the
+// lane groups
 // (every lane of a row gets the row's sum).
 template <int QB, int SB>
 __device__ __forceinline__ float stage_rowsum(const StageRegs<QB, SB>& v, uint32_t sbase,

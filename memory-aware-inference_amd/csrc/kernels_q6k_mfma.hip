@@ -15,15 +15,16 @@
 //
 // Per block and lane: T_d = sum_t sc_t * C_t[d] in integers, y += d * (sum_d
 // T_d * 256^d) * 2^(e_b - 30) (the digit images of the activations are built
-// as for Q4_K, mfma_common.h), plus w_i x_i for the block's side elements.
-// Blocks whose activations are not finite or reach 2^100, or that have more
-// side elements than the list holds, take an exact per-weight f32 path
+// as for Q4_K, mfma_common.h).  A block with side elements is a rounded
+// block, whose rows recompute it exactly when its error bound fails the
+// rounded-block check (mfma_common.h); blocks whose activations are not
+// finite or reach 2^100 take the exact per-weight f32 path whole
 // (w = (d * sc) * (q - 32), quant.rs rounding).
 //
 // Data path.  Blocks are 210 bytes, so they are not 16-byte aligned; with an
 // even block count nb every row and every stage of two blocks (420 bytes)
 // starts on a 4-byte boundary, which the 16-byte buffer->LDS copies need (odd
-// nb is left to the generic kernel).  Each row's 420 bytes of a stage arrive
+// nb runs as row pairs, PAIRED below).  Each row's 420 bytes of a stage arrive
 // with 27 copies in piece-major order, piece q of row r at LDS byte
 // 16 (16 q + r), so every read is a conflict-free 16-lane sweep.  Pieces 0..25
 // are bytes 16 q .. 16 q + 15; piece 26 is bytes 404..419, so no copy runs
