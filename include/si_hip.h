@@ -267,7 +267,13 @@ int si_hip_matmul_many_device(si_hip_context *ctx, const si_hip_quant_weight *we
                               size_t rows, size_t columns, size_t batch, const float *d_inputs,
                               float *d_outputs);
 /* d_logits: rows floats; d_result: one uint64 packed (key<<32 | index),
- * decoded by si_hip_argmax_result_index. */
+ * decoded by si_hip_argmax_result_index.  packed == 0 means no logit
+ * qualified: under SI_HIP_ARGMAX_FIRST_GREATER (no logit beat -inf: all NaN
+ * or -inf) the index is 0, the id the reference's scan keeps
+ * (qwen35_runtime.rs:2237-2244); under SI_HIP_ARGMAX_LAST_FINITE (no finite
+ * logit, runtime.rs:4301-4309 returns an error) it is SI_HIP_ARGMAX_NONE,
+ * which no vocabulary row has. */
+#define SI_HIP_ARGMAX_NONE 0xffffffffu
 int si_hip_matvec_argmax_device(si_hip_context *ctx, const si_hip_quant_weight *head,
                                 size_t rows, size_t columns, const float *d_input,
                                 uint32_t rule, float *d_logits, uint64_t *d_result);

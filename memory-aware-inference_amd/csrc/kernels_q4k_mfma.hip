@@ -20,13 +20,18 @@
 //    lanes that hold that unit's scale and min.
 //
 // Per block and lane: C_e, C_o (4 digits each) from four MFMAs; T_d = sc_e *
-// C_e[d] + sc_o * C_o[d] in integers (|T_d| < 2^23, exact in f32); y += d *
-// (sum_d T_d * 256^d) * 2^(e_b-30) - dmin * (m_e * X_e + m_o * X_o), X_u the
-// f32 sum of unit u's activations.  The factored form rounds differently
-// from the per-weight w * x of quant.rs; the result stays within the 2e-5 *
-// sum|w*x| bar.  Blocks whose activations are not finite or reach 2^100 take
-// an exact per-weight f32 path instead, so NaN/Inf propagate as in the
-// reference.
+// C_e[d] + sc_o * C_o[d] in integers (|T_d| < 2^23, exact in f32); y +=
+// (d * (sum_d T_d * 256^d) - dmin * (m_e * X_e + m_o * X_o)) * 2^(e_b-30),
+// X_u the sum of unit u's fixed-point activations (exact, rounded once), so
+// both terms see the same rounded activations and, in exact arithmetic, the
+// pair is sum_i w_i X_i 2^(e_b-30) with w_i the weight of quant.rs.  Their
+// f32 rounding is bounded by 2^-21 (|d T| + |dmin| (m_e |X_e| + m_o |X_o|))
+// per block, which can exceed the bar where w_i cancels inside its own decode
+// (d sc q close to dmin m); every stage of a row checks that bound (stage_ok)
+// and a row that fails recomputes the stage on the exact per-weight path, so
+// the dot stays within 2e-5 * sum|w*x| on every input.  Blocks whose
+// activations are not finite or reach 2^100 take the exact per-weight f32
+// path instead, so NaN/Inf propagate as in the reference.
 //
 // Data path.  One persistent workgroup of WAVES waves per CU.  At start it
 // turns all of x into digit images in LDS (1 KB per block, plus unit sums and
@@ -240,9 +245,16 @@ __device__ __forceinline__ BlockQ4 decode_q4(const u32x4& h, const u32x4& qa, co
   return w;
 }
 
-// Fast-path dot of one decoded block with one activation vector's images.
+// Fast-path dot of one decoded block with one activation vector's images
+// (xs: the fixed-point sums of the lane's two units); `err` gets the bound on
+// its f32 rounding.  tc below is the exact integer sum_d T_d 256^d to within
+// 5 * 2^-24 |tc| (a step of the fma chain rounds only when what is left of tc
+// is far larger than the terms still to come), um = m_e X_e + m_o X_o to
+// within 3 * 2^-24 (m_e |X_e| + m_o |X_o|), and the last fma rounds once:
+// 2^-21 of the two terms' magnitudes covers all of it.
 __device__ __forceinline__ float block_dot(const BlockQ4& w, const i32x4& a0, const i32x4& a1,
-                                           const i32x4& a2, const i32x4& a3, u32x2 xs, int eb) {
+                                           const i32x4& a2, const i32x4& a3, u32x2 xs, int eb,
+                                           float& err) {
   const i32x4 zero = {0, 0, 0, 0};
   i32x4 ce = __builtin_amdgcn_mfma_i32_16x16x64_i8(a0, w.la, zero, 0, 0, 0);
   i32x4 co = __builtin_amdgcn_mfma_i32_16x16x64_i8(a2, w.ha, zero, 0, 0, 0);
@@ -254,8 +266,12 @@ __device__ __forceinline__ float block_dot(const BlockQ4& w, const i32x4& a0, co
   const int t3 = __mul24(w.sce, ce[3]) + __mul24(w.sco, co[3]);
   const float tc =
       fmaf(fmaf(fmaf((float)t3, 256.0f, (float)t2), 256.0f, (float)t1), 256.0f, (float)t0);
-  const float um = fmaf(w.mne, __uint_as_float(xs[0]), w.mno * __uint_as_float(xs[1]));
-  return __builtin_amdgcn_ldexpf(w.d * tc, eb) - w.dmin * um;
+  const float sxe = __uint_as_float(xs[0]), sxo = __uint_as_float(xs[1]);
+  const float dt = w.d * tc;
+  const float um = fmaf(w.mne, sxe, w.mno * sxo);
+  const float ua = fmaf(w.mne, fabsf(sxe), w.mno * fabsf(sxo));
+  err = __builtin_amdgcn_ldexpf(fmaf(fabsf(w.dmin), ua, fabsf(dt)), eb - 21);
+  return __builtin_amdgcn_ldexpf(fmaf(-w.dmin, um, dt), eb);
 }
 
 // Exact per-weight path of one block (activations not finite or >= 2^100).
@@ -467,6 +483,7 @@ __device__ __forceinline__ float stage_rowsum(const StageRegs<QB, SB>& v, uint32
   else
     lds_read_sums2(sbase + L.xsum + 64u * ls + 8u * grp, sbase + L.expo + 8u * ls, xs, ex, cnt);
   float part[SB];
+  float err = 0.0f;  // bound on the error of the fast-path partials
   bool bad_any = false;
 #pragma unroll
   for (int h = 0; h < SB / 2; ++h) {
@@ -477,22 +494,30 @@ __device__ __forceinline__ float stage_rowsum(const StageRegs<QB, SB>& v, uint32
       const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
       const bool use = (uint32_t)b < nlive;
       bad_any |= use && eb == kBadBlock;
+      float e;
       const float c = block_dot(v.decode(b, hi_units, bsh, rot_lo, rot_hi), A[4 * b2],
-                                A[4 * b2 + 1], A[4 * b2 + 2], A[4 * b2 + 3], xs[b], eb);
-      part[b] = (use && eb != kBadBlock) ? c : 0.0f;
+                                A[4 * b2 + 1], A[4 * b2 + 2], A[4 * b2 + 3], xs[b], eb, e);
+      const bool fast = use && eb != kBadBlock;
+      part[b] = fast ? c : 0.0f;
+      err += fast ? e : 0.0f;
     }
   }
-  // the rounded blocks' check; blocks on the exact path, and rounded blocks
-  // of rows that fail the check, take the per-weight path
+  // the stage check (the factored form's rounding plus the rounded blocks'
+  // bound); blocks on the exact path, and every live block of a row that
+  // fails the check, take the per-weight path
   const uint32_t counts = live_counts(__builtin_amdgcn_readfirstlane(cnt), nlive);
-  uint32_t redo = 0u;
-  if (counts != 0u) {
+  const uint32_t rmask = rounded_mask(counts);
+  if (rmask != 0u) {
     const uint32_t list = sbase + L.expo + L.side_off + (uint32_t)SB * kSideBytes * ls;
-    redo = rounded_redo<SB>(list, counts, grp, part, [&](auto b) {
+    err += rounded_bound<SB>(list, rmask, grp, [&](auto b) {
       return k4_bound<QB == 5 ? 31 : 15>(
           v.decode(decltype(b)::value, hi_units, bsh, rot_lo, rot_hi));
     });
   }
+  float apart = 0.0f;
+#pragma unroll
+  for (int b = 0; b < SB; ++b) apart += fabsf(part[b]);
+  const uint32_t redo = stage_ok(err, apart) ? 0u : (1u << nlive) - 1u;
   if (bad_any || redo != 0u) {
 #pragma unroll
     for (int b = 0; b < SB; ++b)
@@ -688,6 +713,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
         lds_read_sums(sbase + L.xsum + t * L.xsum_stride + 128u * s + 8u * grp,
                       sbase + L.expo + t * L.expo_stride + 16u * s, xs, ex, cnt);
         float part[4];
+        float err = 0.0f;
         bool bad_any = false;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
@@ -699,20 +725,25 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
             const int eb = __builtin_amdgcn_readfirstlane(ex[b]);
             const bool use = (uint32_t)b < nlive;
             bad_any |= use && eb == kBadBlock;
+            float e;
             const float c = block_dot(bw[b], A[4 * b2], A[4 * b2 + 1], A[4 * b2 + 2],
-                                      A[4 * b2 + 3], xs[b], eb);
-            part[b] = (use && eb != kBadBlock) ? c : 0.0f;
+                                      A[4 * b2 + 3], xs[b], eb, e);
+            const bool fast = use && eb != kBadBlock;
+            part[b] = fast ? c : 0.0f;
+            err += fast ? e : 0.0f;
           }
         }
         const uint32_t counts = live_counts(__builtin_amdgcn_readfirstlane(cnt), nlive);
-        uint32_t redo = 0u;
-        if (counts != 0u) {
+        const uint32_t rmask = rounded_mask(counts);
+        if (rmask != 0u) {
           const uint32_t list =
               sbase + L.expo + t * L.expo_stride + L.side_off + 4u * kSideBytes * s;
-          redo = rounded_redo<4>(list, counts, grp, part, [&](auto b) {
+          err += rounded_bound<4>(list, rmask, grp, [&](auto b) {
             return k4_bound<QB == 5 ? 31 : 15>(bw[decltype(b)::value]);
           });
         }
+        const float apart = (fabsf(part[0]) + fabsf(part[1])) + (fabsf(part[2]) + fabsf(part[3]));
+        const uint32_t redo = stage_ok(err, apart) ? 0u : (1u << nlive) - 1u;
         if (bad_any || redo != 0u) {
 #pragma unroll
           for (int b = 0; b < 4; ++b)
@@ -859,8 +890,7 @@ __device__ __forceinline__ void build_group_images(uint32_t sbase, const Layout&
     }
     if (rounded)  // chunk c's error sum at position c (read whole by tok_side)
       lds_write_b32(list + 4u * c, __float_as_uint(cs.err_side));
-    float xsum = rounded ? cs.xsum : cs.xsum - cs.xsum_side;
-    xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit c / 2
+    const float xsum = unit_fixed_sum(uq);  // odd lanes: unit c / 2 (listed elements as 0)
     if (c & 1u)
       lds_write_b32(sbase + L.xsum + v * L.xsum_stride + 32u * b + 4u * u, __float_as_uint(xsum));
     if (c == 0u) {
@@ -926,9 +956,13 @@ __device__ __forceinline__ int64_t as_i64(uint32_t lo, uint32_t hi) {
 }
 
 // One block of row n against vector g (the lane's), fast path: eight MFMAs,
-// the integer scale combine and the f32 digit and min terms.
+// the integer scale combine and the f32 digit and min terms over the
+// fixed-point unit sums xs; `err` gets the bound on its f32 rounding (the
+// eight-term um adds up to 9 * 2^-24 sum_u m_u |X_u|, so 2^-20 of the two
+// terms' magnitudes, as block_dot's 2^-21 for two units).
 __device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[16], int b,
-                                               const u32x4 (&a)[4], const u32x4 (&xs)[2], int eb) {
+                                               const u32x4 (&a)[4], const u32x4 (&xs)[2], int eb,
+                                               float& err) {
   const i32x4 zero = {0, 0, 0, 0};
   const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
   const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
@@ -953,24 +987,37 @@ __device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[
   }
   const float tc =
       fmaf(fmaf(fmaf((float)t[3], 256.0f, (float)t[2]), 256.0f, (float)t[1]), 256.0f, (float)t[0]);
-  float um = 0.0f;
+  float um = 0.0f, ua = 0.0f;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
     const float m = (float)(((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu);
-    um = fmaf(m, __uint_as_float(xs[u >> 2][u & 3]), um);
+    const float sx = __uint_as_float(xs[u >> 2][u & 3]);
+    um = fmaf(m, sx, um);
+    ua = fmaf(m, fabsf(sx), ua);
   }
   const float d = half_bits_to_float(h[0] & 0xffffu);
   const float dmin = half_bits_to_float(h[0] >> 16);
-  return __builtin_amdgcn_ldexpf(d * tc, eb) - dmin * um;
+  const float dt = d * tc;
+  err = __builtin_amdgcn_ldexpf(fmaf(fabsf(dmin), ua, fabsf(dt)), eb - 20);
+  return __builtin_amdgcn_ldexpf(fmaf(-dmin, um, dt), eb);
 }
 
 // Exact per-weight path of one block of row n against 256 activations: the
-// header and qs pieces 1..8 at hp + 256 k, k = 0..8, of the stage buffer.
-__device__ __forceinline__ float block_exact_row(uint32_t hp, const float* __restrict__ xs) {
-  u32x4 h, qa[4], qb[4];
-  asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(h) : "v"(hp) : "memory");
-  lds_read4<256>(hp + 256u, qa);
-  lds_read4<256>(hp + 1280u, qb);
+// block's 144 bytes at byte `off` of the buffer `wr` (read from memory: by
+// then the stage buffer may hold the next stage; bytes past the buffer's end,
+// those of rows past the matrix, read as zero).
+__device__ __forceinline__ float block_exact_row(__amdgpu_buffer_rsrc_t wr, uint32_t off,
+                                                 const float* __restrict__ xs) {
+  auto ld = [&](uint32_t o) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off + o, 0, 0));
+  };
+  const u32x4 h = ld(0u);
+  u32x4 qa[4], qb[4];
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    qa[k] = ld(16u + 16u * k);
+    qb[k] = ld(80u + 16u * k);
+  }
   const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
   const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
   const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
@@ -1012,24 +1059,29 @@ __host__ __device__ constexpr Layout tok_layout(uint32_t waves, uint32_t nbl, ui
 // One vector group's sum over the live blocks of a stage (the weights in h,
 // q) on the fast path; blocks of the lane's vector that must take the exact
 // path count zero here.  iabase/xabase/eabase: the group's images, the
-// vector's unit sums and exponents at the stage's first block.
+// vector's unit sums and exponents at the stage's first block.  abs_part and
+// err get the lane's sum of |block dot| and the bound on their rounding.
 __device__ __forceinline__ float tok_group_stage(const u32x4 (&h)[4], const u32x2 (&q)[16],
                                                  uint32_t nlive, uint32_t iabase,
                                                  uint32_t xabase, uint32_t eabase,
-                                                 float& abs_part) {
+                                                 float& abs_part, float& err) {
   i32x4 ex;
   asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(ex) : "v"(eabase) : "memory");
   float part = 0.0f;
   abs_part = 0.0f;
+  err = 0.0f;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
     if ((uint32_t)b < nlive) {
       u32x4 a[4], xs[2];
       lds_read_group_block(iabase + 4096u * b, xabase + 32u * b, a, xs);
-      const float v = block_dot_tok(h[b], q, b, a, xs, ex[b]);
-      const float c = ex[b] == kBadBlock ? 0.0f : v;
+      float e;
+      const float v = block_dot_tok(h[b], q, b, a, xs, ex[b], e);
+      const bool fast = ex[b] != kBadBlock;
+      const float c = fast ? v : 0.0f;
       part += c;
       abs_part += fabsf(c);
+      err += fast ? e : 0.0f;
     }
   }
   return part;
@@ -1112,26 +1164,19 @@ __device__ __forceinline__ float tok_listed(const u32x4 (&h)[4], const u32x2 (&q
   return part;
 }
 
-// Whether the lane (vector r of the group, row n) must recompute its stage
-// exactly: its vector has rounded blocks whose error bound (largest |w| of the
-// block x its error sum) exceeds kRoundedTol of abs_part, the sum of the
-// stage's per-block |dot|.  The headers come from the stage buffer (hb: the
-// row's header at the stage's first block), which is still intact whenever a
-// rounded block is present.
-__device__ __forceinline__ bool tok_rounded_redo(uint32_t mine, uint32_t mylist, uint32_t hb,
-                                                 float abs_part) {
+// The lane's (vector r of the group, row n) error bound from its vector's
+// rounded blocks of the stage: the largest |w| of each such block (from its
+// header in h) times the block's error sum.
+__device__ __forceinline__ float tok_rounded_bound(uint32_t mine, uint32_t mylist,
+                                                   const u32x4 (&h)[4]) {
   const uint32_t rmask = rounded_mask(mine);
-  if (__builtin_amdgcn_ballot_w64(rmask != 0u) == 0u) return false;
   float err = 0.0f;
-#pragma unroll 1
-  for (uint32_t b = 0; b < 4u; ++b) {
-    if ((rmask >> b) & 1u) {
-      u32x4 h;
-      asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(h) : "v"(hb + 2304u * b) : "memory");
-      err = fmaf(k4_block_bound(h), rounded_err_all(mylist + kSideBytes * b), err);
-    }
-  }
-  return !(err * 1.01f <= kRoundedTol * (abs_part - err));
+  if (__builtin_amdgcn_ballot_w64(rmask != 0u) == 0u) return err;
+#pragma unroll
+  for (int b = 0; b < 4; ++b)
+    if ((rmask >> b) & 1u)
+      err = fmaf(k4_block_bound(h[b]), rounded_err_all(mylist + kSideBytes * b), err);
+  return err;
 }
 
 template <int WAVES, int NG>
@@ -1222,11 +1267,16 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
     u32x4 h[4];
     u32x2 q[16];
     lds_read_weights_tok(hb0, qb0, h, q);
+    // the stage is in registers: the buffer takes the next stage's copy (the
+    // exact path reads its blocks from memory)
+    if (j + 1u < my_pairs) {
+      pr_next = pair_of(wave + (j + 1u) * WAVES);
+      issue(pr_next);
+    }
     const uint32_t nlive = min(4u, nb - 4u * s);
-    // a block that takes the exact path reads the stage buffer afterwards
-    bool any_bad = false;
-    // (so does a rounded block, should a row need it exactly); the lane's
-    // vector's side counts of each group are kept for the groups' passes
+    bool any_bad = false;  // a block on the exact path
+    // the lane's vector's side counts of each group, kept for the groups'
+    // passes
     uint32_t counts[NG];
 #pragma unroll
     for (int g = 0; g < NG; ++g) counts[g] = 0u;
@@ -1246,14 +1296,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
         if ((uint32_t)gg == g) counts[gg] = cw;
       bool bad = false;
 #pragma unroll
-      for (int b = 0; b < 4; ++b)
-        bad |= (uint32_t)b < nlive &&
-               (ex[b] == kBadBlock || ((cw >> (8 * b)) & 0xffu) == kSideRounded);
+      for (int b = 0; b < 4; ++b) bad |= (uint32_t)b < nlive && ex[b] == kBadBlock;
       any_bad |= __builtin_amdgcn_ballot_w64(bad) != 0u;
-    }
-    if (!any_bad && j + 1u < my_pairs) {
-      pr_next = pair_of(wave + (j + 1u) * WAVES);
-      issue(pr_next);
     }
     float part[NG];
 #pragma unroll
@@ -1271,20 +1315,29 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       const uint32_t list0 =
           sbase + L.expo + 4u * g * L.expo_stride + L.side_off + 4u * kSideBytes * sl;
       const float side = any ? tok_listed(h, q, list0, mine, L.expo_stride, lane) : 0.0f;
-      float abs_pg;
+      float abs_pg, err;
       const float pg = side + tok_group_stage(h, q, nlive,
                                               sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane,
                                               sbase + L.xsum + v * L.xsum_stride + 128u * sl,
-                                              sbase + L.expo + v * L.expo_stride + 16u * sl, abs_pg);
-      if (any && tok_rounded_redo(mine, list0 + grp * L.expo_stride, hb0, abs_pg + fabsf(side)))
-        redo |= 1u << g;
+                                              sbase + L.expo + v * L.expo_stride + 16u * sl,
+                                              abs_pg, err);
+      // the stage check of the lane's (vector, row): the fast path's rounding
+      // plus its rounded blocks against kStageTol of sum |partial|
+      if (any) err += tok_rounded_bound(mine, list0 + grp * L.expo_stride, h);
+      const float ap = abs_pg + fabsf(side);
+      if (!(err * 1.01f <= kStageTol * (ap - err))) redo |= 1u << g;
 #pragma unroll
       for (int gg = 0; gg < NG; ++gg)
         if ((uint32_t)gg == g) part[gg] = pg;
     }
-    if (any_bad) {
-      // the rare exact path: one loop over (group, block), everything
-      // addressed in LDS (no register array indexed at run time)
+    if (any_bad || __builtin_amdgcn_ballot_w64(redo != 0u) != 0u) {
+      // the rare exact path: one loop over (group, block), weights read from
+      // memory, the rest addressed in LDS (no register array indexed at run
+      // time)
+      const uint32_t row0 = pr.tile * 16u;
+      const __amdgpu_buffer_rsrc_t wr = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(w + (size_t)row0 * row_bytes), 0,
+          (int)(min(16u, rows - row0) * row_bytes), kBufferWord3);
 #pragma unroll 1
       for (uint32_t g = 0; g < ng; ++g) {
         const uint32_t v = 4u * g + grp;
@@ -1295,16 +1348,13 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
         for (uint32_t b = 0; b < nlive; ++b) {
           const uint32_t eb = lds_read_b32(sbase + L.expo + v * L.expo_stride + 4u * (4u * sl + b));
           if ((int)eb == kBadBlock || whole)
-            e += block_exact_row(hb0 + 2304u * b, xv + kBlockElems * (4u * s + b));
+            e += block_exact_row(wr, n * row_bytes + kQ4Bytes * (4u * s + b),
+                                 xv + kBlockElems * (4u * s + b));
         }
 #pragma unroll
         for (int gg = 0; gg < NG; ++gg)
           if ((uint32_t)gg == g) part[gg] = (whole ? 0.0f : part[gg]) + e;
       }
-    }
-    if (any_bad && j + 1u < my_pairs) {
-      pr_next = pair_of(wave + (j + 1u) * WAVES);
-      issue(pr_next);
     }
     if (!sliced) {
       hand_off_lane_tokens(sbase, L, FastDiv{ta.slots, ta.m_slots}, pr, nstages, part[0], lane,

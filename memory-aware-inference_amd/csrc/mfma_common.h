@@ -71,6 +71,12 @@ constexpr uint32_t kSideRounded = 0xffu;  // side count of a rounded block
 // A row's stage passes when (error bound) * 1.01 <= kRoundedTol *
 // (sum |partial| - error bound); 1.01 covers the f32 rounding of both sums.
 constexpr float kRoundedTol = 4e-6f;
+// The Q4_K / Q5_K kernels check every stage (stage_ok): the bound of the f32
+// rounding of their factored dots plus that of their rounded blocks against
+// kStageTol of the row's sum |partial|.  With the fixed point's 2^-17 on kept
+// elements and the f32 accumulation of the partials (under 3e-6) the dot stays
+// within 2e-5 * sum|w x|.
+constexpr float kStageTol = 8e-6f;
 
 constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
 
@@ -357,10 +363,30 @@ __device__ __forceinline__ void biased_values(const ChunkSplit& cs, bool listed,
     u[k] = ((listed && ((cs.smask >> k) & 1u)) ? 0u : cs.fx[k]) + 0x80808080u;
 }
 
+// Sum of the fixed-point values X of a 32-element unit whose two 16-element
+// halves are held by this lane (biased digit words u = X + 0x80808080) and the
+// lane before it in its DPP row; the result is valid in the odd lanes.  The
+// sum is exact (X = hi 2^15 + lo with both parts summed as integers below
+// 2^20) and rounded to f32 once, so the min term d_min * m * sum X of a unit
+// sees the activations rounded exactly as the MFMA digit sums do.
+__device__ __forceinline__ float unit_fixed_sum(const uint32_t (&u)[16]) {
+  uint32_t hi = 0u, lo = 0u;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int32_t X = (int32_t)(u[k] - 0x80808080u);
+    hi += (uint32_t)(X >> 15);
+    lo += (uint32_t)X & 0x7fffu;
+  }
+  hi += dpp_u<kRowShr1>(hi);
+  lo += dpp_u<kRowShr1>(lo);
+  return fmaf((float)(int32_t)hi, 32768.0f, (float)lo);
+}
+
 // Turns the copied blocks of activation vector `tok` into digit images in
 // place, plus exponents, the error sums of rounded blocks, side counts
-// (kSideRounded or 0) and, when the layout keeps them, the f32 sums of each
-// 32-element unit.  The caller has waited for the copies.  CHUNK_SLOT(c)
+// (kSideRounded or 0) and, when the layout keeps them, the sums of each
+// 32-element unit's fixed-point values (unit_fixed_sum, in units of
+// 2^(e_b - 30)).  The caller has waited for the copies.  CHUNK_SLOT(c)
 // gives the byte offset, inside the block's 1 KB, of the A row 4 p (digit 0)
 // of MFMA t that holds chunk c (elements 16 c .. 16 c + 15): 256 t + 64 p.  A
 // block with an activation that is not finite or reaches 2^100 gets exponent
@@ -410,8 +436,7 @@ __device__ __forceinline__ void build_images(uint32_t sbase, const Layout& L, ui
                       __float_as_uint(cs.err_side));
     }
     if (want_sums) {
-      float xsum = cs.xsum;
-      xsum += dpp<kRowShr1>(xsum);  // odd lanes: sum of unit n / 2
+      const float xsum = unit_fixed_sum(u);  // odd lanes: unit n / 2
       if (store && (n & 1u))
         lds_write_b32(sbase + xsb + 32u * pb + 4u * (n >> 1), __float_as_uint(xsum));
     }
@@ -476,6 +501,30 @@ __device__ __forceinline__ uint32_t rounded_redo(uint32_t list, uint32_t counts,
     a += fabsf(part[b]);
   });
   return rounded_ok(err, a) ? 0u : rmask;
+}
+
+// The lane's error bound from the rounded blocks of a stage (rmask: bit b
+// for a rounded block b): the largest |w| of its share of the block times
+// that share's rounding-error sum.
+template <int NB, typename Bound>
+__device__ __forceinline__ float rounded_bound(uint32_t list, uint32_t rmask, uint32_t grp,
+                                               Bound bound) {
+  float err = 0.0f;
+  static_for<NB>([&](auto bc) {
+    constexpr int b = decltype(bc)::value;
+    if ((rmask >> b) & 1u) err = fmaf(bound(bc), rounded_err(list + kSideBytes * b, grp), err);
+  });
+  return err;
+}
+
+// The stage check of the Q4_K / Q5_K kernels: whether the row of this lane
+// passes with `err`, the lane's bound on the error of its fast-path partials
+// (their f32 rounding plus its rounded blocks), and `abs_part`, its sum of
+// |partial| (both summed over the row's four lane groups here).  A row that
+// fails recomputes the stage on the exact per-weight path.
+__device__ __forceinline__ bool stage_ok(float err, float abs_part) {
+  const float e = sum_lane_groups(err), a = sum_lane_groups(abs_part);
+  return e * 1.01f <= kStageTol * (a - e);
 }
 
 // Slot ring set-up: every slot empty and owned by local tile == its index.

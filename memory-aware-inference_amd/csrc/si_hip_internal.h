@@ -97,7 +97,14 @@ __host__ __device__ __forceinline__ uint64_t argmax_candidate(float v, uint32_t 
   return ((uint64_t)ukey << 32) | tie;
 }
 
+// The index a packed best candidate names.  With no candidate (c == 0, no
+// logit beat -inf or none was finite): 0 under kArgmaxFirstGreater, the id
+// the reference's strict '>' scan keeps when nothing beats its starting -inf
+// (qwen35_runtime.rs:2237-2244); kArgmaxNone under kArgmaxLastFinite, where
+// the reference returns "logits contain no finite values" (runtime.rs:4301-4309).
+constexpr uint32_t kArgmaxNone = 0xffffffffu;
 __host__ __device__ __forceinline__ uint32_t argmax_candidate_index(uint64_t c, uint32_t rule) {
+  if (c == 0u) return rule == kArgmaxFirstGreater ? 0u : kArgmaxNone;
   const uint32_t lo = (uint32_t)c;
   return rule == kArgmaxFirstGreater ? 0xffffffffu - lo : lo;
 }
