@@ -76,11 +76,57 @@ __host__ __device__ constexpr uint32_t stage_bytes(int qb, int sb = 4) {
 static_assert(stage_bytes(4) == 64u * kQ4Bytes && stage_bytes(5) == 64u * kQ5Bytes,
               "four-block stages fill their copies exactly");
 
+// Full-line copies (LINES: Q4_K in four-block stages, nb = 4 mod 8 blocks per
+// row, the matrix 128-byte aligned).  A row's four blocks of a stage are 576
+// bytes, four and a half 128-byte lines, and rows of 144 nb bytes start 64
+// bytes apart modulo a line, so even rows start their even stages on a line
+// and odd rows 64 bytes into one, the other way round in odd stages.  A stage
+// moves as the five whole lines that hold it (the half line it shares with
+// the next or the previous stage included): ten copies, copy (j, c) taking
+// line j of the eight rows 2 i + c, lane 8 i + ((k + (i >> 1)) & 7) of it
+// piece k of its row's line, into LDS region 2 j + (c ^ parity of the
+// stage).  Every copy reads whole lines, which the nontemporal policy streams
+// without fetching a line twice.  In odd stages lane n of the matrix-core
+// layout takes row n ^ 1, so that every lane meets a row of one alignment in
+// one LDS region at every stage and keeps one table of read addresses; a
+// 16-lane read of one piece of the 16 rows meets 16 different LDS bank groups
+// (the rotation by i >> 1 spreads the rows that share a line slot, and the
+// two alignments sit half a line apart).
+constexpr uint32_t kLineCopies = 10u;
+constexpr uint32_t kLineStage = 1024u * kLineCopies;  // 16 rows x 5 lines
+constexpr int kNontemporal = 2;                       // buffer cache policy: NT
+
 // LDS map (make_layout): SB-block stages, 32 bytes of unit sums per block.
 __host__ __device__ constexpr Layout layout(uint32_t waves, uint32_t depth, uint32_t nb,
                                             uint32_t slots, uint32_t mats, uint32_t ntok = 1u,
-                                            int qb = 4, int sb = 4) {
-  return make_layout(stage_bytes(qb, sb), (uint32_t)sb, 32u, waves, depth, nb, slots, mats, ntok);
+                                            int qb = 4, int sb = 4, bool lines = false) {
+  return make_layout(lines ? kLineStage : stage_bytes(qb, sb), (uint32_t)sb, 32u, waves, depth,
+                     nb, slots, mats, ntok);
+}
+
+// The lane's header and two qs pieces of the four blocks of a full-line stage
+// buffer, each at its own address (a[3 b], a[3 b + 1], a[3 b + 2]) plus IMM.
+template <int IMM>
+__device__ __forceinline__ void lds_read_weights_at(const uint32_t (&a)[12], u32x4 (&v)[12]) {
+  asm volatile(
+      "ds_read_b128 %0, %12 offset:%24\n"
+      "ds_read_b128 %1, %13 offset:%24\n"
+      "ds_read_b128 %2, %14 offset:%24\n"
+      "ds_read_b128 %3, %15 offset:%24\n"
+      "ds_read_b128 %4, %16 offset:%24\n"
+      "ds_read_b128 %5, %17 offset:%24\n"
+      "ds_read_b128 %6, %18 offset:%24\n"
+      "ds_read_b128 %7, %19 offset:%24\n"
+      "ds_read_b128 %8, %20 offset:%24\n"
+      "ds_read_b128 %9, %21 offset:%24\n"
+      "ds_read_b128 %10, %22 offset:%24\n"
+      "ds_read_b128 %11, %23 offset:%24\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+        "=&v"(v[6]), "=&v"(v[7]), "=&v"(v[8]), "=&v"(v[9]), "=&v"(v[10]), "=&v"(v[11])
+      : "v"(a[0]), "v"(a[1]), "v"(a[2]), "v"(a[3]), "v"(a[4]), "v"(a[5]), "v"(a[6]), "v"(a[7]),
+        "v"(a[8]), "v"(a[9]), "v"(a[10]), "v"(a[11]), "i"(IMM)
+      : "memory");
 }
 
 // The lane's header and two qs pieces of the four blocks of a stage buffer:
@@ -435,6 +481,12 @@ struct StageRegs {
     else
       lds_read_weights2(hb, qb, v);
   }
+  // a full-line stage buffer (Q4_K, four blocks): each piece at its own address
+  template <int IMM>
+  __device__ __forceinline__ void read_at(const uint32_t (&a)[12]) {
+    static_assert(QB == 4 && SB == 4, "full-line stages: Q4_K, four blocks");
+    lds_read_weights_at<IMM>(a, v);
+  }
   __device__ __forceinline__ BlockQ4 decode(int b, bool hi_units, int bsh, uint32_t rot_lo,
                                             uint32_t rot_hi) const {
     if constexpr (QB == 5)
@@ -541,8 +593,10 @@ __device__ __forceinline__ float stage_rowsum(const StageRegs<QB, SB>& v, uint32
 // slice only, stage s of the matrix at local stage s - r_lo.
 // SB (one matrix, one vector): blocks per stage, 4, or 2 for shapes whose
 // workgroups have few pairs per wave (finer pairs, a shorter last one).
+// LINES (Q4_K, one vector, four-block stages of whole rows, nb a multiple of
+// 4, every matrix 128-byte aligned): full-line copies (kLineCopies above).
 template <int WAVES, int DEPTH, int MATS, int NTOK, int QB, bool GROUPED, bool SLICED = false,
-          int SB = 4>
+          int SB = 4, bool LINES = false>
 __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __restrict__ w,
                                                               const uint8_t* __restrict__ w2,
                                                               const float* __restrict__ x,
@@ -555,11 +609,14 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   static_assert(QB == 4 || QB == 5, "Q4_K or Q5_K");
   static_assert(!SLICED || (MATS == 1 && NTOK == 1 && !GROUPED), "slices of one matrix and vector");
   static_assert(SB == 4 || (SB == 2 && MATS == 1 && NTOK == 1), "two-block stages: one vector");
+  static_assert(!LINES || (QB == 4 && SB == 4 && NTOK == 1 && !SLICED && DEPTH <= 2),
+                "full-line stages: Q4_K, four blocks, one vector, whole rows");
   if constexpr (GROUPED) load_group_args_early(ga);
   const uint32_t slots = sa.packed & 0xffu;
-  constexpr uint32_t kPieces = stage_copies(QB, SB);    // copy instructions per stage
+  // copy instructions per stage
+  constexpr uint32_t kPieces = LINES ? kLineCopies : stage_copies(QB, SB);
   constexpr uint32_t kRowPieces = SB * block_pieces(QB);  // 16-byte pieces per row and stage
-  constexpr uint32_t kStage = stage_bytes(QB, SB);
+  constexpr uint32_t kStage = LINES ? kLineStage : stage_bytes(QB, SB);
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = (nb + SB - 1u) / SB;
   const uint32_t tstages = MATS * nstages;  // pairs (and partials) per tile
@@ -574,7 +631,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   const uint32_t st0 = SLICED ? ss.r_lo : 0u;
   const uint32_t nbl = SLICED ? min(SB * ss.ns, nb - SB * st0) : nb;
   const Layout L =
-      layout(WAVES, DEPTH, SLICED ? SB * ss.pstride : nb, slots, MATS, NTOK, QB, SB);
+      layout(WAVES, DEPTH, SLICED ? SB * ss.pstride : nb, slots, MATS, NTOK, QB, SB, LINES);
   const SplitWs ws = split_ws(wsp);
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
@@ -604,6 +661,15 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   };
   const uint32_t npairs = SLICED ? ss.npairs : sc.npairs;
   const uint32_t voff = n * row_bytes + 16u * grp;
+  // LINES: lcopy0 / lcopy1, the copy lane's byte offset in its tile for rows
+  // 2 i and 2 i + 1 before 576 s - 64 m (the row's stage starts 64 m bytes
+  // into its first line, m = c ^ parity of the stage).
+  uint32_t lcopy0 = 0u, lcopy1 = 0u;
+  if constexpr (LINES) {
+    const uint32_t li = lane >> 3, k = ((lane & 7u) - (li >> 1)) & 7u;
+    lcopy0 = 2u * li * row_bytes + 16u * k;
+    lcopy1 = lcopy0 + row_bytes;
+  }
   const uint32_t my_pairs = wave < npairs ? (npairs - 1u - wave) / WAVES + 1u : 0u;
   auto issue = [&](uint32_t j, const Pair& pr) {
     const uint32_t mat = MATS > 1 && pr.r >= nstages ? 1u : 0u, st = pr.r - mat * nstages;
@@ -621,6 +687,29 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
         }
     }
     const uint32_t nrows = min(16u, mrows - row0);
+    if constexpr (LINES) {
+      // the tile's rows from its first byte (128-byte aligned); rows past
+      // the tile's last read zero
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(wm + (size_t)row0 * row_bytes), 0, (int)(nrows * row_bytes),
+          kBufferWord3);
+      uint8_t* dst = wstage + (j % DEPTH) * kStage;
+      const uint32_t odd = st & 1u;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        // (the stage's terms are uniform: one add per copy class)
+        const uint32_t vo =
+            (c ? lcopy1 : lcopy0) + (4u * kQ4Bytes * st - 64u * ((uint32_t)c ^ odd));
+        uint8_t* const region = dst + 1024u * ((uint32_t)c ^ odd);
+        // (the line's offset goes into the lane offset: an instruction offset
+        // would move the LDS destination by the same amount)
+#pragma unroll
+        for (int jl = 0; jl < 5; ++jl)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(region + 2048 * jl), 16,
+                                                    vo + 128u * jl, 0, 0, kNontemporal);
+      }
+      return;
+    }
     const uint8_t* sb = wm + (size_t)row0 * row_bytes + SB * block_bytes(QB) * st;
     // the descriptor ends at the tile's last row: pieces past it read zero
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
@@ -678,6 +767,26 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   i32x4 A[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t) A[t] = i32x4{0, 0, 0, 0};
+  // LINES: the lane's 12 pieces of a stage in buffer 0 (the header, qs
+  // pieces 1 + 2 grp and 2 + 2 grp of each block), the same at every stage:
+  // the lane's row (n, or n ^ 1 in odd stages) starts its stage 64 m bytes
+  // into its first line, m = n & 1, so piece q sits at position q + 4 m of
+  // the row's five lines, line j = pos / 8 in LDS region 2 j + (n & 1), slot
+  // 8 (n >> 1) + ((pos + (n >> 2)) & 7).
+  uint32_t lread[12];
+  if constexpr (LINES) {
+    const uint32_t ri = n >> 1, rc = n & 1u, phi = n >> 2;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+#pragma unroll
+      for (int pc = 0; pc < 3; ++pc) {
+        const uint32_t q = 9u * b + (pc == 0 ? 0u : (uint32_t)pc + 2u * grp);
+        const uint32_t pos = q + 4u * rc;
+        lread[3 * b + pc] = sbase + wave * DEPTH * kStage + 1024u * (2u * (pos >> 3) + rc) +
+                            128u * ri + 16u * (((pos & 7u) + phi) & 7u);
+      }
+    }
+  }
   uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
   for (uint32_t j = 0; j < my_pairs; ++j) {
     const Pair pr = DEPTH == 1 ? pr_next : pair_of(wave + j * WAVES);
@@ -691,7 +800,14 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
     const uint32_t buf = (j % DEPTH) * kStage;
     StageRegs<QB, SB> v;
-    v.read(hb0 + buf, qb0 + buf);
+    if constexpr (LINES) {
+      if (DEPTH > 1 && (j & 1u) != 0u)
+        v.template read_at<(int)kLineStage>(lread);
+      else
+        v.template read_at<0>(lread);
+    } else {
+      v.read(hb0 + buf, qb0 + buf);
+    }
     if (j + DEPTH < my_pairs) {  // the buffer just read is free again
       const Pair pn = pair_of(wave + (j + DEPTH) * WAVES);
       issue(j + DEPTH, pn);
@@ -757,8 +873,10 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
       hand_off_tokens<NTOK>(sbase, L, sc.by_slots, pr, tstages, rs, lane, rows, y, fail);
       continue;
     }
-    const float rowsum = stage_rowsum(v, sbase, L, s - st0, s, nlive, grp, n, A, hi_units, bsh,
-                                      rot_lo, rot_hi, x);
+    float rowsum = stage_rowsum(v, sbase, L, s - st0, s, nlive, grp, n, A, hi_units, bsh,
+                                rot_lo, rot_hi, x);
+    // LINES: in odd stages lane n summed row n ^ 1; swap adjacent lanes back
+    if (LINES && (s & 1u) != 0u) rowsum = dpp<kQuadSwap>(rowsum);
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
     if constexpr (SLICED)
@@ -955,20 +1073,11 @@ __device__ __forceinline__ int64_t as_i64(uint32_t lo, uint32_t hi) {
   return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
-// One block of row n against vector g (the lane's), fast path: eight MFMAs,
-// the integer scale combine and the f32 digit and min terms over the
-// fixed-point unit sums xs; `err` gets the bound on its f32 rounding (the
-// eight-term um adds up to 9 * 2^-24 sum_u m_u |X_u|, so 2^-20 of the two
-// terms' magnitudes, as block_dot's 2^-21 for two units).
-__device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[16], int b,
-                                               const u32x4 (&a)[4], const u32x4 (&xs)[2], int eb,
-                                               float& err) {
+// The eight MFMAs of one block of row n against the lane's vector: c[u] the
+// four digit sums of unit u.
+__device__ __forceinline__ void block_mfma_tok(const u32x2 (&q)[16], int b, const u32x4 (&a)[4],
+                                               i32x4 (&c)[8]) {
   const i32x4 zero = {0, 0, 0, 0};
-  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
-  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
-  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
-  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
-  i32x4 c[8];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const u32x2 w = q[4 * b + j];
@@ -978,6 +1087,23 @@ __device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[
         as_i64(a[j][2], a[j][3]),
         as_i64((w[0] >> 4) & 0x0f0f0f0fu, (w[1] >> 4) & 0x0f0f0f0fu), zero, 0, 0, 0);
   }
+}
+
+// One block of row n against vector g (the lane's), fast path: eight MFMAs,
+// the integer scale combine and the f32 digit and min terms over the
+// fixed-point unit sums xs; `err` gets the bound on its f32 rounding.  The
+// eight-term um is summed in pairs (within 5 * 2^-24 sum_u m_u |X_u| with the
+// sums' own rounding), so as in block_dot 2^-21 of the two terms' magnitudes
+// covers the whole.
+__device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[16], int b,
+                                               const u32x4 (&a)[4], const u32x4 (&xs)[2], int eb,
+                                               float& err) {
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  i32x4 c[8];
+  block_mfma_tok(q, b, a, c);
   int t[4] = {0, 0, 0, 0};
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
@@ -987,18 +1113,22 @@ __device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[
   }
   const float tc =
       fmaf(fmaf(fmaf((float)t[3], 256.0f, (float)t[2]), 256.0f, (float)t[1]), 256.0f, (float)t[0]);
-  float um = 0.0f, ua = 0.0f;
+  float pr[4], ua = 0.0f;
 #pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const float m = (float)(((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu);
-    const float sx = __uint_as_float(xs[u >> 2][u & 3]);
-    um = fmaf(m, sx, um);
-    ua = fmaf(m, fabsf(sx), ua);
+  for (int k = 0; k < 4; ++k) {
+    const int u = 2 * k;
+    const float m0 = (float)(((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu);
+    const float m1 = (float)(((u < 4 ? mn03 : mn47) >> (8 * ((u + 1) & 3))) & 0xffu);
+    const float s0 = __uint_as_float(xs[u >> 2][u & 3]);
+    const float s1 = __uint_as_float(xs[u >> 2][(u + 1) & 3]);
+    pr[k] = fmaf(m1, s1, m0 * s0);
+    ua = fmaf(m1, fabsf(s1), fmaf(m0, fabsf(s0), ua));
   }
+  const float um = (pr[0] + pr[1]) + (pr[2] + pr[3]);
   const float d = half_bits_to_float(h[0] & 0xffffu);
   const float dmin = half_bits_to_float(h[0] >> 16);
   const float dt = d * tc;
-  err = __builtin_amdgcn_ldexpf(fmaf(fabsf(dmin), ua, fabsf(dt)), eb - 20);
+  err = __builtin_amdgcn_ldexpf(fmaf(fabsf(dmin), ua, fabsf(dt)), eb - 21);
   return __builtin_amdgcn_ldexpf(fmaf(-dmin, um, dt), eb);
 }
 
@@ -1303,6 +1433,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
 #pragma unroll
     for (int g = 0; g < NG; ++g) part[g] = 0.0f;
     uint32_t redo = 0u;  // bit g: the lane recomputes group g's stage exactly
+    uint32_t redo_out = 0u;  // (K slices: bit g, tok_reduce recomputes it)
     // (groups one after another: unrolled, their registers would add up)
 #pragma unroll 1
     for (uint32_t g = 0; g < (NG == 1 ? 1u : ng); ++g) {
@@ -1316,21 +1447,23 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
           sbase + L.expo + 4u * g * L.expo_stride + L.side_off + 4u * kSideBytes * sl;
       const float side = any ? tok_listed(h, q, list0, mine, L.expo_stride, lane) : 0.0f;
       float abs_pg, err;
-      const float pg = side + tok_group_stage(h, q, nlive,
-                                              sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane,
-                                              sbase + L.xsum + v * L.xsum_stride + 128u * sl,
-                                              sbase + L.expo + v * L.expo_stride + 16u * sl,
-                                              abs_pg, err);
+      const float pg = side + tok_group_stage(
+                                  h, q, nlive, sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane,
+                                  sbase + L.xsum + v * L.xsum_stride + 128u * sl,
+                                  sbase + L.expo + v * L.expo_stride + 16u * sl, abs_pg, err);
       // the stage check of the lane's (vector, row): the fast path's rounding
       // plus its rounded blocks against kStageTol of sum |partial|
       if (any) err += tok_rounded_bound(mine, list0 + grp * L.expo_stride, h);
-      const float ap = abs_pg + fabsf(side);
-      if (!(err * 1.01f <= kStageTol * (ap - err))) redo |= 1u << g;
+      if (!(err * 1.01f <= kStageTol * (abs_pg + fabsf(side) - err))) redo |= 1u << g;
 #pragma unroll
       for (int gg = 0; gg < NG; ++gg)
         if ((uint32_t)gg == g) part[gg] = pg;
     }
-    if (any_bad || __builtin_amdgcn_ballot_w64(redo != 0u) != 0u) {
+    // a K-sliced launch leaves the stages of lanes that failed the check to
+    // tok_reduce (kPartRedo below); the others take the exact path here
+    if (sliced) redo_out = redo;
+    const uint32_t redo_here = sliced ? 0u : redo;
+    if (any_bad || __builtin_amdgcn_ballot_w64(redo_here != 0u) != 0u) {
       // the rare exact path: one loop over (group, block), weights read from
       // memory, the rest addressed in LDS (no register array indexed at run
       // time)
@@ -1342,7 +1475,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       for (uint32_t g = 0; g < ng; ++g) {
         const uint32_t v = 4u * g + grp;
         const float* const xv = x + (size_t)min(v, ntok - 1u) * nb * kBlockElems;
-        const bool whole = (redo >> g) & 1u;
+        const bool whole = (redo_here >> g) & 1u;
         float e = 0.0f;
 #pragma unroll 1
         for (uint32_t b = 0; b < nlive; ++b) {
@@ -1367,7 +1500,9 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
 #pragma unroll
       for (int g = 0; g < NG; ++g) {
         const uint32_t v = 4u * g + grp;
-        if (v < ntok) part_out[((size_t)s * 4u * NG + v) * rows + row] = part[g];
+        if (v < ntok)
+          part_out[((size_t)s * 4u * NG + v) * rows + row] =
+              ((redo_out >> g) & 1u) ? __uint_as_float(kPartRedo) : part[g];
       }
     }
   }
@@ -1375,23 +1510,108 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
 }
 
 // y[t * rows + row] = sum over the stages s of part[(s * nv + t) * rows + row],
-// in stage order (the sliced launch's second kernel).
+// in stage order (the sliced launch's second kernel).  A partial that holds
+// kPartRedo (its lane failed the stage check in q4k_tokens_mfma) is the
+// stage's exact dot instead: quant.rs's per-weight values of blocks 4 s ..
+// 4 s + 3 of the row (decode_unit_exact) times vector t of the batch-major x,
+// summed in f64 and rounded once.  The workgroup's 256 threads (256 rows of
+// one vector) take such stages together from a queue in LDS, eight at a time,
+// 32 threads per stage and a 32-weight unit per thread; a stage past the
+// queue's room is taken by its own thread.
+constexpr uint32_t kRedoQueue = 64;
+__device__ __noinline__ float stage_exact_q4(const uint8_t* __restrict__ w, uint32_t row,
+                                             uint32_t nb, uint32_t s,
+                                             const float* __restrict__ x) {
+  const uint8_t* const r = w + (size_t)row * nb * kQ4Bytes;
+  double acc = 0.0;
+  for (uint32_t b = 4u * s; b < min(4u * s + 4u, nb); ++b) {
+    for (uint32_t u = 0; u < 8u; ++u) {
+      float wv[32];
+      decode_unit_exact<kTypeQ4K>(r + (size_t)b * kQ4Bytes, u, wv);
+      const float* const xu = x + (size_t)b * kBlockElems + 32u * u;
+#pragma unroll
+      for (int i = 0; i < 32; ++i) acc = fma((double)wv[i], (double)xu[i], acc);
+    }
+  }
+  return (float)acc;
+}
+
 __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part,
                                                   float* __restrict__ y, uint32_t rows,
-                                                  uint32_t nstages, uint32_t nv) {
-  const uint32_t row = blockIdx.x * 256u + threadIdx.x, t = blockIdx.y;
-  if (row >= rows) return;
+                                                  uint32_t nstages, uint32_t nv,
+                                                  const uint8_t* __restrict__ w,
+                                                  const float* __restrict__ x, uint32_t nb) {
+  __shared__ uint32_t queue[kRedoQueue];  // (row in the workgroup) << 16 | stage
+  __shared__ float value[kRedoQueue];
+  __shared__ double red[256];
+  __shared__ uint32_t queued;
+  const uint32_t tid = threadIdx.x, row = blockIdx.x * 256u + tid, t = blockIdx.y;
   const float* const p = part + (size_t)t * rows + row;
+  const float* const xt = x + (size_t)t * nb * kBlockElems;
   const size_t step = (size_t)nv * rows;
+  if (tid == 0u) queued = 0u;
+  __syncthreads();
+  // the stages' sum with eight loads in flight, in stage order; the stages
+  // this thread's row leaves to the workgroup go to the queue
   float sum = 0.0f;
-  // eight loads in flight, added in stage order
-  for (uint32_t base = 0; base < nstages; base += 8u) {
-    float v[8];
+  bool mine = false;
+  if (row < rows) {
+    for (uint32_t base = 0; base < nstages; base += 8u) {
+      float v[8];
 #pragma unroll
-    for (uint32_t i = 0; i < 8u; ++i) v[i] = base + i < nstages ? p[(base + i) * step] : 0.0f;
+      for (uint32_t i = 0; i < 8u; ++i) v[i] = base + i < nstages ? p[(base + i) * step] : 0.0f;
 #pragma unroll
-    for (uint32_t i = 0; i < 8u; ++i)
-      if (base + i < nstages) sum += v[i];
+      for (uint32_t i = 0; i < 8u; ++i) {
+        if (base + i >= nstages) continue;
+        if (__float_as_uint(v[i]) == kPartRedo) {
+          const uint32_t k = atomicAdd(&queued, 1u);
+          if (k < kRedoQueue) queue[k] = (tid << 16) | (base + i);
+          mine = true;
+        }
+        sum += v[i];
+      }
+    }
+  }
+  if (__syncthreads_or(mine)) {
+    const uint32_t nq = min(queued, kRedoQueue);
+    const uint32_t e = tid >> 5, l = tid & 31u;  // stage e of a batch; its unit l
+    for (uint32_t k0 = 0; k0 < nq; k0 += 8u) {
+      const uint32_t k = k0 + e;
+      double acc = 0.0;
+      if (k < nq) {
+        const uint32_t r = blockIdx.x * 256u + (queue[k] >> 16), st = queue[k] & 0xffffu;
+        const uint32_t b = 4u * st + (l >> 3), u = l & 7u;  // unit u of block b
+        if (b < nb) {
+          float wv[32];
+          decode_unit_exact<kTypeQ4K>(w + ((size_t)r * nb + b) * kQ4Bytes, u, wv);
+          const float* const xu = xt + (size_t)b * kBlockElems + 32u * u;
+#pragma unroll
+          for (int i = 0; i < 32; ++i) acc = fma((double)wv[i], (double)xu[i], acc);
+        }
+      }
+      red[tid] = acc;
+      __syncthreads();
+      for (uint32_t h = 16u; h > 0u; h >>= 1) {  // each stage's 32 unit sums
+        if (l < h) red[tid] += red[tid + h];
+        __syncthreads();
+      }
+      if (l == 0u && k < nq) value[k] = (float)red[tid];
+      __syncthreads();
+    }
+  }
+  if (row >= rows) return;
+  if (mine) {  // the sum again, with the recomputed stages
+    sum = 0.0f;
+    for (uint32_t st = 0; st < nstages; ++st) {
+      float v = p[st * step];
+      if (__float_as_uint(v) == kPartRedo) {
+        uint32_t k = 0;
+        const uint32_t nq = min(queued, kRedoQueue);
+        while (k < nq && queue[k] != ((tid << 16) | st)) ++k;
+        v = k < nq ? value[k] : stage_exact_q4(w, row, nb, st, xt);
+      }
+      sum += v;
+    }
   }
   y[(size_t)t * rows + row] = sum;
 }
@@ -1449,7 +1669,7 @@ bool launch_tokens_td(const uint8_t* w, const float* x, float* y, uint32_t rows,
   *err = hipGetLastError();
   if (*err == hipSuccess && ta.slices > 1u) {
     hipLaunchKernelGGL(tok_reduce, dim3((rows + 255u) / 256u, ntok), dim3(256), 0, s, ws.scratch,
-                       y, rows, nstages, 4u * NG);
+                       y, rows, nstages, 4u * NG, w, x, nb);
     *err = hipGetLastError();
   }
   return true;
@@ -1470,7 +1690,8 @@ bool launch_tokens_groups(const uint8_t* w, const float* x, float* y, uint32_t r
          launch_tokens_td<6, 4>(w, x, y, rows, nb, ntok, ws, s, err);
 }
 
-template <int W, int D, int M, int NT = 1, int QB = 4, bool G = false, int SB = 4>
+template <int W, int D, int M, int NT = 1, int QB = 4, bool G = false, int SB = 4,
+          bool LN = false>
 bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, uint32_t rows,
                uint32_t nb, const Workspace& ws, hipStream_t s, hipError_t* err,
                const GroupArgs& ga = GroupArgs{}) {
@@ -1480,20 +1701,30 @@ bool launch_wd(const uint8_t* w, const uint8_t* w2, const float* x, float* y, ui
   const LaunchShape ls = launch_shape(ntiles, tstages, W, NT == 1 ? ws.bytes : 0u, M);
   const uint32_t grid = ls.groups;
   const uint32_t slots = ring_slots(W, D, ls.tiles_per_group, tstages);
-  const uint32_t lds = layout(W, D, nb, slots, M, NT, QB, SB).total;
+  const uint32_t lds = layout(W, D, nb, slots, M, NT, QB, SB, LN).total;
   SchedArgs sa;
   if (lds > kLdsBytes || !make_sched_args(ntiles, tstages, slots, ls, &sa)) return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT, QB, G, false, SB>),
+      reinterpret_cast<const void*>(&q4k_matvec_mfma<W, D, M, NT, QB, G, false, SB, LN>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT, QB, G, false, SB>), dim3(grid), dim3(W * 64),
-                     lds, s, w, w2, x, y, rows, nb, ws.ptr, sa, ga, SliceArgs{});
+  hipLaunchKernelGGL((q4k_matvec_mfma<W, D, M, NT, QB, G, false, SB, LN>), dim3(grid),
+                     dim3(W * 64), lds, s, w, w2, x, y, rows, nb, ws.ptr, sa, ga, SliceArgs{});
   *err = hipGetLastError();
   return true;
+}
+
+// Whether a Q4_K launch of whole rows can take full-line copies: four-block
+// stages that fill every row, rows of 144 nb bytes with nb = 4 mod 8 (64
+// bytes past a whole number of lines) and 128-byte aligned matrices, so that
+// every tile starts on a line.
+bool lines_fit(uint32_t nb, const uint8_t* w, const uint8_t* w2 = nullptr) {
+  static const int env = env_int("SI_HIP_Q4K_LINES", 1);
+  auto aligned = [](const uint8_t* p) { return ((uintptr_t)p & 127u) == 0u; };
+  return env != 0 && nb % 8u == 4u && aligned(w) && (w2 == nullptr || aligned(w2));
 }
 
 // A K-sliced launch of one vector in S slices (false when the shape or the
@@ -1805,8 +2036,25 @@ bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t
     case 2: return launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
     case 3: return launch_wd<4, 3, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
     case 4: return launch_wd<5, 3, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
+    case 6:
+      return lines_fit(nb, w) &&
+             launch_wd<6, 2, 1, 1, 4, false, 4, true>(w, nullptr, x, y, rows, nb, ws, s, err);
+    case 7:
+      return lines_fit(nb, w) &&
+             launch_wd<12, 1, 1, 1, 4, false, 4, true>(w, nullptr, x, y, rows, nb, ws, s, err);
+    case 8:
+      return lines_fit(nb, w) &&
+             launch_wd<8, 1, 1, 1, 4, false, 4, true>(w, nullptr, x, y, rows, nb, ws, s, err);
     default: break;
   }
+  // full-line copies where the shape allows them, measured on MI355X
+  // (17408 x 5120, us, back to back over 8 resident copies): 12 waves 13.1,
+  // 8 waves 13.5, 6 waves with two stages in flight 15.9 (the stage
+  // arithmetic needs three waves per SIMD to hide its latency); the
+  // half-line copies at 12 waves 13.6
+  if (lines_fit(nb, w) &&
+      launch_wd<12, 1, 1, 1, 4, false, 4, true>(w, nullptr, x, y, rows, nb, ws, s, err))
+    return true;
   return launch_wd<12, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err) ||
          launch_wd<8, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err) ||
          launch_wd<4, 1, 1>(w, nullptr, x, y, rows, nb, ws, s, err);
@@ -1890,8 +2138,19 @@ bool launch_q4k_gate_up_mfma(const uint8_t* gate, const uint8_t* up, const float
     case 1: return launch_wd<12, 1, 2>(gate, up, x, h, rows, nb, ws, s, err);
     case 2: return launch_wd<8, 1, 2>(gate, up, x, h, rows, nb, ws, s, err);
     case 3: return launch_wd<10, 1, 2>(gate, up, x, h, rows, nb, ws, s, err);
+    case 4:
+      return lines_fit(nb, gate, up) &&
+             launch_wd<6, 2, 2, 1, 4, false, 4, true>(gate, up, x, h, rows, nb, ws, s, err);
+    case 5:
+      return lines_fit(nb, gate, up) &&
+             launch_wd<12, 1, 2, 1, 4, false, 4, true>(gate, up, x, h, rows, nb, ws, s, err);
     default: break;
   }
+  // full-line copies at 12 waves: 17408 x 5120 22.9 us against 23.5 (27.7
+  // with 6 waves and two stages in flight)
+  if (lines_fit(nb, gate, up) &&
+      launch_wd<12, 1, 2, 1, 4, false, 4, true>(gate, up, x, h, rows, nb, ws, s, err))
+    return true;
   // 12 waves (161 VGPRs, no spills): measured on MI355X against 8, us:
   // 17408 x 5120 23.1 / 24.0, 14336 x 4096 15.5 / 16.6, 11008 x 4096
   // 12.8 / 13.5, 8192 x 2048 6.9 / 7.1-7.4, 4096 x 4096 7.0 / 7.1-7.4

@@ -77,6 +77,10 @@ constexpr float kRoundedTol = 4e-6f;
 // elements and the f32 accumulation of the partials (under 3e-6) the dot stays
 // within 2e-5 * sum|w x|.
 constexpr float kStageTol = 8e-6f;
+// A stage partial the vectors-in-rows kernel leaves for its reduce kernel to
+// recompute exactly (its lane failed the stage check): a signalling-NaN
+// pattern, which no arithmetic result has.
+constexpr uint32_t kPartRedo = 0x7f8c0de5u;
 
 constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 4) | (0xf << 8); }
 
@@ -143,6 +147,7 @@ __device__ __forceinline__ uint32_t dpp_u(uint32_t v) {
   return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, 0xf, 0xf, true);
 }
 constexpr int kRowShr1 = 0x111, kRowShr2 = 0x112, kRowShr4 = 0x114, kRowShr8 = 0x118;
+constexpr int kQuadSwap = 0xb1;  // quad_perm [1, 0, 3, 2]: lanes 2 k and 2 k + 1 trade
 constexpr int kRowBcast15 = 0x15f;
 
 // Word k (uniform, 0..3) of a 16-byte piece.
