@@ -35,6 +35,20 @@ HBM_PEAK_GBS = 8000.0
 TRAFFIC_PROFILE = REPO / "profiles" / "q4k_matvec_mfma_17408x5120_traffic.md"
 METRIC = "Q4_K matvec achieved HBM GB/s (% of peak) + µs/call at 17408×5120, batch 1"
 NCOPIES = 8
+# every timed leg cycles through distinct resident weight copies whose bytes
+# together exceed the 256 MB Infinity Cache (MALL) with room to spare, so
+# that its rate is an HBM rate, not a cache rate
+RESIDENT_MIN_BYTES = 300_000_000
+WARM_MS = 20.0  # least warm-up of every timed leg (an idle GPU clocks down)
+
+
+def copies_for(bytes_per_call: int, least: int = 2) -> int:
+    """Distinct copies a leg rotates: more than RESIDENT_MIN_BYTES in all."""
+    return max(least, RESIDENT_MIN_BYTES // bytes_per_call + 1)
+
+
+def residency(bytes_per_call: int, copies: int) -> dict:
+    return {"weight_copies": copies, "resident_bytes": bytes_per_call * copies}
 
 
 def log(msg: str) -> None:
@@ -42,9 +56,11 @@ def log(msg: str) -> None:
 
 
 def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: int,
-                copies: int = NCOPIES, seed: int = 17, detail: bool = False,
+                copies: int | None = None, seed: int = 17, detail: bool = False,
                 graph: bool = True) -> dict:
     nbytes = rows * (cols // 256) * si_hip.BLOCK_BYTES[ggml_type]
+    if copies is None:
+        copies = copies_for(nbytes)
     weights = []
     host0 = None  # copy 0's host bytes, for the borrowed-bytes timing
     for c in range(copies):
@@ -60,11 +76,18 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
     lib = si_hip.lib()
     import ctypes as C
     harr = (C.c_void_p * copies)(*[w.handle.value for w in weights])
-    rc = lib.si_hip_quant_matvec_device_repeat(ctx.handle, harr, copies, rows, cols,
-                                               C.c_void_p(d_x), C.c_void_p(d_y), warmup)
-    if rc:
-        raise si_hip.HipError(rc, si_hip.last_error())
-    ctx.synchronize()
+    # at least `warmup` calls and WARM_MS of them
+    t0 = time.perf_counter()
+    warm_calls = 0
+    while warm_calls < warmup or (time.perf_counter() - t0) * 1e3 < WARM_MS:
+        n = max(warmup - warm_calls, 25)
+        rc = lib.si_hip_quant_matvec_device_repeat(ctx.handle, harr, copies, rows, cols,
+                                                   C.c_void_p(d_x), C.c_void_p(d_y), n)
+        if rc:
+            raise si_hip.HipError(rc, si_hip.last_error())
+        ctx.synchronize()
+        warm_calls += n
+    warm_ms = (time.perf_counter() - t0) * 1e3
     ctx.event_record(0)
     rc = lib.si_hip_quant_matvec_device_repeat(ctx.handle, harr, copies, rows, cols,
                                                C.c_void_p(d_x), C.c_void_p(d_y), steps)
@@ -89,7 +112,8 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
     gbs = nbytes / (us * 1e-6) / 1e9
     out = {"rows": rows, "cols": cols, "ggml_type": ggml_type, "bytes_per_call": nbytes,
            "us_per_call": round(us, 3), "gb_per_s": round(gbs, 1),
-           "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4)}
+           "frac_of_peak": round(gbs / HBM_PEAK_GBS, 4), **residency(nbytes, copies),
+           "warmup_calls": warm_calls, "warmup_ms": round(warm_ms, 1)}
     out.update(extra)
     return out
 
@@ -222,7 +246,7 @@ def call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, samples: int,
                               f"averaged over {n_wall} calls"}
 
 
-def _timed(ctx, fn, steps: int, warmup: int, warm_ms: float = 20.0) -> float:
+def _timed(ctx, fn, steps: int, warmup: int, warm_ms: float = WARM_MS) -> float:
     """Average ms per call of fn(i) enqueued back to back on the compute stream,
     after at least `warmup` untimed calls and warm_ms of them (a GPU left idle
     by host work, e.g. weight uploads, clocks down and needs some 10 ms of
@@ -277,8 +301,8 @@ def _rate(nbytes: int, ms: float) -> dict:
 
 
 CONFIG_NAMES = ("sweep", "mlp", "q5k", "head", "embedding", "many", "aggregate")
-# (the aggregate uploads 10 GB)
-DEFAULT_CONFIGS = ("sweep", "mlp", "q5k", "head", "embedding", "many")
+# (the aggregate uploads 10 GB of weights, a few seconds)
+DEFAULT_CONFIGS = CONFIG_NAMES
 
 
 def run_configs(ctx, steps: int, warmup: int, only=CONFIG_NAMES) -> dict:
@@ -312,7 +336,8 @@ def run_configs(ctx, steps: int, warmup: int, only=CONFIG_NAMES) -> dict:
             m = time_matvec(ctx, Q4, r, c, steps, warmup)
             log(f"configs: sweep {r}x{c}: {m['us_per_call']} us, {m['gb_per_s']} GB/s")
             sweep[f"{r}x{c}"] = {k: m[k] for k in ("bytes_per_call", "us_per_call", "gb_per_s",
-                                                  "frac_of_peak")}
+                                                  "frac_of_peak", "weight_copies",
+                                                  "resident_bytes")}
         res["q4k_sweep"] = sweep
     if "mlp" in only:
         res.update(_config_mlp(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K))
@@ -342,8 +367,11 @@ def _config_mlp(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     mlp_ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_fused_mlp_device(
         ctx.handle, mlp[i % 3][0].handle, mlp[i % 3][1].handle, mlp[i % 3][2].handle, N, K, K,
         C.c_void_p(x), C.c_void_p(h), C.c_void_p(y))), steps, warmup)
-    res["fused_gate_up_q4k_17408x5120"] = _rate(2 * bpc(Q4, N, K), gu_ms)
-    res["fused_mlp_q4k_gate_up_q6k_down"] = _rate(2 * bpc(Q4, N, K) + bpc(Q6, K, N), mlp_ms)
+    res["fused_gate_up_q4k_17408x5120"] = {**_rate(2 * bpc(Q4, N, K), gu_ms),
+                                           **residency(2 * bpc(Q4, N, K), 3)}
+    res["fused_mlp_q4k_gate_up_q6k_down"] = {
+        **_rate(2 * bpc(Q4, N, K) + bpc(Q6, K, N), mlp_ms),
+        **residency(2 * bpc(Q4, N, K) + bpc(Q6, K, N), 3)}
     for g, u, d in mlp:
         g.free(); u.free(); d.free()
     for p in (x, h, y):
@@ -360,13 +388,15 @@ def _config_mixed(ctx, lib, upload, dev_f32, bpc, steps, warmup, K, only) -> dic
     x = dev_f32(si_hip.synth_normal(401, K))
     y = ctx.device_alloc(K * 4)
     if "q5k" in only:
-        q5 = [upload(Q5, 400 + c, K, K) for c in range(8)]
+        n5 = copies_for(bpc(Q5, K, K))
+        q5 = [upload(Q5, 400 + c, K, K) for c in range(n5)]
 
         def q5_call(i):
             si_hip._check(lib.si_hip_quant_matvec_device(
-                ctx.handle, q5[i % 8].handle, K, K, C.c_void_p(x), C.c_void_p(y)))
+                ctx.handle, q5[i % n5].handle, K, K, C.c_void_p(x), C.c_void_p(y)))
 
-        res["q5k_matvec_5120x5120"] = _rate(bpc(Q5, K, K), _timed(ctx, q5_call, steps, warmup))
+        res["q5k_matvec_5120x5120"] = {**_rate(bpc(Q5, K, K), _timed(ctx, q5_call, steps, warmup)),
+                                       **residency(bpc(Q5, K, K), n5)}
         res["q5k_matvec_5120x5120"]["graph_us_per_call"] = round(
             1000.0 * _timed_graph(ctx, q5_call, 64, steps, warmup), 3)
         for w in q5:
@@ -379,20 +409,29 @@ def _config_mixed(ctx, lib, upload, dev_f32, bpc, steps, warmup, K, only) -> dic
         ms = _timed(ctx, lambda i: si_hip._check(lib.si_hip_matvec_argmax_device(
             ctx.handle, head.handle, V, K, C.c_void_p(x), 0, C.c_void_p(logits),
             C.c_void_p(packed))), max(steps // 4, 10), max(warmup // 4, 2))
-        res["q6k_head_argmax_151936x5120"] = _rate(bpc(Q6, V, K), ms)
+        res["q6k_head_argmax_151936x5120"] = {**_rate(bpc(Q6, V, K), ms),
+                                              **residency(bpc(Q6, V, K), 1)}
         head.free()
         ctx.device_free(logits); ctx.device_free(packed)
     if "embedding" in only:
         table = upload(Q4, 420, V, K)
-        ids = ctx.device_alloc(64 * 4)
-        ctx.to_device(ids, si_hip.synth_token_ids(421, 64, V).astype(np.uint32))
+        # calls rotate through id sets of distinct rows (a seeded permutation
+        # of the table's rows) that together exceed the MALL
+        row_b = bpc(Q4, 1, K)
+        nsets = min(V // 64, copies_for(64 * row_b))
+        ids = ctx.device_alloc(nsets * 64 * 4)
+        perm = np.random.default_rng(421).permutation(V)[:nsets * 64]
+        ctx.to_device(ids, perm.astype(np.uint32))
         emb = ctx.device_alloc(64 * K * 4)
         def emb_call(i):
             si_hip._check(lib.si_hip_embedding_device(
-                ctx.handle, table.handle, K, V, C.c_void_p(ids), 64, C.c_void_p(emb)))
+                ctx.handle, table.handle, K, V, C.c_void_p(ids + 256 * (i % nsets)), 64,
+                C.c_void_p(emb)))
 
-        res["q4k_embedding_64_tokens"] = _rate(64 * bpc(Q4, 1, K), _timed(ctx, emb_call, steps,
-                                                                          warmup))
+        res["q4k_embedding_64_tokens"] = _rate(64 * row_b, _timed(ctx, emb_call, steps, warmup))
+        res["q4k_embedding_64_tokens"].update(
+            {"id_sets": nsets, "resident_bytes": nsets * 64 * row_b,
+             "note": "each call 64 ids of a different set, every row of every set distinct"})
         res["q4k_embedding_64_tokens"]["graph_us_per_call"] = round(
             1000.0 * _timed_graph(ctx, emb_call, 64, steps, warmup), 3)
         table.free()
@@ -418,6 +457,7 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
         r = _rate(bpc(Q4, N, K), ms)
         r["tflop_per_s"] = round(2.0 * m * N * K / (ms * 1e-3) / 1e12, 3)
         many[f"M{m}"] = r
+    many.update(residency(bpc(Q4, N, K), 8))
     res["matmul_many_q4k_17408x5120"] = many
     for w in ws:
         w.free()
@@ -425,15 +465,16 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     # grouped matvec over one x (q/k/v-like projections): one launch against
     # one launch per matrix
     g_rows = (6144, 1024, 1024)
-    gws = [[upload(Q4, 510 + 3 * c + i, r, K) for i, r in enumerate(g_rows)] for c in range(4)]
+    g_bytes = sum(bpc(Q4, r, K) for r in g_rows)
+    ng = copies_for(g_bytes)
+    gws = [[upload(Q4, 510 + 3 * c + i, r, K) for i, r in enumerate(g_rows)] for c in range(ng)]
     Xg = dev_f32(si_hip.synth_normal(511, K))
     Yg = ctx.device_alloc(sum(g_rows) * 4)
-    g_bytes = sum(bpc(Q4, r, K) for r in g_rows)
     g_handles = [(C.c_void_p * 3)(*[wq.handle.value for wq in grp]) for grp in gws]
     g_rarr = (C.c_size_t * 3)(*g_rows)
 
     def one_launch(i):
-        si_hip._check(lib.si_hip_quant_matvec_many_device(ctx.handle, g_handles[i % 4], g_rarr, 3,
+        si_hip._check(lib.si_hip_quant_matvec_many_device(ctx.handle, g_handles[i % ng], g_rarr, 3,
                                                           K, C.c_void_p(Xg), C.c_void_p(Yg)))
 
     ms_one = _timed(ctx, one_launch, steps, warmup)
@@ -441,7 +482,7 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
 
     def per_matrix(i):
         off = 0
-        for wq, r in zip(gws[i % 4], g_rows):
+        for wq, r in zip(gws[i % ng], g_rows):
             si_hip._check(lib.si_hip_quant_matvec_device(ctx.handle, wq.handle, r, K,
                                                          C.c_void_p(Xg), C.c_void_p(Yg + 4 * off)))
             off += r
@@ -449,7 +490,7 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     ms_each = _timed(ctx, per_matrix, steps, warmup)
     res["grouped_q4k_6144+1024+1024x5120"] = {
         "bytes_per_call": g_bytes, "one_launch": _rate(g_bytes, ms_one),
-        "launch_per_matrix": _rate(g_bytes, ms_each)}
+        "launch_per_matrix": _rate(g_bytes, ms_each), **residency(g_bytes, ng)}
     res["grouped_q4k_6144+1024+1024x5120"]["one_launch"]["graph_us_per_call"] = round(
         1000.0 * ms_one_graph, 3)
     for grp in gws:
@@ -470,6 +511,7 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
         r = _rate(bpc(Q6, HN, K), ms)
         r["tflop_per_s"] = round(2.0 * m * HN * K / (ms * 1e-3) / 1e12, 3)
         many[f"M{m}"] = r
+    many.update(residency(bpc(Q6, HN, K), 1))
     res["matmul_many_q6k_head_151936x5120"] = many
     head.free()
     ctx.device_free(X); ctx.device_free(Y)
@@ -506,6 +548,9 @@ def _config_aggregate(ctx, lib, dev_f32, bpc) -> dict:
                                                       C.c_void_p(ybuf)))
     ms = _timed(ctx, token, 5, 1)
     agg = _rate(64 * layer_bytes, ms)
+    agg["ms_per_token"] = round(ms, 3)
+    agg["tb_per_s"] = round(64 * layer_bytes / (ms * 1e-3) / 1e12, 3)
+    agg.update(residency(64 * layer_bytes, 1))
     agg["layers"] = 64
     agg["per_layer"] = "qkv Q4_K 16384x5120, o Q4_K 5120x6144, gate/up Q4_K 17408x5120 fused, down Q6_K 5120x17408"
     res["aggregate_64_layers"] = agg
@@ -597,7 +642,8 @@ def main() -> int:
     rows, cols = 17408, 5120
     log(f"timing Q4_K {rows}x{cols}, {args.steps} steps, {NCOPIES} resident copies")
     b2b = args.back_to_back_only
-    head = time_matvec(ctx, 12, rows, cols, args.steps, args.warmup, detail=not b2b, graph=not b2b)
+    head = time_matvec(ctx, 12, rows, cols, args.steps, args.warmup, copies=NCOPIES,
+                       detail=not b2b, graph=not b2b)
     log(f"  {head['us_per_call']} us/call, {head['gb_per_s']} GB/s")
     out = {
         "metric": METRIC,
@@ -606,6 +652,8 @@ def main() -> int:
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
+        "warmup_done": {"calls": head["warmup_calls"], "ms": head["warmup_ms"],
+                        "note": f"at least --warmup calls and {WARM_MS:g} ms of them"},
         "ms_per_step": round(head["us_per_call"] / 1000.0, 6),
         "us_per_call": head["us_per_call"],
         "higher_is_better": True,
@@ -618,6 +666,7 @@ def main() -> int:
         "data": "synthetic (seeded generator, BASELINE.json config 2)",
         "config": {"workload": "Q4_K matvec N=17408 x K=5120, batch 1", "rows": rows,
                    "cols": cols, "batch": 1, "weight_copies": NCOPIES,
+                   "resident_bytes": head["resident_bytes"],
                    "bytes_per_call": head["bytes_per_call"]},
         "roofline": {"bound": "hbm", "achieved": head["gb_per_s"], "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": head["frac_of_peak"],
@@ -657,7 +706,8 @@ def main() -> int:
         # config 1: the matrix the reference's CPU path is quoted on
         c1 = time_matvec(ctx, 12, 4096, 5120, args.steps, cfg_warmup)
         out["configs"]["q4k_matvec_4096x5120"] = {k: c1[k] for k in (
-            "bytes_per_call", "us_per_call", "gb_per_s", "frac_of_peak")}
+            "bytes_per_call", "us_per_call", "gb_per_s", "frac_of_peak", "weight_copies",
+            "resident_bytes")}
     ctx.close()
     if not args.no_cpu:
         log("timing the CPU baseline")

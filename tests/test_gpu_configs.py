@@ -6,7 +6,9 @@
   4  Q5_K 5120 x 5120; the Q6_K head 151936 x 5120 + greedy argmax (both tie
      rules, top-2 margin reported); the chained Q5_K -> head; 64 Q4_K
      embedding rows from the 151936 x 5120 table
-  5  matmul-many on Q4_K 17408 x 5120 for M = 2, 4, 8, 16
+  5  matmul-many on Q4_K 17408 x 5120 for M = 2, 4, 8, 16; the 64-layer
+     aggregate's per-layer shapes, and one token of it through the device
+     calls against the host calls, bit for bit
 
 Bars: dots within 2e-5 * sum|w*x| of the f64 value of
 the exact products; embedding rows bit-exact; argmax identical.  Weights come
@@ -145,3 +147,72 @@ def test_config5_matmul_many_full_size(hip_ctx, batch):
         _, y64, ab = O.matvec(Q4, w, N, K, X[b], threads=16)
         assert_dot_close(outs[b], y64, ab, what=f"M={batch} candidate {b}")
     W.free()
+
+
+# ---- config 5b: the 64-layer aggregate's per-layer shapes ---------------------------------
+# bench.py streams 64 synthetic 27B-class layers per token: Q4_K 16384 x 5120
+# (q/k/v), Q4_K 5120 x 6144 (o), the fused Q4_K gate/up 17408 x 5120 and the
+# Q6_K down 5120 x 17408 (the reference's layer loop, qwen35_runtime.rs:1809-1938).
+@pytest.mark.parametrize("rows,cols", [(16384, 5120), (5120, 6144)])
+def test_config5_aggregate_layer_shapes(hip_ctx, rows, cols):
+    log(f"config 5 aggregate layer shape Q4_K {rows} x {cols}")
+    w = si_hip.synth_matrix(Q4, seed=6000 + rows, rows=rows, cols=cols, threads=16)
+    x = si_hip.synth_normal(6001 + cols, cols)
+    _, y64, ab = O.matvec(Q4, w, rows, cols, x, threads=16)
+    W = hip_ctx.upload_quant_weight_private(w, Q4)
+    try:
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+    finally:
+        W.free()
+    worst = assert_dot_close(y, y64, ab, what=f"layer {rows}x{cols}")
+    log(f"  worst {worst:.4f} of the bar")
+
+
+def test_config5_aggregate_token_matches_single_calls(hip_ctx):
+    """Two layers of the aggregate's token, issued as bench.py issues them (the
+    device-resident calls back to back on the context's stream, one wait at
+    the end), give the same bits as the synchronous host calls one by one."""
+    import ctypes as C
+    lib = si_hip.lib()
+    shapes = [(Q4, 16384, 5120), (Q4, 5120, 6144), (Q4, N, K), (Q4, N, K), (Q6, K, N)]
+    layers = []
+    for layer in range(2):
+        layers.append([hip_ctx.upload_quant_weight_private(
+            si_hip.synth_matrix(t, seed=6100 + 10 * layer + i, rows=r, cols=c, threads=16), t)
+            for i, (t, r, c) in enumerate(shapes)])
+    x6 = si_hip.synth_normal(6200, 6144)
+    xk = x6[:K].copy()
+    xm = (si_hip.synth_normal(6201, K) * np.float32(0.1)).astype(np.float32)
+    d_x6, d_xk, d_xm = (hip_ctx.device_alloc(a.nbytes) for a in (x6, xk, xm))
+    for p, a in ((d_x6, x6), (d_xk, xk), (d_xm, xm)):
+        hip_ctx.to_device(p, a)
+    outs = [(hip_ctx.device_alloc(16384 * 4), hip_ctx.device_alloc(K * 4),
+             hip_ctx.device_alloc(N * 4), hip_ctx.device_alloc(K * 4)) for _ in layers]
+    try:
+        for L, (yq, yo, h, yd) in zip(layers, outs):
+            si_hip._check(lib.si_hip_quant_matvec_device(hip_ctx.handle, L[0].handle, 16384, K,
+                                                         C.c_void_p(d_xk), C.c_void_p(yq)))
+            si_hip._check(lib.si_hip_quant_matvec_device(hip_ctx.handle, L[1].handle, K, 6144,
+                                                         C.c_void_p(d_x6), C.c_void_p(yo)))
+            si_hip._check(lib.si_hip_fused_mlp_device(hip_ctx.handle, L[2].handle, L[3].handle,
+                                                      L[4].handle, N, K, K, C.c_void_p(d_xm),
+                                                      C.c_void_p(h), C.c_void_p(yd)))
+        hip_ctx.synchronize()
+        for i, (L, (yq, yo, h, yd)) in enumerate(zip(layers, outs)):
+            log(f"  layer {i}: device token against single host calls")
+            assert np.array_equal(hip_ctx.from_device(yq, (16384,)),
+                                  hip_ctx.gguf_quant_matvec_weight(L[0], 16384, K, xk))
+            assert np.array_equal(hip_ctx.from_device(yo, (K,)),
+                                  hip_ctx.gguf_quant_matvec_weight(L[1], K, 6144, x6))
+            assert np.array_equal(hip_ctx.from_device(yd, (K,)),
+                                  hip_ctx.gguf_quant_fused_mlp_weights(L[2], L[3], L[4], N, K, K,
+                                                                       xm))
+    finally:
+        for L in layers:
+            for w in L:
+                w.free()
+        for p in (d_x6, d_xk, d_xm):
+            hip_ctx.device_free(p)
+        for group in outs:
+            for p in group:
+                hip_ctx.device_free(p)
