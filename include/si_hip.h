@@ -329,6 +329,21 @@ int si_hip_quant_matvec_device_repeat(si_hip_context *ctx,
 int si_hip_quant_matvec_noalloc(uint32_t ggml_type, const void *weights, size_t weight_bytes,
                                 size_t rows, size_t columns, const float *d_input,
                                 float *d_output, void *stream);
+/* No counterpart in the reference; for the callers of
+ * si_hip_quant_matvec_noalloc.  A kernel that gives up one of its bounded
+ * waits (the workgroups' exchange of split-tile sums, seconds of polling)
+ * records it in a device word of the current GPU instead of failing the
+ * call, and may leave the shared workspace out of its rest state.  This call
+ * waits for `stream`, reads and clears that word, and when it was set puts
+ * the workspace back into its rest state and returns SI_HIP_ERR_DEVICE
+ * (results of no-alloc calls since the last check may then be wrong); else 0.
+ * Not under graph capture.  Allocates nothing. */
+int si_hip_noalloc_check(void *stream);
+/* Test hook, no counterpart in the reference: the no-alloc workspace's
+ * bounded waits give up after `polls` polls (0: their normal course); puts
+ * the workspace into its rest state, waiting for `stream`.  Not under graph
+ * capture. */
+int si_hip_noalloc_debug_set_wait_give_up(uint32_t polls, void *stream);
 
 /* ---- captured submission (HIP graphs) ------------------------------------
  * No counterpart in the reference: every Metal call there commits its command

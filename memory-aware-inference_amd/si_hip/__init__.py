@@ -197,6 +197,8 @@ _SIGS = {
     "si_hip_synth_token_ids": (_I, [_U64, _SZ, _U32, _U32P]),
     "si_hip_quant_matvec_noalloc": (_I, [_U32, C.c_void_p, _SZ, _SZ, _SZ, C.c_void_p,
                                          C.c_void_p, C.c_void_p]),
+    "si_hip_noalloc_check": (_I, [C.c_void_p]),
+    "si_hip_noalloc_debug_set_wait_give_up": (_I, [_U32, C.c_void_p]),
     "si_hip_synth_f32_to_f16": (C.c_uint16, [C.c_float]),
 }
 

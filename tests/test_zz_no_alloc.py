@@ -6,6 +6,12 @@ slices in its static device workspace instead of a context's.  Results must be b
 (the combine order is fixed for a given grid), and therefore within the
 oracle's 2e-5 * sum|w*x| bar.  Each type runs two calls in a row, the second
 on a smaller matrix, so the second finds the workspace as the first left it.
+
+A kernel that gives up a bounded wait records it in the library's device
+failure word; si_hip_noalloc_check reports it (SI_HIP_ERR_DEVICE), clears it
+and puts the workspace back into its rest state.  The give-up is forced from
+the host with the test hook (every wait gives up after 16 polls), so every
+kernel still ends normally.
 """
 import ctypes as C
 
@@ -92,3 +98,45 @@ def test_noalloc_rejections(hip_ctx):
     finally:
         hip_ctx.device_free(d)
         W.free()
+
+
+# split-tile (17408 x 5120 Q4_K) and K-sliced (2560 x 17408 Q6_K) launches: the
+# two kinds of bounded wait in the no-alloc path
+@pytest.mark.parametrize("t,rows,cols", [(12, 17408, 5120), (14, 2560, 17408)])
+def test_noalloc_give_up_is_reported(hip_ctx, t, rows, cols):
+    hip = _hip()
+    lib = si_hip.lib()
+    w = si_hip.synth_matrix(t, seed=7700 + t, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(7701, cols)
+    W = hip_ctx.upload_quant_weight_private(w, t)
+    d_x = hip_ctx.device_alloc(cols * 4)
+    d_y = hip_ctx.device_alloc(rows * 4)
+    d_ref = hip_ctx.device_alloc(rows * 4)
+    try:
+        hip_ctx.to_device(d_x, x)
+        hip_ctx.synchronize()
+        assert lib.si_hip_noalloc_check(None) == 0, si_hip.last_error()
+        print(f"no-alloc forced give-up t={t} {rows}x{cols}", flush=True)
+        assert lib.si_hip_noalloc_debug_set_wait_give_up(16, None) == 0, si_hip.last_error()
+        try:
+            assert _noalloc(W, t, rows, cols, d_x, d_y) == 0, si_hip.last_error()
+            rc = lib.si_hip_noalloc_check(None)
+            assert rc == -9 and "gave up" in si_hip.last_error()
+            assert lib.si_hip_noalloc_check(None) == 0  # the word was cleared
+        finally:
+            assert lib.si_hip_noalloc_debug_set_wait_give_up(0, None) == 0, si_hip.last_error()
+        print(f"no-alloc after the give-up t={t} {rows}x{cols}", flush=True)
+        assert _noalloc(W, t, rows, cols, d_x, d_y) == 0, si_hip.last_error()
+        assert lib.si_hip_noalloc_check(None) == 0, si_hip.last_error()
+        assert hip.hipDeviceSynchronize() == 0
+        rc = lib.si_hip_quant_matvec_device(hip_ctx.handle, W.handle, rows, cols,
+                                            C.c_void_p(d_x), C.c_void_p(d_ref))
+        assert rc == 0, si_hip.last_error()
+        hip_ctx.synchronize()
+        y = hip_ctx.from_device(d_y, (rows,))
+        ref = hip_ctx.from_device(d_ref, (rows,))
+    finally:
+        for p in (d_x, d_y, d_ref):
+            hip_ctx.device_free(p)
+        W.free()
+    assert np.array_equal(y.view(np.uint32), ref.view(np.uint32))
