@@ -103,7 +103,8 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
                  "graph_gb_per_s": round(nbytes / (graph_ms * 1e-3) / 1e9, 1)}
     if detail:
         extra.update(call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, steps, host0))
-        extra["floor"] = stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps, warmup)
+        extra["floor"] = stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps, warmup,
+                                      ggml_type)
     ctx.device_free(d_x)
     ctx.device_free(d_y)
     for w in weights:
@@ -118,18 +119,26 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
     return out
 
 
-def stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps: int, warmup: int) -> dict:
+def stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps: int, warmup: int,
+                 ggml_type: int = 12) -> dict:
     """Back-to-back launches of si_hip_stream_probe over the same resident
     copies: the matvec kernel's weight copies alone (its grid, 12 waves per
     CU, 16-row x 64-byte buffer->LDS copies, one stage in flight per wave), the
-    same with the nontemporal bit, an empty kernel of the launch shape, and
-    the same stages read as 4-row x 256-byte copies.  The matvec cannot beat
-    the first on this copy path."""
+    same with the nontemporal bit, an empty kernel of the launch shape, the
+    same stages read as 4-row x 256-byte copies, the one-vector kernel's
+    full-line copies (rows of 4 mod 8 blocks), and the lanes' operands loaded
+    straight into registers with two stages in flight per wave (Q4_K).  The
+    matvec cannot beat its own copy form's time."""
     out = {}
     per_graph = copies * max(1, GRAPH_CALLS // copies)
     reps = max(1, steps // per_graph)
-    for mode, name in ((0, "copies_us"), (1, "copies_nontemporal_us"), (2, "empty_launch_us"),
-                       (3, "copies_4x256_us")):
+    modes = [(0, "copies_us"), (1, "copies_nontemporal_us"), (2, "empty_launch_us"),
+             (3, "copies_4x256_us")]
+    if (cols // 256) % 8 == 4:  # Q4_K rows of 4 mod 8 blocks: the kernel's full-line copies
+        modes.append((4, "copies_lines_us"))
+    if ggml_type == 12:
+        modes += [(5, "registers_2_in_flight_us"), (6, "registers_2_in_flight_nontemporal_us")]
+    for mode, name in modes:
         # recorded into a HIP graph and replayed, so that host launch cost
         # does not pace the short launches
         ctx.capture_begin()
@@ -149,7 +158,10 @@ def stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps: int, warmup:
         ctx.synchronize()
         graph.free()
         out[name] = round(us, 3)
-    out["copies_frac_of_peak"] = round(nbytes / (out["copies_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+    for name in ("copies_us", "copies_lines_us", "registers_2_in_flight_us"):
+        if name in out:
+            out[name.replace("_us", "_frac_of_peak")] = round(
+                nbytes / (out[name] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
     out["note"] = ("si_hip_stream_probe: the matvec's weight copies without arithmetic, "
                    "back to back over the same resident copies, replayed from a HIP graph")
     return out

@@ -294,8 +294,14 @@ int si_hip_embedding_device(si_hip_context *ctx, const si_hip_quant_weight *tabl
  * CU, 16-row x 64-byte buffer->LDS copies, one stage in flight per wave --
  * and no arithmetic.  mode 0: the kernels' default cache policy; 1: the
  * nontemporal bit; 2: an empty kernel of the same launch shape; 3: the same
- * stages read as 4-row x 256-byte copies.  Timed with the event slots, it
- * bounds what the matvec can reach on its copy path. */
+ * stages read as 4-row x 256-byte copies.  Modes 4 and 5 (Q4_K, the matrix
+ * 128-byte aligned) deal the (tile, stage) pairs evenly to the workgroups,
+ * as the kernel's split schedule does: 4 copies each stage as the whole
+ * 128-byte lines of its rows (the one-vector kernel's copies; columns / 256
+ * = 4 mod 8); 5 loads each lane's matrix-core operands straight into
+ * registers (16-byte loads, eight waves per CU, two stages in flight per
+ * wave); 6 the same with the nontemporal bit.  Timed with the event slots,
+ * it bounds what the matvec can reach on its copy path. */
 int si_hip_stream_probe(si_hip_context *ctx, const si_hip_quant_weight *const *weights, size_t n,
                         size_t rows, size_t columns, uint32_t mode, size_t iters);
 

@@ -1914,12 +1914,23 @@ int si_hip_quant_matvec_device_repeat(si_hip_context *ctx, const si_hip_quant_we
 int si_hip_stream_probe(si_hip_context *ctx, const si_hip_quant_weight *const *ws, size_t n,
                         size_t rows, size_t cols, uint32_t mode, size_t iters) {
   if (!ws || n == 0) return fail(SI_HIP_ERR_NULL, "stream probe needs at least one weight");
-  if (mode > sihip::kProbeWide) return fail(SI_HIP_ERR_RANGE, "unknown stream probe mode %u", mode);
+  if (mode > sihip::kProbeRegistersNontemporal)
+    return fail(SI_HIP_ERR_RANGE, "unknown stream probe mode %u", mode);
   for (size_t i = 0; i < n; ++i) {
     int rc = validate_device_matvec(ws[i], rows, cols, 1);
     if (rc) return rc;
     if (ws[i]->ggml_type != SI_HIP_GGML_TYPE_Q4_K && ws[i]->ggml_type != SI_HIP_GGML_TYPE_Q5_K)
       return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "the stream probe reads Q4_K or Q5_K weights");
+  }
+  if (mode >= sihip::kProbeLines) {
+    for (size_t i = 0; i < n; ++i) {
+      if (ws[i]->ggml_type != SI_HIP_GGML_TYPE_Q4_K)
+        return fail(SI_HIP_ERR_UNSUPPORTED_TYPE, "stream probe mode %u reads Q4_K weights", mode);
+      if ((reinterpret_cast<uintptr_t>(ws[i]->data()) & 127u) != 0u)
+        return fail(SI_HIP_ERR_RANGE, "stream probe mode %u needs 128-byte aligned weights", mode);
+    }
+    if (mode == sihip::kProbeLines && (cols / 256u) % 8u != 4u)
+      return fail(SI_HIP_ERR_DIMENSIONS, "stream probe mode 4 needs rows of 4 mod 8 blocks");
   }
   if (!ctx) return fail(SI_HIP_ERR_NULL, "HIP context is null");
   int cus = 0;

@@ -144,6 +144,9 @@ enum ProbeMode : uint32_t {
   kProbeNontemporal = 1,  // the same with the nontemporal bit
   kProbeEmpty = 2,        // the launch shape with no work
   kProbeWide = 3,         // the same stages as 4-row x 256-byte copies
+  kProbeLines = 4,        // Q4_K: whole 128-byte lines (the one-vector kernel's copies)
+  kProbeRegisters = 5,    // Q4_K: 16-byte loads into registers, two stages in flight
+  kProbeRegistersNontemporal = 6,  // the same with the nontemporal bit
 };
 hipError_t launch_stream_probe(uint32_t mode, const uint8_t* w, uint32_t rows, uint32_t cols,
                                uint32_t block_bytes, uint32_t cus, hipStream_t s);

@@ -24,9 +24,20 @@ def test_probe_modes(hip_ctx, t):
     try:
         for mode in (0, 1, 2, 3):
             assert _probe(hip_ctx, W, rows, cols, mode) == 0, si_hip.last_error()
+        for mode in (4, 5, 6):  # Q4_K only
+            assert _probe(hip_ctx, W, rows, cols, mode) == (0 if t == 12 else -5)
         hip_ctx.synchronize()
-        assert _probe(hip_ctx, W, rows, cols, 4) == -7
+        assert _probe(hip_ctx, W, rows, cols, 7) == -7
         assert _probe(hip_ctx, W, rows, cols + 256, 0) != 0  # byte length mismatch
+        if t == 12:  # full-line copies need rows of 4 mod 8 blocks
+            V = [hip_ctx.upload_quant_weight_private(
+                si_hip.synth_matrix(t, seed=9010, rows=64, cols=4096), t)]
+            try:
+                assert _probe(hip_ctx, V, 64, 4096, 4) == -2
+                assert _probe(hip_ctx, V, 64, 4096, 5) == 0, si_hip.last_error()
+                hip_ctx.synchronize()
+            finally:
+                V[0].free()
     finally:
         for w in W:
             w.free()
