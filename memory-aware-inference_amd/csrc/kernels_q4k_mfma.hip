@@ -729,30 +729,43 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   // (with one stage in flight, the pair of the next stage, worked out when
   // its copy is issued, is kept for its turn)
   Pair pr_next = pair_of(wave);
+  auto issue_first = [&]() {
 #pragma unroll
-  for (int j = 0; j < DEPTH; ++j)
-    if ((uint32_t)j < my_pairs) issue(j, j == 0 ? pr_next : pair_of(wave + j * WAVES));
+    for (int j = 0; j < DEPTH; ++j)
+      if ((uint32_t)j < my_pairs) issue(j, j == 0 ? pr_next : pair_of(wave + j * WAVES));
+  };
 
-  // 3. ring slots, then (once the x copies have landed) digit images, unit
-  //    sums and exponents
+  // 3. ring slots and the builders' count, set before any wave goes on (the
+  //    waves start together, so this barrier costs little); then every wave
+  //    issues its first copies, and the waves that copied x (the builders)
+  //    turn it into digit images, unit sums and exponents once it has landed
+  //    (the copies complete in issue order).  A wave reads images only once
+  //    every builder has counted itself done (wait_images): no barrier makes
+  //    a wave whose stage has landed wait for the waves whose copies the
+  //    memory queue still holds back.
   init_slots<WAVES>(sbase, L, slots);
-  // the stage copies were issued after x's and complete in order
-  const uint32_t early = min((uint32_t)DEPTH, my_pairs);
-  if (early >= 3u)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * kPieces));
-  else if (early == 2u)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kPieces));
-  else if (early == 1u)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kPieces));
-  else
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-  // chunk c = 4 p + t: units 2p, 2p + 1 of lane group p, MFMA t
-#pragma unroll
-  for (int t = 0; t < NTOK; ++t)
-    build_images<WAVES>(sbase, L, nbl, wave, grp, n,
-                        [](uint32_t c) { return 256u * (c & 3u) + 64u * (c >> 2); }, t);
   lds_wait();
   __builtin_amdgcn_s_barrier();
+  const uint32_t builders = min((uint32_t)WAVES, (nbl + 3u) / 4u);
+  issue_first();
+  if (wave < builders) {
+    const uint32_t early = min((uint32_t)DEPTH, my_pairs);
+    if (early >= 3u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * kPieces));
+    else if (early == 2u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kPieces));
+    else if (early == 1u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kPieces));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    // chunk c = 4 p + t: units 2p, 2p + 1 of lane group p, MFMA t
+#pragma unroll
+    for (int t = 0; t < NTOK; ++t)
+      build_images<WAVES>(sbase, L, nbl, wave, grp, n,
+                          [](uint32_t c) { return 256u * (c & 3u) + 64u * (c >> 2); }, t);
+    lds_wait();
+    if (lane == 0u) (void)lds_add_rtn(sbase + L.ready, 1u);
+  }
 
   // 4. the wave's pairs
   const bool hi_units = grp >= 2u;       // units 4..7 use the packed upper scales
@@ -788,6 +801,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     }
   }
   uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
+  bool images = false;  // every builder's images seen done
   for (uint32_t j = 0; j < my_pairs; ++j) {
     const Pair pr = DEPTH == 1 ? pr_next : pair_of(wave + j * WAVES);
     const uint32_t s = MATS > 1 && pr.r >= nstages ? pr.r - nstages : pr.r;  // stage
@@ -808,12 +822,23 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     } else {
       v.read(hb0 + buf, qb0 + buf);
     }
-    if (j + DEPTH < my_pairs) {  // the buffer just read is free again
-      const Pair pn = pair_of(wave + (j + DEPTH) * WAVES);
-      issue(j + DEPTH, pn);
-      if (DEPTH == 1) pr_next = pn;
-    }
+    // The buffer just read is free again.  With one vector its next copy
+    // goes out after the stage's arithmetic: while the memory queue is full,
+    // issuing a copy holds the wave, and the stage in registers would wait
+    // for it.
+    auto issue_next = [&]() {
+      if (j + DEPTH < my_pairs) {
+        const Pair pn = pair_of(wave + (j + DEPTH) * WAVES);
+        issue(j + DEPTH, pn);
+        if (DEPTH == 1) pr_next = pn;
+      }
+    };
+    if (NTOK > 1) issue_next();
     const uint32_t nlive = min((uint32_t)SB, nb - SB * s);
+    if (!images) {
+      wait_images(sbase, L, builders, fail);
+      images = true;
+    }
     if constexpr (NTOK > 1) {
       // the stage's weights are decoded once and meet every vector in turn
       BlockQ4 bw[4];
@@ -877,6 +902,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
                                 rot_lo, rot_hi, x);
     // LINES: in odd stages lane n summed row n ^ 1; swap adjacent lanes back
     if (LINES && (s & 1u) != 0u) rowsum = dpp<kQuadSwap>(rowsum);
+    issue_next();
 
     // hand the 16 row partials to the tile's slot; the last stage finishes it
     if constexpr (SLICED)

@@ -102,7 +102,7 @@ constexpr int waitcnt_vm(int n) { return (n & 0xf) | ((n >> 4) << 14) | (0x7 << 
 constexpr uint32_t kCountOff = 512;
 constexpr uint32_t kMaxMetaBlocks = kCountOff / 4u;
 struct Layout {
-  uint32_t img, xsum, expo, part, cnt, owner, total;
+  uint32_t img, xsum, expo, part, cnt, owner, ready, total;
   // per activation vector
   uint32_t img_stride, xsum_stride, expo_stride;
   uint32_t side_off, bps;  // side areas in the metadata; blocks per stage
@@ -125,7 +125,8 @@ __host__ __device__ constexpr Layout make_layout(uint32_t stage_bytes, uint32_t 
   l.part = l.expo + ntok * l.expo_stride + 16u;
   l.cnt = l.part + slots * partials * 64u * ntok;
   l.owner = l.cnt + slots * 4u;
-  l.total = l.owner + slots * 4u;
+  l.ready = l.owner + slots * 4u;  // count of image builders done (16 bytes)
+  l.total = l.ready + 16u;
   return l;
 }
 // Offset of block b's side count in its vector's metadata.
@@ -532,13 +533,25 @@ __device__ __forceinline__ bool stage_ok(float err, float abs_part) {
   return e * 1.01f <= kStageTol * (a - e);
 }
 
-// Slot ring set-up: every slot empty and owned by local tile == its index.
+// Slot ring set-up: every slot empty and owned by local tile == its index;
+// no image builder done.
 template <int WAVES>
 __device__ __forceinline__ void init_slots(uint32_t sbase, const Layout& L, uint32_t slots) {
   for (uint32_t k = threadIdx.x; k < slots; k += WAVES * 64u) {
     lds_write_b32(sbase + L.cnt + 4u * k, 0u);
     lds_write_b32(sbase + L.owner + 4u * k, k);
   }
+  if (threadIdx.x == 0u) lds_write_b32(sbase + L.ready, 0u);
+}
+
+// Waits until `builders` waves have counted their images done at L.ready.
+// Bounded like wait_slot: a wave that gives up sets `fail`.
+__device__ __forceinline__ void wait_images(uint32_t sbase, const Layout& L, uint32_t builders,
+                                            uint32_t& fail) {
+  uint32_t spin = 0;
+  for (; lds_read_b32(sbase + L.ready) < builders && spin < (1u << 24); ++spin)
+    __builtin_amdgcn_s_sleep(1);
+  if (__builtin_amdgcn_readfirstlane(spin) == (1u << 24)) fail = kDevErrSlotWait;
 }
 
 // Division by a launch constant d as a multiply-high: m = ceil(2^32 / d) (0
