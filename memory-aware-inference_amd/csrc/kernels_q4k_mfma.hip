@@ -1398,18 +1398,29 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
                                                 voff + 64u * i, 0, 0, 0);
   };
   Pair pr_next = pair_of(wave);
-  if (my_pairs > 0u) issue(pr_next);
 
-  // 3. ring slots; once the x copies have landed, the group images (a wave
-  //    converts exactly the blocks it copied)
+  // 3. ring slots and the builders' count, set before any wave goes on (the
+  //    waves start together, so this barrier costs little); then every wave
+  //    issues its first copy, and the waves that copied x blocks (a wave
+  //    converts exactly the blocks it copied) build the group images once
+  //    they have landed and count themselves done.  A wave reads images only
+  //    once every builder has (wait_images), so no barrier makes a wave
+  //    whose stage has landed wait for the waves whose copies the memory
+  //    queue still holds back.
   init_slots<WAVES>(sbase, L, ta.slots);
-  if (my_pairs > 0u)
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(kPieces));
-  else
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-  build_group_images<WAVES>(sbase, L, nbl, ng, wave, lane);
   lds_wait();
   __builtin_amdgcn_s_barrier();
+  if (my_pairs > 0u) issue(pr_next);
+  const uint32_t builders = min((uint32_t)WAVES, ng * nbl);
+  if (wave < builders) {
+    if (my_pairs > 0u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kPieces));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    build_group_images<WAVES>(sbase, L, nbl, ng, wave, lane);
+    lds_wait();
+    if (lane == 0u) (void)lds_add_rtn(sbase + L.ready, 1u);
+  }
 
   // 4. the wave's pairs: lane (grp, n) accumulates, for each group g, vector
   //    4 g + grp, row n
@@ -1424,11 +1435,16 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
     u32x2 q[16];
     lds_read_weights_tok(hb0, qb0, h, q);
     // the stage is in registers: the buffer takes the next stage's copy (the
-    // exact path reads its blocks from memory)
-    if (j + 1u < my_pairs) {
-      pr_next = pair_of(wave + (j + 1u) * WAVES);
-      issue(pr_next);
-    }
+    // exact path reads its blocks from memory), issued once the stage's
+    // arithmetic is done: while the memory queue is full, issuing a copy
+    // holds the wave
+    auto issue_next = [&]() {
+      if (j + 1u < my_pairs) {
+        pr_next = pair_of(wave + (j + 1u) * WAVES);
+        issue(pr_next);
+      }
+    };
+    if (j == 0u) wait_images(sbase, L, builders, fail);
     const uint32_t nlive = min(4u, nb - 4u * s);
     bool any_bad = false;  // a block on the exact path
     // the lane's vector's side counts of each group, kept for the groups'
@@ -1515,6 +1531,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
           if ((uint32_t)gg == g) part[gg] = (whole ? 0.0f : part[gg]) + e;
       }
     }
+    issue_next();
     if (!sliced) {
       hand_off_lane_tokens(sbase, L, FastDiv{ta.slots, ta.m_slots}, pr, nstages, part[0], lane,
                            rows, ntok, y, fail);
