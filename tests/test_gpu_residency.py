@@ -80,6 +80,46 @@ def test_changed_bytes_are_copied_again(rctx):
     assert same_bits(y2, y3)
 
 
+def _unsampled_byte(nbytes, lo):
+    """An offset at or past `lo` that none of the resident-range fingerprint's
+    64 windows of 64 bytes covers (windows at (len - 64) // 63 * k)."""
+    step = (nbytes - 64) // 63
+    for off in range(lo, nbytes):
+        k = off // step
+        if not any(o <= off < o + 64 for o in (step * k, step * (k + 1)) if o <= nbytes - 64):
+            return off
+    raise AssertionError("every byte sampled")
+
+
+def test_change_outside_the_sampled_windows_needs_evict(rctx):
+    """The documented contract (si_hip.h, residency): bytes changed in place
+    outside the sampled windows go unseen, so the next call reuses the
+    resident copy, bit for bit; si_hip_residency_evict on the changed range
+    makes the next call copy the new bytes."""
+    rows, cols = 512, 2048
+    w = si_hip.synth_matrix(Q4, seed=8250, rows=rows, cols=cols)
+    x = si_hip.synth_normal(8251, cols)
+    y1 = rctx.q4_k_matvec(w, rows, cols, x)
+    rb = w.size // rows
+    # a qs byte of some row, between two windows: its low nibble's weight moves
+    off = _unsampled_byte(w.size, 100 * rb + 40)
+    assert (off % 144) >= 16  # a qs byte, not a block header
+    row = off // rb
+    w[off] ^= 0x0F
+    s0 = rctx.residency_stats()
+    y2 = rctx.q4_k_matvec(w, rows, cols, x)
+    assert _delta(s0, rctx.residency_stats()) == {"hits": 1, "uploads": 0, "uploaded_bytes": 0,
+                                                  "evictions": 0}
+    assert same_bits(y2, y1)  # the stale resident copy, as documented
+    rctx.residency_evict(w[off:off + 1])
+    s1 = rctx.residency_stats()
+    y3 = rctx.q4_k_matvec(w, rows, cols, x)
+    assert _delta(s1, rctx.residency_stats())["uploads"] == 1
+    _, y64, ab = O.matvec(Q4, w, rows, cols, x)
+    assert_dot_close(y3, y64, ab, what="after the evict")
+    assert y3[row] != y1[row]
+
+
 def test_budget_zero_and_small_budget_stage_per_call(rctx):
     rows, cols = 1024, 1024
     w = si_hip.synth_matrix(Q6, seed=8300, rows=rows, cols=cols)
