@@ -736,18 +736,23 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   };
 
   // 3. ring slots and the builders' count, set before any wave goes on (the
-  //    waves start together, so this barrier costs little); then every wave
-  //    issues its first copies, and the waves that copied x (the builders)
-  //    turn it into digit images, unit sums and exponents once it has landed
-  //    (the copies complete in issue order).  A wave reads images only once
-  //    every builder has counted itself done (wait_images): no barrier makes
-  //    a wave whose stage has landed wait for the waves whose copies the
+  //    waves start together, so this barrier costs little).  The first round
+  //    of waves (one per SIMD), whose copies the empty memory queue takes at
+  //    once, issue their first copies before it; the later waves, whose
+  //    copies the queue holds back, after it, so that none of them keeps the
+  //    others at the barrier.  The waves that copied x (the builders) turn it
+  //    into digit images, unit sums and exponents once it has landed (the
+  //    copies complete in issue order).  A wave reads images only once every
+  //    builder has counted itself done (wait_images): no barrier makes a
+  //    wave whose stage has landed wait for the waves whose copies the
   //    memory queue still holds back.
+  const bool first_round = wave < 4u;
+  if (first_round) issue_first();
   init_slots<WAVES>(sbase, L, slots);
   lds_wait();
   __builtin_amdgcn_s_barrier();
   const uint32_t builders = min((uint32_t)WAVES, (nbl + 3u) / 4u);
-  issue_first();
+  if (!first_round) issue_first();
   if (wave < builders) {
     const uint32_t early = min((uint32_t)DEPTH, my_pairs);
     if (early >= 3u)
@@ -1400,17 +1405,20 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
   Pair pr_next = pair_of(wave);
 
   // 3. ring slots and the builders' count, set before any wave goes on (the
-  //    waves start together, so this barrier costs little); then every wave
+  //    waves start together, so this barrier costs little); every wave
   //    issues its first copy, and the waves that copied x blocks (a wave
   //    converts exactly the blocks it copied) build the group images once
   //    they have landed and count themselves done.  A wave reads images only
   //    once every builder has (wait_images), so no barrier makes a wave
   //    whose stage has landed wait for the waves whose copies the memory
-  //    queue still holds back.
+  //    queue still holds back.  The first round of waves issues before the
+  //    barrier (the empty queue takes their copies at once), the rest after.
+  const bool first_round = wave < 4u;
+  if (first_round && my_pairs > 0u) issue(pr_next);
   init_slots<WAVES>(sbase, L, ta.slots);
   lds_wait();
   __builtin_amdgcn_s_barrier();
-  if (my_pairs > 0u) issue(pr_next);
+  if (!first_round && my_pairs > 0u) issue(pr_next);
   const uint32_t builders = min((uint32_t)WAVES, ng * nbl);
   if (wave < builders) {
     if (my_pairs > 0u)
