@@ -737,16 +737,18 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
 
   // 3. ring slots and the builders' count, set before any wave goes on (the
   //    waves start together, so this barrier costs little).  The first round
-  //    of waves (one per SIMD), whose copies the empty memory queue takes at
-  //    once, issue their first copies before it; the later waves, whose
-  //    copies the queue holds back, after it, so that none of them keeps the
-  //    others at the barrier.  The waves that copied x (the builders) turn it
+  //    of waves (one per SIMD, and every builder), whose copies the empty
+  //    memory queue takes at once, issue their first copies before it; the
+  //    later waves, whose copies the queue holds back, after it, so that none
+  //    of them keeps the others at the barrier.  A builder that issued late
+  //    would hold every wave's first arithmetic back with its images.  The
+  //    waves that copied x (the builders) turn it
   //    into digit images, unit sums and exponents once it has landed (the
   //    copies complete in issue order).  A wave reads images only once every
   //    builder has counted itself done (wait_images): no barrier makes a
   //    wave whose stage has landed wait for the waves whose copies the
   //    memory queue still holds back.
-  const bool first_round = wave < 4u;
+  const bool first_round = wave < max(4u, min((uint32_t)WAVES, (nbl + 3u) / 4u));
   if (first_round) issue_first();
   init_slots<WAVES>(sbase, L, slots);
   lds_wait();
