@@ -347,34 +347,51 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * (kCopies - 1)), 16,
                                               voff_last, 0, 0, 0);
   };
-#pragma unroll
-  for (int j = 0; j < DEPTH; ++j)
-    if ((uint32_t)j < my_pairs) issue(j);
+  // A long image build (48 blocks or more in the workgroup's range, every
+  // wave a builder): the ring slots are set and a barrier passed first, so
+  // that every wave's x copies go out ahead of all weight copies, and a
+  // builder past the first round of waves (one per SIMD) builds before it
+  // issues its own copies -- the memory queue, full of the first round's
+  // copies, would hold it at them, and its images, for microseconds (the
+  // 68-block down projection's images were done 3 us later that way).
+  const bool long_build = nbl >= 48u;
+  if (long_build) {
+    init_slots<WAVES>(sbase, L, slots);
+    lds_wait();
+    __builtin_amdgcn_s_barrier();
+  }
+  const bool build_first = long_build && wave >= 4u && 4u * wave < nbl;
   // With one stage in flight, up to `prefetch` (<= 2) later pairs of the wave
   // are touched into L2 while the images are built: every 128-byte line of
   // their rows' 420 bytes is read 4 bytes wide (offsets 0, 128, 256, 384 and
   // 416 of each row) into a 256-byte LDS sink past the layout that nothing
   // reads.  Their copies then find the lines in L2.
   const uint32_t npf = DEPTH == 1 && my_pairs > 1u ? min(min(prefetch, 2u), my_pairs - 1u) : 0u;
-  for (uint32_t j = 1; j <= npf; ++j) {
-    const Pair pr = pair_of(wave + j * WAVES);
-    uint32_t nrows;
-    const uint8_t* sb = tile_at(pr, nrows);
-    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - kStageRowBytes * pr.r),
-        kBufferWord3);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(smem + L.total), 4,
-                                              n * row_bytes + 128u * grp, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(smem + L.total), 4,
-                                              n * row_bytes + kStageRowBytes - 4u, 0, 0, 0);
-  }
+  auto issue_first = [&]() {
+#pragma unroll
+    for (int j = 0; j < DEPTH; ++j)
+      if ((uint32_t)j < my_pairs) issue(j);
+    for (uint32_t j = 1; j <= npf; ++j) {
+      const Pair pr = pair_of(wave + j * WAVES);
+      uint32_t nrows;
+      const uint8_t* sb = tile_at(pr, nrows);
+      const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - kStageRowBytes * pr.r),
+          kBufferWord3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(smem + L.total), 4,
+                                                n * row_bytes + 128u * grp, 0, 0, 0);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(smem + L.total), 4,
+                                                n * row_bytes + kStageRowBytes - 4u, 0, 0, 0);
+    }
+  };
+  if (!build_first) issue_first();
 
-  // 3. ring slots, then (once the x copies have landed) digit images and
-  //    exponents
-  init_slots<WAVES>(sbase, L, slots);
+  // 3. ring slots (unless set above), then (once the x copies have landed)
+  //    digit images and exponents
+  if (!long_build) init_slots<WAVES>(sbase, L, slots);
   // the stage copies (then the touches) were issued after x's and complete in
   // order
-  const uint32_t early = min((uint32_t)DEPTH, my_pairs);
+  const uint32_t early = build_first ? 0u : min((uint32_t)DEPTH, my_pairs);
   if (early >= 3u)
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(3 * kCopies));
   else if (early == 2u)
@@ -393,6 +410,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
     build_images<WAVES>(sbase, L, nbl, wave, grp, n, [](uint32_t c) {
       return 256u * ((c >> 1) & 3u) + 64u * (2u * (c >> 3) + (c & 1u));
     }, t);
+  if (build_first) issue_first();
   lds_wait();
   __builtin_amdgcn_s_barrier();
 
