@@ -133,6 +133,50 @@ def _category(v):
     return np.where(np.isnan(v), 3, np.where(np.isposinf(v), 1, np.where(np.isneginf(v), 2, 0)))
 
 
+# Q6_K rows of 48 blocks or more, where each wave converts its own pairs' x
+# blocks: one tile, fewer pairs than waves, ragged tiles, a long grid
+@pytest.mark.parametrize("rows,cols", [(16, 12288), (7, 16384), (300, 13312), (1040, 24576)])
+def test_q6_k_long_rows(hip_ctx, rows, cols):
+    log(f"q6_k long rows {rows}x{cols}")
+    w = si_hip.synth_matrix(14, seed=rows + cols, rows=rows, cols=cols, threads=8)
+    x = si_hip.synth_normal(rows + 11, cols)
+    _, y64, ab = O.matvec(14, w, rows, cols, x, threads=8)
+    weight = hip_ctx.upload_quant_weight_private(w, 14)
+    y = hip_ctx.gguf_quant_matvec_weight(weight, rows, cols, x)
+    assert_dot_close(y, y64, ab, what=f"{rows}x{cols}")
+    weight.free()
+
+
+def test_q6_k_long_rows_special_activations(hip_ctx):
+    """The blocks a long row's waves convert themselves: huge (exact path),
+    subnormal, zero and rounded blocks (a large element among tiny ones) within
+    the bound, and one infinite or NaN activation giving +-inf / NaN rows
+    exactly where per-weight f32 products do."""
+    rows, cols = 80, 17408
+    log("q6_k long rows, special activations")
+    w = si_hip.synth_matrix(14, seed=1960, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, 14)
+    base = si_hip.synth_normal(1961, cols)
+    x = base.copy()
+    x[600:620] = np.float32(3e30)
+    x[621] = np.float32(-2.5e33)
+    x[1024:1280] = np.float32(1e-41)
+    x[1280:1536] = 0.0
+    x[9000:9256] *= np.float32(1e-7)     # rounded: one element far above the rest
+    x[9100] = np.float32(40.0)
+    x[17000:17152] *= np.float32(1e-6)   # half a block tiny
+    _, y64, ab = O.matvec(14, w, rows, cols, x, threads=8)
+    y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+    assert_dot_close(y, y64, ab, what="huge/subnormal/rounded activations")
+    for k, v in [(300, np.inf), (12000, -np.inf), (17407, np.nan)]:
+        x = base.copy()
+        x[k] = v
+        y32, _, _ = O.matvec(14, w, rows, cols, x, threads=8)
+        y = hip_ctx.gguf_quant_matvec_weight(W, rows, cols, x)
+        assert np.array_equal(_category(y), _category(y32)), f"x[{k}] = {v}"
+    W.free()
+
+
 @pytest.mark.parametrize("policy", POLICIES)
 def test_fused_gate_up_nonfinite_activations(hip_ctx, policy):
     """h = silu(gate.x) * (up.x) with an infinite or NaN activation: +-inf /
