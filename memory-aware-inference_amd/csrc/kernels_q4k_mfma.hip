@@ -809,7 +809,21 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
   }
   uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
   bool images = false;  // every builder's images seen done
-  for (uint32_t j = 0; j < my_pairs; ++j) {
+  // The fused gate/up (two matrices) with one stage in flight and three or
+  // more pairs per wave: a wave claims the workgroup's pairs after its first
+  // (pair `wave`) from a counter (L.ready + 4) as it issues their copies, so
+  // the waves whose first copies went out late take fewer pairs instead of
+  // finishing after the rest (17408 x 5120, 42 pairs per workgroup: 20.9 ->
+  // 19.3 us).  With fewer pairs per wave an early wave would take a third
+  // pair and end a whole pair later (the 17408 x 5120 matvec, 21 pairs per
+  // workgroup: 11.2 -> 12.7 us), and in one-matrix kernels the claim's code
+  // alone cost the headline 0.13 us, so there wave w takes pairs w,
+  // w + WAVES, ...  Which wave computes a pair changes no sum: a tile's
+  // finishing wave adds its partials in order.
+  constexpr bool kClaimable = DEPTH == 1 && MATS == 2;
+  const bool claims = kClaimable && npairs >= 3u * (uint32_t)WAVES;
+  uint32_t knext = wave;  // claims: the index of pr_next
+  for (uint32_t j = 0; claims ? knext < npairs : j < my_pairs; ++j) {
     const Pair pr = DEPTH == 1 ? pr_next : pair_of(wave + j * WAVES);
     const uint32_t s = MATS > 1 && pr.r >= nstages ? pr.r - nstages : pr.r;  // stage
     const uint32_t later = min((uint32_t)DEPTH - 1u, my_pairs - 1u - j);
@@ -834,7 +848,14 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
     // issuing a copy holds the wave, and the stage in registers would wait
     // for it.
     auto issue_next = [&]() {
-      if (j + DEPTH < my_pairs) {
+      if (kClaimable && claims) {
+        knext = lds_claim(sbase + L.ready + 4u);
+        if (knext < npairs) {
+          const Pair pn = pair_of(knext);
+          issue(0u, pn);
+          pr_next = pn;
+        }
+      } else if (j + DEPTH < my_pairs) {
         const Pair pn = pair_of(wave + (j + DEPTH) * WAVES);
         issue(j + DEPTH, pn);
         if (DEPTH == 1) pr_next = pn;

@@ -186,6 +186,24 @@ __device__ __forceinline__ uint32_t lds_add_rtn(uint32_t addr, uint32_t v) {
   asm volatile("ds_add_rtn_u32 %0, %1, %2\ns_waitcnt lgkmcnt(0)" : "=&v"(old) : "v"(addr), "v"(v) : "memory");
   return old;
 }
+// The wave's claim on an LDS counter: one atomic add of 1 by lane 0 (the
+// exec mask narrowed inside the asm), the old value returned in a scalar
+// register so that loop conditions on it stay uniform.
+__device__ __forceinline__ uint32_t lds_claim(uint32_t addr) {
+  uint32_t v, s;
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %[sv], exec\n"
+      "s_mov_b64 exec, 1\n"
+      "ds_add_rtn_u32 %[v], %[a], %[one]\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      "s_mov_b64 exec, %[sv]\n"
+      "v_readlane_b32 %[s], %[v], 0"
+      : [v] "=&v"(v), [sv] "=&s"(saved), [s] "=s"(s)
+      : [a] "v"(addr), [one] "v"(1u)
+      : "memory");
+  return s;
+}
 __device__ __forceinline__ uint32_t lds_read_b32(uint32_t addr) {
   uint32_t v;
   asm volatile("ds_read_b32 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(v) : "v"(addr) : "memory");
@@ -534,14 +552,18 @@ __device__ __forceinline__ bool stage_ok(float err, float abs_part) {
 }
 
 // Slot ring set-up: every slot empty and owned by local tile == its index;
-// no image builder done.
+// no image builder done; the next pair to claim (L.ready + 4, for kernels
+// whose waves claim their pairs after the first, pair `wave`) is WAVES.
 template <int WAVES>
 __device__ __forceinline__ void init_slots(uint32_t sbase, const Layout& L, uint32_t slots) {
   for (uint32_t k = threadIdx.x; k < slots; k += WAVES * 64u) {
     lds_write_b32(sbase + L.cnt + 4u * k, 0u);
     lds_write_b32(sbase + L.owner + 4u * k, k);
   }
-  if (threadIdx.x == 0u) lds_write_b32(sbase + L.ready, 0u);
+  if (threadIdx.x == 0u) {
+    lds_write_b32(sbase + L.ready, 0u);
+    lds_write_b32(sbase + L.ready + 4u, (uint32_t)WAVES);
+  }
 }
 
 // Waits until `builders` waves have counted their images done at L.ready.
