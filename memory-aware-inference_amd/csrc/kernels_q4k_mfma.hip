@@ -1186,6 +1186,43 @@ __device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[
   return __builtin_amdgcn_ldexpf(fmaf(-dmin, um, dt), eb);
 }
 
+// block_dot_tok's second try for a lane whose stage failed its check: the
+// same eight MFMAs, then the digit sums combined and scaled exactly in f64
+// (each unit's |sum_d 256^d c_d| < 2^41, the scaled sum of eight < 2^50) and
+// the min term's products (exact in f64) summed in f64.  What rounding is
+// left is that of the f32 unit sums xs (2^-24 each) and the f64 steps, so
+// err = 2^(eb-24) 1.01 |dmin| sum_u m_u |xs_u| + 2^(eb-48) of the two terms,
+// about an eighth of the fast path's bound.
+__device__ __forceinline__ double block_dot_tok_f64(const u32x4& h, const u32x2 (&q)[16], int b,
+                                                    const u32x4 (&a)[4], const u32x4 (&xs)[2],
+                                                    int eb, float& err) {
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  i32x4 c[8];
+  block_mfma_tok(q, b, a, c);
+  double tc = 0.0, um = 0.0, ua = 0.0;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const double sc = (double)((((u < 4 ? sc03 : sc47) >> (8 * (u & 3))) & 0xffu));
+    const double mn = (double)((((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu));
+    const double su = fma(fma(fma((double)c[u][3], 256.0, (double)c[u][2]), 256.0,
+                              (double)c[u][1]),
+                          256.0, (double)c[u][0]);
+    tc = fma(sc, su, tc);
+    const double xu = (double)__uint_as_float(xs[u >> 2][u & 3]);
+    um = fma(mn, xu, um);
+    ua = fma(mn, fabs(xu), ua);
+  }
+  const double d = (double)half_bits_to_float(h[0] & 0xffffu);
+  const double dmin = (double)half_bits_to_float(h[0] >> 16);
+  const double dt = d * tc;
+  const double mt = fabs(dmin) * ua;
+  err = (float)ldexp(fma(0x1.02p-24, mt, 0x1p-48 * (fabs(dt) + mt)), eb);
+  return ldexp(fma(-dmin, um, dt), eb);
+}
+
 // Exact per-weight path of one block of row n against 256 activations: the
 // block's 144 bytes at byte `off` of the buffer `wr` (read from memory: by
 // then the stage buffer may hold the next stage; bytes past the buffer's end,
@@ -1269,6 +1306,43 @@ __device__ __forceinline__ float tok_group_stage(const u32x4 (&h)[4], const u32x
     }
   }
   return part;
+}
+
+// tok_group_stage with block_dot_tok_f64: the sum in f64, with abs_part and
+// err (the bound on its rounding) as there.  Not inlined, and reading the
+// stage again from its LDS buffer (hb0, qb0: the lane's addresses there), so
+// that its registers are taken on this rare path only.
+struct StageF64 {
+  double part;
+  float abs_part, err;
+};
+__device__ __noinline__ StageF64 tok_group_stage_f64(uint32_t hb0, uint32_t qb0, uint32_t nlive,
+                                                     uint32_t iabase, uint32_t xabase,
+                                                     uint32_t eabase) {
+  u32x4 h[4];
+  u32x2 q[16];
+  lds_read_weights_tok(hb0, qb0, h, q);
+  float abs_part, err;
+  i32x4 ex;
+  asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(ex) : "v"(eabase) : "memory");
+  double part = 0.0;
+  abs_part = 0.0f;
+  err = 0.0f;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    if ((uint32_t)b < nlive) {
+      u32x4 a[4], xs[2];
+      lds_read_group_block(iabase + 4096u * b, xabase + 32u * b, a, xs);
+      float e;
+      const double v = block_dot_tok_f64(h[b], q, b, a, xs, ex[b], e);
+      const bool fast = ex[b] != kBadBlock;
+      const double c = fast ? v : 0.0;
+      part += c;
+      abs_part += (float)fabs(c);
+      err += fast ? e : 0.0f;
+    }
+  }
+  return StageF64{part, abs_part, err};
 }
 
 // Side elements of a stage for the four vectors of one group (lane group r
@@ -1520,14 +1594,34 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
           sbase + L.expo + 4u * g * L.expo_stride + L.side_off + 4u * kSideBytes * sl;
       const float side = any ? tok_listed(h, q, list0, mine, L.expo_stride, lane) : 0.0f;
       float abs_pg, err;
-      const float pg = side + tok_group_stage(
-                                  h, q, nlive, sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane,
-                                  sbase + L.xsum + v * L.xsum_stride + 128u * sl,
-                                  sbase + L.expo + v * L.expo_stride + 16u * sl, abs_pg, err);
+      const uint32_t iabase = sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane;
+      const uint32_t xabase = sbase + L.xsum + v * L.xsum_stride + 128u * sl;
+      const uint32_t eabase = sbase + L.expo + v * L.expo_stride + 16u * sl;
+      float pg = side + tok_group_stage(h, q, nlive, iabase, xabase, eabase, abs_pg, err);
       // the stage check of the lane's (vector, row): the fast path's rounding
       // plus its rounded blocks against kStageTol of sum |partial|
-      if (any) err += tok_rounded_bound(mine, list0 + grp * L.expo_stride, h);
-      if (!(err * 1.01f <= kStageTol * (abs_pg + fabsf(side) - err))) redo |= 1u << g;
+      const float rb = any ? tok_rounded_bound(mine, list0 + grp * L.expo_stride, h) : 0.0f;
+      err += rb;
+      const bool failed = !(err * 1.01f <= kStageTol * (abs_pg + fabsf(side) - err));
+      // One group (M <= 4): a lane that fails tries the stage again with the
+      // digit sums combined in f64 (a bound about eight times tighter; the
+      // stage is still in its LDS buffer, the images beside it) before it is
+      // left to the exact path, whose reads of weights from memory cost a
+      // launch 2.5 us of tail at about one failing lane in 2e4: M = 4 20.5 ->
+      // 18.6 us.  The call costs the two- and four-group kernels spills in
+      // their main loop (M = 8 31 -> 45 us), so they go straight to it.
+      if (NG == 1 && __builtin_amdgcn_ballot_w64(failed) != 0u) {
+        const StageF64 sp = tok_group_stage_f64(hb0, qb0, nlive, iabase, xabase, eabase);
+        const float err_p = sp.err + rb;
+        if (failed) {
+          if (err_p * 1.01f <= kStageTol * (sp.abs_part + fabsf(side) - err_p))
+            pg = side + (float)sp.part;
+          else
+            redo |= 1u << g;
+        }
+      } else if (NG > 1 && failed) {
+        redo |= 1u << g;
+      }
 #pragma unroll
       for (int gg = 0; gg < NG; ++gg)
         if ((uint32_t)gg == g) part[gg] = pg;
