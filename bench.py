@@ -103,8 +103,9 @@ def time_matvec(ctx, ggml_type: int, rows: int, cols: int, steps: int, warmup: i
                  "graph_gb_per_s": round(nbytes / (graph_ms * 1e-3) / 1e9, 1)}
     if detail:
         extra.update(call_detail(ctx, lib, harr, weights, rows, cols, x, d_x, d_y, steps, host0))
-        extra["floor"] = stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps, warmup,
-                                      ggml_type)
+        if GRAPHS:  # (the probe's launches are replayed from a graph)
+            extra["floor"] = stream_floor(ctx, lib, harr, copies, rows, cols, nbytes, steps,
+                                          warmup, ggml_type)
     ctx.device_free(d_x)
     ctx.device_free(d_y)
     for w in weights:
@@ -279,10 +280,16 @@ def _timed(ctx, fn, steps: int, warmup: int, warm_ms: float = WARM_MS) -> float:
     return ms / steps
 
 
-def _timed_graph(ctx, fn, per_graph: int, steps: int, warmup: int) -> float:
+GRAPHS = True  # False (--no-graphs): no leg replays a HIP graph
+
+
+def _timed_graph(ctx, fn, per_graph: int, steps: int, warmup: int) -> float | None:
     """Average ms per call of fn(i) when per_graph calls are recorded once
     into a HIP graph and the graph is replayed back to back: the device time
-    of short calls without the Python and host launch cost of each call."""
+    of short calls without the Python and host launch cost of each call.
+    None when graph legs are off."""
+    if not GRAPHS:
+        return None
     ctx.capture_begin()
     try:
         for i in range(per_graph):
@@ -409,8 +416,9 @@ def _config_mixed(ctx, lib, upload, dev_f32, bpc, steps, warmup, K, only) -> dic
 
         res["q5k_matvec_5120x5120"] = {**_rate(bpc(Q5, K, K), _timed(ctx, q5_call, steps, warmup)),
                                        **residency(bpc(Q5, K, K), n5)}
-        res["q5k_matvec_5120x5120"]["graph_us_per_call"] = round(
-            1000.0 * _timed_graph(ctx, q5_call, 64, steps, warmup), 3)
+        g = _timed_graph(ctx, q5_call, 64, steps, warmup)
+        if g is not None:
+            res["q5k_matvec_5120x5120"]["graph_us_per_call"] = round(1000.0 * g, 3)
         for w in q5:
             w.free()
     V = 151936
@@ -444,8 +452,9 @@ def _config_mixed(ctx, lib, upload, dev_f32, bpc, steps, warmup, K, only) -> dic
         res["q4k_embedding_64_tokens"].update(
             {"id_sets": nsets, "resident_bytes": nsets * 64 * row_b,
              "note": "each call 64 ids of a different set, every row of every set distinct"})
-        res["q4k_embedding_64_tokens"]["graph_us_per_call"] = round(
-            1000.0 * _timed_graph(ctx, emb_call, 64, steps, warmup), 3)
+        g = _timed_graph(ctx, emb_call, 64, steps, warmup)
+        if g is not None:
+            res["q4k_embedding_64_tokens"]["graph_us_per_call"] = round(1000.0 * g, 3)
         table.free()
         ctx.device_free(ids); ctx.device_free(emb)
     for p in (x, y):
@@ -503,8 +512,9 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     res["grouped_q4k_6144+1024+1024x5120"] = {
         "bytes_per_call": g_bytes, "one_launch": _rate(g_bytes, ms_one),
         "launch_per_matrix": _rate(g_bytes, ms_each), **residency(g_bytes, ng)}
-    res["grouped_q4k_6144+1024+1024x5120"]["one_launch"]["graph_us_per_call"] = round(
-        1000.0 * ms_one_graph, 3)
+    if ms_one_graph is not None:
+        res["grouped_q4k_6144+1024+1024x5120"]["one_launch"]["graph_us_per_call"] = round(
+            1000.0 * ms_one_graph, 3)
     for grp in gws:
         for wq in grp:
             wq.free()
@@ -640,6 +650,9 @@ def main() -> int:
     ap.add_argument("--back-to-back-only", action="store_true",
                     help="time the headline's back-to-back calls alone (no graph, isolated, "
                          "host-call or floor legs), for a kernel trace of exactly those calls")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="skip every leg that replays a HIP graph (for profiler runs: "
+                         "rocprofv3's kernel trace has crashed in a graph launch)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also time device-to-device copies of the matrix size (the yardstick "
                          "that scales HBM traffic counters)")
@@ -654,8 +667,10 @@ def main() -> int:
     rows, cols = 17408, 5120
     log(f"timing Q4_K {rows}x{cols}, {args.steps} steps, {NCOPIES} resident copies")
     b2b = args.back_to_back_only
+    global GRAPHS
+    GRAPHS = not args.no_graphs
     head = time_matvec(ctx, 12, rows, cols, args.steps, args.warmup, copies=NCOPIES,
-                       detail=not b2b, graph=not b2b)
+                       detail=not b2b, graph=GRAPHS and not b2b)
     log(f"  {head['us_per_call']} us/call, {head['gb_per_s']} GB/s")
     out = {
         "metric": METRIC,
