@@ -526,7 +526,7 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     X = dev_f32(si_hip.synth_normal(503, 16 * K))
     Y = ctx.device_alloc(16 * HN * 4)
     many = {}
-    for m in (1, 4, 16):
+    for m in (1, 4, 8, 16):
         ms = _timed(ctx, lambda i, m=m: si_hip._check(lib.si_hip_matmul_many_device(
             ctx.handle, head.handle, HN, K, m, C.c_void_p(X), C.c_void_p(Y))),
             max(4, steps // 4), min(warmup, 2))

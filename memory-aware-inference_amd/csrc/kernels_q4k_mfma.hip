@@ -54,6 +54,7 @@
 // counts nor orders buffer->LDS copies, and a fence would drain them.
 #include "mfma_common.h"
 #include "si_hip_tuned.h"
+#include "tokens_common.h"
 
 namespace sihip {
 namespace {
@@ -973,105 +974,6 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
 // stores the rows (deterministic).  With S == 1 a workgroup keeps the whole
 // row's images and sums a tile's stages in its LDS slot ring.
 
-// The image blocks a wave owns: group-blocks q = wave, wave + WAVES, ... of
-// the ng x nbl of a launch (group q / nbl, local block q % nbl), walked
-// without a division.
-template <int WAVES, typename F>
-__device__ __forceinline__ void for_group_blocks(uint32_t ng, uint32_t nbl, uint32_t wave, F f) {
-  uint32_t g = 0u, i = wave;
-  while (i >= nbl && g < ng) {
-    i -= nbl;
-    ++g;
-  }
-  for (; g < ng;) {
-    f(g, i);
-    i += WAVES;
-    while (i >= nbl && g < ng) {
-      i -= nbl;
-      ++g;
-    }
-  }
-}
-
-// Copies of the vectors' blocks blk0 .. blk0 + nbl - 1: vector 4 g + t's
-// block blk0 + i at img + 4096 (g nbl + i) + 1024 t; the slots of vectors past
-// ntok are cleared.
-template <int WAVES>
-__device__ __forceinline__ void copy_x_group(uint8_t* smem, uint32_t img, const float* x,
-                                             uint32_t nb, uint32_t blk0, uint32_t nbl,
-                                             uint32_t ng, uint32_t ntok, uint32_t wave,
-                                             uint32_t lane) {
-  const __amdgpu_buffer_rsrc_t xr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<float*>(x), 0, (int)(ntok * nb * 1024u), kBufferWord3);
-  for_group_blocks<WAVES>(ng, nbl, wave, [&](uint32_t g, uint32_t i) {
-    const uint32_t dst = img + 4096u * (g * nbl + i);
-#pragma unroll
-    for (uint32_t t = 0; t < 4u; ++t) {
-      const uint32_t v = 4u * g + t;
-      if (v < ntok)
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(xr, (lds_void*)(smem + dst + 1024u * t), 16,
-                                                  (v * nb + blk0 + i) * 1024u + 16u * lane, 0, 0,
-                                                  0);
-      else
-        lds_write_b128((uint32_t)(uintptr_t)smem + dst + 1024u * t + 16u * lane,
-                       u32x4{0u, 0u, 0u, 0u});
-    }
-  });
-}
-
-// Group images, exponents, side lists and unit sums of the copied blocks, in
-// place: a wave converts exactly the group-blocks it copied; lane (t, c)
-// takes elements 16 c .. 16 c + 15 of vector 4 g + t.  Blocks follow
-// build_images' rules (side elements, exponent kBadBlock for blocks that
-// must take the exact path).
-template <int WAVES>
-__device__ __forceinline__ void build_group_images(uint32_t sbase, const Layout& L, uint32_t nbl,
-                                                   uint32_t ng, uint32_t wave, uint32_t lane) {
-  const uint32_t t = lane >> 4, c = lane & 15u;
-  const uint32_t u = c >> 1;                                  // unit of the lane's chunk
-  const uint32_t g0 = 2u * (c & 1u);                          // K slice of its first 8
-  const uint32_t woff = 1024u * (u >> 1) + 16u * (16u * g0 + 4u * t) + 8u * (u & 1u);
-  for_group_blocks<WAVES>(ng, nbl, wave, [&](uint32_t g, uint32_t b) {
-    const uint32_t blk = sbase + L.img + 4096u * (g * nbl + b);
-    const uint32_t v = 4u * g + t;  // the lane's vector
-    u32x4 xq[4];
-    lds_read4<16>(blk + 1024u * t + 64u * c, xq);
-    float xv[16];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) xv[4 * k + i] = __uint_as_float(xq[k][i]);
-    const ChunkSplit cs = split_chunk(xv);
-    const bool bad_blk = (__builtin_amdgcn_ballot_w64(cs.bad) >> (16u * t)) & 0xffffull;
-    const uint32_t meta = sbase + L.expo + v * L.expo_stride;
-    const uint32_t list = meta + L.side_off + kSideBytes * b;
-    const uint32_t nside =
-        __builtin_amdgcn_ballot_w64(cs.smask != 0u) ? side_list(xv, cs.smask, c, list, !bad_blk) : 0u;
-    const bool rounded = !bad_blk && nside > kSideMax;
-    uint32_t uq[16];
-    biased_values(cs, !rounded, uq);
-    uint32_t dg[4][4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      transpose_digits(uq[4 * k], uq[4 * k + 1], uq[4 * k + 2], uq[4 * k + 3], dg[k]);
-    // the wave has read the whole block (lds_read4 waits) before any write
-#pragma unroll
-    for (int d = 0; d < 4; ++d) {
-      lds_write_b64(blk + woff + 16u * d, u32x2{dg[0][d], dg[1][d]});
-      lds_write_b64(blk + woff + 16u * d + 256u, u32x2{dg[2][d], dg[3][d]});
-    }
-    if (rounded)  // chunk c's error sum at position c (read whole by tok_side)
-      lds_write_b32(list + 4u * c, __float_as_uint(cs.err_side));
-    const float xsum = unit_fixed_sum(uq);  // odd lanes: unit c / 2 (listed elements as 0)
-    if (c & 1u)
-      lds_write_b32(sbase + L.xsum + v * L.xsum_stride + 32u * b + 4u * u, __float_as_uint(xsum));
-    if (c == 0u) {
-      lds_write_b32(meta + 4u * b, (uint32_t)(bad_blk ? kBadBlock : cs.e - kFixBits));
-      lds_write_b8(meta + count_pos(L, b), bad_blk ? 0u : rounded ? kSideRounded : nside);
-    }
-  });
-}
-
 // Headers and the lane's four 8-byte qs slices of the four blocks of a stage
 // buffer: header of block b at hb + 2304 b, slice j at qb + 2304 b + 512 j.
 __device__ __forceinline__ void lds_read_weights_tok(uint32_t hb, uint32_t qb, u32x4 (&h)[4],
@@ -1121,10 +1023,6 @@ __device__ __forceinline__ void lds_read_group_block(uint32_t ia, uint32_t xa, u
       : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3]), "=&v"(xs[0]), "=&v"(xs[1])
       : "v"(ia), "v"(xa)
       : "memory");
-}
-
-__device__ __forceinline__ int64_t as_i64(uint32_t lo, uint32_t hi) {
-  return (int64_t)(((uint64_t)hi << 32) | lo);
 }
 
 // The eight MFMAs of one block of row n against the lane's vector: c[u] the
@@ -1390,12 +1288,6 @@ __device__ __forceinline__ float k4_block_bound(const u32x4& h) {
     mx = fmaxf(mx, fmaf(ad, (float)(15u * sc), am * (float)mn));
   }
   return mx;
-}
-
-// Sum of all 16 error sums of a rounded block.
-__device__ __forceinline__ float rounded_err_all(uint32_t list) {
-  return (rounded_err(list, 0u) + rounded_err(list, 1u)) +
-         (rounded_err(list, 2u) + rounded_err(list, 3u));
 }
 
 // Listed side elements of a stage for the four vectors of one group: lane
@@ -1677,113 +1569,6 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
   if (fail != 0u) report_device_error(ta.wsp, fail);
 }
 
-// y[t * rows + row] = sum over the stages s of part[(s * nv + t) * rows + row],
-// in stage order (the sliced launch's second kernel).  A partial that holds
-// kPartRedo (its lane failed the stage check in q4k_tokens_mfma) is the
-// stage's exact dot instead: quant.rs's per-weight values of blocks 4 s ..
-// 4 s + 3 of the row (decode_unit_exact) times vector t of the batch-major x,
-// summed in f64 and rounded once.  The workgroup's 256 threads (256 rows of
-// one vector) take such stages together from a queue in LDS, eight at a time,
-// 32 threads per stage and a 32-weight unit per thread; a stage past the
-// queue's room is taken by its own thread.
-constexpr uint32_t kRedoQueue = 64;
-__device__ __noinline__ float stage_exact_q4(const uint8_t* __restrict__ w, uint32_t row,
-                                             uint32_t nb, uint32_t s,
-                                             const float* __restrict__ x) {
-  const uint8_t* const r = w + (size_t)row * nb * kQ4Bytes;
-  double acc = 0.0;
-  for (uint32_t b = 4u * s; b < min(4u * s + 4u, nb); ++b) {
-    for (uint32_t u = 0; u < 8u; ++u) {
-      float wv[32];
-      decode_unit_exact<kTypeQ4K>(r + (size_t)b * kQ4Bytes, u, wv);
-      const float* const xu = x + (size_t)b * kBlockElems + 32u * u;
-#pragma unroll
-      for (int i = 0; i < 32; ++i) acc = fma((double)wv[i], (double)xu[i], acc);
-    }
-  }
-  return (float)acc;
-}
-
-__global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part,
-                                                  float* __restrict__ y, uint32_t rows,
-                                                  uint32_t nstages, uint32_t nv,
-                                                  const uint8_t* __restrict__ w,
-                                                  const float* __restrict__ x, uint32_t nb) {
-  __shared__ uint32_t queue[kRedoQueue];  // (row in the workgroup) << 16 | stage
-  __shared__ float value[kRedoQueue];
-  __shared__ double red[256];
-  __shared__ uint32_t queued;
-  const uint32_t tid = threadIdx.x, row = blockIdx.x * 256u + tid, t = blockIdx.y;
-  const float* const p = part + (size_t)t * rows + row;
-  const float* const xt = x + (size_t)t * nb * kBlockElems;
-  const size_t step = (size_t)nv * rows;
-  if (tid == 0u) queued = 0u;
-  __syncthreads();
-  // the stages' sum with eight loads in flight, in stage order; the stages
-  // this thread's row leaves to the workgroup go to the queue
-  float sum = 0.0f;
-  bool mine = false;
-  if (row < rows) {
-    for (uint32_t base = 0; base < nstages; base += 8u) {
-      float v[8];
-#pragma unroll
-      for (uint32_t i = 0; i < 8u; ++i) v[i] = base + i < nstages ? p[(base + i) * step] : 0.0f;
-#pragma unroll
-      for (uint32_t i = 0; i < 8u; ++i) {
-        if (base + i >= nstages) continue;
-        if (__float_as_uint(v[i]) == kPartRedo) {
-          const uint32_t k = atomicAdd(&queued, 1u);
-          if (k < kRedoQueue) queue[k] = (tid << 16) | (base + i);
-          mine = true;
-        }
-        sum += v[i];
-      }
-    }
-  }
-  if (__syncthreads_or(mine)) {
-    const uint32_t nq = min(queued, kRedoQueue);
-    const uint32_t e = tid >> 5, l = tid & 31u;  // stage e of a batch; its unit l
-    for (uint32_t k0 = 0; k0 < nq; k0 += 8u) {
-      const uint32_t k = k0 + e;
-      double acc = 0.0;
-      if (k < nq) {
-        const uint32_t r = blockIdx.x * 256u + (queue[k] >> 16), st = queue[k] & 0xffffu;
-        const uint32_t b = 4u * st + (l >> 3), u = l & 7u;  // unit u of block b
-        if (b < nb) {
-          float wv[32];
-          decode_unit_exact<kTypeQ4K>(w + ((size_t)r * nb + b) * kQ4Bytes, u, wv);
-          const float* const xu = xt + (size_t)b * kBlockElems + 32u * u;
-#pragma unroll
-          for (int i = 0; i < 32; ++i) acc = fma((double)wv[i], (double)xu[i], acc);
-        }
-      }
-      red[tid] = acc;
-      __syncthreads();
-      for (uint32_t h = 16u; h > 0u; h >>= 1) {  // each stage's 32 unit sums
-        if (l < h) red[tid] += red[tid + h];
-        __syncthreads();
-      }
-      if (l == 0u && k < nq) value[k] = (float)red[tid];
-      __syncthreads();
-    }
-  }
-  if (row >= rows) return;
-  if (mine) {  // the sum again, with the recomputed stages
-    sum = 0.0f;
-    for (uint32_t st = 0; st < nstages; ++st) {
-      float v = p[st * step];
-      if (__float_as_uint(v) == kPartRedo) {
-        uint32_t k = 0;
-        const uint32_t nq = min(queued, kRedoQueue);
-        while (k < nq && queue[k] != ((tid << 16) | st)) ++k;
-        v = k < nq ? value[k] : stage_exact_q4(w, row, nb, st, xt);
-      }
-      sum += v;
-    }
-  }
-  y[(size_t)t * rows + row] = sum;
-}
-
 // Slice count of a launch: one per stage when the stages' partial sums of
 // nv vectors fit the workspace's scratch and every slice still has a
 // workgroup, else 1 (whole rows).
@@ -1836,8 +1621,8 @@ bool launch_tokens_td(const uint8_t* w, const float* x, float* y, uint32_t rows,
                      nb, ntok, ws.scratch, ta);
   *err = hipGetLastError();
   if (*err == hipSuccess && ta.slices > 1u) {
-    hipLaunchKernelGGL(tok_reduce, dim3((rows + 255u) / 256u, ntok), dim3(256), 0, s, ws.scratch,
-                       y, rows, nstages, 4u * NG, w, x, nb);
+    hipLaunchKernelGGL(tok_reduce<kTypeQ4K>, dim3((rows + 255u) / 256u, ntok), dim3(256), 0, s,
+                       ws.scratch, y, rows, nstages, 4u * NG, w, x, nb, 4u);
     *err = hipGetLastError();
   }
   return true;

@@ -36,6 +36,7 @@
 #include "argmax_device.h"
 #include "mfma_common.h"
 #include "si_hip_tuned.h"
+#include "tokens_common.h"
 
 namespace sihip {
 namespace {
@@ -567,6 +568,466 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
   }
 }
 
+// ---- Several activation vectors in the MFMA rows ---------------------------
+//
+// A pass over the weights with up to eight activation vectors (matmul-many,
+// replacing si_q6_k_matmul_many, metal.rs:1052-1262; the batched head of
+// qwen35_runtime.rs:2194-2197 takes up to eight candidates) puts the vectors
+// in the rows of the A operand of v_mfma_i32_16x16x32_i8, so that each
+// decoded weight meets all of them in one instruction.  K = 32 is one
+// 32-element chunk j of a block, which spans two of its scales (2 j, 2 j + 1):
+//
+//  * B lane (k, n) holds weights 8 k .. 8 k + 7 of chunk j for tile row n as
+//    the int8 4 (q - 32): (q ^ 32) << 2 puts q - 32 in two's complement in
+//    bits 2..7, so each weight takes one mask-and-merge of its ql nibble and
+//    its qh pair (the pairs XORed with 0b10 once per slice of qh).
+//  * A row 4 (2 v + h) + d holds digit d of vector 4 G + 2 q + v over the
+//    chunk's elements 16 h .. 16 h + 15 (scale 2 j + h) and zero elsewhere,
+//    from group G's images (tokens_common.h): lane (k, i) reads its 8 bytes
+//    only when k / 2 is its row's h; the other lanes hold zeros for the whole
+//    kernel.  Four MFMAs per chunk, (G, q) in {0, 1}^2, cover eight vectors.
+//  * Result lane (2 v + h, n) holds the four digit sums of vector
+//    4 G + 2 q + v, row n, over scale 2 j + h alone, so T_d += sc C_d in
+//    integers (|C_d| <= 2^18, |T_d| < 2^29) and per block the lane adds
+//    d (sum_d 256^d T_d) 2^(eb - 2), eb the block's stored exponent (x = X
+//    2^eb) and 2^-2 the weights' factor 4.  The lanes h = 0 and 1 of a vector
+//    and row hold its even and odd scales; they are added once per tile.
+//
+// K slices.  Eight vectors' images take 8 KB per block, so a launch cuts K
+// into S slices of nbs blocks: workgroup g works on slice g / GS for tiles
+// g % GS, g % GS + GS, ..., keeping that slice's images; each wave takes
+// whole (tile, slice) pairs, their two-block stages one after another (the
+// next stage's copy in flight while it computes), and stores each vector's
+// and row's sum over the slice in the scratch; tok_reduce adds the S sums
+// in slice order.  Side elements of a block (up to kSideMax, listed by the
+// image build) are added as w_i x_i with w_i decoded exactly from the stage
+// buffer before the next copy overwrites it; a rounded block is checked as
+// in the one-vector kernel.  A (vector, row) that meets a block on the exact
+// path, or whose rounded-block check fails, stores kPartRedo for the slice,
+// and tok_reduce recomputes that slice exactly.
+constexpr uint64_t kTokActiveLanes = 0xF0F0F0F00F0F0F0Full;  // lane (k, i): k / 2 == (i / 4) % 2
+
+struct Q6TokArgs {
+  uint32_t slices, groups_per_slice, m_gps, nbs;
+  void* wsp;  // the workspace, for failure reports
+};
+
+// LDS map: per-wave stage buffers, then two groups' images of nbl blocks and
+// their metadata (8 vectors); one unused ring slot.
+__host__ __device__ constexpr Layout tok6_layout(uint32_t waves, uint32_t nbl) {
+  return make_layout(kStageBytes, 2u, 32u, waves, 1u, nbl, 1u, 1u, 8u);
+}
+
+// The lane's share of a two-block stage buffer (piece p of row n at 256 p +
+// 16 n; a0 = buffer + 16 n + 256 (k / 2) + 8 (k % 2), srow = buffer + 16 n):
+// block 0's 8-byte ql slices (half h, t & 1) at a0 + 512 (2 h + (t & 1)), its
+// qh slices h at a0 + 2048 + 512 h, its scales (piece 12) and the word that
+// holds d (piece 13); block 1 starts 2 bytes into piece 13, so for each of
+// its slices the 8 bytes that start 2 before it (from a0 + 3328) and the 4
+// after those (from a2 = a0 + 3328 + 8, or + 248 where that crosses into the
+// next piece), its scales 0..13 as bytes 2..15 of piece 25 and the word of
+// scales 14, 15 and d (stage bytes 416..419: the last word of piece 26).
+struct Stage6 {
+  u32x2 ql0[4], qh0[2];
+  u32x4 sc0;
+  uint32_t dw0;
+  u32x2 ql1[4], qh1[2];
+  uint32_t ql1n[4], qh1n[2];
+  u32x4 sc1;
+  uint32_t tail1;
+};
+__device__ __forceinline__ void lds_read_stage6(uint32_t a0, uint32_t a2, uint32_t srow,
+                                                Stage6& s) {
+  asm volatile(
+      "ds_read_b64 %0, %22\n"
+      "ds_read_b64 %1, %22 offset:512\n"
+      "ds_read_b64 %2, %22 offset:1024\n"
+      "ds_read_b64 %3, %22 offset:1536\n"
+      "ds_read_b64 %4, %22 offset:2048\n"
+      "ds_read_b64 %5, %22 offset:2560\n"
+      "ds_read_b128 %6, %24 offset:3072\n"
+      "ds_read_b32 %7, %24 offset:3328\n"
+      "ds_read_b64 %8, %22 offset:3328\n"
+      "ds_read_b64 %9, %22 offset:3840\n"
+      "ds_read_b64 %10, %22 offset:4352\n"
+      "ds_read_b64 %11, %22 offset:4864\n"
+      "ds_read_b64 %12, %22 offset:5376\n"
+      "ds_read_b64 %13, %22 offset:5888\n"
+      "ds_read_b32 %14, %23\n"
+      "ds_read_b32 %15, %23 offset:512\n"
+      "ds_read_b32 %16, %23 offset:1024\n"
+      "ds_read_b32 %17, %23 offset:1536\n"
+      "ds_read_b32 %18, %23 offset:2048\n"
+      "ds_read_b32 %19, %23 offset:2560\n"
+      "ds_read_b128 %20, %24 offset:6400\n"
+      "ds_read_b32 %21, %24 offset:6668\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(s.ql0[0]), "=&v"(s.ql0[1]), "=&v"(s.ql0[2]), "=&v"(s.ql0[3]), "=&v"(s.qh0[0]),
+        "=&v"(s.qh0[1]), "=&v"(s.sc0), "=&v"(s.dw0), "=&v"(s.ql1[0]), "=&v"(s.ql1[1]),
+        "=&v"(s.ql1[2]), "=&v"(s.ql1[3]), "=&v"(s.qh1[0]), "=&v"(s.qh1[1]), "=&v"(s.ql1n[0]),
+        "=&v"(s.ql1n[1]), "=&v"(s.ql1n[2]), "=&v"(s.ql1n[3]), "=&v"(s.qh1n[0]),
+        "=&v"(s.qh1n[1]), "=&v"(s.sc1), "=&v"(s.tail1)
+      : "v"(a0), "v"(a2), "v"(srow)
+      : "memory");
+}
+
+// The A operands of chunks 2 JP and 2 JP + 1 of a block for (G, q) = (0, 0),
+// (0, 1), (1, 0), (1, 1): group G's image of the block at i0 (G = 0) or i1,
+// + 1024 JP + 128 q.  Only the lanes in kTokActiveLanes read; the others keep
+// their zeros.
+template <int JP>
+__device__ __forceinline__ void lds_read_tok6_images(uint32_t i0, uint32_t i1, i32x4 (&a)[4]) {
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %[sv], exec\n"
+      "s_mov_b64 exec, %[m]\n"
+      "ds_read_b128 %0, %[p] offset:%[o0]\n"
+      "ds_read_b128 %1, %[p] offset:%[o1]\n"
+      "ds_read_b128 %2, %[r] offset:%[o0]\n"
+      "ds_read_b128 %3, %[r] offset:%[o1]\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      "s_mov_b64 exec, %[sv]"
+      : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), [sv] "=&s"(saved)
+      : [p] "v"(i0), [r] "v"(i1), [m] "s"(kTokActiveLanes), [o0] "i"(1024 * JP),
+        [o1] "i"(1024 * JP + 128)
+      : "memory");
+}
+
+// Exponents of the stage's two blocks and their side counts (one byte each)
+// for the lane's four vectors, from their metadata at m[0..3] (already
+// offset to the stage).
+__device__ __forceinline__ void lds_read_tok6_meta(const uint32_t (&m)[4], u32x2 (&ex)[4],
+                                                   uint32_t (&cnt)[4]) {
+  static_assert(kCountOff == 512, "the offset below");
+  asm volatile(
+      "ds_read_b64 %0, %8\n"
+      "ds_read_b64 %1, %9\n"
+      "ds_read_b64 %2, %10\n"
+      "ds_read_b64 %3, %11\n"
+      "ds_read_u16 %4, %8 offset:512\n"
+      "ds_read_u16 %5, %9 offset:512\n"
+      "ds_read_u16 %6, %10 offset:512\n"
+      "ds_read_u16 %7, %11 offset:512\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(ex[0]), "=&v"(ex[1]), "=&v"(ex[2]), "=&v"(ex[3]), "=&v"(cnt[0]), "=&v"(cnt[1]),
+        "=&v"(cnt[2]), "=&v"(cnt[3])
+      : "v"(m[0]), "v"(m[1]), "v"(m[2]), "v"(m[3])
+      : "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_read_u8(uint32_t addr) {
+  uint32_t v;
+  asm volatile("ds_read_u8 %0, %1\ns_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr) : "memory");
+  return v;
+}
+
+// Byte o (< 420) of row n of a stage buffer (srow = buffer + 16 n).
+__device__ __forceinline__ uint32_t stage6_byte(uint32_t srow, uint32_t o) {
+  return lds_read_u8(o < kLastPiece ? srow + 256u * (o >> 4) + (o & 15u)
+                                    : srow + 256u * (kRowPieces - 1u) + (o - kLastPiece));
+}
+
+// quant.rs's value of element i of block b of the stage for row n (quant.rs:
+// 145-171: half h = i / 128, t = (i / 32) % 4, l = i % 32), d the block's
+// scale factor.
+__device__ __forceinline__ float stage6_weight(uint32_t srow, uint32_t b, uint32_t i, float d) {
+  const uint32_t ob = kQ6Bytes * b, h = i >> 7, t = (i >> 5) & 3u, l = i & 31u;
+  const uint32_t lo = stage6_byte(srow, ob + 64u * h + 32u * (t & 1u) + l);
+  const uint32_t hi = stage6_byte(srow, ob + 128u + 32u * h + l);
+  const int sc = (int)(int8_t)stage6_byte(srow, ob + 192u + (i >> 4));
+  const int q = (int)(((lo >> (4u * (t >> 1))) & 0xfu) | (((hi >> (2u * t)) & 3u) << 4)) - 32;
+  return k6_value_exact(d, sc, q);
+}
+
+// The lane's 8 weights 4 (q - 32) of chunk 4 h + T from its ql slice (h, T & 1)
+// and its qh slice h XORed with 0xAA in every byte.
+template <int T>
+__device__ __forceinline__ u32x2 q6_chunk(u32x2 ql, u32x2 qx) {
+  u32x2 r;
+#pragma unroll
+  for (int k = 0; k < 2; ++k) {
+    const uint32_t lo = T >= 2 ? (ql[k] >> 2) & 0x3c3c3c3cu : (ql[k] << 2) & 0x3c3c3c3cu;
+    const uint32_t hi = (T == 3 ? qx[k] : qx[k] << (6 - 2 * T)) & 0xc0c0c0c0u;
+    r[k] = lo | hi;
+  }
+  return r;
+}
+
+// Largest |scale| among the four int8 bytes of w from byte `from`.
+__device__ __forceinline__ int max_abs_i8(uint32_t w, int from = 0, int to = 4) {
+  int m = 0;
+  for (int k = from; k < to; ++k) m = max(m, abs(scale_at(w, 8u * k)));
+  return m;
+}
+
+// Up to eight vectors (vectors past ntok are zero and not stored): the
+// slice partial sums part_out[(k * 8 + v) * rows + row] of slice k.
+template <int WAVES>
+__global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __restrict__ w,
+                                                              const float* __restrict__ x,
+                                                              uint32_t rows, uint32_t nb,
+                                                              uint32_t ntok,
+                                                              float* __restrict__ part_out,
+                                                              Q6TokArgs ta) {
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+  const uint32_t wave = uniform(threadIdx.x >> 6);
+  const uint32_t lane = threadIdx.x & 63u;
+  const uint32_t grp = lane >> 4, n = lane & 15u;
+  const uint32_t vh = grp >> 1, hs = grp & 1u;  // result lanes: vector 4 G + 2 q + vh, scales 2 j + hs
+  const uint32_t row_bytes = nb * kQ6Bytes;
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t sbase = (uint32_t)(uintptr_t)smem;
+  uint8_t* const wstage = smem + wave * kStageBytes;
+
+  // this workgroup's slice k (blocks blk0 .. blk0 + nbl - 1) and its tiles
+  // tg, tg + GS, ...
+  const FastDiv by_gps{ta.groups_per_slice, ta.m_gps};
+  const uint32_t k = quo(blockIdx.x, by_gps);
+  const uint32_t tg = blockIdx.x - k * ta.groups_per_slice;
+  const uint32_t blk0 = k * ta.nbs, nbl = min(ta.nbs, nb - blk0);
+  const uint32_t nst = nbl / 2u;
+  const Layout L = tok6_layout(WAVES, nbl);
+  const uint32_t ntw = tg < ntiles ? quo(ntiles - 1u - tg, by_gps) + 1u : 0u;
+  const uint32_t my_tiles = wave < ntw ? (ntw - 1u - wave) / WAVES + 1u : 0u;
+  const uint32_t my_pairs = my_tiles * nst;
+
+  // 1. the vectors' blocks of the slice into the image area
+  copy_x_group<WAVES>(smem, L.img, x, nb, blk0, nbl, 2u, ntok, wave, lane);
+
+  // 2. the copy of a pair's stage: local tile lt (tile tg + lt GS), stage s of
+  //    the slice.  Copy i, lane l moves piece 4 i + l / 16 of row l % 16 (the
+  //    16 lanes of the 28th piece re-read the 27th), all inside the stage's
+  //    420 bytes of their row; rows past the matrix read zero.
+  const uint32_t voff = n * row_bytes + 16u * grp;
+  const uint32_t voff_last = n * row_bytes + (grp < 2u ? 16u * (24u + grp) : kLastPiece);
+  auto issue = [&](uint32_t lt, uint32_t s) {
+    const uint32_t row0 = (tg + lt * ta.groups_per_slice) * 16u;
+    const uint32_t nrows = min(16u, rows - row0);
+    const uint32_t st = blk0 / 2u + s;
+    const uint8_t* sb = w + (size_t)row0 * row_bytes + kStageRowBytes * st;
+    const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - kStageRowBytes * st),
+        kBufferWord3);
+#pragma unroll
+    for (int i = 0; i < (int)kCopies - 1; ++i)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(wstage + 1024 * i), 16,
+                                                voff + 64u * i, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(wstage + 1024 * (kCopies - 1)), 16,
+                                              voff_last, 0, 0, 0);
+  };
+
+  // 3. ring state (the builders' count), then the first copies and the group
+  //    images (as in q4k_tokens_mfma: the first round of waves issues before
+  //    the barrier, the rest after; a builder converts exactly the blocks it
+  //    copied)
+  const bool first_round = wave < 4u;
+  if (first_round && my_pairs > 0u) issue(wave, 0u);
+  init_slots<WAVES>(sbase, L, 1u);
+  lds_wait();
+  __builtin_amdgcn_s_barrier();
+  if (!first_round && my_pairs > 0u) issue(wave, 0u);
+  const uint32_t builders = min((uint32_t)WAVES, 2u * nbl);
+  if (wave < builders) {
+    if (my_pairs > 0u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    build_group_images<WAVES>(sbase, L, nbl, 2u, wave, lane);
+    lds_wait();
+    if (lane == 0u) (void)lds_add_rtn(sbase + L.ready, 1u);
+  }
+
+  // 4. the wave's pairs
+  const uint32_t srow = sbase + wave * kStageBytes + 16u * n;
+  const uint32_t a0 = srow + 256u * (grp >> 1) + 8u * (grp & 1u);
+  const uint32_t a2 = a0 + 3328u + ((grp & 1u) ? 248u : 8u);
+  // the A lane (k, i) = (grp, n): digit n % 4 of vector 2 q + n / 8 of a group
+  const uint32_t ibase = sbase + L.img + 256u * grp + 64u * (n >> 3) + 16u * (n & 3u);
+  const uint32_t gstride = 4096u * nbl;
+  // the metadata of the result lane's vectors 4 G + 2 q + vh, (G, q) = gq
+  uint32_t meta[4];
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) meta[gq] = sbase + L.expo + (2u * gq + vh) * L.expo_stride;
+  const uint32_t o_lo = 8u * hs, o_hi = 16u + 8u * hs;  // bit offsets of the lane's scales
+  i32x4 A[4];
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) A[gq] = i32x4{0, 0, 0, 0};
+  float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  uint32_t redo = 0u;  // bit gq: the slice of vector gq is recomputed exactly
+  uint32_t lt = wave, sl = 0u;
+  uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
+  for (uint32_t p = 0; p < my_pairs; ++p) {
+    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    Stage6 sv;
+    lds_read_stage6(a0, a2, srow, sv);
+    if (p == 0u) wait_images(sbase, L, builders, fail);
+    uint32_t m[4];
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) m[gq] = meta[gq] + 8u * sl;
+    u32x2 ex[4];
+    uint32_t cnt[4];
+    lds_read_tok6_meta(m, ex, cnt);
+    const float d0 = half_bits_to_float(sv.dw0 & 0xffffu);
+    const float d1 = half_bits_to_float(sv.tail1 >> 16);
+
+    // listed side elements, from the stage buffer before the next copy: the
+    // h = 0 lane of each vector and row adds them
+    uint32_t rounded = 0u;  // bit 2 gq + b: block b of vector gq is rounded
+    uint32_t any_side = 0u;
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) any_side |= cnt[gq];
+    if (__builtin_amdgcn_ballot_w64(any_side != 0u) != 0u) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+#pragma unroll
+        for (int b = 0; b < 2; ++b) {
+          const uint32_t c = (cnt[gq] >> (8 * b)) & 0xffu;
+          if (c == kSideRounded) {
+            rounded |= 1u << (2 * gq + b);
+          } else if (hs == 0u) {
+            const uint32_t list = meta[gq] + L.side_off + kSideBytes * (2u * sl + b);
+            for (uint32_t e = 0; e < c; ++e) {
+              const u32x2 ent = lds_read_b64(list + kSideEntryBytes * e);
+              const float wv = stage6_weight(srow, (uint32_t)b, ent[0], b == 0 ? d0 : d1);
+              part[gq] = fmaf(wv, __uint_as_float(ent[1]), part[gq]);
+            }
+          }
+        }
+      }
+    }
+
+    // the next pair's copy: the stage is in registers
+    const bool last_stage = sl + 1u == nst;
+    const uint32_t lt_next = last_stage ? lt + WAVES : lt;
+    const uint32_t sl_next = last_stage ? 0u : sl + 1u;
+    if (p + 1u < my_pairs) issue(lt_next, sl_next);
+
+    // the two blocks: per chunk four MFMAs and the integer scale combine
+    float absp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t ib0 = ibase + 4096u * (2u * sl);
+    static_for<2>([&](auto bc) {
+      constexpr int b = decltype(bc)::value;
+      const uint32_t i0 = ib0 + 4096u * b, i1 = i0 + gstride;
+      u32x2 ql[4], qx[2];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        if constexpr (b == 0) {
+          ql[c] = sv.ql0[c];
+        } else {
+          ql[c] = u32x2{__builtin_amdgcn_alignbyte(sv.ql1[c][1], sv.ql1[c][0], 2),
+                        __builtin_amdgcn_alignbyte(sv.ql1n[c], sv.ql1[c][1], 2)};
+        }
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const u32x2 qh = b == 0 ? sv.qh0[c]
+                                : u32x2{__builtin_amdgcn_alignbyte(sv.qh1[c][1], sv.qh1[c][0], 2),
+                                        __builtin_amdgcn_alignbyte(sv.qh1n[c], sv.qh1[c][1], 2)};
+        qx[c] = u32x2{qh[0] ^ 0xaaaaaaaau, qh[1] ^ 0xaaaaaaaau};
+      }
+      int t[4][4];
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+        for (int d = 0; d < 4; ++d) t[gq][d] = 0;
+      static_for<8>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        constexpr int h = j >> 2, tt = j & 3;
+        if constexpr ((j & 1) == 0) lds_read_tok6_images<j / 2>(i0, i1, A);
+        const u32x2 wq = q6_chunk<tt>(ql[2 * h + (tt & 1)], qx[h]);
+        // scale 2 j + hs: block 0 byte 2 j + hs of its 16; block 1 byte 2 + 2 j + hs of
+        // piece 25 (j < 7) or byte hs of the tail word (j = 7)
+        int sc;
+        if constexpr (b == 0)
+          sc = scale_at(sv.sc0[j >> 1], (j & 1) ? o_hi : o_lo);
+        else if constexpr (j == 7)
+          sc = scale_at(sv.tail1, o_lo);
+        else
+          sc = scale_at(sv.sc1[(j + 1) >> 1], (j & 1) ? o_lo : o_hi);
+        const int64_t bw = as_i64(wq[0], wq[1]);
+        const i32x4 zero = {0, 0, 0, 0};
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+              as_i64(A[gq][2 * (j & 1)], A[gq][2 * (j & 1) + 1]), bw, zero, 0, 0, 0);
+#pragma unroll
+          for (int d = 0; d < 4; ++d) t[gq][d] = __mul24(sc, c[d]) + t[gq][d];
+        }
+      });
+      const float db = b == 0 ? d0 : d1;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int eb = (int)ex[gq][b];
+        const float tc = fmaf(fmaf(fmaf((float)t[gq][3], 256.0f, (float)t[gq][2]), 256.0f,
+                                   (float)t[gq][1]),
+                              256.0f, (float)t[gq][0]);
+        const float v = __builtin_amdgcn_ldexpf(db * tc, eb - 2);
+        const bool bad = eb == kBadBlock;
+        part[gq] += bad ? 0.0f : v;
+        absp[gq] += bad ? 0.0f : fabsf(v);
+        redo |= (uint32_t)bad << gq;
+      }
+    });
+
+    // rounded blocks: the bound of their rounding against kRoundedTol of the
+    // stage's sum |partial| of the vector and row (both lanes h = 0, 1)
+    if (__builtin_amdgcn_ballot_w64(rounded != 0u) != 0u) {
+      const float bound0 =
+          fabsf(d0) * (float)(32 * max(max(max_abs_i8(sv.sc0[0]), max_abs_i8(sv.sc0[1])),
+                                        max(max_abs_i8(sv.sc0[2]), max_abs_i8(sv.sc0[3]))));
+      const float bound1 =
+          fabsf(d1) * (float)(32 * max(max(max_abs_i8(sv.sc1[0], 2), max_abs_i8(sv.sc1[1])),
+                                        max(max(max_abs_i8(sv.sc1[2]), max_abs_i8(sv.sc1[3])),
+                                            max_abs_i8(sv.tail1, 0, 2))));
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        auto a2s = __builtin_amdgcn_permlane16_swap(__float_as_uint(absp[gq]),
+                                                    __float_as_uint(absp[gq]), false, false);
+        const float a = __uint_as_float(a2s[0]) + __uint_as_float(a2s[1]);
+        float err = 0.0f;
+        const uint32_t list = meta[gq] + L.side_off + kSideBytes * (2u * sl);
+        if ((rounded >> (2 * gq)) & 1u) err = fmaf(bound0, rounded_err_all(list), err);
+        if ((rounded >> (2 * gq + 1)) & 1u)
+          err = fmaf(bound1, rounded_err_all(list + kSideBytes), err);
+        if (!(err * 1.01f <= kRoundedTol * (a - err))) redo |= 1u << gq;
+      }
+    }
+
+    if (last_stage) {
+      // the tile's sums over the slice: lanes h = 0, 1 added; lane h stores
+      // group G = h
+      float tot[4];
+      uint32_t rd = 0u;
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(part[gq]),
+                                                   __float_as_uint(part[gq]), false, false);
+        tot[gq] = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
+      }
+      {
+        auto r2 = __builtin_amdgcn_permlane16_swap(redo, redo, false, false);
+        rd = r2[0] | r2[1];
+      }
+      const uint32_t row = (tg + lt * ta.groups_per_slice) * 16u + n;
+      if (row < rows) {
+        const float val0 = hs != 0u ? tot[2] : tot[0];
+        const float val1 = hs != 0u ? tot[3] : tot[1];
+        const uint32_t r2 = rd >> (2u * hs);
+        const uint32_t v0 = 4u * hs + vh, v1 = v0 + 2u;
+        float* const out = part_out + (size_t)k * 8u * rows + row;
+        if (v0 < ntok) out[(size_t)v0 * rows] = (r2 & 1u) ? __uint_as_float(kPartRedo) : val0;
+        if (v1 < ntok) out[(size_t)v1 * rows] = (r2 & 2u) ? __uint_as_float(kPartRedo) : val1;
+      }
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) part[gq] = 0.0f;
+      redo = 0u;
+    }
+    lt = lt_next;
+    sl = sl_next;
+  }
+  if (fail != 0u) report_device_error(ta.wsp, fail);
+}
+
 // P: rows and nb are the launch's (row pairs of a matrix of nb / 2 blocks).
 template <int W, int D, int NT = 1, bool G = false, bool AM = false, bool P = false>
 bool launch_wd(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
@@ -731,6 +1192,65 @@ bool launch_pairs(const uint8_t* w, const float* x, float* y, uint32_t rows, uin
           launch_wd<8, 1, 1, false, false, true>(w, x, y, prows, pnb, ws, s, err) ||
           launch_wd<4, 1, 1, false, false, true>(w, x, y, prows, pnb, ws, s, err));
 }
+
+// Up to eight vectors in one pass over the weights: q6k_tokens_mfma in K
+// slices of nbs blocks, then tok_reduce.  false when the shape does not fit
+// (q6_shape_ok, the slices' partial sums within the scratch, the LDS).
+template <int W>
+bool launch_tok6(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+                 uint32_t ntok, uint32_t nbs, const Workspace& ws, hipStream_t s,
+                 hipError_t* err) {
+  if (ntok == 0u || ntok > 8u || nbs < 2u || (nbs & 1u) != 0u || !q6_shape_ok(rows, nb))
+    return false;
+  const uint32_t ntiles = (rows + 15u) / 16u;
+  const uint32_t cus = (uint32_t)cu_count();
+  Q6TokArgs ta{};
+  ta.nbs = min(nbs, nb);
+  ta.slices = (nb + ta.nbs - 1u) / ta.nbs;
+  if (ta.slices > cus || (size_t)ta.slices * 8u * rows * sizeof(float) > ws.scratch_bytes)
+    return false;
+  ta.groups_per_slice = min(cus / ta.slices, ntiles);
+  const uint32_t grid = ta.groups_per_slice * ta.slices;
+  // block and tile indices divided by GS
+  if ((uint64_t)(grid + ntiles) * ta.groups_per_slice >= (1ull << 32)) return false;
+  ta.m_gps = div_magic(ta.groups_per_slice);
+  ta.wsp = ws.ptr;
+  const uint32_t lds = tok6_layout(W, ta.nbs).total;
+  if (lds > kLdsBytes) return false;
+  static const hipError_t attr =
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&q6k_tokens_mfma<W>),
+                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
+  if (attr != hipSuccess) {
+    *err = attr;
+    return true;
+  }
+  hipLaunchKernelGGL(q6k_tokens_mfma<W>, dim3(grid), dim3(W * 64), lds, s, w, x, rows, nb, ntok,
+                     ws.scratch, ta);
+  *err = hipGetLastError();
+  if (*err == hipSuccess) {
+    hipLaunchKernelGGL(tok_reduce<kTypeQ6K>, dim3((rows + 255u) / 256u, ntok), dim3(256), 0, s,
+                       ws.scratch, y, rows, ta.slices, 8u, w, x, nb, ta.nbs);
+    *err = hipGetLastError();
+  }
+  return true;
+}
+
+// The vectors-in-rows pass for ntok <= 8 vectors: 12 waves with four-block
+// slices, else (the partial sums of more slices than the scratch holds) the
+// fewest slices whose images leave 8 waves their stage buffers.
+bool launch_tok6_any(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
+                     uint32_t ntok, const Workspace& ws, hipStream_t s, hipError_t* err) {
+  static const int nbs_env = env_int("SI_HIP_Q6K_TOK_NBS", 0);
+  static const int w_env = env_int("SI_HIP_Q6K_TOK_WAVES", 0);
+  if (nbs_env > 0) {
+    const uint32_t nbs = (uint32_t)nbs_env;
+    return w_env == 8 ? launch_tok6<8>(w, x, y, rows, nb, ntok, nbs, ws, s, err)
+                      : launch_tok6<12>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+  }
+  return launch_tok6<12>(w, x, y, rows, nb, ntok, 4u, ws, s, err) ||
+         launch_tok6<12>(w, x, y, rows, nb, ntok, 6u, ws, s, err) ||
+         launch_tok6<8>(w, x, y, rows, nb, ntok, 10u, ws, s, err);
+}
 }  // namespace
 
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
@@ -793,12 +1313,16 @@ bool launch_q6k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t
                             hipError_t* err) {
   const uint32_t nb = cols / kBlockElems;
   if (!q6_shape_ok(rows, nb)) return false;
+  static const int tok_min = env_int("SI_HIP_Q6K_TOKENS_MIN", 3);
   for (uint32_t b = 0; b < batch;) {
     const uint32_t left = batch - b;
     const float* xb = x + (size_t)b * cols;
     float* yb = y + (size_t)b * rows;
     uint32_t nt = 0;
-    if (left >= 4u && (launch_wd<8, 1, 4>(w, xb, yb, rows, nb, ws, s, err) ||
+    if (tok_min > 0 && left >= (uint32_t)tok_min &&
+        launch_tok6_any(w, xb, yb, rows, nb, min(8u, left), ws, s, err))
+      nt = min(8u, left);
+    else if (left >= 4u && (launch_wd<8, 1, 4>(w, xb, yb, rows, nb, ws, s, err) ||
                        launch_wd<6, 1, 4>(w, xb, yb, rows, nb, ws, s, err)))
       nt = 4;
     else if (left == 3u && (launch_wd<8, 1, 3>(w, xb, yb, rows, nb, ws, s, err) ||

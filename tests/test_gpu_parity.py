@@ -579,6 +579,72 @@ def test_q6_k_matmul_many_head_shape(hip_ctx):
         log(f"  candidate {b}: worst error / bound = {worst:.4f}")
 
 
+# Q6_K candidates up to eight per pass (the vectors in the matrix-core rows,
+# K slices of four blocks summed by the reduce kernel): ragged tiles, fewer
+# vectors than eight, two passes, the down projection's K and the head.
+@pytest.mark.parametrize("rows,cols,batch", [(33, 2560, 3), (1000, 5120, 5), (100, 1024, 6),
+                                             (4096, 4096, 16), (5120, 17408, 8),
+                                             (1040, 2048, 11)])
+def test_q6_k_matmul_many_eight_per_pass(hip_ctx, rows, cols, batch):
+    log(f"q6_k matmul_many {rows}x{cols} batch={batch}")
+    w = si_hip.synth_matrix(14, seed=rows * 5 + cols + batch, rows=rows, cols=cols, threads=8)
+    X = si_hip.synth_normal(rows + 3 * batch, batch * cols).reshape(batch, cols)
+    W = hip_ctx.upload_quant_weight_private(w, 14)
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    again = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(batch):
+        _, y64, ab = O.matvec(14, w, rows, cols, X[b], threads=8)
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+        assert np.array_equal(outs[b], again[b])
+
+
+def test_q6_k_matmul_many_eight_side_rounded_and_exact_blocks(hip_ctx):
+    """Eight Q6_K candidates in one pass whose blocks differ: listed side
+    elements (a few tiny activations beside large ones), rounded blocks (more
+    than eight), subnormal and zero blocks, blocks on the exact path (huge,
+    infinite, NaN) in some vectors only, and a vector of zeros."""
+    rows, cols, batch = 300, 5120, 8
+    w = si_hip.synth_matrix(14, seed=4250, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, 14)
+    X = si_hip.synth_normal(4251, batch * cols).reshape(batch, cols).copy()
+    X[0, 256:259] = np.float32(3e-9)               # listed side elements
+    X[0, 1000] = np.float32(-1e-12)
+    X[1, 512:540] = np.float32(2e-9)               # a rounded block
+    X[1, 4096:4352:3] = np.float32(-5e-10)         # another, spread out
+    X[2, 1024:1280] = np.float32(1e-41)            # subnormal block
+    X[2, 2048:2304] = 0.0                          # zero block
+    X[3, 600:620] = np.float32(3e30)               # huge: exact path
+    X[4] = 0.0
+    X[5, 300] = np.float32(1e6)
+    X[5, 301:309] = np.float32(1e-4)               # side elements of a large block
+    X[6, 700] = np.inf
+    X[7, 1500] = np.nan
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    again = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(6):
+        _, y64, ab = O.matvec(14, w, rows, cols, X[b], threads=8)
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+        assert np.array_equal(outs[b], again[b])
+    assert not np.any(outs[4])
+    for b in (6, 7):
+        y32, _, _ = O.matvec(14, w, rows, cols, X[b], threads=8)
+        assert np.array_equal(_category(outs[b]), _category(y32)), f"candidate {b}"
+
+
+def test_q6_k_matmul_many_head_eight(hip_ctx):
+    """Eight candidates through the 151936 x 5120 Q6_K output head in one
+    pass over its 638 MB: each within the bound of the oracle."""
+    rows, cols, batch = 151936, 5120, 8
+    w = si_hip.synth_matrix(14, seed=2026, rows=rows, cols=cols, threads=8)
+    X = si_hip.synth_normal(2031, batch * cols).reshape(batch, cols)
+    W = hip_ctx.upload_quant_weight_private(w, 14)
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(batch):
+        _, y64, ab = O.matvec(14, w, rows, cols, X[b], threads=8)
+        worst = assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+        log(f"  candidate {b}: worst error / bound = {worst:.4f}")
+
+
 @pytest.mark.parametrize("types,rows,cols", [
     ((12, 12, 12), (6144, 1024, 1024), 5120),   # one launch (two-block stages)
     ((12, 12), (8192, 8192), 5120),             # one launch (four-block stages)
