@@ -753,6 +753,16 @@ __device__ __forceinline__ u32x2 q6_chunk(u32x2 ql, u32x2 qx) {
   return r;
 }
 
+// a * b + c with a, b signed 24-bit, as one v_mad_i32_i24: the empty asm
+// keeps the compiler from pairing two products of a sum into v_add3_u32
+// (three instructions for two products).  The product itself stays compiler
+// code, which orders the MFMA result reads that feed it.
+__device__ __forceinline__ int mad_i24(int a, int b, int c) {
+  int d = __mul24(a, b) + c;
+  asm("" : "+v"(d));
+  return d;
+}
+
 // Largest |scale| among the four int8 bytes of w from byte `from`.
 __device__ __forceinline__ int max_abs_i8(uint32_t w, int from = 0, int to = 4) {
   int m = 0;
@@ -951,7 +961,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
           const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(
               as_i64(A[gq][2 * (j & 1)], A[gq][2 * (j & 1) + 1]), bw, zero, 0, 0, 0);
 #pragma unroll
-          for (int d = 0; d < 4; ++d) t[gq][d] = __mul24(sc, c[d]) + t[gq][d];
+          for (int d = 0; d < 4; ++d) t[gq][d] = mad_i24(sc, c[d], t[gq][d]);
         }
       });
       const float db = b == 0 ? d0 : d1;
@@ -1244,9 +1254,13 @@ bool launch_tok6_any(const uint8_t* w, const float* x, float* y, uint32_t rows, 
   static const int w_env = env_int("SI_HIP_Q6K_TOK_WAVES", 0);
   if (nbs_env > 0) {
     const uint32_t nbs = (uint32_t)nbs_env;
-    return w_env == 8 ? launch_tok6<8>(w, x, y, rows, nb, ntok, nbs, ws, s, err)
-                      : launch_tok6<12>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+    switch (w_env) {
+      case 8: return launch_tok6<8>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+      case 16: return launch_tok6<16>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+      default: return launch_tok6<12>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+    }
   }
+  if (w_env == 16) return launch_tok6<16>(w, x, y, rows, nb, ntok, 4u, ws, s, err);
   return launch_tok6<12>(w, x, y, rows, nb, ntok, 4u, ws, s, err) ||
          launch_tok6<12>(w, x, y, rows, nb, ntok, 6u, ws, s, err) ||
          launch_tok6<8>(w, x, y, rows, nb, ntok, 10u, ws, s, err);
