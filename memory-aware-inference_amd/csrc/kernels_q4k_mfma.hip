@@ -1061,7 +1061,7 @@ __device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[
   for (int u = 0; u < 8; ++u) {
     const int s = (int)(((u < 4 ? sc03 : sc47) >> (8 * (u & 3))) & 0xffu);
 #pragma unroll
-    for (int d = 0; d < 4; ++d) t[d] = __mul24(s, c[u][d]) + t[d];
+    for (int d = 0; d < 4; ++d) t[d] = mad_i24(s, c[u][d], t[d]);
   }
   const float tc =
       fmaf(fmaf(fmaf((float)t[3], 256.0f, (float)t[2]), 256.0f, (float)t[1]), 256.0f, (float)t[0]);

@@ -167,8 +167,8 @@ __device__ __forceinline__ float block_terms(const i32x4 (&q)[4], const int (&sc
   int t[4];
 #pragma unroll
   for (int k = 0; k < 4; ++k)
-    t[k] = __mul24(sc[0], c0[k]) + __mul24(sc[1], c1[k]) + __mul24(sc[2], c2[k]) +
-           __mul24(sc[3], c3[k]);
+    t[k] = mad_i24(sc[3], c3[k],
+                   mad_i24(sc[2], c2[k], mad_i24(sc[1], c1[k], __mul24(sc[0], c0[k]))));
   const float tc =
       fmaf(fmaf(fmaf((float)t[3], 256.0f, (float)t[2]), 256.0f, (float)t[1]), 256.0f, (float)t[0]);
   return __builtin_amdgcn_ldexpf(d * tc, eb);
@@ -751,16 +751,6 @@ __device__ __forceinline__ u32x2 q6_chunk(u32x2 ql, u32x2 qx) {
     r[k] = lo | hi;
   }
   return r;
-}
-
-// a * b + c with a, b signed 24-bit, as one v_mad_i32_i24: the empty asm
-// keeps the compiler from pairing two products of a sum into v_add3_u32
-// (three instructions for two products).  The product itself stays compiler
-// code, which orders the MFMA result reads that feed it.
-__device__ __forceinline__ int mad_i24(int a, int b, int c) {
-  int d = __mul24(a, b) + c;
-  asm("" : "+v"(d));
-  return d;
 }
 
 // Largest |scale| among the four int8 bytes of w from byte `from`.

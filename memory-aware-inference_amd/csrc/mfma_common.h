@@ -139,6 +139,16 @@ constexpr uint64_t kActiveLanes = 0xF0000F0000F0000Full;
 
 __device__ __forceinline__ uint32_t uniform(uint32_t v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// a * b + c with a, b signed 24-bit, as one v_mad_i32_i24: the empty asm
+// keeps the compiler from pairing two products of a sum into v_add3_u32
+// (three instructions for two products).  The product itself stays compiler
+// code, which orders the MFMA result reads that feed it.
+__device__ __forceinline__ int mad_i24(int a, int b, int c) {
+  int d = __mul24(a, b) + c;
+  asm("" : "+v"(d));
+  return d;
+}
+
 template <int CTRL>
 __device__ __forceinline__ float dpp(float v) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xf, 0xf, true));
