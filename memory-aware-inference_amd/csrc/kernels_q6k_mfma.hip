@@ -614,8 +614,8 @@ struct Q6TokArgs {
 
 // LDS map: per-wave stage buffers, then two groups' images of nbl blocks and
 // their metadata (8 vectors); one unused ring slot.
-__host__ __device__ constexpr Layout tok6_layout(uint32_t waves, uint32_t nbl) {
-  return make_layout(kStageBytes, 2u, 32u, waves, 1u, nbl, 1u, 1u, 8u);
+__host__ __device__ constexpr Layout tok6_layout(uint32_t waves, uint32_t nbl, uint32_t depth) {
+  return make_layout(kStageBytes, 2u, 32u, waves, depth, nbl, 1u, 1u, 8u);
 }
 
 // The lane's share of a two-block stage buffer (piece p of row n at 256 p +
@@ -761,8 +761,9 @@ __device__ __forceinline__ int max_abs_i8(uint32_t w, int from = 0, int to = 4) 
 }
 
 // Up to eight vectors (vectors past ntok are zero and not stored): the
-// slice partial sums part_out[(k * 8 + v) * rows + row] of slice k.
-template <int WAVES>
+// slice partial sums part_out[(k * 8 + v) * rows + row] of slice k.  DEPTH
+// stage buffers per wave: the copies of its next DEPTH pairs in flight.
+template <int WAVES, int DEPTH>
 __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               uint32_t rows, uint32_t nb,
@@ -777,7 +778,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   const uint32_t row_bytes = nb * kQ6Bytes;
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
-  uint8_t* const wstage = smem + wave * kStageBytes;
+  uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
 
   // this workgroup's slice k (blocks blk0 .. blk0 + nbl - 1) and its tiles
   // tg, tg + GS, ...
@@ -786,7 +787,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   const uint32_t tg = blockIdx.x - k * ta.groups_per_slice;
   const uint32_t blk0 = k * ta.nbs, nbl = min(ta.nbs, nb - blk0);
   const uint32_t nst = nbl / 2u;
-  const Layout L = tok6_layout(WAVES, nbl);
+  const Layout L = tok6_layout(WAVES, nbl, DEPTH);
   const uint32_t ntw = tg < ntiles ? quo(ntiles - 1u - tg, by_gps) + 1u : 0u;
   const uint32_t my_tiles = wave < ntw ? (ntw - 1u - wave) / WAVES + 1u : 0u;
   const uint32_t my_pairs = my_tiles * nst;
@@ -794,13 +795,20 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   // 1. the vectors' blocks of the slice into the image area
   copy_x_group<WAVES>(smem, L.img, x, nb, blk0, nbl, 2u, ntok, wave, lane);
 
-  // 2. the copy of a pair's stage: local tile lt (tile tg + lt GS), stage s of
-  //    the slice.  Copy i, lane l moves piece 4 i + l / 16 of row l % 16 (the
-  //    16 lanes of the 28th piece re-read the 27th), all inside the stage's
-  //    420 bytes of their row; rows past the matrix read zero.
+  // 2. the copy of a pair's stage into buffer buf: local tile lt (tile
+  //    tg + lt GS), stage s of the slice.  Copy i, lane l moves piece
+  //    4 i + l / 16 of row l % 16 (the 16 lanes of the 28th piece re-read the
+  //    27th), all inside the stage's 420 bytes of their row; rows past the
+  //    matrix read zero.  The wave's pairs go tile by tile, a tile's stages in
+  //    order: (lti, sli) is the next pair to issue.
   const uint32_t voff = n * row_bytes + 16u * grp;
   const uint32_t voff_last = n * row_bytes + (grp < 2u ? 16u * (24u + grp) : kLastPiece);
-  auto issue = [&](uint32_t lt, uint32_t s) {
+  uint32_t lti = wave, sli = 0u;
+  auto issue = [&](uint32_t buf) {
+    const uint32_t lt = lti, s = sli;
+    uint8_t* const dst = wstage + buf * kStageBytes;
+    sli = sli + 1u == nst ? 0u : sli + 1u;
+    lti = sli == 0u ? lti + WAVES : lti;
     const uint32_t row0 = (tg + lt * ta.groups_per_slice) * 16u;
     const uint32_t nrows = min(16u, rows - row0);
     const uint32_t st = blk0 / 2u + s;
@@ -810,10 +818,16 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
         kBufferWord3);
 #pragma unroll
     for (int i = 0; i < (int)kCopies - 1; ++i)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(wstage + 1024 * i), 16,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * i), 16,
                                                 voff + 64u * i, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(wstage + 1024 * (kCopies - 1)), 16,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(dst + 1024 * (kCopies - 1)), 16,
                                               voff_last, 0, 0, 0);
+  };
+  const uint32_t early = min((uint32_t)DEPTH, my_pairs);  // the copies issued first
+  auto issue_first = [&]() {
+#pragma unroll
+    for (int d = 0; d < DEPTH; ++d)
+      if ((uint32_t)d < early) issue((uint32_t)d);
   };
 
   // 3. ring state (the builders' count), then the first copies and the group
@@ -821,14 +835,17 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   //    the barrier, the rest after; a builder converts exactly the blocks it
   //    copied)
   const bool first_round = wave < 4u;
-  if (first_round && my_pairs > 0u) issue(wave, 0u);
+  if (first_round) issue_first();
   init_slots<WAVES>(sbase, L, 1u);
   lds_wait();
   __builtin_amdgcn_s_barrier();
-  if (!first_round && my_pairs > 0u) issue(wave, 0u);
+  if (!first_round) issue_first();
   const uint32_t builders = min((uint32_t)WAVES, 2u * nbl);
   if (wave < builders) {
-    if (my_pairs > 0u)
+    // (the stage copies went out after the x copies and complete in order)
+    if (DEPTH >= 2 && early >= 2u)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(2 * kCopies));
+    else if (early >= 1u)
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies));
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
@@ -838,9 +855,9 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   }
 
   // 4. the wave's pairs
-  const uint32_t srow = sbase + wave * kStageBytes + 16u * n;
-  const uint32_t a0 = srow + 256u * (grp >> 1) + 8u * (grp & 1u);
-  const uint32_t a2 = a0 + 3328u + ((grp & 1u) ? 248u : 8u);
+  const uint32_t srow0 = sbase + wave * DEPTH * kStageBytes + 16u * n;
+  const uint32_t a00 = srow0 + 256u * (grp >> 1) + 8u * (grp & 1u);
+  const uint32_t a20 = a00 + 3328u + ((grp & 1u) ? 248u : 8u);
   // the A lane (k, i) = (grp, n): digit n % 4 of vector 2 q + n / 8 of a group
   const uint32_t ibase = sbase + L.img + 256u * grp + 64u * (n >> 3) + 16u * (n & 3u);
   const uint32_t gstride = 4096u * nbl;
@@ -857,9 +874,15 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   uint32_t lt = wave, sl = 0u;
   uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
   for (uint32_t p = 0; p < my_pairs; ++p) {
-    __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    // pair p's stage in buffer p % DEPTH, the copies of later pairs still out
+    const uint32_t buf = DEPTH == 1 ? 0u : p % (uint32_t)DEPTH;
+    if (DEPTH >= 2 && p + 1u < my_pairs)
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies));
+    else
+      __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
+    const uint32_t srow = srow0 + buf * kStageBytes;
     Stage6 sv;
-    lds_read_stage6(a0, a2, srow, sv);
+    lds_read_stage6(a00 + buf * kStageBytes, a20 + buf * kStageBytes, srow, sv);
     if (p == 0u) wait_images(sbase, L, builders, fail);
     uint32_t m[4];
 #pragma unroll
@@ -896,11 +919,10 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
       }
     }
 
-    // the next pair's copy: the stage is in registers
+    // the copy of pair p + DEPTH into the buffer just read: the stage is in
+    // registers
     const bool last_stage = sl + 1u == nst;
-    const uint32_t lt_next = last_stage ? lt + WAVES : lt;
-    const uint32_t sl_next = last_stage ? 0u : sl + 1u;
-    if (p + 1u < my_pairs) issue(lt_next, sl_next);
+    if (p + DEPTH < my_pairs) issue(buf);
 
     // the two blocks: per chunk four MFMAs and the integer scale combine
     float absp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -930,28 +952,44 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
       for (int gq = 0; gq < 4; ++gq)
 #pragma unroll
         for (int d = 0; d < 4; ++d) t[gq][d] = 0;
-      static_for<8>([&](auto jc) {
+      // software-pipelined: chunk j's four MFMAs go out before chunk j - 1's
+      // products are added, so that no MFMA result is read right after its
+      // MFMA
+      i32x4 cp[4];
+      int scp = 0;
+      static_for<9>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        constexpr int h = j >> 2, tt = j & 3;
-        if constexpr ((j & 1) == 0) lds_read_tok6_images<j / 2>(i0, i1, A);
-        const u32x2 wq = q6_chunk<tt>(ql[2 * h + (tt & 1)], qx[h]);
-        // scale 2 j + hs: block 0 byte 2 j + hs of its 16; block 1 byte 2 + 2 j + hs of
-        // piece 25 (j < 7) or byte hs of the tail word (j = 7)
-        int sc;
-        if constexpr (b == 0)
-          sc = scale_at(sv.sc0[j >> 1], (j & 1) ? o_hi : o_lo);
-        else if constexpr (j == 7)
-          sc = scale_at(sv.tail1, o_lo);
-        else
-          sc = scale_at(sv.sc1[(j + 1) >> 1], (j & 1) ? o_lo : o_hi);
-        const int64_t bw = as_i64(wq[0], wq[1]);
-        const i32x4 zero = {0, 0, 0, 0};
+        i32x4 c[4];
+        int sc = 0;
+        if constexpr (j < 8) {
+          constexpr int h = j >> 2, tt = j & 3;
+          if constexpr ((j & 1) == 0) lds_read_tok6_images<j / 2>(i0, i1, A);
+          const u32x2 wq = q6_chunk<tt>(ql[2 * h + (tt & 1)], qx[h]);
+          // scale 2 j + hs: block 0 byte 2 j + hs of its 16; block 1 byte
+          // 2 + 2 j + hs of piece 25 (j < 7) or byte hs of the tail word (j = 7)
+          if constexpr (b == 0)
+            sc = scale_at(sv.sc0[j >> 1], (j & 1) ? o_hi : o_lo);
+          else if constexpr (j == 7)
+            sc = scale_at(sv.tail1, o_lo);
+          else
+            sc = scale_at(sv.sc1[(j + 1) >> 1], (j & 1) ? o_lo : o_hi);
+          const int64_t bw = as_i64(wq[0], wq[1]);
+          const i32x4 zero = {0, 0, 0, 0};
 #pragma unroll
-        for (int gq = 0; gq < 4; ++gq) {
-          const i32x4 c = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-              as_i64(A[gq][2 * (j & 1)], A[gq][2 * (j & 1) + 1]), bw, zero, 0, 0, 0);
+          for (int gq = 0; gq < 4; ++gq)
+            c[gq] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
+                as_i64(A[gq][2 * (j & 1)], A[gq][2 * (j & 1) + 1]), bw, zero, 0, 0, 0);
+        }
+        if constexpr (j > 0) {
 #pragma unroll
-          for (int d = 0; d < 4; ++d) t[gq][d] = mad_i24(sc, c[d], t[gq][d]);
+          for (int gq = 0; gq < 4; ++gq)
+#pragma unroll
+            for (int d = 0; d < 4; ++d) t[gq][d] = mad_i24(scp, cp[gq][d], t[gq][d]);
+        }
+        if constexpr (j < 8) {
+#pragma unroll
+          for (int gq = 0; gq < 4; ++gq) cp[gq] = c[gq];
+          scp = sc;
         }
       });
       const float db = b == 0 ? d0 : d1;
@@ -1022,8 +1060,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
       for (int gq = 0; gq < 4; ++gq) part[gq] = 0.0f;
       redo = 0u;
     }
-    lt = lt_next;
-    sl = sl_next;
+    sl = last_stage ? 0u : sl + 1u;
+    lt = last_stage ? lt + WAVES : lt;
   }
   if (fail != 0u) report_device_error(ta.wsp, fail);
 }
@@ -1196,7 +1234,7 @@ bool launch_pairs(const uint8_t* w, const float* x, float* y, uint32_t rows, uin
 // Up to eight vectors in one pass over the weights: q6k_tokens_mfma in K
 // slices of nbs blocks, then tok_reduce.  false when the shape does not fit
 // (q6_shape_ok, the slices' partial sums within the scratch, the LDS).
-template <int W>
+template <int W, int D>
 bool launch_tok6(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                  uint32_t ntok, uint32_t nbs, const Workspace& ws, hipStream_t s,
                  hipError_t* err) {
@@ -1215,16 +1253,16 @@ bool launch_tok6(const uint8_t* w, const float* x, float* y, uint32_t rows, uint
   if ((uint64_t)(grid + ntiles) * ta.groups_per_slice >= (1ull << 32)) return false;
   ta.m_gps = div_magic(ta.groups_per_slice);
   ta.wsp = ws.ptr;
-  const uint32_t lds = tok6_layout(W, ta.nbs).total;
+  const uint32_t lds = tok6_layout(W, ta.nbs, D).total;
   if (lds > kLdsBytes) return false;
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&q6k_tokens_mfma<W>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&q6k_tokens_mfma<W, D>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL(q6k_tokens_mfma<W>, dim3(grid), dim3(W * 64), lds, s, w, x, rows, nb, ntok,
+  hipLaunchKernelGGL((q6k_tokens_mfma<W, D>), dim3(grid), dim3(W * 64), lds, s, w, x, rows, nb, ntok,
                      ws.scratch, ta);
   *err = hipGetLastError();
   if (*err == hipSuccess) {
@@ -1242,18 +1280,17 @@ bool launch_tok6_any(const uint8_t* w, const float* x, float* y, uint32_t rows, 
                      uint32_t ntok, const Workspace& ws, hipStream_t s, hipError_t* err) {
   static const int nbs_env = env_int("SI_HIP_Q6K_TOK_NBS", 0);
   static const int w_env = env_int("SI_HIP_Q6K_TOK_WAVES", 0);
-  if (nbs_env > 0) {
-    const uint32_t nbs = (uint32_t)nbs_env;
+  if (nbs_env > 0 || w_env > 0) {
+    const uint32_t nbs = nbs_env > 0 ? (uint32_t)nbs_env : 4u;
     switch (w_env) {
-      case 8: return launch_tok6<8>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
-      case 16: return launch_tok6<16>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
-      default: return launch_tok6<12>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+      case 8: return launch_tok6<8, 1>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+      case 82: return launch_tok6<8, 2>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+      default: return launch_tok6<12, 1>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
     }
   }
-  if (w_env == 16) return launch_tok6<16>(w, x, y, rows, nb, ntok, 4u, ws, s, err);
-  return launch_tok6<12>(w, x, y, rows, nb, ntok, 4u, ws, s, err) ||
-         launch_tok6<12>(w, x, y, rows, nb, ntok, 6u, ws, s, err) ||
-         launch_tok6<8>(w, x, y, rows, nb, ntok, 10u, ws, s, err);
+  return launch_tok6<12, 1>(w, x, y, rows, nb, ntok, 4u, ws, s, err) ||
+         launch_tok6<12, 1>(w, x, y, rows, nb, ntok, 6u, ws, s, err) ||
+         launch_tok6<8, 1>(w, x, y, rows, nb, ntok, 10u, ws, s, err);
 }
 }  // namespace
 
