@@ -609,7 +609,9 @@ constexpr uint64_t kTokActiveLanes = 0xF0F0F0F00F0F0F0Full;  // lane (k, i): k /
 
 struct Q6TokArgs {
   uint32_t slices, groups_per_slice, m_gps, nbs;
-  void* wsp;  // the workspace, for failure reports
+  uint32_t m_slices;  // XCD-grouped launches: the division constant of the slice count
+  uint32_t xcd;       // 1: the slices of a tile group share an XCD (GS a multiple of 8)
+  void* wsp;          // the workspace, for failure reports
 };
 
 // LDS map: per-wave stage buffers, then two groups' images of nbl blocks and
@@ -781,10 +783,21 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   uint8_t* const wstage = smem + wave * DEPTH * kStageBytes;
 
   // this workgroup's slice k (blocks blk0 .. blk0 + nbl - 1) and its tiles
-  // tg, tg + GS, ...
+  // tg, tg + GS, ...  Workgroups go to the eight XCDs round robin (workgroup
+  // b to XCD b % 8); XCD-grouped, the S workgroups of a tile group are
+  // b = 8 (S i + k) + x for tile group 8 i + x, so they share that XCD's L2,
+  // where a row's line that two slices' runs share is then read once.
   const FastDiv by_gps{ta.groups_per_slice, ta.m_gps};
-  const uint32_t k = quo(blockIdx.x, by_gps);
-  const uint32_t tg = blockIdx.x - k * ta.groups_per_slice;
+  uint32_t k, tg;
+  if (ta.xcd != 0u) {
+    const uint32_t i = blockIdx.x >> 3;
+    const uint32_t q = quo(i, FastDiv{ta.slices, ta.m_slices});
+    k = i - q * ta.slices;
+    tg = 8u * q + (blockIdx.x & 7u);
+  } else {
+    k = quo(blockIdx.x, by_gps);
+    tg = blockIdx.x - k * ta.groups_per_slice;
+  }
   const uint32_t blk0 = k * ta.nbs, nbl = min(ta.nbs, nb - blk0);
   const uint32_t nst = nbl / 2u;
   const Layout L = tok6_layout(WAVES, nbl, DEPTH);
@@ -1248,6 +1261,19 @@ bool launch_tok6(const uint8_t* w, const float* x, float* y, uint32_t rows, uint
   if (ta.slices > cus || (size_t)ta.slices * 8u * rows * sizeof(float) > ws.scratch_bytes)
     return false;
   ta.groups_per_slice = min(cus / ta.slices, ntiles);
+  // XCD-grouped on request (SI_HIP_Q6K_TOK_XCD=1), when a multiple of 8 groups
+  // per slice keeps nearly every CU busy (S = 2 on 256 CUs: all of them).  On
+  // the head it cuts the L2 fills from 1.18 to 1.10 (four-block slices) or
+  // 1.065 (ten-block slices) of the weight bytes but costs 4 us at M = 8, so
+  // it is off by default.
+  static const int xcd_env = env_int("SI_HIP_Q6K_TOK_XCD", 0);
+  const uint32_t gs8 = ta.groups_per_slice & ~7u;
+  if (xcd_env != 0 && ta.slices > 1u && gs8 >= 8u &&
+      (uint64_t)gs8 * ta.slices * 16u >= (uint64_t)cus * 15u) {
+    ta.groups_per_slice = gs8;
+    ta.xcd = 1u;
+    ta.m_slices = div_magic(ta.slices);
+  }
   const uint32_t grid = ta.groups_per_slice * ta.slices;
   // block and tile indices divided by GS
   if ((uint64_t)(grid + ntiles) * ta.groups_per_slice >= (1ull << 32)) return false;
