@@ -483,6 +483,24 @@ def _config_many(ctx, lib, upload, dev_f32, bpc, steps, warmup, N, K) -> dict:
     for w in ws:
         w.free()
     ctx.device_free(X); ctx.device_free(Y)
+    # the same verify on Q5_K 5120x5120 (BASELINE config 3's matrix)
+    Q5, N5, K5 = si_hip.GGML_TYPE_Q5_K, 5120, 5120
+    n5 = copies_for(bpc(Q5, N5, K5))
+    w5 = [upload(Q5, 520 + c, N5, K5) for c in range(n5)]
+    X5 = dev_f32(si_hip.synth_normal(521, 16 * K5))
+    Y5 = ctx.device_alloc(16 * N5 * 4)
+    many5 = {}
+    for m in (1, 4, 8, 16):
+        ms = _timed(ctx, lambda i, m=m: si_hip._check(lib.si_hip_matmul_many_device(
+            ctx.handle, w5[i % n5].handle, N5, K5, m, C.c_void_p(X5), C.c_void_p(Y5))), steps, warmup)
+        r = _rate(bpc(Q5, N5, K5), ms)
+        r["tflop_per_s"] = round(2.0 * m * N5 * K5 / (ms * 1e-3) / 1e12, 3)
+        many5[f"M{m}"] = r
+    many5.update(residency(bpc(Q5, N5, K5), n5))
+    res["matmul_many_q5k_5120x5120"] = many5
+    for w in w5:
+        w.free()
+    ctx.device_free(X5); ctx.device_free(Y5)
     # grouped matvec over one x (q/k/v-like projections): one launch against
     # one launch per matrix
     g_rows = (6144, 1024, 1024)

@@ -976,8 +976,8 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
 
 // Headers and the lane's four 8-byte qs slices of the four blocks of a stage
 // buffer: header of block b at hb + 2304 b, slice j at qb + 2304 b + 512 j.
-__device__ __forceinline__ void lds_read_weights_tok(uint32_t hb, uint32_t qb, u32x4 (&h)[4],
-                                                     u32x2 (&q)[16]) {
+__device__ __forceinline__ void lds_read_weights_tok4(uint32_t hb, uint32_t qb, u32x4 (&h)[4],
+                                                      u32x2 (&q)[16]) {
   asm volatile(
       "ds_read_b128 %0, %20\n"
       "ds_read_b64 %4, %21\n"
@@ -1008,6 +1008,68 @@ __device__ __forceinline__ void lds_read_weights_tok(uint32_t hb, uint32_t qb, u
       : "memory");
 }
 
+// Q5_K (176-byte blocks: header, qh at +16, qs at +48): the same for a stage
+// buffer of Q5_K blocks -- header of block b at hb + 2816 b, qs slice j at
+// qb + 2816 b + 512 j -- and the lane's 8-byte qh slice of each block (the qh
+// bytes of its elements 8 g .. 8 g + 7, bit u for unit u) at qhb + 2816 b.
+__device__ __forceinline__ void lds_read_weights_tok5(uint32_t hb, uint32_t qb, uint32_t qhb,
+                                                      u32x4 (&h)[4], u32x2 (&q)[16],
+                                                      u32x2 (&qh)[4]) {
+  asm volatile(
+      "ds_read_b128 %0, %24\n"
+      "ds_read_b64 %4, %25\n"
+      "ds_read_b64 %5, %25 offset:512\n"
+      "ds_read_b64 %6, %25 offset:1024\n"
+      "ds_read_b64 %7, %25 offset:1536\n"
+      "ds_read_b64 %20, %26\n"
+      "ds_read_b128 %1, %24 offset:2816\n"
+      "ds_read_b64 %8, %25 offset:2816\n"
+      "ds_read_b64 %9, %25 offset:3328\n"
+      "ds_read_b64 %10, %25 offset:3840\n"
+      "ds_read_b64 %11, %25 offset:4352\n"
+      "ds_read_b64 %21, %26 offset:2816\n"
+      "ds_read_b128 %2, %24 offset:5632\n"
+      "ds_read_b64 %12, %25 offset:5632\n"
+      "ds_read_b64 %13, %25 offset:6144\n"
+      "ds_read_b64 %14, %25 offset:6656\n"
+      "ds_read_b64 %15, %25 offset:7168\n"
+      "ds_read_b64 %22, %26 offset:5632\n"
+      "ds_read_b128 %3, %24 offset:8448\n"
+      "ds_read_b64 %16, %25 offset:8448\n"
+      "ds_read_b64 %17, %25 offset:8960\n"
+      "ds_read_b64 %18, %25 offset:9472\n"
+      "ds_read_b64 %19, %25 offset:9984\n"
+      "ds_read_b64 %23, %26 offset:8448\n"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(h[0]), "=&v"(h[1]), "=&v"(h[2]), "=&v"(h[3]), "=&v"(q[0]), "=&v"(q[1]),
+        "=&v"(q[2]), "=&v"(q[3]), "=&v"(q[4]), "=&v"(q[5]), "=&v"(q[6]), "=&v"(q[7]),
+        "=&v"(q[8]), "=&v"(q[9]), "=&v"(q[10]), "=&v"(q[11]), "=&v"(q[12]), "=&v"(q[13]),
+        "=&v"(q[14]), "=&v"(q[15]), "=&v"(qh[0]), "=&v"(qh[1]), "=&v"(qh[2]), "=&v"(qh[3])
+      : "v"(hb), "v"(qb), "v"(qhb)
+      : "memory");
+}
+
+// The stage of a vectors-in-rows pass in registers: per block its header,
+// the lane's four 8-byte qs slices and (Q5_K) its qh slice.
+template <int QB>
+struct TokStage {
+  u32x4 h[4];
+  u32x2 q[16];
+  u32x2 qh[QB == 5 ? 4 : 1];
+};
+// The lane's stage addresses: header (hb0), qs slices (qb0) and qh slice
+// (qhb0, Q5_K) of the stage's first block.
+struct TokAddr {
+  uint32_t hb0, qb0, qhb0;
+};
+template <int QB>
+__device__ __forceinline__ void lds_read_weights_tok(const TokAddr& a, TokStage<QB>& st) {
+  if constexpr (QB == 5)
+    lds_read_weights_tok5(a.hb0, a.qb0, a.qhb0, st.h, st.q, st.qh);
+  else
+    lds_read_weights_tok4(a.hb0, a.qb0, st.h, st.q);
+}
+
 // The lane's group-image quarters of one block (unit pairs 0..3) and its
 // vector's eight unit sums.
 __device__ __forceinline__ void lds_read_group_block(uint32_t ia, uint32_t xa, u32x4 (&a)[4],
@@ -1026,18 +1088,29 @@ __device__ __forceinline__ void lds_read_group_block(uint32_t ia, uint32_t xa, u
 }
 
 // The eight MFMAs of one block of row n against the lane's vector: c[u] the
-// four digit sums of unit u.
-__device__ __forceinline__ void block_mfma_tok(const u32x2 (&q)[16], int b, const u32x4 (&a)[4],
-                                               i32x4 (&c)[8]) {
+// four digit sums of unit u.  Q5_K: bit u of each qh byte is the weight's
+// fifth bit (rotated to bit 4: v_alignbit of a word with itself).
+template <int QB>
+__device__ __forceinline__ void block_mfma_tok(const TokStage<QB>& st, int b,
+                                               const u32x4 (&a)[4], i32x4 (&c)[8]) {
   const i32x4 zero = {0, 0, 0, 0};
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
-    const u32x2 w = q[4 * b + j];
-    c[2 * j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-        as_i64(a[j][0], a[j][1]), as_i64(w[0] & 0x0f0f0f0fu, w[1] & 0x0f0f0f0fu), zero, 0, 0, 0);
-    c[2 * j + 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-        as_i64(a[j][2], a[j][3]),
-        as_i64((w[0] >> 4) & 0x0f0f0f0fu, (w[1] >> 4) & 0x0f0f0f0fu), zero, 0, 0, 0);
+    const u32x2 w = st.q[4 * b + j];
+    uint32_t lo0 = w[0] & 0x0f0f0f0fu, lo1 = w[1] & 0x0f0f0f0fu;
+    uint32_t hi0 = (w[0] >> 4) & 0x0f0f0f0fu, hi1 = (w[1] >> 4) & 0x0f0f0f0fu;
+    if constexpr (QB == 5) {
+      const u32x2 qh = st.qh[b];
+      const uint32_t rl = (2u * j + 28u) & 31u, rh = (2u * j + 29u) & 31u;  // bit u -> bit 4
+      lo0 |= __builtin_amdgcn_alignbit(qh[0], qh[0], rl) & 0x10101010u;
+      lo1 |= __builtin_amdgcn_alignbit(qh[1], qh[1], rl) & 0x10101010u;
+      hi0 |= __builtin_amdgcn_alignbit(qh[0], qh[0], rh) & 0x10101010u;
+      hi1 |= __builtin_amdgcn_alignbit(qh[1], qh[1], rh) & 0x10101010u;
+    }
+    c[2 * j] = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_i64(a[j][0], a[j][1]), as_i64(lo0, lo1),
+                                                     zero, 0, 0, 0);
+    c[2 * j + 1] = __builtin_amdgcn_mfma_i32_16x16x32_i8(as_i64(a[j][2], a[j][3]),
+                                                         as_i64(hi0, hi1), zero, 0, 0, 0);
   }
 }
 
@@ -1047,15 +1120,17 @@ __device__ __forceinline__ void block_mfma_tok(const u32x2 (&q)[16], int b, cons
 // eight-term um is summed in pairs (within 5 * 2^-24 sum_u m_u |X_u| with the
 // sums' own rounding), so as in block_dot 2^-21 of the two terms' magnitudes
 // covers the whole.
-__device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[16], int b,
+template <int QB>
+__device__ __forceinline__ float block_dot_tok(const TokStage<QB>& st, int b,
                                                const u32x4 (&a)[4], const u32x4 (&xs)[2], int eb,
                                                float& err) {
+  const u32x4 h = st.h[b];
   const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
   const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
   const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
   const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
   i32x4 c[8];
-  block_mfma_tok(q, b, a, c);
+  block_mfma_tok<QB>(st, b, a, c);
   int t[4] = {0, 0, 0, 0};
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
@@ -1091,15 +1166,17 @@ __device__ __forceinline__ float block_dot_tok(const u32x4& h, const u32x2 (&q)[
 // left is that of the f32 unit sums xs (2^-24 each) and the f64 steps, so
 // err = 2^(eb-24) 1.01 |dmin| sum_u m_u |xs_u| + 2^(eb-48) of the two terms,
 // about an eighth of the fast path's bound.
-__device__ __forceinline__ double block_dot_tok_f64(const u32x4& h, const u32x2 (&q)[16], int b,
+template <int QB>
+__device__ __forceinline__ double block_dot_tok_f64(const TokStage<QB>& st, int b,
                                                     const u32x4 (&a)[4], const u32x4 (&xs)[2],
                                                     int eb, float& err) {
+  const u32x4 h = st.h[b];
   const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
   const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
   const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
   const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
   i32x4 c[8];
-  block_mfma_tok(q, b, a, c);
+  block_mfma_tok<QB>(st, b, a, c);
   double tc = 0.0, um = 0.0, ua = 0.0;
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
@@ -1122,11 +1199,15 @@ __device__ __forceinline__ double block_dot_tok_f64(const u32x4& h, const u32x2 
 }
 
 // Exact per-weight path of one block of row n against 256 activations: the
-// block's 144 bytes at byte `off` of the buffer `wr` (read from memory: by
-// then the stage buffer may hold the next stage; bytes past the buffer's end,
-// those of rows past the matrix, read as zero).
+// block's 144 (Q4_K) or 176 (Q5_K) bytes at byte `off` of the buffer `wr`
+// (read from memory: by then the stage buffer may hold the next stage; bytes
+// past the buffer's end, those of rows past the matrix, read as zero).
+__device__ __forceinline__ float block_exact_row5(__amdgpu_buffer_rsrc_t wr, uint32_t off,
+                                                  const float* __restrict__ xs);
+template <int QB>
 __device__ __forceinline__ float block_exact_row(__amdgpu_buffer_rsrc_t wr, uint32_t off,
                                                  const float* __restrict__ xs) {
+  if constexpr (QB == 5) return block_exact_row5(wr, off, xs);
   auto ld = [&](uint32_t o) {
     return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off + o, 0, 0));
   };
@@ -1158,6 +1239,47 @@ __device__ __forceinline__ float block_exact_row(__amdgpu_buffer_rsrc_t wr, uint
   return acc;
 }
 
+// Q5_K: unit u of the block is the low (even u) or high nibbles of qs bytes
+// 32 (u / 2) .. + 31 (at 48) with bit u of qh bytes 0 .. 31 (at 16) as the
+// fifth bit (quant.rs:67-125); the same order as the Q4_K form.
+__device__ __forceinline__ float block_exact_row5(__amdgpu_buffer_rsrc_t wr, uint32_t off,
+                                                  const float* __restrict__ xs) {
+  auto ld = [&](uint32_t o) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(wr, off + o, 0, 0));
+  };
+  const u32x4 h = ld(0u);
+  const u32x4 qh[2] = {ld(16u), ld(32u)};
+  u32x4 qs[8];
+#pragma unroll
+  for (int k = 0; k < 8; ++k) qs[k] = ld(48u + 16u * k);
+  const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
+  const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
+  const uint32_t sc47 = (h[3] & 0x0f0f0f0fu) | ((h[1] >> 2) & 0x30303030u);
+  const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
+  const float d = half_bits_to_float(h[0] & 0xffffu);
+  const float dmin = half_bits_to_float(h[0] >> 16);
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const uint32_t sc = ((u < 4 ? sc03 : sc47) >> (8 * (u & 3))) & 0xffu;
+    const uint32_t mn = ((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu;
+    const float d1 = __fmul_rn(d, (float)sc), m1 = __fmul_rn(dmin, (float)mn);
+    const int shift = 4 * (u & 1);
+    const int k = u & ~1;
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const u32x4 q = qs[k + half], hbits = qh[half];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t wq = ((q[j >> 2] >> (8 * (j & 3) + shift)) & 0x0fu) |
+                            (((hbits[j >> 2] >> (8 * (j & 3) + u)) & 1u) << 4);
+        acc = fmaf(k4_value_exact(d1, m1, wq), xs[32 * u + 16 * half + j], acc);
+      }
+    }
+  }
+  return acc;
+}
+
 // Launch constants: the slice count S (1: whole rows), GS workgroups per
 // slice (all of them when S == 1), the ring's slot count, and the division
 // constants of GS, of the stages per tile and of the slot count.
@@ -1170,9 +1292,10 @@ struct TokArgs {
 // LDS map: per-wave stage buffers; the images of ng groups of nbl blocks
 // (4 ng vectors), their unit sums and exponents; the slot ring (unused with
 // K slices).
+template <int QB>
 __host__ __device__ constexpr Layout tok_layout(uint32_t waves, uint32_t nbl, uint32_t ng,
                                                 uint32_t slots) {
-  return make_layout(stage_bytes(4), 4u, 32u, waves, 1u, nbl, slots, 1u, 4u * ng);
+  return make_layout(stage_bytes(QB), 4u, 32u, waves, 1u, nbl, slots, 1u, 4u * ng);
 }
 
 // One vector group's sum over the live blocks of a stage (the weights in h,
@@ -1180,10 +1303,10 @@ __host__ __device__ constexpr Layout tok_layout(uint32_t waves, uint32_t nbl, ui
 // path count zero here.  iabase/xabase/eabase: the group's images, the
 // vector's unit sums and exponents at the stage's first block.  abs_part and
 // err get the lane's sum of |block dot| and the bound on their rounding.
-__device__ __forceinline__ float tok_group_stage(const u32x4 (&h)[4], const u32x2 (&q)[16],
-                                                 uint32_t nlive, uint32_t iabase,
-                                                 uint32_t xabase, uint32_t eabase,
-                                                 float& abs_part, float& err) {
+template <int QB>
+__device__ __forceinline__ float tok_group_stage(const TokStage<QB>& st, uint32_t nlive,
+                                                 uint32_t iabase, uint32_t xabase,
+                                                 uint32_t eabase, float& abs_part, float& err) {
   i32x4 ex;
   asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(ex) : "v"(eabase) : "memory");
   float part = 0.0f;
@@ -1195,7 +1318,7 @@ __device__ __forceinline__ float tok_group_stage(const u32x4 (&h)[4], const u32x
       u32x4 a[4], xs[2];
       lds_read_group_block(iabase + 4096u * b, xabase + 32u * b, a, xs);
       float e;
-      const float v = block_dot_tok(h[b], q, b, a, xs, ex[b], e);
+      const float v = block_dot_tok<QB>(st, b, a, xs, ex[b], e);
       const bool fast = ex[b] != kBadBlock;
       const float c = fast ? v : 0.0f;
       part += c;
@@ -1208,18 +1331,17 @@ __device__ __forceinline__ float tok_group_stage(const u32x4 (&h)[4], const u32x
 
 // tok_group_stage with block_dot_tok_f64: the sum in f64, with abs_part and
 // err (the bound on its rounding) as there.  Not inlined, and reading the
-// stage again from its LDS buffer (hb0, qb0: the lane's addresses there), so
-// that its registers are taken on this rare path only.
+// stage again from its LDS buffer (ta: the lane's addresses there), so that
+// its registers are taken on this rare path only.
 struct StageF64 {
   double part;
   float abs_part, err;
 };
-__device__ __noinline__ StageF64 tok_group_stage_f64(uint32_t hb0, uint32_t qb0, uint32_t nlive,
-                                                     uint32_t iabase, uint32_t xabase,
-                                                     uint32_t eabase) {
-  u32x4 h[4];
-  u32x2 q[16];
-  lds_read_weights_tok(hb0, qb0, h, q);
+template <int QB>
+__device__ __noinline__ StageF64 tok_group_stage_f64(TokAddr ta, uint32_t nlive, uint32_t iabase,
+                                                     uint32_t xabase, uint32_t eabase) {
+  TokStage<QB> st;
+  lds_read_weights_tok<QB>(ta, st);
   float abs_part, err;
   i32x4 ex;
   asm volatile("ds_read_b128 %0, %1\ns_waitcnt lgkmcnt(0)" : "=&v"(ex) : "v"(eabase) : "memory");
@@ -1232,7 +1354,7 @@ __device__ __noinline__ StageF64 tok_group_stage_f64(uint32_t hb0, uint32_t qb0,
       u32x4 a[4], xs[2];
       lds_read_group_block(iabase + 4096u * b, xabase + 32u * b, a, xs);
       float e;
-      const double v = block_dot_tok_f64(h[b], q, b, a, xs, ex[b], e);
+      const double v = block_dot_tok_f64<QB>(st, b, a, xs, ex[b], e);
       const bool fast = ex[b] != kBadBlock;
       const double c = fast ? v : 0.0;
       part += c;
@@ -1248,13 +1370,13 @@ __device__ __noinline__ StageF64 tok_group_stage_f64(uint32_t hb0, uint32_t qb0,
 // counts of the group's first vector at the stage's first block; the other
 // vectors follow at side_stride).  For an entry (i, x_i) of
 // vector r's block b, the lanes of group (i & 31) / 8 hold the qs byte of
-// element i for their rows (slice (i / 32) / 2 of the block); lane group r
-// takes w_i from them and adds w_i x_i.
-template <int B>
+// element i for their rows (slice (i / 32) / 2 of the block; Q5_K: and the
+// qh byte of element i % 32 in their qh slice qh); lane group r takes w_i
+// from them and adds w_i x_i.
+template <int B, int QB>
 __device__ __forceinline__ float tok_side_block(u32x4 h, u32x2 s0, u32x2 s1, u32x2 s2, u32x2 s3,
-                                                uint32_t list,
-                                                uint32_t counts, uint32_t r, uint32_t lane,
-                                                float part) {
+                                                u32x2 qh, uint32_t list, uint32_t counts,
+                                                uint32_t r, uint32_t lane, float part) {
   const uint32_t grp = lane >> 4, n = lane & 15u;
   uint32_t c = (counts >> (8 * B)) & 0xffu;
   if (c == kSideRounded) c = 0u;
@@ -1265,14 +1387,21 @@ __device__ __forceinline__ float tok_side_block(u32x4 h, u32x2 s0, u32x2 s1, u32
     const uint32_t u = i >> 5, l = i & 31u, j = u >> 1;
     const u32x2 sl = j == 0u ? s0 : j == 1u ? s1 : j == 2u ? s2 : s3;
     const uint32_t byte = (((l & 4u) ? sl[1] : sl[0]) >> (8u * (l & 3u))) & 0xffu;
-    const float wv = k4_weight(h, u, (byte >> (4u * (u & 1u))) & 0x0fu);
+    uint32_t qv = (byte >> (4u * (u & 1u))) & 0x0fu;
+    if constexpr (QB == 5) {
+      const uint32_t hb = (((l & 4u) ? qh[1] : qh[0]) >> (8u * (l & 3u))) & 0xffu;
+      qv |= ((hb >> u) & 1u) << 4;
+    }
+    const float wv = k4_weight(h, u, qv);
     const float wr = __int_as_float(
         __builtin_amdgcn_ds_bpermute((int)(4u * (16u * (l >> 3) + n)), __float_as_int(wv)));
     if (grp == r) part = fmaf(wr, xi, part);
   }
   return part;
 }
-// Largest |w| of a Q4_K block (all eight units) from its header.
+// Largest |w| of a Q4_K (QMAX 15) or Q5_K (QMAX 31) block (all eight units)
+// from its header.
+template <int QMAX>
 __device__ __forceinline__ float k4_block_bound(const u32x4& h) {
   const uint32_t sc03 = h[1] & 0x3f3f3f3fu;
   const uint32_t mn03 = h[2] & 0x3f3f3f3fu;
@@ -1285,7 +1414,7 @@ __device__ __forceinline__ float k4_block_bound(const u32x4& h) {
   for (int u = 0; u < 8; ++u) {
     const uint32_t sc = ((u < 4 ? sc03 : sc47) >> (8 * (u & 3))) & 0xffu;
     const uint32_t mn = ((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu;
-    mx = fmaxf(mx, fmaf(ad, (float)(15u * sc), am * (float)mn));
+    mx = fmaxf(mx, fmaf(ad, (float)((uint32_t)QMAX * sc), am * (float)mn));
   }
   return mx;
 }
@@ -1295,9 +1424,12 @@ __device__ __forceinline__ float k4_block_bound(const u32x4& h) {
 // side areas and counts of the group's first vector at the stage's first
 // block (the other vectors at side_stride); `mine`: the lane's
 // vector's counts.
-__device__ __forceinline__ float tok_listed(const u32x4 (&h)[4], const u32x2 (&q)[16],
-                                            uint32_t list0, uint32_t mine, uint32_t side_stride,
-                                            uint32_t lane) {
+template <int QB>
+__device__ __forceinline__ float tok_listed(const TokStage<QB>& st, uint32_t list0, uint32_t mine,
+                                            uint32_t side_stride, uint32_t lane) {
+  const u32x4(&h)[4] = st.h;
+  const u32x2(&q)[16] = st.q;
+  auto qh = [&](int b) { return QB == 5 ? st.qh[QB == 5 ? b : 0] : u32x2{0u, 0u}; };
   float part = 0.0f;
   if (__builtin_amdgcn_ballot_w64((mine & ~(rounded_mask(mine) * 0xffu)) != 0u) == 0u)
     return part;
@@ -1306,10 +1438,14 @@ __device__ __forceinline__ float tok_listed(const u32x4 (&h)[4], const u32x2 (&q
     const uint32_t counts = __builtin_amdgcn_readlane(mine, 16 * r);
     if (counts == 0u) continue;
     const uint32_t list = list0 + r * side_stride;
-    part = tok_side_block<0>(h[0], q[0], q[1], q[2], q[3], list, counts, r, lane, part);
-    part = tok_side_block<1>(h[1], q[4], q[5], q[6], q[7], list, counts, r, lane, part);
-    part = tok_side_block<2>(h[2], q[8], q[9], q[10], q[11], list, counts, r, lane, part);
-    part = tok_side_block<3>(h[3], q[12], q[13], q[14], q[15], list, counts, r, lane, part);
+    part = tok_side_block<0, QB>(h[0], q[0], q[1], q[2], q[3], qh(0), list, counts, r, lane,
+                                 part);
+    part = tok_side_block<1, QB>(h[1], q[4], q[5], q[6], q[7], qh(1), list, counts, r, lane,
+                                 part);
+    part = tok_side_block<2, QB>(h[2], q[8], q[9], q[10], q[11], qh(2), list, counts, r, lane,
+                                 part);
+    part = tok_side_block<3, QB>(h[3], q[12], q[13], q[14], q[15], qh(3), list, counts, r, lane,
+                                 part);
   }
   return part;
 }
@@ -1317,6 +1453,7 @@ __device__ __forceinline__ float tok_listed(const u32x4 (&h)[4], const u32x2 (&q
 // The lane's (vector r of the group, row n) error bound from its vector's
 // rounded blocks of the stage: the largest |w| of each such block (from its
 // header in h) times the block's error sum.
+template <int QB>
 __device__ __forceinline__ float tok_rounded_bound(uint32_t mine, uint32_t mylist,
                                                    const u32x4 (&h)[4]) {
   const uint32_t rmask = rounded_mask(mine);
@@ -1325,11 +1462,12 @@ __device__ __forceinline__ float tok_rounded_bound(uint32_t mine, uint32_t mylis
 #pragma unroll
   for (int b = 0; b < 4; ++b)
     if ((rmask >> b) & 1u)
-      err = fmaf(k4_block_bound(h[b]), rounded_err_all(mylist + kSideBytes * b), err);
+      err = fmaf(k4_block_bound<QB == 5 ? 31 : 15>(h[b]), rounded_err_all(mylist + kSideBytes * b),
+                 err);
   return err;
 }
 
-template <int WAVES, int NG>
+template <int WAVES, int NG, int QB>
 __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               float* __restrict__ y, uint32_t rows,
@@ -1337,12 +1475,13 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
                                                               float* __restrict__ part_out,
                                                               TokArgs ta) {
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  constexpr uint32_t kPieces = block_pieces(4);
-  constexpr uint32_t kStage = stage_bytes(4);
+  constexpr uint32_t kPieces = block_pieces(QB);
+  constexpr uint32_t kStage = stage_bytes(QB);
+  constexpr uint32_t kBytes = QB == 5 ? kQ5Bytes : kQ4Bytes;
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t grp = lane >> 4, n = lane & 15u;
-  const uint32_t row_bytes = nb * kQ4Bytes;
+  const uint32_t row_bytes = nb * kBytes;
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t nstages = (nb + 3u) / 4u;
   const uint32_t sbase = (uint32_t)(uintptr_t)smem;
@@ -1358,7 +1497,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
   const uint32_t tstep = ta.groups_per_slice;
   const uint32_t s0 = sliced ? k : 0u, spt = sliced ? 1u : nstages;
   const uint32_t blk0 = 4u * s0, nbl = min(4u * spt, nb - blk0);
-  const Layout L = tok_layout(WAVES, nbl, NG, ta.slots);
+  const Layout L = tok_layout<QB>(WAVES, nbl, NG, ta.slots);
   const uint32_t ntw = tg < ntiles ? quo(ntiles - 1u - tg, by_gps) + 1u : 0u;
   const uint32_t npairs = ntw * spt;
   const FastDiv by_parts{spt, sliced ? 0u : ta.m_parts};
@@ -1383,9 +1522,9 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
   auto issue = [&](const Pair& pr) {
     const uint32_t row0 = pr.tile * 16u;
     const uint32_t nrows = min(16u, rows - row0);
-    const uint8_t* sb = w + (size_t)row0 * row_bytes + 4u * kQ4Bytes * pr.r;
+    const uint8_t* sb = w + (size_t)row0 * row_bytes + 4u * kBytes * pr.r;
     const __amdgpu_buffer_rsrc_t rsrc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - 4u * kQ4Bytes * pr.r), kBufferWord3);
+        const_cast<uint8_t*>(sb), 0, (int)(nrows * row_bytes - 4u * kBytes * pr.r), kBufferWord3);
 #pragma unroll
     for (int i = 0; i < (int)kPieces; ++i)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)(wstage + 1024 * i), 16,
@@ -1421,16 +1560,19 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
 
   // 4. the wave's pairs: lane (grp, n) accumulates, for each group g, vector
   //    4 g + grp, row n
-  const uint32_t hb0 = sbase + wave * kStage + 16u * n;
-  const uint32_t qb0 = hb0 + 256u * (1u + (grp >> 1)) + 8u * (grp & 1u);
+  //    (the lane's 8-byte slices: qs bytes 32 j + 8 grp .. + 7 of unit pair j
+  //    and, Q5_K, qh bytes 8 grp .. + 7)
+  TokAddr sa;
+  sa.hb0 = sbase + wave * kStage + 16u * n;
+  sa.qhb0 = sa.hb0 + 256u * (1u + (grp >> 1)) + 8u * (grp & 1u);
+  sa.qb0 = QB == 5 ? sa.qhb0 + 512u : sa.qhb0;
   uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
   for (uint32_t j = 0; j < my_pairs; ++j) {
     const Pair pr = pr_next;
     const uint32_t s = pr.r, sl = s - s0;  // stage, and its place in the image range
     __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    u32x4 h[4];
-    u32x2 q[16];
-    lds_read_weights_tok(hb0, qb0, h, q);
+    TokStage<QB> st;
+    lds_read_weights_tok<QB>(sa, st);
     // the stage is in registers: the buffer takes the next stage's copy (the
     // exact path reads its blocks from memory), issued once the stage's
     // arithmetic is done: while the memory queue is full, issuing a copy
@@ -1484,15 +1626,15 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       const bool any = __builtin_amdgcn_ballot_w64(mine != 0u) != 0u;
       const uint32_t list0 =
           sbase + L.expo + 4u * g * L.expo_stride + L.side_off + 4u * kSideBytes * sl;
-      const float side = any ? tok_listed(h, q, list0, mine, L.expo_stride, lane) : 0.0f;
+      const float side = any ? tok_listed<QB>(st, list0, mine, L.expo_stride, lane) : 0.0f;
       float abs_pg, err;
       const uint32_t iabase = sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane;
       const uint32_t xabase = sbase + L.xsum + v * L.xsum_stride + 128u * sl;
       const uint32_t eabase = sbase + L.expo + v * L.expo_stride + 16u * sl;
-      float pg = side + tok_group_stage(h, q, nlive, iabase, xabase, eabase, abs_pg, err);
+      float pg = side + tok_group_stage<QB>(st, nlive, iabase, xabase, eabase, abs_pg, err);
       // the stage check of the lane's (vector, row): the fast path's rounding
       // plus its rounded blocks against kStageTol of sum |partial|
-      const float rb = any ? tok_rounded_bound(mine, list0 + grp * L.expo_stride, h) : 0.0f;
+      const float rb = any ? tok_rounded_bound<QB>(mine, list0 + grp * L.expo_stride, st.h) : 0.0f;
       err += rb;
       const bool failed = !(err * 1.01f <= kStageTol * (abs_pg + fabsf(side) - err));
       // One group (M <= 4): a lane that fails tries the stage again with the
@@ -1503,7 +1645,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       // 18.6 us.  The call costs the two- and four-group kernels spills in
       // their main loop (M = 8 31 -> 45 us), so they go straight to it.
       if (NG == 1 && __builtin_amdgcn_ballot_w64(failed) != 0u) {
-        const StageF64 sp = tok_group_stage_f64(hb0, qb0, nlive, iabase, xabase, eabase);
+        const StageF64 sp = tok_group_stage_f64<QB>(sa, nlive, iabase, xabase, eabase);
         const float err_p = sp.err + rb;
         if (failed) {
           if (err_p * 1.01f <= kStageTol * (sp.abs_part + fabsf(side) - err_p))
@@ -1540,7 +1682,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
         for (uint32_t b = 0; b < nlive; ++b) {
           const uint32_t eb = lds_read_b32(sbase + L.expo + v * L.expo_stride + 4u * (4u * sl + b));
           if ((int)eb == kBadBlock || whole)
-            e += block_exact_row(wr, n * row_bytes + kQ4Bytes * (4u * s + b),
+            e += block_exact_row<QB>(wr, n * row_bytes + kBytes * (4u * s + b),
                                  xv + kBlockElems * (4u * s + b));
         }
 #pragma unroll
@@ -1581,7 +1723,7 @@ inline uint32_t tok_slices(uint32_t rows, uint32_t nstages, uint32_t nv, size_t 
 
 // ntok <= 4 NG vectors in one pass; false when the shape does not fit this
 // kernel (K slices need room in the scratch when NG > 1).
-template <int W, int NG>
+template <int W, int NG, int QB = 4>
 bool launch_tokens_td(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                       uint32_t ntok, const Workspace& ws, hipStream_t s, hipError_t* err) {
   const uint32_t ntiles = (rows + 15u) / 16u;
@@ -1593,14 +1735,14 @@ bool launch_tokens_td(const uint8_t* w, const float* x, float* y, uint32_t rows,
     ta.groups_per_slice = min((uint32_t)cu_count() / ta.slices, ntiles);
     ta.slots = 1u;
     grid = ta.groups_per_slice * ta.slices;
-    lds = tok_layout(W, min(4u, nb), NG, 1u).total;
+    lds = tok_layout<QB>(W, min(4u, nb), NG, 1u).total;
   } else {
     if (NG > 1) return false;  // whole rows: one group's images already fill the LDS
     ta.groups_per_slice = grid = min(ntiles, (uint32_t)cu_count());
     const uint32_t tiles_per_group = (ntiles + grid - 1u) / grid;
     ta.slots = ring_slots(W, 1, tiles_per_group, nstages);
     ta.m_parts = div_magic(nstages);
-    lds = tok_layout(W, nb, NG, ta.slots).total;
+    lds = tok_layout<QB>(W, nb, NG, ta.slots).total;
     // pair indices below tiles_per_group * nstages, divided by nstages
     if ((uint64_t)tiles_per_group * nstages * nstages >= (1ull << 32)) return false;
   }
@@ -1611,17 +1753,18 @@ bool launch_tokens_td(const uint8_t* w, const float* x, float* y, uint32_t rows,
   if ((uint64_t)(grid + ntiles) * ta.groups_per_slice >= (1ull << 32)) return false;
   if (lds > kLdsBytes) return false;
   static const hipError_t attr = hipFuncSetAttribute(
-      reinterpret_cast<const void*>(&q4k_tokens_mfma<W, NG>),
+      reinterpret_cast<const void*>(&q4k_tokens_mfma<W, NG, QB>),
       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q4k_tokens_mfma<W, NG>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
+  hipLaunchKernelGGL((q4k_tokens_mfma<W, NG, QB>), dim3(grid), dim3(W * 64), lds, s, w, x, y, rows,
                      nb, ntok, ws.scratch, ta);
   *err = hipGetLastError();
   if (*err == hipSuccess && ta.slices > 1u) {
-    hipLaunchKernelGGL(tok_reduce<kTypeQ4K>, dim3((rows + 255u) / 256u, ntok), dim3(256), 0, s,
+    hipLaunchKernelGGL(tok_reduce<QB == 5 ? kTypeQ5K : kTypeQ4K>, dim3((rows + 255u) / 256u, ntok),
+                       dim3(256), 0, s,
                        ws.scratch, y, rows, nstages, 4u * NG, w, x, nb, 4u);
     *err = hipGetLastError();
   }
@@ -1630,17 +1773,21 @@ bool launch_tokens_td(const uint8_t* w, const float* x, float* y, uint32_t rows,
 
 // 3..16 vectors in one launch (with its reduce): the group count and wave
 // count that fit.
+template <int QB>
 bool launch_tokens_groups(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                           uint32_t ntok, const Workspace& ws, hipStream_t s, hipError_t* err) {
-  if (ntok <= 4u)
-    return launch_tokens_td<12, 1>(w, x, y, rows, nb, ntok, ws, s, err) ||
-           launch_tokens_td<8, 1>(w, x, y, rows, nb, ntok, ws, s, err) ||
-           launch_tokens_td<4, 1>(w, x, y, rows, nb, ntok, ws, s, err);
+  if (ntok <= 4u) {
+    if constexpr (QB == 4) {
+      if (launch_tokens_td<12, 1, QB>(w, x, y, rows, nb, ntok, ws, s, err)) return true;
+    }
+    return launch_tokens_td<8, 1, QB>(w, x, y, rows, nb, ntok, ws, s, err) ||
+           launch_tokens_td<4, 1, QB>(w, x, y, rows, nb, ntok, ws, s, err);
+  }
   // (the weights' decoded operands stay in registers across the groups: two
   // waves per SIMD)
-  if (ntok <= 8u) return launch_tokens_td<8, 2>(w, x, y, rows, nb, ntok, ws, s, err);
-  return launch_tokens_td<8, 4>(w, x, y, rows, nb, ntok, ws, s, err) ||
-         launch_tokens_td<6, 4>(w, x, y, rows, nb, ntok, ws, s, err);
+  if (ntok <= 8u) return launch_tokens_td<8, 2, QB>(w, x, y, rows, nb, ntok, ws, s, err);
+  return launch_tokens_td<8, 4, QB>(w, x, y, rows, nb, ntok, ws, s, err) ||
+         launch_tokens_td<6, 4, QB>(w, x, y, rows, nb, ntok, ws, s, err);
 }
 
 template <int W, int D, int M, int NT = 1, int QB = 4, bool G = false, int SB = 4,
@@ -1943,11 +2090,11 @@ bool matmul_passes(const uint8_t* w, const float* x, float* y, uint32_t rows, ui
     const float* xb = x + (size_t)b * cols;
     float* yb = y + (size_t)b * rows;
     bool ok;
-    if (QB == 4 && nt >= 2 && td_policy()) {
+    if (nt >= 2 && td_policy()) {
       // up to sixteen vectors share the matrix-core rows in one pass (two
       // go faster one vector per MFMA)
       const uint32_t ng = batch - b >= 3u ? min(16u, batch - b) : nt;
-      if (ng >= 3u && launch_tokens_groups(w, xb, yb, rows, nb, ng, ws, s, err)) {
+      if (ng >= 3u && launch_tokens_groups<QB>(w, xb, yb, rows, nb, ng, ws, s, err)) {
         if (*err != hipSuccess) return true;
         b += ng;
         continue;

@@ -510,6 +510,51 @@ def test_matmul_many_nonfinite_and_outlier_vectors(hip_ctx):
     assert np.array_equal(_category(outs[3]), _category(y32))
 
 
+@pytest.mark.parametrize("rows,cols,batch", [(100, 2304, 3), (1040, 5120, 8), (33, 1280, 7),
+                                             (300, 17408, 5), (5120, 5120, 16)])
+def test_q5_k_matmul_many_vectors_in_rows(hip_ctx, rows, cols, batch):
+    """Q5_K candidates in the matrix-core rows (the qh bit as the weights'
+    fifth bit): partial tiles, a short last stage, K slices, a long K and
+    sixteen vectors in one pass; repeat calls bit-identical."""
+    log(f"q5_k matmul_many {rows}x{cols} batch={batch}")
+    w = si_hip.synth_matrix(13, seed=rows * 11 + cols + batch, rows=rows, cols=cols, threads=8)
+    X = si_hip.synth_normal(rows + 5 * batch, batch * cols).reshape(batch, cols)
+    W = hip_ctx.upload_quant_weight_private(w, 13)
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    again = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(batch):
+        _, y64, ab = O.matvec(13, w, rows, cols, X[b], threads=8)
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+        assert np.array_equal(outs[b], again[b])
+
+
+def test_q5_k_matmul_many_nonfinite_side_and_rounded(hip_ctx):
+    """Eight Q5_K candidates: listed side elements, rounded blocks, huge,
+    subnormal and zero blocks, and non-finite activations in some vectors
+    only."""
+    rows, cols, batch = 300, 5120, 8
+    w = si_hip.synth_matrix(13, seed=4260, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, 13)
+    X = si_hip.synth_normal(4261, batch * cols).reshape(batch, cols).copy()
+    X[0, 256:259] = np.float32(3e-9)
+    X[1, 512:540] = np.float32(2e-9)
+    X[2, 1024:1280] = np.float32(1e-41)
+    X[2, 2048:2304] = 0.0
+    X[3, 600:620] = np.float32(3e30)
+    X[4, 300] = np.float32(1e6)
+    X[5] = 0.0
+    X[6, 700] = np.inf
+    X[7, 1500] = np.nan
+    outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    for b in range(6):
+        _, y64, ab = O.matvec(13, w, rows, cols, X[b], threads=8)
+        assert_dot_close(outs[b], y64, ab, what=f"candidate {b}")
+    assert not np.any(outs[5])
+    for b in (6, 7):
+        y32, _, _ = O.matvec(13, w, rows, cols, X[b], threads=8)
+        assert np.array_equal(_category(outs[b]), _category(y32)), f"candidate {b}"
+
+
 def test_matmul_many_baseline_shape(hip_ctx):
     """M = 6 candidates on the 17408 x 5120 Q4_K matrix: one pass over the
     weights for four vectors and one for two; each candidate matches its own
