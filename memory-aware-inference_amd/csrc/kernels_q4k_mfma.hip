@@ -968,11 +968,11 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_matvec_mfma(const uint8_t* __r
 // a launch with S > 1 cuts K into its S stages: GS workgroups per stage,
 // workgroup g works on stage k = g / GS for tiles g % GS, g % GS + GS, ...,
 // and keeps the images of that stage only.  Each pair is then its
-// workgroup's whole share of a tile: the wave publishes the 4 x 16 sums in
-// the workspace (entry tile * S + k), counts them on the tile's counter, and
-// the wave that completes the count adds the S entries in stage order and
-// stores the rows (deterministic).  With S == 1 a workgroup keeps the whole
-// row's images and sums a tile's stages in its LDS slot ring.
+// workgroup's whole share of a tile: the wave stores each vector's and row's
+// sum over the stage in the scratch (part_out[(k * 4 NG + v) * rows + row],
+// or kPartRedo for a stage left to the exact path), and tok_reduce adds the
+// S sums in stage order (deterministic).  With S == 1 a workgroup keeps the
+// whole row's images and sums a tile's stages in its LDS slot ring.
 
 // Headers and the lane's four 8-byte qs slices of the four blocks of a stage
 // buffer: header of block b at hb + 2304 b, slice j at qb + 2304 b + 512 j.
