@@ -92,19 +92,25 @@ def test_two_block_special_activations(hip_ctx, t):
         W.free()
 
 
-def test_two_block_q5_k_matmul_many_leftover(hip_ctx):
-    """Five Q5_K vectors: a pass of four, then the fifth alone through the
-    one-vector dispatch (two-block stages), each within its bound."""
+def test_two_block_q5_k_matmul_many_and_one_vector(hip_ctx):
+    """Five Q5_K vectors of an odd block count (21) in one vectors-in-rows
+    pass (two groups, the second holding one vector), each within its bound
+    and the same bits on a second call; a batch of one goes through the
+    one-vector dispatch (two-block stages) and equals the plain matvec bit
+    for bit."""
     rows, cols, batch = 1000, 5376, 5
     w = si_hip.synth_matrix(Q5, seed=4800, rows=rows, cols=cols, threads=8)
     X = si_hip.synth_normal(4801, batch * cols).reshape(batch, cols)
     W = hip_ctx.upload_quant_weight_private(w, Q5)
     try:
         outs = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+        again = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
         for b in range(batch):
             _, y64, ab = O.matvec(Q5, w, rows, cols, X[b], threads=8)
             assert_dot_close(outs[b], y64, ab, what=f"vector {b}")
-        assert same_bits(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, X[4]), outs[4])
+            assert same_bits(outs[b], again[b])
+        one = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, 1, X[4:5])
+        assert same_bits(hip_ctx.gguf_quant_matvec_weight(W, rows, cols, X[4]), one[0])
     finally:
         W.free()
 
