@@ -614,10 +614,11 @@ struct Q6TokArgs {
   void* wsp;          // the workspace, for failure reports
 };
 
-// LDS map: per-wave stage buffers, then two groups' images of nbl blocks and
-// their metadata (8 vectors); one unused ring slot.
-__host__ __device__ constexpr Layout tok6_layout(uint32_t waves, uint32_t nbl, uint32_t depth) {
-  return make_layout(kStageBytes, 2u, 32u, waves, depth, nbl, 1u, 1u, 8u);
+// LDS map: per-wave stage buffers, then ng groups' images of nbl blocks and
+// their metadata (4 ng vectors); one unused ring slot.
+__host__ __device__ constexpr Layout tok6_layout(uint32_t waves, uint32_t nbl, uint32_t depth,
+                                                 uint32_t ng) {
+  return make_layout(kStageBytes, 2u, 32u, waves, depth, nbl, 1u, 1u, 4u * ng);
 }
 
 // The lane's share of a two-block stage buffer (piece p of row n at 256 p +
@@ -696,10 +697,12 @@ __device__ __forceinline__ void lds_read_tok6_images(uint32_t i0, uint32_t i1, i
 }
 
 // Exponents of the stage's two blocks and their side counts (one byte each)
-// for the lane's four vectors, from their metadata at m[0..3] (already
-// offset to the stage).
-__device__ __forceinline__ void lds_read_tok6_meta(const uint32_t (&m)[4], u32x2 (&ex)[4],
-                                                   uint32_t (&cnt)[4]) {
+// for four of the lane's vectors, from their metadata at m[O .. O + 3]
+// (already offset to the stage).
+template <int O, int N>
+__device__ __forceinline__ void lds_read_tok6_meta(const uint32_t (&m)[N], u32x2 (&ex)[N],
+                                                   uint32_t (&cnt)[N]) {
+  static_assert(O + 4 <= N, "four vectors from O");
   static_assert(kCountOff == 512, "the offset below");
   asm volatile(
       "ds_read_b64 %0, %8\n"
@@ -711,9 +714,9 @@ __device__ __forceinline__ void lds_read_tok6_meta(const uint32_t (&m)[4], u32x2
       "ds_read_u16 %6, %10 offset:512\n"
       "ds_read_u16 %7, %11 offset:512\n"
       "s_waitcnt lgkmcnt(0)"
-      : "=&v"(ex[0]), "=&v"(ex[1]), "=&v"(ex[2]), "=&v"(ex[3]), "=&v"(cnt[0]), "=&v"(cnt[1]),
-        "=&v"(cnt[2]), "=&v"(cnt[3])
-      : "v"(m[0]), "v"(m[1]), "v"(m[2]), "v"(m[3])
+      : "=&v"(ex[O]), "=&v"(ex[O + 1]), "=&v"(ex[O + 2]), "=&v"(ex[O + 3]), "=&v"(cnt[O]),
+        "=&v"(cnt[O + 1]), "=&v"(cnt[O + 2]), "=&v"(cnt[O + 3])
+      : "v"(m[O]), "v"(m[O + 1]), "v"(m[O + 2]), "v"(m[O + 3])
       : "memory");
 }
 
@@ -762,16 +765,20 @@ __device__ __forceinline__ int max_abs_i8(uint32_t w, int from = 0, int to = 4) 
   return m;
 }
 
-// Up to eight vectors (vectors past ntok are zero and not stored): the
-// slice partial sums part_out[(k * 8 + v) * rows + row] of slice k.  DEPTH
+// Up to 4 NG vectors (vectors past ntok are zero and not stored): the slice
+// partial sums part_out[(k * 4 NG + v) * rows + row] of slice k.  DEPTH
 // stage buffers per wave: the copies of its next DEPTH pairs in flight.
-template <int WAVES, int DEPTH>
+// NG = 2 (eight vectors) or 4 (sixteen): GQ = 2 NG MFMAs per chunk, (G, q)
+// = (gq / 2, gq % 2) for vectors 4 G + 2 q + v.
+template <int WAVES, int DEPTH, int NG>
 __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __restrict__ w,
                                                               const float* __restrict__ x,
                                                               uint32_t rows, uint32_t nb,
                                                               uint32_t ntok,
                                                               float* __restrict__ part_out,
                                                               Q6TokArgs ta) {
+  static_assert(NG == 2 || NG == 4, "eight or sixteen vectors");
+  constexpr int GQ = 2 * NG;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t wave = uniform(threadIdx.x >> 6);
   const uint32_t lane = threadIdx.x & 63u;
@@ -800,13 +807,13 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   }
   const uint32_t blk0 = k * ta.nbs, nbl = min(ta.nbs, nb - blk0);
   const uint32_t nst = nbl / 2u;
-  const Layout L = tok6_layout(WAVES, nbl, DEPTH);
+  const Layout L = tok6_layout(WAVES, nbl, DEPTH, NG);
   const uint32_t ntw = tg < ntiles ? quo(ntiles - 1u - tg, by_gps) + 1u : 0u;
   const uint32_t my_tiles = wave < ntw ? (ntw - 1u - wave) / WAVES + 1u : 0u;
   const uint32_t my_pairs = my_tiles * nst;
 
   // 1. the vectors' blocks of the slice into the image area
-  copy_x_group<WAVES>(smem, L.img, x, nb, blk0, nbl, 2u, ntok, wave, lane);
+  copy_x_group<WAVES>(smem, L.img, x, nb, blk0, nbl, NG, ntok, wave, lane);
 
   // 2. the copy of a pair's stage into buffer buf: local tile lt (tile
   //    tg + lt GS), stage s of the slice.  Copy i, lane l moves piece
@@ -853,7 +860,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   lds_wait();
   __builtin_amdgcn_s_barrier();
   if (!first_round) issue_first();
-  const uint32_t builders = min((uint32_t)WAVES, 2u * nbl);
+  const uint32_t builders = min((uint32_t)WAVES, (uint32_t)NG * nbl);
   if (wave < builders) {
     // (the stage copies went out after the x copies and complete in order)
     if (DEPTH >= 2 && early >= 2u)
@@ -862,7 +869,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(kCopies));
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    build_group_images<WAVES>(sbase, L, nbl, 2u, wave, lane);
+    build_group_images<WAVES>(sbase, L, nbl, NG, wave, lane);
     lds_wait();
     if (lane == 0u) (void)lds_add_rtn(sbase + L.ready, 1u);
   }
@@ -875,14 +882,18 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
   const uint32_t ibase = sbase + L.img + 256u * grp + 64u * (n >> 3) + 16u * (n & 3u);
   const uint32_t gstride = 4096u * nbl;
   // the metadata of the result lane's vectors 4 G + 2 q + vh, (G, q) = gq
-  uint32_t meta[4];
+  uint32_t meta[GQ];
 #pragma unroll
-  for (int gq = 0; gq < 4; ++gq) meta[gq] = sbase + L.expo + (2u * gq + vh) * L.expo_stride;
+  for (int gq = 0; gq < GQ; ++gq) meta[gq] = sbase + L.expo + (2u * gq + vh) * L.expo_stride;
   const uint32_t o_lo = 8u * hs, o_hi = 16u + 8u * hs;  // bit offsets of the lane's scales
-  i32x4 A[4];
+  i32x4 A[NG / 2][4];  // per pair of groups: (G, q) = (2 p, 0), (2 p, 1), (2 p + 1, 0), (2 p + 1, 1)
 #pragma unroll
-  for (int gq = 0; gq < 4; ++gq) A[gq] = i32x4{0, 0, 0, 0};
-  float part[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int pg = 0; pg < NG / 2; ++pg)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) A[pg][i] = i32x4{0, 0, 0, 0};
+  float part[GQ];
+#pragma unroll
+  for (int gq = 0; gq < GQ; ++gq) part[gq] = 0.0f;
   uint32_t redo = 0u;  // bit gq: the slice of vector gq is recomputed exactly
   uint32_t lt = wave, sl = 0u;
   uint32_t fail = 0u;  // a bounded wait that gave up (kDevErr*)
@@ -897,12 +908,13 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
     Stage6 sv;
     lds_read_stage6(a00 + buf * kStageBytes, a20 + buf * kStageBytes, srow, sv);
     if (p == 0u) wait_images(sbase, L, builders, fail);
-    uint32_t m[4];
+    uint32_t m[GQ];
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) m[gq] = meta[gq] + 8u * sl;
-    u32x2 ex[4];
-    uint32_t cnt[4];
-    lds_read_tok6_meta(m, ex, cnt);
+    for (int gq = 0; gq < GQ; ++gq) m[gq] = meta[gq] + 8u * sl;
+    u32x2 ex[GQ];
+    uint32_t cnt[GQ];
+    lds_read_tok6_meta<0>(m, ex, cnt);
+    if constexpr (GQ == 8) lds_read_tok6_meta<4>(m, ex, cnt);
     const float d0 = half_bits_to_float(sv.dw0 & 0xffffu);
     const float d1 = half_bits_to_float(sv.tail1 >> 16);
 
@@ -911,10 +923,10 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
     uint32_t rounded = 0u;  // bit 2 gq + b: block b of vector gq is rounded
     uint32_t any_side = 0u;
 #pragma unroll
-    for (int gq = 0; gq < 4; ++gq) any_side |= cnt[gq];
+    for (int gq = 0; gq < GQ; ++gq) any_side |= cnt[gq];
     if (__builtin_amdgcn_ballot_w64(any_side != 0u) != 0u) {
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
+      for (int gq = 0; gq < GQ; ++gq) {
 #pragma unroll
         for (int b = 0; b < 2; ++b) {
           const uint32_t c = (cnt[gq] >> (8 * b)) & 0xffu;
@@ -938,11 +950,13 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
     if (p + DEPTH < my_pairs) issue(buf);
 
     // the two blocks: per chunk four MFMAs and the integer scale combine
-    float absp[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    float absp[GQ];
+#pragma unroll
+    for (int gq = 0; gq < GQ; ++gq) absp[gq] = 0.0f;
     const uint32_t ib0 = ibase + 4096u * (2u * sl);
     static_for<2>([&](auto bc) {
       constexpr int b = decltype(bc)::value;
-      const uint32_t i0 = ib0 + 4096u * b, i1 = i0 + gstride;
+      const uint32_t i0 = ib0 + 4096u * b;
       u32x2 ql[4], qx[2];
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
@@ -960,23 +974,28 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
                                         __builtin_amdgcn_alignbyte(sv.qh1n[c], sv.qh1[c][1], 2)};
         qx[c] = u32x2{qh[0] ^ 0xaaaaaaaau, qh[1] ^ 0xaaaaaaaau};
       }
-      int t[4][4];
+      int t[GQ][4];
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq)
+      for (int gq = 0; gq < GQ; ++gq)
 #pragma unroll
         for (int d = 0; d < 4; ++d) t[gq][d] = 0;
       // software-pipelined: chunk j's four MFMAs go out before chunk j - 1's
       // products are added, so that no MFMA result is read right after its
       // MFMA
-      i32x4 cp[4];
+      i32x4 cp[GQ];
       int scp = 0;
       static_for<9>([&](auto jc) {
         constexpr int j = decltype(jc)::value;
-        i32x4 c[4];
+        i32x4 c[GQ];
         int sc = 0;
         if constexpr (j < 8) {
           constexpr int h = j >> 2, tt = j & 3;
-          if constexpr ((j & 1) == 0) lds_read_tok6_images<j / 2>(i0, i1, A);
+          if constexpr ((j & 1) == 0) {
+#pragma unroll
+            for (int pg = 0; pg < NG / 2; ++pg)
+              lds_read_tok6_images<j / 2>(i0 + 2u * pg * gstride, i0 + (2u * pg + 1u) * gstride,
+                                          A[pg]);
+          }
           const u32x2 wq = q6_chunk<tt>(ql[2 * h + (tt & 1)], qx[h]);
           // scale 2 j + hs: block 0 byte 2 j + hs of its 16; block 1 byte
           // 2 + 2 j + hs of piece 25 (j < 7) or byte hs of the tail word (j = 7)
@@ -989,25 +1008,27 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
           const int64_t bw = as_i64(wq[0], wq[1]);
           const i32x4 zero = {0, 0, 0, 0};
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq)
+          for (int gq = 0; gq < GQ; ++gq) {
+            const i32x4& a = A[gq / 4][gq % 4];
             c[gq] = __builtin_amdgcn_mfma_i32_16x16x32_i8(
-                as_i64(A[gq][2 * (j & 1)], A[gq][2 * (j & 1) + 1]), bw, zero, 0, 0, 0);
+                as_i64(a[2 * (j & 1)], a[2 * (j & 1) + 1]), bw, zero, 0, 0, 0);
+          }
         }
         if constexpr (j > 0) {
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq)
+          for (int gq = 0; gq < GQ; ++gq)
 #pragma unroll
             for (int d = 0; d < 4; ++d) t[gq][d] = mad_i24(scp, cp[gq][d], t[gq][d]);
         }
         if constexpr (j < 8) {
 #pragma unroll
-          for (int gq = 0; gq < 4; ++gq) cp[gq] = c[gq];
+          for (int gq = 0; gq < GQ; ++gq) cp[gq] = c[gq];
           scp = sc;
         }
       });
       const float db = b == 0 ? d0 : d1;
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
+      for (int gq = 0; gq < GQ; ++gq) {
         const int eb = (int)ex[gq][b];
         const float tc = fmaf(fmaf(fmaf((float)t[gq][3], 256.0f, (float)t[gq][2]), 256.0f,
                                    (float)t[gq][1]),
@@ -1031,7 +1052,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
                                         max(max(max_abs_i8(sv.sc1[2]), max_abs_i8(sv.sc1[3])),
                                             max_abs_i8(sv.tail1, 0, 2))));
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
+      for (int gq = 0; gq < GQ; ++gq) {
         auto a2s = __builtin_amdgcn_permlane16_swap(__float_as_uint(absp[gq]),
                                                     __float_as_uint(absp[gq]), false, false);
         const float a = __uint_as_float(a2s[0]) + __uint_as_float(a2s[1]);
@@ -1046,11 +1067,11 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
 
     if (last_stage) {
       // the tile's sums over the slice: lanes h = 0, 1 added; lane h stores
-      // group G = h
-      float tot[4];
+      // (G, q) = gq for gq in [h NG, h NG + NG), vector 2 gq + vh
+      float tot[GQ];
       uint32_t rd = 0u;
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) {
+      for (int gq = 0; gq < GQ; ++gq) {
         auto s2 = __builtin_amdgcn_permlane16_swap(__float_as_uint(part[gq]),
                                                    __float_as_uint(part[gq]), false, false);
         tot[gq] = __uint_as_float(s2[0]) + __uint_as_float(s2[1]);
@@ -1061,16 +1082,16 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
       }
       const uint32_t row = (tg + lt * ta.groups_per_slice) * 16u + n;
       if (row < rows) {
-        const float val0 = hs != 0u ? tot[2] : tot[0];
-        const float val1 = hs != 0u ? tot[3] : tot[1];
-        const uint32_t r2 = rd >> (2u * hs);
-        const uint32_t v0 = 4u * hs + vh, v1 = v0 + 2u;
-        float* const out = part_out + (size_t)k * 8u * rows + row;
-        if (v0 < ntok) out[(size_t)v0 * rows] = (r2 & 1u) ? __uint_as_float(kPartRedo) : val0;
-        if (v1 < ntok) out[(size_t)v1 * rows] = (r2 & 2u) ? __uint_as_float(kPartRedo) : val1;
+        float* const out = part_out + (size_t)k * (4u * NG) * rows + row;
+#pragma unroll
+        for (int gq = 0; gq < GQ; ++gq) {
+          const uint32_t v = 2u * gq + vh;
+          if ((uint32_t)(gq / NG) == hs && v < ntok)
+            out[(size_t)v * rows] = ((rd >> gq) & 1u) ? __uint_as_float(kPartRedo) : tot[gq];
+        }
       }
 #pragma unroll
-      for (int gq = 0; gq < 4; ++gq) part[gq] = 0.0f;
+      for (int gq = 0; gq < GQ; ++gq) part[gq] = 0.0f;
       redo = 0u;
     }
     sl = last_stage ? 0u : sl + 1u;
@@ -1247,18 +1268,18 @@ bool launch_pairs(const uint8_t* w, const float* x, float* y, uint32_t rows, uin
 // Up to eight vectors in one pass over the weights: q6k_tokens_mfma in K
 // slices of nbs blocks, then tok_reduce.  false when the shape does not fit
 // (q6_shape_ok, the slices' partial sums within the scratch, the LDS).
-template <int W, int D>
+template <int W, int D, int NG>
 bool launch_tok6(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                  uint32_t ntok, uint32_t nbs, const Workspace& ws, hipStream_t s,
                  hipError_t* err) {
-  if (ntok == 0u || ntok > 8u || nbs < 2u || (nbs & 1u) != 0u || !q6_shape_ok(rows, nb))
+  if (ntok == 0u || ntok > 4u * NG || nbs < 2u || (nbs & 1u) != 0u || !q6_shape_ok(rows, nb))
     return false;
   const uint32_t ntiles = (rows + 15u) / 16u;
   const uint32_t cus = (uint32_t)cu_count();
   Q6TokArgs ta{};
   ta.nbs = min(nbs, nb);
   ta.slices = (nb + ta.nbs - 1u) / ta.nbs;
-  if (ta.slices > cus || (size_t)ta.slices * 8u * rows * sizeof(float) > ws.scratch_bytes)
+  if (ta.slices > cus || (size_t)ta.slices * 4u * NG * rows * sizeof(float) > ws.scratch_bytes)
     return false;
   ta.groups_per_slice = min(cus / ta.slices, ntiles);
   // XCD-grouped on request (SI_HIP_Q6K_TOK_XCD=1), when a multiple of 8 groups
@@ -1279,44 +1300,49 @@ bool launch_tok6(const uint8_t* w, const float* x, float* y, uint32_t rows, uint
   if ((uint64_t)(grid + ntiles) * ta.groups_per_slice >= (1ull << 32)) return false;
   ta.m_gps = div_magic(ta.groups_per_slice);
   ta.wsp = ws.ptr;
-  const uint32_t lds = tok6_layout(W, ta.nbs, D).total;
+  const uint32_t lds = tok6_layout(W, ta.nbs, D, NG).total;
   if (lds > kLdsBytes) return false;
   static const hipError_t attr =
-      hipFuncSetAttribute(reinterpret_cast<const void*>(&q6k_tokens_mfma<W, D>),
+      hipFuncSetAttribute(reinterpret_cast<const void*>(&q6k_tokens_mfma<W, D, NG>),
                           hipFuncAttributeMaxDynamicSharedMemorySize, (int)kLdsBytes);
   if (attr != hipSuccess) {
     *err = attr;
     return true;
   }
-  hipLaunchKernelGGL((q6k_tokens_mfma<W, D>), dim3(grid), dim3(W * 64), lds, s, w, x, rows, nb, ntok,
+  hipLaunchKernelGGL((q6k_tokens_mfma<W, D, NG>), dim3(grid), dim3(W * 64), lds, s, w, x, rows, nb, ntok,
                      ws.scratch, ta);
   *err = hipGetLastError();
   if (*err == hipSuccess) {
     hipLaunchKernelGGL(tok_reduce<kTypeQ6K>, dim3((rows + 255u) / 256u, ntok), dim3(256), 0, s,
-                       ws.scratch, y, rows, ta.slices, 8u, w, x, nb, ta.nbs);
+                       ws.scratch, y, rows, ta.slices, 4u * NG, w, x, nb, ta.nbs);
     *err = hipGetLastError();
   }
   return true;
 }
 
-// The vectors-in-rows pass for ntok <= 8 vectors: 12 waves with four-block
-// slices, else (the partial sums of more slices than the scratch holds) the
-// fewest slices whose images leave 8 waves their stage buffers.
+// The vectors-in-rows pass for ntok <= 16 vectors.  Up to eight: 12 waves
+// with four-block slices, else (the partial sums of more slices than the
+// scratch holds) the fewest slices whose images leave 8 waves their stage
+// buffers.  Nine to sixteen: 8 waves with four-block slices, or false (the
+// caller then runs passes of eight).
 bool launch_tok6_any(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t nb,
                      uint32_t ntok, const Workspace& ws, hipStream_t s, hipError_t* err) {
   static const int nbs_env = env_int("SI_HIP_Q6K_TOK_NBS", 0);
   static const int w_env = env_int("SI_HIP_Q6K_TOK_WAVES", 0);
+  if (ntok > 8u)  // sixteen vectors: 8 waves (the registers of four groups)
+    return launch_tok6<8, 1, 4>(w, x, y, rows, nb, ntok, nbs_env > 0 ? (uint32_t)nbs_env : 4u,
+                                ws, s, err);
   if (nbs_env > 0 || w_env > 0) {
     const uint32_t nbs = nbs_env > 0 ? (uint32_t)nbs_env : 4u;
     switch (w_env) {
-      case 8: return launch_tok6<8, 1>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
-      case 82: return launch_tok6<8, 2>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
-      default: return launch_tok6<12, 1>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+      case 8: return launch_tok6<8, 1, 2>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+      case 82: return launch_tok6<8, 2, 2>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
+      default: return launch_tok6<12, 1, 2>(w, x, y, rows, nb, ntok, nbs, ws, s, err);
     }
   }
-  return launch_tok6<12, 1>(w, x, y, rows, nb, ntok, 4u, ws, s, err) ||
-         launch_tok6<12, 1>(w, x, y, rows, nb, ntok, 6u, ws, s, err) ||
-         launch_tok6<8, 1>(w, x, y, rows, nb, ntok, 10u, ws, s, err);
+  return launch_tok6<12, 1, 2>(w, x, y, rows, nb, ntok, 4u, ws, s, err) ||
+         launch_tok6<12, 1, 2>(w, x, y, rows, nb, ntok, 6u, ws, s, err) ||
+         launch_tok6<8, 1, 2>(w, x, y, rows, nb, ntok, 10u, ws, s, err);
 }
 }  // namespace
 
@@ -1386,8 +1412,11 @@ bool launch_q6k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t
     const float* xb = x + (size_t)b * cols;
     float* yb = y + (size_t)b * rows;
     uint32_t nt = 0;
-    if (tok_min > 0 && left >= (uint32_t)tok_min &&
-        launch_tok6_any(w, xb, yb, rows, nb, min(8u, left), ws, s, err))
+    if (tok_min > 0 && left > 8u &&
+        launch_tok6_any(w, xb, yb, rows, nb, min(16u, left), ws, s, err))
+      nt = min(16u, left);
+    else if (tok_min > 0 && left >= (uint32_t)tok_min &&
+             launch_tok6_any(w, xb, yb, rows, nb, min(8u, left), ws, s, err))
       nt = min(8u, left);
     else if (left >= 4u && (launch_wd<8, 1, 4>(w, xb, yb, rows, nb, ws, s, err) ||
                        launch_wd<6, 1, 4>(w, xb, yb, rows, nb, ws, s, err)))

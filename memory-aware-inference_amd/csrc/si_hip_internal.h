@@ -20,7 +20,7 @@ struct Workspace {
   size_t scratch_bytes = 0;
 };
 constexpr size_t kWorkspaceBytes = size_t(2) << 20;
-constexpr size_t kWorkspaceScratchBytes = size_t(32) << 20;
+constexpr size_t kWorkspaceScratchBytes = size_t(64) << 20;
 constexpr size_t kWorkspaceCounterBytes = size_t(1) << 20;
 // a signalling-NaN pattern: no arithmetic result has it (results of
 // operations are quiet NaNs)

@@ -676,10 +676,11 @@ def test_q6_k_matmul_many_eight_side_rounded_and_exact_blocks(hip_ctx):
         assert np.array_equal(_category(outs[b]), _category(y32)), f"candidate {b}"
 
 
-def test_q6_k_matmul_many_head_eight(hip_ctx):
-    """Eight candidates through the 151936 x 5120 Q6_K output head in one
-    pass over its 638 MB: each within the bound of the oracle."""
-    rows, cols, batch = 151936, 5120, 8
+@pytest.mark.parametrize("batch", [8, 16])
+def test_q6_k_matmul_many_head_eight(hip_ctx, batch):
+    """Eight and sixteen candidates through the 151936 x 5120 Q6_K output
+    head in one pass over its 638 MB: each within the bound of the oracle."""
+    rows, cols = 151936, 5120
     w = si_hip.synth_matrix(14, seed=2026, rows=rows, cols=cols, threads=8)
     X = si_hip.synth_normal(2031, batch * cols).reshape(batch, cols)
     W = hip_ctx.upload_quant_weight_private(w, 14)
