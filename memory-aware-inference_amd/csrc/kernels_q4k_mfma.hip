@@ -1553,7 +1553,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(kPieces));
     else
       __builtin_amdgcn_s_waitcnt(waitcnt_vm(0));
-    build_group_images<WAVES>(sbase, L, nbl, ng, wave, lane);
+    build_group_images<WAVES, NG == 1>(sbase, L, nbl, ng, wave, lane);
     lds_wait();
     if (lane == 0u) (void)lds_add_rtn(sbase + L.ready, 1u);
   }
@@ -1626,7 +1626,11 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       const bool any = __builtin_amdgcn_ballot_w64(mine != 0u) != 0u;
       const uint32_t list0 =
           sbase + L.expo + 4u * g * L.expo_stride + L.side_off + 4u * kSideBytes * sl;
-      const float side = any ? tok_listed<QB>(st, list0, mine, L.expo_stride, lane) : 0.0f;
+      // (listed side elements: one group only; with more, side elements make
+      // rounded blocks)
+      float side = 0.0f;
+      if constexpr (NG == 1)
+        side = any ? tok_listed<QB>(st, list0, mine, L.expo_stride, lane) : 0.0f;
       float abs_pg, err;
       const uint32_t iabase = sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane;
       const uint32_t xabase = sbase + L.xsum + v * L.xsum_stride + 128u * sl;

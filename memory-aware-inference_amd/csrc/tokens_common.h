@@ -72,8 +72,13 @@ __device__ __forceinline__ void copy_x_group(uint8_t* smem, uint32_t img, const 
 // place: a wave converts exactly the group-blocks it copied; lane (t, c)
 // takes elements 16 c .. 16 c + 15 of vector 4 g + t.  Blocks follow
 // build_images' rules (side elements, exponent kBadBlock for blocks that
-// must take the exact path).
-template <int WAVES>
+// must take the exact path).  LIST: up to kSideMax side elements of a block
+// are listed (and zero in the image) for the kernel to add exactly; without
+// it every block with side elements is a rounded block, which the kernel
+// checks with the block's error sums instead (the two- and four-group Q4_K
+// and Q5_K kernels: the listed elements' exact decode took registers enough
+// to spill their main loops).
+template <int WAVES, bool LIST = true>
 __device__ __forceinline__ void build_group_images(uint32_t sbase, const Layout& L, uint32_t nbl,
                                                    uint32_t ng, uint32_t wave, uint32_t lane) {
   const uint32_t t = lane >> 4, c = lane & 15u;
@@ -94,9 +99,17 @@ __device__ __forceinline__ void build_group_images(uint32_t sbase, const Layout&
     const bool bad_blk = (__builtin_amdgcn_ballot_w64(cs.bad) >> (16u * t)) & 0xffffull;
     const uint32_t meta = sbase + L.expo + v * L.expo_stride;
     const uint32_t list = meta + L.side_off + kSideBytes * b;
-    const uint32_t nside =
-        __builtin_amdgcn_ballot_w64(cs.smask != 0u) ? side_list(xv, cs.smask, c, list, !bad_blk) : 0u;
-    const bool rounded = !bad_blk && nside > kSideMax;
+    uint32_t nside = 0u;
+    bool rounded;
+    if constexpr (LIST) {
+      nside = __builtin_amdgcn_ballot_w64(cs.smask != 0u)
+                  ? side_list(xv, cs.smask, c, list, !bad_blk)
+                  : 0u;
+      rounded = !bad_blk && nside > kSideMax;
+    } else {
+      rounded = !bad_blk &&
+                ((__builtin_amdgcn_ballot_w64(cs.smask != 0u) >> (16u * t)) & 0xffffull) != 0u;
+    }
     uint32_t uq[16];
     biased_values(cs, !rounded, uq);
     uint32_t dg[4][4];
