@@ -696,13 +696,41 @@ __device__ __forceinline__ void lds_read_tok6_images(uint32_t i0, uint32_t i1, i
       : "memory");
 }
 
+// The same for one group: (G, q) = (0, 0), (0, 1) into a[0], a[1].
+template <int JP>
+__device__ __forceinline__ void lds_read_tok6_images1(uint32_t i0, i32x4 (&a)[4]) {
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %[sv], exec\n"
+      "s_mov_b64 exec, %[m]\n"
+      "ds_read_b128 %0, %[p] offset:%[o0]\n"
+      "ds_read_b128 %1, %[p] offset:%[o1]\n"
+      "s_waitcnt lgkmcnt(0)\n"
+      "s_mov_b64 exec, %[sv]"
+      : "+v"(a[0]), "+v"(a[1]), [sv] "=&s"(saved)
+      : [p] "v"(i0), [m] "s"(kTokActiveLanes), [o0] "i"(1024 * JP), [o1] "i"(1024 * JP + 128)
+      : "memory");
+}
+
 // Exponents of the stage's two blocks and their side counts (one byte each)
 // for four of the lane's vectors, from their metadata at m[O .. O + 3]
 // (already offset to the stage).
 template <int O, int N>
 __device__ __forceinline__ void lds_read_tok6_meta(const uint32_t (&m)[N], u32x2 (&ex)[N],
                                                    uint32_t (&cnt)[N]) {
-  static_assert(O + 4 <= N, "four vectors from O");
+  static_assert(O + 4 <= N || N == 2, "four vectors from O (or the two of one group)");
+  if constexpr (N == 2) {
+    asm volatile(
+        "ds_read_b64 %0, %4\n"
+        "ds_read_b64 %1, %5\n"
+        "ds_read_u16 %2, %4 offset:512\n"
+        "ds_read_u16 %3, %5 offset:512\n"
+        "s_waitcnt lgkmcnt(0)"
+        : "=&v"(ex[0]), "=&v"(ex[1]), "=&v"(cnt[0]), "=&v"(cnt[1])
+        : "v"(m[0]), "v"(m[1])
+        : "memory");
+    return;
+  }
   static_assert(kCountOff == 512, "the offset below");
   asm volatile(
       "ds_read_b64 %0, %8\n"
@@ -777,7 +805,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
                                                               uint32_t ntok,
                                                               float* __restrict__ part_out,
                                                               Q6TokArgs ta) {
-  static_assert(NG == 2 || NG == 4, "eight or sixteen vectors");
+  static_assert(NG == 1 || NG == 2 || NG == 4, "four, eight or sixteen vectors");
   constexpr int GQ = 2 * NG;
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
   const uint32_t wave = uniform(threadIdx.x >> 6);
@@ -886,9 +914,10 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
 #pragma unroll
   for (int gq = 0; gq < GQ; ++gq) meta[gq] = sbase + L.expo + (2u * gq + vh) * L.expo_stride;
   const uint32_t o_lo = 8u * hs, o_hi = 16u + 8u * hs;  // bit offsets of the lane's scales
-  i32x4 A[NG / 2][4];  // per pair of groups: (G, q) = (2 p, 0), (2 p, 1), (2 p + 1, 0), (2 p + 1, 1)
+  // per pair of groups: (G, q) = (2 p, 0), (2 p, 1), (2 p + 1, 0), (2 p + 1, 1)
+  i32x4 A[(NG + 1) / 2][4];
 #pragma unroll
-  for (int pg = 0; pg < NG / 2; ++pg)
+  for (int pg = 0; pg < (NG + 1) / 2; ++pg)
 #pragma unroll
     for (int i = 0; i < 4; ++i) A[pg][i] = i32x4{0, 0, 0, 0};
   float part[GQ];
@@ -990,7 +1019,9 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_tokens_mfma(const uint8_t* __r
         int sc = 0;
         if constexpr (j < 8) {
           constexpr int h = j >> 2, tt = j & 3;
-          if constexpr ((j & 1) == 0) {
+          if constexpr ((j & 1) == 0 && NG == 1) {
+            lds_read_tok6_images1<j / 2>(i0, A[0]);
+          } else if constexpr ((j & 1) == 0) {
 #pragma unroll
             for (int pg = 0; pg < NG / 2; ++pg)
               lds_read_tok6_images<j / 2>(i0 + 2u * pg * gstride, i0 + (2u * pg + 1u) * gstride,
@@ -1329,6 +1360,12 @@ bool launch_tok6_any(const uint8_t* w, const float* x, float* y, uint32_t rows, 
                      uint32_t ntok, const Workspace& ws, hipStream_t s, hipError_t* err) {
   static const int nbs_env = env_int("SI_HIP_Q6K_TOK_NBS", 0);
   static const int w_env = env_int("SI_HIP_Q6K_TOK_WAVES", 0);
+  if (ntok <= 4u) {  // one group: 12 waves (16 on request)
+    const uint32_t nbs = nbs_env > 0 ? (uint32_t)nbs_env : 4u;
+    if (w_env == 16 ? launch_tok6<16, 1, 1>(w, x, y, rows, nb, ntok, nbs, ws, s, err)
+                    : launch_tok6<12, 1, 1>(w, x, y, rows, nb, ntok, nbs, ws, s, err))
+      return true;
+  }
   if (ntok > 8u)  // sixteen vectors: 8 waves (the registers of four groups)
     return launch_tok6<8, 1, 4>(w, x, y, rows, nb, ntok, nbs_env > 0 ? (uint32_t)nbs_env : 4u,
                                 ws, s, err);
