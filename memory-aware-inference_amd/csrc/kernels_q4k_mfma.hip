@@ -2083,8 +2083,9 @@ inline bool td_policy() {
   return v != 0;
 }
 
-// batch >= 2 vectors, up to four per pass over the weights (their activation
-// images share the LDS with the stage buffers)
+// batch >= 2 vectors: three to sixteen in one pass of the vectors-in-rows
+// kernel, two (or, under SI_HIP_TOKENS_TD=0, up to four) per pass of the
+// one-vector-per-MFMA kernel
 template <int QB>
 bool matmul_passes(const uint8_t* w, const float* x, float* y, uint32_t rows, uint32_t cols,
                    uint32_t batch, const Workspace& ws, hipStream_t s, hipError_t* err) {

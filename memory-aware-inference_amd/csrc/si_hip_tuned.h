@@ -18,13 +18,14 @@ bool launch_matvec_tuned(uint32_t type, const uint8_t* w, const float* x, float*
 // slices of at most 8 stages still fit the LDS).
 bool launch_q4k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
-// Q4_K, batch >= 2 vectors (batch-major x and y): up to four per pass over the
-// weights, which are decoded once per pass.
+// Q4_K, batch >= 2 vectors (batch-major x and y): two in one pass of the
+// one-vector-per-MFMA kernel, three to sixteen in one pass of the
+// vectors-in-rows kernel (the weights decoded once per pass).
 bool launch_q4k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, uint32_t batch, const Workspace& ws, hipStream_t s,
                             hipError_t* err);
-// Q5_K, one vector / batch >= 2 vectors, on the matrix cores (the Q4_K kernel
-// reading 176-byte blocks).
+// Q5_K, one vector / batch >= 2 vectors, on the matrix cores (the Q4_K kernels
+// reading 176-byte blocks; batches as for Q4_K).
 bool launch_q5k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
 bool launch_q5k_matmul_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
@@ -37,8 +38,9 @@ constexpr size_t kMaxGroupWeights = 8;  // = kMaxGroup of the kernels
 bool launch_matvec_group(uint32_t type, const uint8_t* const* w, const uint32_t* rows,
                          uint32_t count, uint32_t cols, const float* x, float* y,
                          const Workspace& ws, hipStream_t s, hipError_t* err);
-// Q6_K, one vector / batch >= 2 vectors (up to four per pass over the
-// weights), on the matrix cores.
+// Q6_K, one vector / batch >= 2 vectors (two in one pass of the per-vector
+// loop, three to sixteen in one pass of the vectors-in-rows kernel), on the
+// matrix cores.
 bool launch_q6k_matvec_mfma(const uint8_t* w, const float* x, float* y, uint32_t rows,
                             uint32_t cols, const Workspace& ws, hipStream_t s, hipError_t* err);
 // The Q6_K matvec with the greedy argmax of its output fused (rule: an
