@@ -629,7 +629,8 @@ def test_q6_k_matmul_many_head_shape(hip_ctx):
 # vectors than eight, two passes, the down projection's K and the head.
 @pytest.mark.parametrize("rows,cols,batch", [(33, 2560, 3), (1000, 5120, 5), (100, 1024, 6),
                                              (4096, 4096, 16), (5120, 17408, 8),
-                                             (1040, 2048, 11)])
+                                             (1040, 2048, 11), (17, 512, 4), (40, 1536, 16),
+                                             (2000, 5120, 13)])
 def test_q6_k_matmul_many_eight_per_pass(hip_ctx, rows, cols, batch):
     log(f"q6_k matmul_many {rows}x{cols} batch={batch}")
     w = si_hip.synth_matrix(14, seed=rows * 5 + cols + batch, rows=rows, cols=cols, threads=8)
