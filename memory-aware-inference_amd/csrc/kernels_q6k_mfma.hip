@@ -570,12 +570,12 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
 
 // ---- Several activation vectors in the MFMA rows ---------------------------
 //
-// A pass over the weights with up to eight activation vectors (matmul-many,
+// A pass over the weights with up to sixteen activation vectors (matmul-many,
 // replacing si_q6_k_matmul_many, metal.rs:1052-1262; the batched head of
 // qwen35_runtime.rs:2194-2197 takes up to eight candidates) puts the vectors
 // in the rows of the A operand of v_mfma_i32_16x16x32_i8, so that each
-// decoded weight meets all of them in one instruction.  K = 32 is one
-// 32-element chunk j of a block, which spans two of its scales (2 j, 2 j + 1):
+// decoded weight meets them in few instructions.  K = 32 is one 32-element
+// chunk j of a block, which spans two of its scales (2 j, 2 j + 1):
 //
 //  * B lane (k, n) holds weights 8 k .. 8 k + 7 of chunk j for tile row n as
 //    the int8 4 (q - 32): (q ^ 32) << 2 puts q - 32 in two's complement in
@@ -585,7 +585,8 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
 //    chunk's elements 16 h .. 16 h + 15 (scale 2 j + h) and zero elsewhere,
 //    from group G's images (tokens_common.h): lane (k, i) reads its 8 bytes
 //    only when k / 2 is its row's h; the other lanes hold zeros for the whole
-//    kernel.  Four MFMAs per chunk, (G, q) in {0, 1}^2, cover eight vectors.
+//    kernel.  Two MFMAs per chunk and group of four vectors (q in {0, 1}):
+//    groups G < NG, NG = 1, 2 or 4.
 //  * Result lane (2 v + h, n) holds the four digit sums of vector
 //    4 G + 2 q + v, row n, over scale 2 j + h alone, so T_d += sc C_d in
 //    integers (|C_d| <= 2^18, |T_d| < 2^29) and per block the lane adds
@@ -593,7 +594,7 @@ __global__ __launch_bounds__(WAVES * 64) void q6k_matvec_mfma(const uint8_t* __r
 //    2^eb) and 2^-2 the weights' factor 4.  The lanes h = 0 and 1 of a vector
 //    and row hold its even and odd scales; they are added once per tile.
 //
-// K slices.  Eight vectors' images take 8 KB per block, so a launch cuts K
+// K slices.  Each group's images take 4 KB per block, so a launch cuts K
 // into S slices of nbs blocks: workgroup g works on slice g / GS for tiles
 // g % GS, g % GS + GS, ..., keeping that slice's images; each wave takes
 // whole (tile, slice) pairs, their two-block stages one after another (the
