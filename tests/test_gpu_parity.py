@@ -1020,16 +1020,18 @@ def test_graph_replay_matches_eager(hip_ctx):
         hip_ctx.device_free(p)
 
 
-def test_graph_replay_matmul_many_groups(hip_ctx):
-    """Multi-token verify on the grouped path (a K-sliced launch whose stage
-    sums a second kernel adds up): 3, 8 and 16 vectors recorded in one graph,
-    replayed with other launches of the same workspace in between, bit for
-    bit equal to the eager calls and to the oracle's bound."""
+@pytest.mark.parametrize("t", [12, 13, 14])
+def test_graph_replay_matmul_many_groups(hip_ctx, t):
+    """Multi-token verify on the vectors-in-rows path (a K-sliced launch whose
+    stage or slice sums a second kernel adds up; Q4_K, Q5_K and Q6_K): 3, 8
+    and 16 vectors recorded in one graph, replayed with other launches of the
+    same workspace in between, bit for bit equal to the eager calls and to the
+    oracle's bound."""
     import ctypes as C
     lib = si_hip.lib()
     rows, cols = 1040, 5120
-    w = si_hip.synth_matrix(12, seed=3101, rows=rows, cols=cols, threads=8)
-    W = hip_ctx.upload_quant_weight_private(w, 12)
+    w = si_hip.synth_matrix(t, seed=3101 + t, rows=rows, cols=cols, threads=8)
+    W = hip_ctx.upload_quant_weight_private(w, t)
     X = si_hip.synth_normal(3102, 16 * cols).reshape(16, cols)
     d_x = hip_ctx.device_alloc(16 * cols * 4)
     hip_ctx.to_device(d_x, X)
@@ -1049,7 +1051,7 @@ def test_graph_replay_matmul_many_groups(hip_ctx):
     enqueue()
     ref = results()
     for b in range(16):
-        _, y64, ab = O.matvec(12, w, rows, cols, X[b], threads=8)
+        _, y64, ab = O.matvec(t, w, rows, cols, X[b], threads=8)
         assert_dot_close(ref[16][b], y64, ab, what=f"eager vector {b}")
         if b < 3:
             assert_dot_close(ref[3][b], y64, ab, what=f"eager vector {b} of 3")
