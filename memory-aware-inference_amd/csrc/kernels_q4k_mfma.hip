@@ -1614,6 +1614,7 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
 #pragma unroll
     for (int g = 0; g < NG; ++g) part[g] = 0.0f;
     uint32_t redo = 0u;  // bit g: the lane recomputes group g's stage exactly
+    float rbs[NG];  // (two or four groups: each group's rounded-block bound)
     uint32_t redo_out = 0u;  // (K slices: bit g, tok_reduce recomputes it)
     // (groups one after another: unrolled, their registers would add up)
 #pragma unroll 1
@@ -1646,8 +1647,9 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       // stage is still in its LDS buffer, the images beside it) before it is
       // left to the exact path, whose reads of weights from memory cost a
       // launch 2.5 us of tail at about one failing lane in 2e4: M = 4 20.5 ->
-      // 18.6 us.  The call costs the two- and four-group kernels spills in
-      // their main loop (M = 8 31 -> 45 us), so they go straight to it.
+      // 18.6 us.  Made here, the call costs the two- and four-group kernels
+      // spills in their main loop (M = 8 31 -> 45 us); they make it after the
+      // groups' loop (below).
       if (NG == 1 && __builtin_amdgcn_ballot_w64(failed) != 0u) {
         const StageF64 sp = tok_group_stage_f64<QB>(sa, nlive, iabase, xabase, eabase);
         const float err_p = sp.err + rb;
@@ -1662,7 +1664,42 @@ __global__ __launch_bounds__(WAVES * 64) void q4k_tokens_mfma(const uint8_t* __r
       }
 #pragma unroll
       for (int gg = 0; gg < NG; ++gg)
-        if ((uint32_t)gg == g) part[gg] = pg;
+        if ((uint32_t)gg == g) {
+          part[gg] = pg;
+          rbs[gg] = rb;
+        }
+    }
+    // Two or four groups: the lanes that failed try their groups' stages
+    // again in f64 once the groups' loop is done, one group at a time; what
+    // still fails goes to the exact path.  At M = 8 on Q4_K 17408x5120 about
+    // one stage lane in 2e4 fails the f32 check: left to tok_reduce, they
+    // gave 35 of its 544 workgroups an exact recompute (a second trip to
+    // memory) and the pass its tail.  Tried here, none is left: M = 8 / 16
+    // 28.5 / 42.6 -> 27.1 / 41.6 us, Q5_K 5120x5120 16.7 / 27.1 -> 15.3 /
+    // 25.1 us.
+    if constexpr (NG > 1) {
+      if (__builtin_amdgcn_ballot_w64(redo != 0u) != 0u) {
+#pragma unroll 1
+        for (uint32_t g = 0; g < ng; ++g) {
+          if (__builtin_amdgcn_ballot_w64((redo >> g) & 1u) == 0u) continue;
+          const uint32_t v = 4u * g + grp;
+          const StageF64 sp = tok_group_stage_f64<QB>(
+              sa, nlive, sbase + L.img + 4096u * (g * nbl + 4u * sl) + 16u * lane,
+              sbase + L.xsum + v * L.xsum_stride + 128u * sl,
+              sbase + L.expo + v * L.expo_stride + 16u * sl);
+          float rb = rbs[0];
+#pragma unroll
+          for (int gg = 1; gg < NG; ++gg)
+            if ((uint32_t)gg == g) rb = rbs[gg];
+          const float err_p = sp.err + rb;
+          if (((redo >> g) & 1u) && err_p * 1.01f <= kStageTol * (sp.abs_part - err_p)) {
+            redo &= ~(1u << g);
+#pragma unroll
+            for (int gg = 0; gg < NG; ++gg)
+              if ((uint32_t)gg == g) part[gg] = (float)sp.part;
+          }
+        }
+      }
     }
     // a K-sliced launch leaves the stages of lanes that failed the check to
     // tok_reduce (kPartRedo below); the others take the exact path here

@@ -149,8 +149,10 @@ __device__ __forceinline__ float rounded_err_all(uint32_t list) {
 // bps s + bps - 1 of the row (decode_unit_exact) times vector t of the
 // batch-major x, summed in f64 and rounded once.  The workgroup's 256
 // threads (256 rows of one vector) take such stages together from a queue in
-// LDS, eight at a time, 32 threads per stage and 32-weight units l, l + 32,
-// ... per thread; a stage past the queue's room is taken by its own thread.
+// LDS, eight at a time, 32 threads (half a wave) per stage and 32-weight units
+// l, l + 32, ... per thread, their f64 sums added with shuffles; a stage past
+// the queue's room is taken by its own thread.  A row with such a stage sums
+// its partials again in stage order, the first eight kept in registers.
 constexpr uint32_t kRedoQueue = 64;
 template <uint32_t T>
 __device__ __noinline__ float stage_exact(const uint8_t* __restrict__ w, uint32_t row,
@@ -181,7 +183,6 @@ __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part
   constexpr uint32_t kBytes = BlockBytes<T>::value;
   __shared__ uint32_t queue[kRedoQueue];  // (row in the workgroup) << 16 | stage
   __shared__ float value[kRedoQueue];
-  __shared__ double red[256];
   __shared__ uint32_t queued;
   const uint32_t tid = threadIdx.x, row = blockIdx.x * 256u + tid, t = blockIdx.y;
   const float* const p = part + (size_t)t * rows + row;
@@ -189,17 +190,24 @@ __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part
   const size_t step = (size_t)nv * rows;
   if (tid == 0u) queued = 0u;
   __syncthreads();
-  // the stages' sum with eight loads in flight, in stage order; the stages
-  // this thread's row leaves to the workgroup go to the queue
+  // stages base .. base + 7 of the row, eight loads in flight
+  auto load8 = [&](uint32_t base, float (&v)[8]) {
+#pragma unroll
+    for (uint32_t i = 0; i < 8u; ++i) v[i] = base + i < nstages ? p[(base + i) * step] : 0.0f;
+  };
+  // the stages' sum in stage order; the stages this thread's row leaves to
+  // the workgroup go to the queue; the first eight stay in registers for the
+  // second sum
   float sum = 0.0f;
+  float first[8];
   bool mine = false;
   if (row < rows) {
     for (uint32_t base = 0; base < nstages; base += 8u) {
       float v[8];
-#pragma unroll
-      for (uint32_t i = 0; i < 8u; ++i) v[i] = base + i < nstages ? p[(base + i) * step] : 0.0f;
+      load8(base, v);
 #pragma unroll
       for (uint32_t i = 0; i < 8u; ++i) {
+        if (base == 0u) first[i] = v[i];
         if (base + i >= nstages) continue;
         if (__float_as_uint(v[i]) == kPartRedo) {
           const uint32_t k = atomicAdd(&queued, 1u);
@@ -211,6 +219,8 @@ __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part
     }
   }
   if (__syncthreads_or(mine)) {
+    // queued stages eight at a time, one per 32 threads (half a wave), which
+    // sum their units' f64 dots with shuffles inside the half wave
     const uint32_t nq = min(queued, kRedoQueue);
     const uint32_t e = tid >> 5, l = tid & 31u;  // stage e of a batch; its units l, l + 32, ...
     for (uint32_t k0 = 0; k0 < nq; k0 += 8u) {
@@ -229,29 +239,36 @@ __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part
           }
         }
       }
-      red[tid] = acc;
-      __syncthreads();
-      for (uint32_t h = 16u; h > 0u; h >>= 1) {  // each stage's 32 thread sums
-        if (l < h) red[tid] += red[tid + h];
-        __syncthreads();
-      }
-      if (l == 0u && k < nq) value[k] = (float)red[tid];
-      __syncthreads();
+#pragma unroll
+      for (int h = 16; h > 0; h >>= 1) acc += __shfl_xor(acc, h, 32);
+      if (l == 0u && k < nq) value[k] = (float)acc;
     }
+    __syncthreads();
   }
   if (row >= rows) return;
   if (mine) {  // the sum again, with the recomputed stages
+    const uint32_t nq = min(queued, kRedoQueue);
     sum = 0.0f;
-    for (uint32_t st = 0; st < nstages; ++st) {
-      float v = p[st * step];
-      if (__float_as_uint(v) == kPartRedo) {
-        uint32_t k = 0;
-        const uint32_t nq = min(queued, kRedoQueue);
-        while (k < nq && queue[k] != ((tid << 16) | st)) ++k;
-        v = k < nq ? value[k]
-                   : stage_exact<T>(w, row, nb, bps * st, min(bps * st + bps, nb), xt);
+    for (uint32_t base = 0; base < nstages; base += 8u) {
+      float v[8];
+      if (base == 0u) {
+#pragma unroll
+        for (uint32_t i = 0; i < 8u; ++i) v[i] = first[i];
+      } else {
+        load8(base, v);
       }
-      sum += v;
+#pragma unroll
+      for (uint32_t i = 0; i < 8u; ++i) {
+        if (base + i >= nstages) continue;
+        const uint32_t st = base + i;
+        if (__float_as_uint(v[i]) == kPartRedo) {
+          uint32_t k = 0;
+          while (k < nq && queue[k] != ((tid << 16) | st)) ++k;
+          v[i] = k < nq ? value[k]
+                        : stage_exact<T>(w, row, nb, bps * st, min(bps * st + bps, nb), xt);
+        }
+        sum += v[i];
+      }
     }
   }
   y[(size_t)t * rows + row] = sum;
