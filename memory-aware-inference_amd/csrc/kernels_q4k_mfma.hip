@@ -1160,9 +1160,9 @@ __device__ __forceinline__ float block_dot_tok(const TokStage<QB>& st, int b,
 }
 
 // block_dot_tok's second try for a lane whose stage failed its check: the
-// same eight MFMAs, then the digit sums combined and scaled exactly in f64
-// (each unit's |sum_d 256^d c_d| < 2^41, the scaled sum of eight < 2^50) and
-// the min term's products (exact in f64) summed in f64.  What rounding is
+// same eight MFMAs and the same int32 digit sums T_d = sum_u sc_u C_u[d], then
+// sum_d 256^d T_d (< 2^50) formed exactly in f64 and the min term's products
+// (exact in f64) summed in f64.  What rounding is
 // left is that of the f32 unit sums xs (2^-24 each) and the f64 steps, so
 // err = 2^(eb-24) 1.01 |dmin| sum_u m_u |xs_u| + 2^(eb-48) of the two terms,
 // about an eighth of the fast path's bound.
@@ -1177,15 +1177,19 @@ __device__ __forceinline__ double block_dot_tok_f64(const TokStage<QB>& st, int 
   const uint32_t mn47 = ((h[3] >> 4) & 0x0f0f0f0fu) | ((h[2] >> 2) & 0x30303030u);
   i32x4 c[8];
   block_mfma_tok<QB>(st, b, a, c);
-  double tc = 0.0, um = 0.0, ua = 0.0;
+  int t[4] = {0, 0, 0, 0};
 #pragma unroll
   for (int u = 0; u < 8; ++u) {
-    const double sc = (double)((((u < 4 ? sc03 : sc47) >> (8 * (u & 3))) & 0xffu));
+    const int s = (int)(((u < 4 ? sc03 : sc47) >> (8 * (u & 3))) & 0xffu);
+#pragma unroll
+    for (int d = 0; d < 4; ++d) t[d] = mad_i24(s, c[u][d], t[d]);
+  }
+  const double tc =
+      fma(fma(fma((double)t[3], 256.0, (double)t[2]), 256.0, (double)t[1]), 256.0, (double)t[0]);
+  double um = 0.0, ua = 0.0;
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
     const double mn = (double)((((u < 4 ? mn03 : mn47) >> (8 * (u & 3))) & 0xffu));
-    const double su = fma(fma(fma((double)c[u][3], 256.0, (double)c[u][2]), 256.0,
-                              (double)c[u][1]),
-                          256.0, (double)c[u][0]);
-    tc = fma(sc, su, tc);
     const double xu = (double)__uint_as_float(xs[u >> 2][u & 3]);
     um = fma(mn, xu, um);
     ua = fma(mn, fabs(xu), ua);
