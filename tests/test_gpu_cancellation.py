@@ -128,7 +128,8 @@ def test_cancelling_fused_mlp(ctx):
     assert np.all(ratio <= 1.0)
 
 
-@pytest.mark.parametrize("t,batch", [(Q4, 2), (Q4, 4), (Q4, 16), (Q5, 4), (Q5, 8), (Q5, 16)])
+@pytest.mark.parametrize("t,batch", [(Q4, 2), (Q4, 4), (Q4, 8), (Q4, 13), (Q4, 16), (Q5, 4), (Q5, 8),
+                                     (Q5, 16)])
 def test_cancelling_matmul_many(ctx, t, batch):
     rows, cols = 4096, 5120
     log(f"cancelling matmul-many type {t} M={batch}")
