@@ -1808,9 +1808,8 @@ bool launch_tokens_td(const uint8_t* w, const float* x, float* y, uint32_t rows,
                      nb, ntok, ws.scratch, ta);
   *err = hipGetLastError();
   if (*err == hipSuccess && ta.slices > 1u) {
-    hipLaunchKernelGGL(tok_reduce<QB == 5 ? kTypeQ5K : kTypeQ4K>, dim3((rows + 255u) / 256u, ntok),
-                       dim3(256), 0, s,
-                       ws.scratch, y, rows, nstages, 4u * NG, w, x, nb, 4u);
+    launch_tok_reduce<QB == 5 ? kTypeQ5K : kTypeQ4K>(ws.scratch, y, rows, nstages, 4u * NG, ntok,
+                                                     w, x, nb, 4u, s);
     *err = hipGetLastError();
   }
   return true;

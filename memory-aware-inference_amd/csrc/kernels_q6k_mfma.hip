@@ -1345,8 +1345,7 @@ bool launch_tok6(const uint8_t* w, const float* x, float* y, uint32_t rows, uint
                      ws.scratch, ta);
   *err = hipGetLastError();
   if (*err == hipSuccess) {
-    hipLaunchKernelGGL(tok_reduce<kTypeQ6K>, dim3((rows + 255u) / 256u, ntok), dim3(256), 0, s,
-                       ws.scratch, y, rows, ta.slices, 4u * NG, w, x, nb, ta.nbs);
+    launch_tok_reduce<kTypeQ6K>(ws.scratch, y, rows, ta.slices, 4u * NG, ntok, w, x, nb, ta.nbs, s);
     *err = hipGetLastError();
   }
   return true;

@@ -148,12 +148,15 @@ __device__ __forceinline__ float rounded_err_all(uint32_t list) {
 // exact dot instead: quant.rs's per-weight values of blocks bps s ..
 // bps s + bps - 1 of the row (decode_unit_exact) times vector t of the
 // batch-major x, summed in f64 and rounded once.  The workgroup's 256
-// threads (256 rows of one vector) take such stages together from a queue in
-// LDS, eight at a time, 32 threads (half a wave) per stage and 32-weight units
-// l, l + 32, ... per thread, their f64 sums added with shuffles; a stage past
-// the queue's room is taken by its own thread.  A row with such a stage sums
-// its partials again in stage order, the first eight kept in registers.
+// threads take such stages together from a queue in LDS, eight at a time,
+// 32 threads (half a wave) per stage and 32-weight units l, l + 32, ... per
+// thread, their f64 sums added with shuffles; a stage past the queue's room
+// is taken by its own thread.  A thread with such a stage sums its rows'
+// partials again in stage order, the first eight stages kept in registers.
+// R rows per thread: 1, or 4 with 16-byte loads and stores (launch_tok_reduce
+// takes 4 when the rows, y and the grid allow it); each row's sum is the same.
 constexpr uint32_t kRedoQueue = 64;
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 template <uint32_t T>
 __device__ __noinline__ float stage_exact(const uint8_t* __restrict__ w, uint32_t row,
                                           uint32_t nb, uint32_t b0, uint32_t b1,
@@ -173,48 +176,71 @@ __device__ __noinline__ float stage_exact(const uint8_t* __restrict__ w, uint32_
   return (float)acc;
 }
 
-template <uint32_t T>
+template <uint32_t T, int R>
 __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part,
                                                   float* __restrict__ y, uint32_t rows,
                                                   uint32_t nstages, uint32_t nv,
                                                   const uint8_t* __restrict__ w,
                                                   const float* __restrict__ x, uint32_t nb,
                                                   uint32_t bps) {
+  static_assert(R == 1 || R == 4, "one or four rows per thread");
   constexpr uint32_t kBytes = BlockBytes<T>::value;
   __shared__ uint32_t queue[kRedoQueue];  // (row in the workgroup) << 16 | stage
   __shared__ float value[kRedoQueue];
   __shared__ uint32_t queued;
-  const uint32_t tid = threadIdx.x, row = blockIdx.x * 256u + tid, t = blockIdx.y;
+  const uint32_t tid = threadIdx.x, t = blockIdx.y;
+  const uint32_t rw = (uint32_t)R * tid;                    // the thread's first row in the workgroup
+  const uint32_t row = blockIdx.x * (256u * R) + rw;        // its rows row .. row + R - 1
   const float* const p = part + (size_t)t * rows + row;
   const float* const xt = x + (size_t)t * nb * kBlockElems;
   const size_t step = (size_t)nv * rows;
   if (tid == 0u) queued = 0u;
   __syncthreads();
-  // stages base .. base + 7 of the row, eight loads in flight
-  auto load8 = [&](uint32_t base, float (&v)[8]) {
+  // stages base .. base + 7 of the thread's rows, eight loads in flight
+  auto load8 = [&](uint32_t base, float (&v)[8][R]) {
 #pragma unroll
-    for (uint32_t i = 0; i < 8u; ++i) v[i] = base + i < nstages ? p[(base + i) * step] : 0.0f;
+    for (uint32_t i = 0; i < 8u; ++i) {
+      if (base + i < nstages) {
+        if constexpr (R == 4) {
+          const f32x4 q = *reinterpret_cast<const f32x4*>(p + (base + i) * step);
+#pragma unroll
+          for (int c = 0; c < R; ++c) v[i][c] = q[c];
+        } else {
+          v[i][0] = p[(base + i) * step];
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < R; ++c) v[i][c] = 0.0f;
+      }
+    }
   };
-  // the stages' sum in stage order; the stages this thread's row leaves to
-  // the workgroup go to the queue; the first eight stay in registers for the
-  // second sum
-  float sum = 0.0f;
-  float first[8];
+  // the stages' sums in stage order; the stages the thread's rows leave to
+  // the workgroup go to the queue
+  float sum[R];
+  float first[8][R];
+#pragma unroll
+  for (int c = 0; c < R; ++c) sum[c] = 0.0f;
   bool mine = false;
-  if (row < rows) {
+  if (row < rows) {  // (rows a multiple of R)
     for (uint32_t base = 0; base < nstages; base += 8u) {
-      float v[8];
+      float v[8][R];
       load8(base, v);
 #pragma unroll
       for (uint32_t i = 0; i < 8u; ++i) {
-        if (base == 0u) first[i] = v[i];
-        if (base + i >= nstages) continue;
-        if (__float_as_uint(v[i]) == kPartRedo) {
-          const uint32_t k = atomicAdd(&queued, 1u);
-          if (k < kRedoQueue) queue[k] = (tid << 16) | (base + i);
-          mine = true;
+        if (base == 0u) {
+#pragma unroll
+          for (int c = 0; c < R; ++c) first[i][c] = v[i][c];
         }
-        sum += v[i];
+        if (base + i >= nstages) continue;
+#pragma unroll
+        for (int c = 0; c < R; ++c) {
+          if (__float_as_uint(v[i][c]) == kPartRedo) {
+            const uint32_t k = atomicAdd(&queued, 1u);
+            if (k < kRedoQueue) queue[k] = ((rw + (uint32_t)c) << 16) | (base + i);
+            mine = true;
+          }
+          sum[c] += v[i][c];
+        }
       }
     }
   }
@@ -227,7 +253,7 @@ __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part
       const uint32_t k = k0 + e;
       double acc = 0.0;
       if (k < nq) {
-        const uint32_t r = blockIdx.x * 256u + (queue[k] >> 16), st = queue[k] & 0xffffu;
+        const uint32_t r = blockIdx.x * (256u * R) + (queue[k] >> 16), st = queue[k] & 0xffffu;
         for (uint32_t uu = l; uu < 8u * bps; uu += 32u) {
           const uint32_t b = bps * st + (uu >> 3), u = uu & 7u;  // unit u of block b
           if (b < nb) {
@@ -246,14 +272,17 @@ __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part
     __syncthreads();
   }
   if (row >= rows) return;
-  if (mine) {  // the sum again, with the recomputed stages
+  if (mine) {  // the sums again, with the recomputed stages (unchanged for rows without one)
     const uint32_t nq = min(queued, kRedoQueue);
-    sum = 0.0f;
+#pragma unroll
+    for (int c = 0; c < R; ++c) sum[c] = 0.0f;
     for (uint32_t base = 0; base < nstages; base += 8u) {
-      float v[8];
+      float v[8][R];
       if (base == 0u) {
 #pragma unroll
-        for (uint32_t i = 0; i < 8u; ++i) v[i] = first[i];
+        for (uint32_t i = 0; i < 8u; ++i)
+#pragma unroll
+          for (int c = 0; c < R; ++c) v[i][c] = first[i][c];
       } else {
         load8(base, v);
       }
@@ -261,17 +290,48 @@ __global__ __launch_bounds__(256) void tok_reduce(const float* __restrict__ part
       for (uint32_t i = 0; i < 8u; ++i) {
         if (base + i >= nstages) continue;
         const uint32_t st = base + i;
-        if (__float_as_uint(v[i]) == kPartRedo) {
-          uint32_t k = 0;
-          while (k < nq && queue[k] != ((tid << 16) | st)) ++k;
-          v[i] = k < nq ? value[k]
-                        : stage_exact<T>(w, row, nb, bps * st, min(bps * st + bps, nb), xt);
+#pragma unroll
+        for (int c = 0; c < R; ++c) {
+          float vc = v[i][c];
+          if (__float_as_uint(vc) == kPartRedo) {
+            const uint32_t key = ((rw + (uint32_t)c) << 16) | st;
+            uint32_t k = 0;
+            while (k < nq && queue[k] != key) ++k;
+            vc = k < nq ? value[k]
+                        : stage_exact<T>(w, row + (uint32_t)c, nb, bps * st,
+                                         min(bps * st + bps, nb), xt);
+          }
+          sum[c] += vc;
         }
-        sum += v[i];
       }
     }
   }
-  y[(size_t)t * rows + row] = sum;
+  float* const yo = y + (size_t)t * rows + row;
+  if constexpr (R == 4) {
+    *reinterpret_cast<f32x4*>(yo) = f32x4{sum[0], sum[1], sum[2], sum[3]};
+  } else {
+    yo[0] = sum[0];
+  }
+}
+
+// The reduce of a sliced launch of ntok vectors: four rows a thread when the
+// row count is a multiple of 4, y is 16-byte aligned (the scratch always is)
+// and the grid still gives every CU two workgroups, else one.  The Q6_K head
+// (151,936 rows) at M = 4 / 8 / 16: 144.6 / 180.1 / 321.5 -> 143.6 / 176.8 /
+// 317.4 us a call; Q4_K 17408 rows at M = 16 (one workgroup a CU) lost
+// 0.4 us, so it keeps one row a thread.
+template <uint32_t T>
+void launch_tok_reduce(const float* part, float* y, uint32_t rows, uint32_t nstages, uint32_t nv,
+                       uint32_t ntok, const uint8_t* w, const float* x, uint32_t nb, uint32_t bps,
+                       hipStream_t s) {
+  const uint32_t g4 = (rows + 1023u) / 1024u;
+  if (rows % 4u == 0u && ((uintptr_t)y & 15u) == 0u &&
+      (uint64_t)g4 * ntok >= 2u * (uint64_t)cu_count())
+    hipLaunchKernelGGL((tok_reduce<T, 4>), dim3(g4, ntok), dim3(256), 0, s, part, y, rows, nstages,
+                       nv, w, x, nb, bps);
+  else
+    hipLaunchKernelGGL((tok_reduce<T, 1>), dim3((rows + 255u) / 256u, ntok), dim3(256), 0, s, part,
+                       y, rows, nstages, nv, w, x, nb, bps);
 }
 
 }  // namespace

@@ -145,6 +145,24 @@ def test_cancelling_matmul_many(ctx, t, batch):
         _check_rows(ys[b], y64, ab, rows, f"type {t} M={batch} vector {b}")
 
 
+def test_cancelling_matmul_many_four_row_reduce(hip_ctx):
+    # 33000 rows x 16 vectors: tok_reduce takes four rows a thread (528
+    # workgroups of 1024 rows, the last one partial, and a partial last tile),
+    # and the fully cancelling rows reach its exact recompute there
+    t, rows, cols, batch = Q4, 33000, 5120, 16
+    log(f"cancelling matmul-many type {t} {rows}x{cols} M={batch}")
+    w = CB.matrix(t, rows, cols, seed=97)
+    X = np.stack([_x(970 + b, cols) for b in range(batch)])
+    W = hip_ctx.upload_quant_weight_private(w, t)
+    try:
+        ys = hip_ctx.gguf_quant_matmul_many_weight(W, rows, cols, batch, X)
+    finally:
+        W.free()
+    for b in range(batch):
+        _, y64, ab = O.matvec(t, w, rows, cols, X[b], threads=16)
+        _check_rows(ys[b], y64, ab, rows, f"type {t} {rows} rows M={batch} vector {b}")
+
+
 def test_cancelling_grouped(ctx):
     cols = 5120
     rows = [6144, 1024, 1024]
